@@ -1,0 +1,186 @@
+"""Benchmark: DIP MLP decode tok/s on the Qwen3-32B-shape 64-layer int4 stack
+(keep 0.6) on one MI355X, with achieved HBM GB/s against the 8 TB/s peak.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--shape qwen3-32b]
+                    [--keep 0.6] [--cpu-seconds 20] [--no-cpu]
+
+A step is one decode token through all layers (64 layers,
+H=5120, I=25600, k=15360, every layer resident in HBM).  Weights are
+synthetic N(0, 0.02) draws quantized int4 g128; x_t ~ N(0, 1) bf16, a fresh
+vector per token.  One token = one HIP-graph replay of all layers; the timed
+region covers exactly `steps` tokens, bracketed by device synchronisation.
+
+Besides the JSON line's `value` (tok/s) it reports:
+  roofline      the dominant kernel's algorithmic bytes / its average
+                duration (HIP events around each launch, on its stream);
+  step_*        whole-token bytes / time against the same peak;
+  cpu_baseline  the reference's forward run literally with PyTorch CPU ops
+                (oracle.torch_cpu_forward) on one layer of the same weights,
+                on this host's cores, scaled to tok/s of the full stack.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "dynamic-input-pruning_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "DIP MLP decode tok/s, Qwen3-32B shape int4 k=0.6; achieved HBM GB/s vs peak"
+
+
+def cpu_baseline(stack, seconds: float):
+    """Time the reference's CPU path on layer 0 of the stack (bounded sample)."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import dip_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    lw = stack.w[0]
+    t = {k: v.cpu() for k, v in lw.items()}
+    x = torch.randn(stack.hidden, generator=torch.Generator().manual_seed(123)).to(torch.bfloat16)
+    args = (t["gate_qw"], t["gate_sc"], t["up_qw"], t["up_sc"], t["down_t_qw"], t["down_t_sc"],
+            x, stack.k)
+    O.torch_cpu_forward(*args)  # warm-up
+    times = []
+    t0 = time.perf_counter()
+    while True:
+        a = time.perf_counter()
+        O.torch_cpu_forward(*args)
+        times.append(time.perf_counter() - a)
+        if len(times) >= 3 and time.perf_counter() - t0 > seconds:
+            break
+        if len(times) >= 50:
+            break
+    t_layer = float(np.median(times))
+    return {
+        "value": 1.0 / (t_layer * stack.layers),
+        "unit": "tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"reference forward with PyTorch CPU ops (dequantize per call, F.linear, "
+                   f"F.silu, top-k, index_select, matmul) on 1 layer of the same "
+                   f"H={stack.hidden} I={stack.inter} k={stack.k} weights, median of "
+                   f"{len(times)} runs = {t_layer * 1e3:.1f} ms/layer, scaled to "
+                   f"{stack.layers} layers"),
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--shape", default="qwen3-32b")
+    ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--keep", type=float, default=0.6)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--down-mode", type=int, default=None)
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the single-GPU DIP decode path; multi-GPU runs are not "
+              "part of this build (--gpus must be 1)", file=sys.stderr)
+        return 2
+
+    import torch
+    import _dip_hip as K
+    from dip_stack import SHAPES, DIPStack
+
+    if args.down_mode is not None:
+        K.set_down_dequant_mode(args.down_mode)
+    shape = dict(SHAPES[args.shape])
+    if args.layers:
+        shape["layers"] = args.layers
+    dev = torch.device("cuda:0")
+    print(f"[bench] building {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
+          flush=True)
+    stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    n_tok = args.warmup + args.steps
+    xs = (torch.randn(n_tok, shape["hidden"], device=dev, generator=gen)).to(torch.bfloat16)
+    stack.capture()
+    print("[bench] graph captured", file=sys.stderr, flush=True)
+
+    for i in range(args.warmup):
+        stack.step(xs[i])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.warmup, n_tok):
+        stack.step(xs[i])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms_total = e0.elapsed_time(e1)
+    ms_step = ms_total / args.steps
+    tok_s = 1000.0 / ms_step
+    step_gbs = stack.bytes_per_token / (ms_step * 1e-3) / 1e9
+    print(f"[bench] {args.steps} tokens: {ms_step:.4f} ms/token (wall {wall:.3f} s)",
+          file=sys.stderr, flush=True)
+
+    # per-stage kernel durations: HIP events around graph replays of each
+    # stage's launches (one per layer, back to back)
+    stages = stack.stage_times_ms(reps=3)
+    H, I, k = stack.hidden, stack.inter, stack.k
+    row = H // 2 + 2 * (H // 128)
+    stage_bytes = {"gate_silu": I * row, "topk": 2 * I,
+                   "up_gather_h": k * row, "down_gather": k * row}
+    dom = max(stages, key=stages.get)
+    ach = stage_bytes[dom] / (stages[dom] * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "bytes_per_launch": stage_bytes[dom],
+                "avg_launch_ms": round(stages[dom], 5)}
+    print(f"[bench] stages (ms): {json.dumps({k_: round(v, 5) for k_, v in stages.items()})}",
+          file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] timing CPU baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(stack, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.shape}-shape {stack.layers}-layer int4 g128 DIP MLP decode, "
+                        f"batch 1, keep {args.keep}, weights resident in HBM",
+            "hidden": H, "inter": I, "layers": stack.layers, "k": k,
+            "weights": "int4 g128 symmetric, bf16 scales; N(0,0.02) draws",
+            "activations": "bf16, fp32 accumulate",
+            "bytes_per_token": stack.bytes_per_token,
+        },
+        "step_hbm_gbs": round(step_gbs, 1),
+        "step_roofline_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "stage_ms": {k_: round(v, 5) for k_, v in stages.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,452 @@
+"""ctypes binding of libdip_hip.so (the gfx950 DIP decode kernels).
+
+Every function here validates dtype / device / shape / contiguity on the host,
+passes raw device pointers plus torch's current HIP stream to the C ABI
+declared in include/dip_hip.h, and raises ``RuntimeError`` on any non-zero
+status.  There is no fallback: if the library is not built, importing this
+module raises ``ImportError``.
+
+Workspaces are cached per (device, tag) as zero-filled byte tensors; the
+kernels leave them zeroed again after every call, and every call that shares
+one is ordered on the same stream (the module layer runs layers one after the
+other, like the reference's SharedBuffers, dip_stream_predispatch.py:123-138).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("DIP_HIP_LIB", _HERE / "libdip_hip.so"))
+HEADER_PATH = _HERE.parent / "include" / "dip_hip.h"
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `python dynamic-input-pruning_amd/build.py` "
+        "(or __graft_entry__.build()) first")
+
+lib = ctypes.CDLL(str(LIB_PATH))
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_sz = ctypes.c_size_t
+
+_SIGS = {
+    "dip_status_string": ([_i32], ctypes.c_char_p),
+    "dip_version": ([], _i32),
+    "dip_topk_max_n": ([], _i64),
+    "dip_int4_gemv": ([_p, _p, _p, _p, _i64, _i64, _i32, _p], _i32),
+    "dip_topk_workspace_size": ([_i64], _sz),
+    "dip_topk_select": ([_p, _p, _i64, _i64, _p, _sz, _p], _i32),
+    "dip_topk_meta": ([_p, _p, _p], _i32),
+    "dip_int4_gather_gemv": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dip_up_gather_h": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dip_gather_down_workspace_size": ([_i64, _i64], _sz),
+    "dip_int4_gather_down": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p], _i32),
+    "dip_ca_fused_gemv": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
+                          _i32),
+    "dip_ca_down": ([_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p], _i32),
+    "dip_ca_assemble": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p], _i32),
+    "dip_dequant_rows": ([_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p], _i32),
+    "dip_mlp_workspace_size": ([_i64, _i64, _i64], _sz),
+    "dip_mlp_decode": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz,
+                        _p], _i32),
+    "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
+    "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
+    "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
+    "dip_set_tuning": ([_i32, _i32], _i32),
+    "dip_get_tuning": ([_i32], _i32),
+}
+for _name, (_args, _res) in _SIGS.items():
+    _fn = getattr(lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _res
+
+GROUP_SIZE = 128
+
+
+def status_string(st: int) -> str:
+    return lib.dip_status_string(st).decode()
+
+
+def _check(st: int, fn: str) -> None:
+    if st != 0:
+        raise RuntimeError(f"{fn} failed: {status_string(st)} (status {st})")
+
+
+# ---------------------------------------------------------------------------
+# host-side validation
+# ---------------------------------------------------------------------------
+def _dev(*ts: torch.Tensor) -> torch.device:
+    d = ts[0].device
+    if d.type != "cuda":
+        raise RuntimeError(f"expected tensors on a HIP device, got {d}")
+    for t in ts[1:]:
+        if t.device != d:
+            raise RuntimeError(f"tensors on different devices: {d} vs {t.device}")
+    return d
+
+
+def _want(t: torch.Tensor, dtype: torch.dtype, name: str, shape=None) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous() or t.data_ptr() % 16 != 0:
+        t = t.contiguous()
+        if t.data_ptr() % 16 != 0:
+            t = t.clone()
+    return t
+
+
+def _weights(qw: torch.Tensor, sc: torch.Tensor, name: str):
+    if qw.dim() != 2 or sc.dim() != 2:
+        raise RuntimeError(f"{name}: qweight and scales must be 2-D")
+    rows, half = qw.shape
+    cols = half * 2
+    if cols % GROUP_SIZE != 0:
+        raise RuntimeError(f"{name}: in_features {cols} is not a multiple of {GROUP_SIZE}")
+    qw = _want(qw, torch.int8, f"{name}.qweight")
+    sc = _want(sc, torch.bfloat16, f"{name}.scales", (rows, cols // GROUP_SIZE))
+    return qw, sc, rows, cols
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+_ws_lock = threading.Lock()
+_ws_cache: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int, tag: str) -> torch.Tensor:
+    """Zero-filled device workspace of at least `nbytes`, cached per
+    (device, tag).  Growing replaces it with a larger zeroed buffer."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), tag)
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+        return buf
+
+
+# ---------------------------------------------------------------------------
+# ops
+# ---------------------------------------------------------------------------
+def int4_gemv(qweight, scales, x, act: int = 0, out=None):
+    """out[r] = bf16(sum (q*s)[r,:] . x); act=1 applies bf16(silu(.))."""
+    qweight, scales, rows, cols = _weights(qweight, scales, "int4_gemv")
+    dev = _dev(qweight, scales, x)
+    x = _want(x.reshape(-1), torch.bfloat16, "x", (cols,))
+    if out is None:
+        out = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    _check(lib.dip_int4_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(out), rows, cols,
+                             int(act), _stream(dev)), "dip_int4_gemv")
+    return out
+
+
+def topk_select(s: torch.Tensor, k: int, out=None):
+    """int32 [k] indices, bit-exact with topk_ops::topk_select."""
+    dev = _dev(s)
+    s = _want(s.reshape(-1), torch.bfloat16, "s")
+    n = s.numel()
+    k = int(k)
+    if k < 0:
+        raise RuntimeError("k must be >= 0")
+    if n > lib.dip_topk_max_n():
+        raise RuntimeError(f"top-k supports n <= {lib.dip_topk_max_n()}, got {n}")
+    if out is None:
+        out = torch.empty(k, dtype=torch.int32, device=dev)
+    nbytes = lib.dip_topk_workspace_size(n)
+    ws = workspace(dev, nbytes, "topk")
+    _check(lib.dip_topk_select(_ptr(s), _ptr(out), n, k, _ptr(ws), ws.numel(), _stream(dev)),
+           "dip_topk_select")
+    return out
+
+
+def topk_meta(device=None) -> dict:
+    """Thresholds and tier sizes of the last top-k run on `device`
+    (t_lo, t_strict as fp32; count_a, count_b)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    ws = workspace(dev, lib.dip_topk_workspace_size(0), "topk")
+    m = torch.empty(16, dtype=torch.uint8, device=dev)
+    _check(lib.dip_topk_meta(_ptr(ws), _ptr(m), _stream(dev)), "dip_topk_meta")
+    f = m[:8].view(torch.float32).cpu()
+    i = m[8:].view(torch.int32).cpu()
+    return dict(t_lo=float(f[0]), t_strict=float(f[1]), count_a=int(i[0]), count_b=int(i[1]))
+
+
+def gate_silu_topk(qweight, scales, x, k, g=None, idx=None):
+    """g = bf16(silu(gate(x))) then idx = topk(|g|, k) (int32, reference
+    order), both on the device with no host synchronisation."""
+    qweight, scales, rows, cols = _weights(qweight, scales, "gate")
+    dev = _dev(qweight, scales, x)
+    x = _want(x.reshape(-1), torch.bfloat16, "x", (cols,))
+    k = int(k)
+    if not 0 <= k:
+        raise RuntimeError("k must be >= 0")
+    if rows > lib.dip_topk_max_n():
+        raise RuntimeError(f"top-k supports n <= {lib.dip_topk_max_n()}, got {rows}")
+    if g is None:
+        g = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    if idx is None:
+        idx = torch.empty(k, dtype=torch.int32, device=dev)
+    ws = workspace(dev, lib.dip_topk_workspace_size(rows), "topk")
+    st = _stream(dev)
+    _check(lib.dip_int4_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(g), rows, cols, 1, st),
+           "dip_int4_gemv")
+    if k:
+        _check(lib.dip_topk_select(_ptr(g), _ptr(idx), rows, k, _ptr(ws), ws.numel(), st),
+               "dip_topk_select")
+    return g, idx
+
+
+def _indices(idx: torch.Tensor, name="indices") -> torch.Tensor:
+    if idx.dtype == torch.int64:
+        idx = idx.to(torch.int32)
+    return _want(idx.reshape(-1), torch.int32, name)
+
+
+def int4_gather_gemv(qweight, scales, x, indices, out=None):
+    qweight, scales, rows, cols = _weights(qweight, scales, "int4_gather_gemv")
+    dev = _dev(qweight, scales, x, indices)
+    x = _want(x.reshape(-1), torch.bfloat16, "x", (cols,))
+    indices = _indices(indices)
+    k = indices.numel()
+    if out is None:
+        out = torch.empty(k, dtype=torch.bfloat16, device=dev)
+    _check(lib.dip_int4_gather_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(indices),
+                                    _ptr(out), rows, cols, k, _stream(dev)),
+           "dip_int4_gather_gemv")
+    return out
+
+
+def up_gather_h(qweight, scales, x, indices, g, out=None):
+    """h[j] = bf16(g[indices[j]] * bf16(up[indices[j]] . x))."""
+    qweight, scales, rows, cols = _weights(qweight, scales, "up_gather_h")
+    dev = _dev(qweight, scales, x, indices, g)
+    x = _want(x.reshape(-1), torch.bfloat16, "x", (cols,))
+    g = _want(g.reshape(-1), torch.bfloat16, "g", (rows,))
+    indices = _indices(indices)
+    k = indices.numel()
+    if out is None:
+        out = torch.empty(k, dtype=torch.bfloat16, device=dev)
+    _check(lib.dip_up_gather_h(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(indices), _ptr(g),
+                               _ptr(out), rows, cols, k, _stream(dev)), "dip_up_gather_h")
+    return out
+
+
+def int4_gather_down(down_t, scales, h, indices=None, out=None):
+    """y[o] = bf16(sum_j h[j] * (q*s)[row_j, o]); row_j = indices[j] or j."""
+    down_t, scales, rows, out_f = _weights(down_t, scales, "int4_gather_down")
+    dev = _dev(down_t, scales, h)
+    h = _want(h.reshape(-1), torch.bfloat16, "h_sel")
+    k = h.numel()
+    if indices is not None:
+        indices = _indices(indices)
+        if indices.numel() != k:
+            raise RuntimeError("indices and h_sel must have the same length")
+    elif k > rows:
+        raise RuntimeError(f"h_sel has {k} entries but down_t_sel has {rows} rows")
+    if out is None:
+        out = torch.empty(out_f, dtype=torch.bfloat16, device=dev)
+    nbytes = lib.dip_gather_down_workspace_size(k, out_f)
+    ws = workspace(dev, nbytes, "down")
+    _check(lib.dip_int4_gather_down(_ptr(down_t), _ptr(scales), _ptr(h), _ptr(indices),
+                                    _ptr(out), rows, out_f, k, _ptr(ws), ws.numel(),
+                                    _stream(dev)), "dip_int4_gather_down")
+    return out
+
+
+def ca_fused_gemv(res_qw, res_sc, str_qw, str_sc, x, src, row, g=None, gid=None, out=None):
+    res_qw, res_sc, res_rows, cols = _weights(res_qw, res_sc, "ca_fused_gemv.res")
+    str_qw, str_sc, str_rows, cols2 = _weights(str_qw, str_sc, "ca_fused_gemv.str")
+    if cols2 != cols:
+        raise RuntimeError("resident and streamed rows differ in width")
+    dev = _dev(res_qw, str_qw, x, src, row)
+    x = _want(x.reshape(-1), torch.bfloat16, "x", (cols,))
+    src = _indices(src, "src")
+    row = _indices(row, "row")
+    k = src.numel()
+    if row.numel() != k:
+        raise RuntimeError("src and row must have the same length")
+    if g is not None:
+        g = _want(g.reshape(-1), torch.bfloat16, "g")
+        gid = _indices(gid, "gid")
+    if out is None:
+        out = torch.empty(k, dtype=torch.bfloat16, device=dev)
+    _check(lib.dip_ca_fused_gemv(_ptr(res_qw), _ptr(res_sc), _ptr(str_qw), _ptr(str_sc),
+                                 _ptr(x), _ptr(src), _ptr(row), _ptr(g), _ptr(gid), _ptr(out),
+                                 res_rows, str_rows, cols, k, _stream(dev)),
+           "dip_ca_fused_gemv")
+    return out
+
+
+def ca_down(res_qw, res_sc, str_qw, str_sc, h, src, row, out=None):
+    res_qw, res_sc, res_rows, out_f = _weights(res_qw, res_sc, "ca_down.res")
+    str_qw, str_sc, str_rows, out_f2 = _weights(str_qw, str_sc, "ca_down.str")
+    if out_f2 != out_f:
+        raise RuntimeError("resident and streamed rows differ in width")
+    dev = _dev(res_qw, str_qw, h, src, row)
+    h = _want(h.reshape(-1), torch.bfloat16, "h")
+    src = _indices(src, "src")
+    row = _indices(row, "row")
+    k = h.numel()
+    if out is None:
+        out = torch.empty(out_f, dtype=torch.bfloat16, device=dev)
+    nbytes = lib.dip_gather_down_workspace_size(k, out_f)
+    ws = workspace(dev, nbytes, "down")
+    _check(lib.dip_ca_down(_ptr(res_qw), _ptr(res_sc), _ptr(str_qw), _ptr(str_sc), _ptr(h),
+                           _ptr(src), _ptr(row), _ptr(out), res_rows, str_rows, out_f, k,
+                           _ptr(ws), ws.numel(), _stream(dev)), "dip_ca_down")
+    return out
+
+
+def ca_assemble(id2slot: torch.Tensor, idx: torch.Tensor):
+    """Returns (combined int32 [k], src int32 [k], row int32 [k],
+    miss_ids int32 [k] (first n_miss valid), counts int32 [2] = n_hit, n_miss)."""
+    dev = _dev(id2slot, idx)
+    id2slot = _want(id2slot.reshape(-1), torch.int64, "id2slot")
+    idx = _indices(idx, "idx")
+    k = idx.numel()
+    combined = torch.empty(k, dtype=torch.int32, device=dev)
+    src = torch.empty_like(combined)
+    row = torch.empty_like(combined)
+    miss = torch.empty_like(combined)
+    counts = torch.empty(2, dtype=torch.int32, device=dev)
+    _check(lib.dip_ca_assemble(_ptr(id2slot), _ptr(idx), _ptr(combined), _ptr(src), _ptr(row),
+                               _ptr(miss), _ptr(counts), id2slot.numel(), k, _stream(dev)),
+           "dip_ca_assemble")
+    return combined, src, row, miss, counts
+
+
+def dequant_rows(qweight, scales, indices=None, mode: int = 0):
+    """mode 0: float32 q*s; mode 1: bf16(q*s) (qlinear.dequantize)."""
+    qweight, scales, rows, cols = _weights(qweight, scales, "dequant_rows")
+    dev = _dev(qweight, scales)
+    if indices is not None:
+        indices = _indices(indices)
+        n = indices.numel()
+    else:
+        n = rows
+    out = torch.empty(n, cols, dtype=torch.float32 if mode == 0 else torch.bfloat16,
+                      device=dev)
+    _check(lib.dip_dequant_rows(_ptr(qweight), _ptr(scales), _ptr(indices), _ptr(out), n, rows,
+                                cols, int(mode), _stream(dev)), "dip_dequant_rows")
+    return out
+
+
+def quantize_int4(w: torch.Tensor):
+    """Device int4 g128 quantization, bit-exact with the reference quantizer."""
+    dev = _dev(w)
+    if w.dim() != 2 or w.shape[1] % GROUP_SIZE:
+        raise RuntimeError("w must be 2-D with in_features a multiple of 128")
+    bf = w.dtype == torch.bfloat16
+    w = w.contiguous() if bf else w.float().contiguous()
+    rows, cols = w.shape
+    qw = torch.empty(rows, cols // 2, dtype=torch.int8, device=dev)
+    sc = torch.empty(rows, cols // GROUP_SIZE, dtype=torch.bfloat16, device=dev)
+    _check(lib.dip_quantize_int4(_ptr(w), int(bf), _ptr(qw), _ptr(sc), rows, cols, _stream(dev)),
+           "dip_quantize_int4")
+    return qw, sc
+
+
+def transpose_down_int4(down_qw, down_sc):
+    """down [out, inter/2] int4 -> down_t [inter, out/2] int4 on the device."""
+    down_qw, down_sc, out_f, inter = _weights(down_qw, down_sc, "down")
+    dev = _dev(down_qw, down_sc)
+    tq = torch.empty(inter, out_f // 2, dtype=torch.int8, device=dev)
+    ts = torch.empty(inter, out_f // GROUP_SIZE, dtype=torch.bfloat16, device=dev)
+    _check(lib.dip_transpose_down_int4(_ptr(down_qw), _ptr(down_sc), _ptr(tq), _ptr(ts), out_f,
+                                       inter, _stream(dev)), "dip_transpose_down_int4")
+    return tq, ts
+
+
+def mlp_workspace_bytes(hidden: int, inter: int, k: int) -> int:
+    return lib.dip_mlp_workspace_size(hidden, inter, k)
+
+
+def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=None, g=None,
+               idx=None, h=None, ws=None):
+    """One resident DIP MLP decode step; returns (y, g, idx, h)."""
+    gate_qw, gate_sc, inter, hidden = _weights(gate_qw, gate_sc, "gate")
+    up_qw, up_sc, inter2, hidden2 = _weights(up_qw, up_sc, "up")
+    down_t_qw, down_t_sc, inter3, hidden3 = _weights(down_t_qw, down_t_sc, "down_t")
+    if not (inter == inter2 == inter3 and hidden == hidden2 == hidden3):
+        raise RuntimeError("gate/up/down_t shapes disagree")
+    dev = _dev(gate_qw, up_qw, down_t_qw, x)
+    x = _want(x.reshape(-1), torch.bfloat16, "x", (hidden,))
+    k = int(k)
+    if not 0 <= k <= inter:
+        raise RuntimeError(f"k={k} outside [0, {inter}]")
+    if y is None:
+        y = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
+    if g is None:
+        g = torch.empty(inter, dtype=torch.bfloat16, device=dev)
+    if idx is None:
+        idx = torch.empty(k, dtype=torch.int32, device=dev)
+    if h is None:
+        h = torch.empty(k, dtype=torch.bfloat16, device=dev)
+    nbytes = lib.dip_mlp_workspace_size(hidden, inter, k)
+    if ws is None:
+        ws = workspace(dev, nbytes, "mlp")
+    elif ws.numel() < nbytes:
+        raise RuntimeError("workspace too small")
+    _check(lib.dip_mlp_decode(_ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc),
+                              _ptr(down_t_qw), _ptr(down_t_sc), _ptr(x), _ptr(y), _ptr(g),
+                              _ptr(idx), _ptr(h), hidden, inter, k, _ptr(ws), ws.numel(),
+                              _stream(dev)), "dip_mlp_decode")
+    return y, g, idx, h
+
+
+TUNE = {"rowdot_wgs_per_cu": 0, "down_lpr": 1, "down_blocks": 2, "down_dequant": 3,
+        "down_unroll": 4, "rowdot_x_lds": 5, "rowdot_depth": 6, "down_cpl": 7}
+
+
+def set_tuning(name: str, value: int) -> None:
+    """Launch tuning knob (speed only; see DIP_TUNE_* in include/dip_hip.h)."""
+    _check(lib.dip_set_tuning(TUNE[name], int(value)), f"dip_set_tuning({name}={value})")
+
+
+def get_tuning(name: str) -> int:
+    return lib.dip_get_tuning(TUNE[name])
+
+
+def set_down_dequant_mode(mode: int) -> None:
+    set_tuning("down_dequant", mode)
+
+
+# DIP_TUNE="knob=value,knob=value" applies launch tuning at import (profiling
+# and sweeps run unmodified programs this way).
+for _kv in filter(None, os.environ.get("DIP_TUNE", "").split(",")):
+    _k, _v = _kv.split("=")
+    set_tuning(_k.strip(), int(_v))
+
+
+def host_gather_rows(src: torch.Tensor, ids: torch.Tensor, dst: torch.Tensor,
+                     threads: int = 8) -> None:
+    """dst[i] = src[ids[i]] row-wise on the host (pinned index_select of
+    dip_ca.py:148-153) with `threads` native threads."""
+    if src.device.type != "cpu" or dst.device.type != "cpu" or ids.device.type != "cpu":
+        raise RuntimeError("host_gather_rows works on host tensors")
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise RuntimeError("host_gather_rows needs contiguous src/dst")
+    ids = ids.to(torch.int32).contiguous()
+    n = ids.numel()
+    row_bytes = src[0].numel() * src.element_size() if src.shape[0] else 0
+    if dst.shape[0] < n or dst[0].numel() * dst.element_size() != row_bytes:
+        raise RuntimeError("dst too small or row size mismatch")
+    _check(lib.dip_host_gather_rows(_ptr(src), _ptr(ids), _ptr(dst), n, row_bytes, src.shape[0],
+                                    int(threads)), "dip_host_gather_rows")

@@ -1,0 +1,163 @@
+// dip_common.h — device helpers shared by the DIP decode kernels (gfx950).
+//
+// Format (reference qlinear.py:25-64, scripts/quantize.py:32-64):
+//   qweight int8 [R, C/2]: byte b of a row holds column 2b in its low nibble
+//   and column 2b+1 in its high nibble, two's-complement int4 in [-8, 7];
+//   scales bf16 [R, C/128]: one scale per group of 128 columns.
+//
+// A "chunk" below is 16 bytes of one packed row = 32 columns, always inside a
+// single 128-column group (a group is 64 bytes = 4 chunks).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DIP_DEV __device__ __forceinline__
+
+namespace dip {
+
+constexpr int kGroupSize = 128;       // columns per scale
+constexpr int kChunkBytes = 16;       // one 128-bit load
+constexpr int kChunkCols = 32;        // columns per chunk
+constexpr int kChunksPerGroup = 4;    // 128 / 32
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+DIP_DEV float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 with NaN -> 0x7FC0; the exact rule of
+// c10::BFloat16 / __float2bfloat16_rn, so outputs can be compared bit for bit.
+DIP_DEV uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// |v| as the bf16 key the top-k orders by: sign dropped, subnormal
+// magnitudes flushed to 0 (the reference's top-k kernels are built with
+// --use_fast_math, so fabsf flushes them).  NaN keys (> 0x7F80) are kept
+// as-is; callers skip them because every comparison with NaN is false.
+DIP_DEV uint32_t topk_key(uint32_t bits16) {
+  uint32_t a = bits16 & 0x7FFFu;
+  return a < 0x0080u ? 0u : a;
+}
+constexpr uint32_t kKeyInf = 0x7F80u;
+
+// ---------------------------------------------------------------------------
+// Nibble expansion for v_dot2_f32_bf16.
+//
+// For a dword w of 8 nibbles n0..n7 (column c+p for nibble p), flipping bit 3
+// of a nibble turns the two's-complement value q into u = q + 8 in [0, 15].
+// Placing u in mantissa bits 3..6 of bf16 1.0 (0x3F80 | u << 3) encodes
+// 1 + u/16 = 1.5 + q/16 exactly.  For j = 0..3, shifting w so nibble j lands
+// on bits 3..6 (and nibble j+4 on bits 19..22), masking with 0x00780078 and
+// XOR-ing 0x3FC03FC0 (1.0 in both halves plus the bit-3 flip of u) gives
+//     pair_j(w) = bf16x2(1.5 + q_j/16, 1.5 + q_{j+4}/16)
+// in one v_bitop3_b32 after the shift.  Then
+//     sum_p (1.5 + q_p/16) x_p = 1.5 sum_p x_p + (1/16) sum_p q_p x_p,
+// so each chunk's dot2 chain starts at -1.5 * sum(x over the chunk) and the
+// result, times 16 * scale, is the chunk's contribution.  Every product is
+// exact in fp32, and the running sums stay within a few times the size of
+// the signal, which keeps fp32 accumulation error small.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPairMask = 0x00780078u;
+constexpr uint32_t kPairMagicFlip = 0x3FC03FC0u;
+constexpr float kPairBias = 1.5f;
+constexpr float kPairScale = 16.0f;
+
+DIP_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                          __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// x pairs for one dword of weights: xp[j] = (x[c+j], x[c+j+4]) as bf16x2,
+// from X0 = (x[c], x[c+1]), X1 = (x[c+2], x[c+3]), X2 = (x[c+4], x[c+5]),
+// X3 = (x[c+6], x[c+7]).
+DIP_DEV void make_xpairs(uint32_t X0, uint32_t X1, uint32_t X2, uint32_t X3, uint32_t xp[4]) {
+  xp[0] = (X0 & 0xFFFFu) | (X2 << 16);
+  xp[1] = (X0 >> 16) | (X2 & 0xFFFF0000u);
+  xp[2] = (X1 & 0xFFFFu) | (X3 << 16);
+  xp[3] = (X1 >> 16) | (X3 & 0xFFFF0000u);
+}
+
+// acc + sum over the 8 nibbles of w of (1.5 + q_p/16) * x_p.
+DIP_DEV float dot8_nibbles(uint32_t w, const uint32_t xp[4], float acc) {
+  acc = dot2_bf16(((w << 3) & kPairMask) ^ kPairMagicFlip, xp[0], acc);
+  acc = dot2_bf16(((w >> 1) & kPairMask) ^ kPairMagicFlip, xp[1], acc);
+  acc = dot2_bf16(((w >> 5) & kPairMask) ^ kPairMagicFlip, xp[2], acc);
+  acc = dot2_bf16(((w >> 9) & kPairMask) ^ kPairMagicFlip, xp[3], acc);
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Per-nibble conversions for the down kernel (one output column per nibble).
+// ---------------------------------------------------------------------------
+// float(byte n of v), n = 0..3 (v_cvt_f32_ubyteN).
+template <int N>
+DIP_DEV float cvt_ubyte(uint32_t v) {
+  float r;
+  if (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  if (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  if (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  if (N == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// sext(low nibble of byte n of v) / 16 as fp32, exactly (v_cvt_off_f32_i4
+// reading byte n through SDWA).
+template <int N>
+DIP_DEV float cvt_nibble_div16(uint32_t v) {
+  float r;
+  if (N == 0)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0"
+        : "=v"(r) : "v"(v));
+  if (N == 1)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+        : "=v"(r) : "v"(v));
+  if (N == 2)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+        : "=v"(r) : "v"(v));
+  if (N == 3)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=v"(r) : "v"(v));
+  return r;
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64), every lane of
+// the group receiving the total: DPP within rows of 16 lanes (xor 1, xor 2,
+// half-row mirror, row mirror), then v_permlane16_swap / a 32-lane swap to
+// combine rows.  All VALU, no LDS round trips.
+template <int CTRL>
+DIP_DEV float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                            0xF, 0xF, true));
+}
+template <int W>
+DIP_DEV float group_sum(float v) {
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "W");
+  if (W >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  if (W >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  if (W >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror: the other quad of 8
+  if (W >= 16) v += dpp_mov<0x140>(v); // row_mirror: the other half of 16
+  if (W >= 32) {
+    // rows (0,1) and (2,3) exchange: r[0] + r[1] = sum of the two rows
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                    __builtin_bit_cast(uint32_t, v), false, false);
+    v = __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+  }
+  if (W >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                    __builtin_bit_cast(uint32_t, v), false, false);
+    v = __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+  }
+  return v;
+}
+
+// 128-bit streaming load (weights are read once per call: non-temporal).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+DIP_DEV uint4 ldg_nt(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+}  // namespace dip

@@ -1,0 +1,386 @@
+// dip_down.hip — transposed-down gather: y[o] = sum_j h[j] * (q*s)[row_j, o].
+//
+// down_t is [rows, out/2] packed int4 (row = one intermediate channel), so a
+// selected channel is one contiguous row.  The work is tiled two ways:
+//   * column block cb: LPR lanes each own CPL 16-byte chunks (32*CPL outputs)
+//     of every row, i.e. LPR*CPL*16 contiguous bytes per row per block;
+//   * row block rb: a contiguous range of selected positions j.
+// A block of 256 threads holds 256/LPR "row slots"; slot s walks rows
+// j = j0+s, j0+s+slots, ...  Lane l of a slot prefetches the row id and h of
+// the slot's l-th row; each row's id and h are then shuffled to the slot and
+// D rows of 128-bit loads are kept in flight.  Each lane keeps 32*CPL fp32
+// accumulators (its outputs).  Slots are reduced through LDS in a fixed
+// order and the block writes one fp32 partial row segment; the reduce kernel
+// sums the row-block partials in a fixed order and rounds to bf16.  No float
+// atomics, so results are identical run to run for a given tiling.
+//
+// Tiling knobs: LPR lanes per row segment, CPL chunks per lane, D rows in
+// flight per slot (DIP_TUNE_DOWN_LPR / _CPL / _UNROLL).
+//
+// Dequant per weight, two interchangeable forms (DQ):
+//   DQ = 0: nibbles flipped to u = q + 8 in [0, 15] per byte and converted
+//           with v_cvt_f32_ubyte{0..3}; acc += u * (h*s), and the accumulated
+//           bias 8 * sum(h*s) is removed once at the end;
+//   DQ = 1: v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for
+//           the low nibble of any byte (high nibbles after one shift);
+//           acc += (q/16) * (16*h*s).  No bias, ~2.1 VALU ops per weight.
+#include "dip_common.h"
+#include "dip_internal.h"
+
+namespace dip {
+
+namespace {
+constexpr int kThreads = 256;
+constexpr uint32_t kBadRow = 0xFFFFFFFFu;
+constexpr uint32_t kSrcB = 0x80000000u;
+constexpr int kRedOut = 32;    // outputs per reduce block
+constexpr int kRedSplit = 8;   // partial subsets per output
+}  // namespace
+
+template <int SRC>
+DIP_DEV uint32_t down_row(const DownArgs& a, int j) {
+  if (SRC == kContig) return (unsigned)j < (unsigned)a.rows_a ? (uint32_t)j : kBadRow;
+  if (SRC == kGather) {
+    const int r = a.sel[j];
+    return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
+  }
+  const int r = a.sel2[j];
+  if (a.sel[j] != 0) return (unsigned)r < (unsigned)a.rows_b ? ((uint32_t)r | kSrcB) : kBadRow;
+  return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
+}
+
+template <int CPL>
+struct DownRow {
+  uint4 w[CPL];
+  uint32_t s;  // bf16 scale of the lane's group
+  uint32_t h;  // bf16 h of the row
+  uint32_t rid;
+};
+
+template <int CPL, int SRC>
+DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, uint32_t hb, int cc0,
+                           size_t row_bytes, int ngroups, DownRow<CPL>& R) {
+  R.rid = rid;
+  R.h = hb;
+  if (rid == kBadRow) return;
+  const int8_t* qw = a.qw_a;
+  const uint16_t* sc = a.sc_a;
+  if (SRC == kDual && (rid & kSrcB)) {
+    qw = a.qw_b;
+    sc = a.sc_b;
+  }
+  const uint32_t r = rid & ~kSrcB;
+  const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes) + cc0;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) R.w[c] = ldg_nt(wr + c);
+  R.s = sc[(size_t)r * ngroups + cc0 / kChunksPerGroup];
+}
+
+// Slot = LPR lanes; lane l of a slot owns CPL consecutive 16-byte chunks
+// (32*CPL outputs, inside one 128-column group) of every row the slot walks.
+// The slot's rows j = j0 + i*slots, i < cnt <= LPR: lane l prefetches the id
+// and h of row l, rows are shuffled in turn, and D rows of loads stay in
+// flight through a ring refilled right after each row is consumed.
+template <int LPR, int CPL, int SRC, int DQ, int D>
+__global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
+  constexpr int kSlots = kThreads / LPR;
+  constexpr int kAcc = CPL * kChunkCols;
+  __shared__ float red[kSlots][kAcc][LPR];
+
+  const int cb = blockIdx.x % a.col_blocks;
+  const int rb = blockIdx.x / a.col_blocks;
+  const int l = threadIdx.x % LPR;
+  const int slot = threadIdx.x / LPR;
+  const int gbase = (threadIdx.x & 63) - l;
+  const int cc0 = (cb * LPR + l) * CPL;  // first chunk of mine within a row
+  const size_t row_bytes = (size_t)(a.out_features >> 1);
+  const int ngroups = a.out_features >> 7;
+  const int j0 = rb * a.rows_per_block + slot;
+  const int j1 = min(a.k, rb * a.rows_per_block + a.rows_per_block);
+  const int cnt = j0 < j1 ? (j1 - 1 - j0) / kSlots + 1 : 0;  // <= LPR
+
+  uint32_t rid_l = kBadRow, h_l = 0;
+  if (l < cnt) {
+    const int j = j0 + l * kSlots;
+    rid_l = down_row<SRC>(a, j);
+    h_l = a.h[j];
+  }
+  DownRow<CPL> ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < cnt)
+      load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + d, 64), __shfl(h_l, gbase + d, 64), cc0,
+                              row_bytes, ngroups, ring[d]);
+
+  float acc[kAcc];
+#pragma unroll
+  for (int m = 0; m < kAcc; ++m) acc[m] = 0.f;
+  float hsum = 0.f;
+
+  for (int i0 = 0; i0 < cnt; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int i = i0 + d;
+      if (i < cnt) {
+        const DownRow<CPL>& R = ring[d];
+        float f = R.rid == kBadRow ? __builtin_nanf("")
+                                   : bf16_to_f32(R.h) * bf16_to_f32(R.s);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const uint32_t wv[4] = {R.w[c].x, R.w[c].y, R.w[c].z, R.w[c].w};
+          float* ac = acc + c * kChunkCols;
+          if (DQ == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t lo = (wv[q] & 0x0F0F0F0Fu) ^ 0x08080808u;
+              const uint32_t hi = ((wv[q] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+              ac[8 * q + 0] = fmaf(cvt_ubyte<0>(lo), f, ac[8 * q + 0]);
+              ac[8 * q + 1] = fmaf(cvt_ubyte<0>(hi), f, ac[8 * q + 1]);
+              ac[8 * q + 2] = fmaf(cvt_ubyte<1>(lo), f, ac[8 * q + 2]);
+              ac[8 * q + 3] = fmaf(cvt_ubyte<1>(hi), f, ac[8 * q + 3]);
+              ac[8 * q + 4] = fmaf(cvt_ubyte<2>(lo), f, ac[8 * q + 4]);
+              ac[8 * q + 5] = fmaf(cvt_ubyte<2>(hi), f, ac[8 * q + 5]);
+              ac[8 * q + 6] = fmaf(cvt_ubyte<3>(lo), f, ac[8 * q + 6]);
+              ac[8 * q + 7] = fmaf(cvt_ubyte<3>(hi), f, ac[8 * q + 7]);
+            }
+          } else {
+            const float f16 = f * 16.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t hi = wv[q] >> 4;
+              ac[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, ac[8 * q + 0]);
+              ac[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, ac[8 * q + 1]);
+              ac[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, ac[8 * q + 2]);
+              ac[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, ac[8 * q + 3]);
+              ac[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, ac[8 * q + 4]);
+              ac[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, ac[8 * q + 5]);
+              ac[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, ac[8 * q + 6]);
+              ac[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, ac[8 * q + 7]);
+            }
+          }
+        }
+        if (DQ == 0) hsum += f;
+        if (i + D < cnt)
+          load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + i + D, 64),
+                                  __shfl(h_l, gbase + i + D, 64), cc0, row_bytes, ngroups,
+                                  ring[d]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int m = 0; m < kAcc; ++m)
+    red[slot][m][l] = DQ == 0 ? fmaf(-8.0f, hsum, acc[m]) : acc[m];
+  __syncthreads();
+
+  // Sum the slots in a fixed order.  Block columns: lane l's CPL chunks are
+  // consecutive, so column = (l*CPL + c)*32 + m = l*kAcc + (c*32 + m).
+  constexpr int kCols = LPR * kAcc;
+  float* out = a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols;
+  for (int col = threadIdx.x; col < kCols; col += kThreads) {
+    const int ln = col / kAcc;
+    const int m = col % kAcc;
+    float s = 0.f;
+#pragma unroll 8
+    for (int sl = 0; sl < kSlots; ++sl) s += red[sl][m][ln];
+    out[col] = s;
+  }
+}
+
+// y[o] = bf16(sum over row blocks of partial[rb][o]): split p of an output
+// sums row blocks p, p+8, p+16, ... in ascending order with its loads issued
+// 16 at a time; the 8 splits are then added in order 0..7.
+__global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
+    const float* __restrict__ partial, int row_blocks, int out_features, uint16_t* __restrict__ y) {
+  __shared__ float part[kRedSplit][kRedOut];
+  const int oo = threadIdx.x % kRedOut;
+  const int p = threadIdx.x / kRedOut;
+  const int o = blockIdx.x * kRedOut + oo;
+  float s = 0.f;
+  if (o < out_features) {
+    int rb = p;
+    for (; rb + 15 * kRedSplit < row_blocks; rb += 16 * kRedSplit) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = partial[(size_t)(rb + u * kRedSplit) * out_features + o];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += v[u];
+    }
+    for (; rb < row_blocks; rb += kRedSplit) s += partial[(size_t)rb * out_features + o];
+  }
+  part[p][oo] = s;
+  __syncthreads();
+  if (p == 0 && o < out_features) {
+    float t = part[0][oo];
+#pragma unroll
+    for (int q = 1; q < kRedSplit; ++q) t += part[q][oo];
+    y[o] = (uint16_t)f32_to_bf16(t);
+  }
+}
+
+namespace {
+
+struct DownPlan {
+  int lpr;
+  int cpl;
+  int col_blocks;
+  int row_blocks;
+  int rows_per_block;
+};
+
+DownPlan plan_down(int64_t k, int64_t out_features) {
+  DownPlan p{};
+  const int64_t chunks = out_features / kChunkCols;
+  const int want = tuning(DIP_TUNE_DOWN_LPR);
+  for (int cpl : {tuning(DIP_TUNE_DOWN_CPL), 1}) {
+    for (int lpr : {32, 16, 8, 4}) {
+      if (want && lpr > want) continue;
+      if (chunks % ((int64_t)lpr * cpl) == 0) {
+        p.lpr = lpr;
+        p.cpl = cpl;
+        break;
+      }
+    }
+    if (p.lpr) break;
+  }
+  if (!p.lpr || k <= 0) return p;
+  p.col_blocks = (int)(chunks / ((int64_t)p.lpr * p.cpl));
+  int rb = tuning(DIP_TUNE_DOWN_BLOCKS) / p.col_blocks;
+  if (rb < 1) rb = 1;
+  const int slots = kThreads / p.lpr;
+  int per = (int)((k + rb - 1) / rb);
+  per = ((per + slots - 1) / slots) * slots;  // whole rounds of slots
+  // a slot walks at most LPR rows (one prefetched batch of row ids)
+  if (per > slots * p.lpr) per = slots * p.lpr;
+  p.rows_per_block = per;
+  p.row_blocks = (int)((k + per - 1) / per);
+  return p;
+}
+
+template <int LPR, int CPL, int DQ, int D>
+void launch_partial4(int src, const DownArgs& a, int blocks, hipStream_t stream) {
+  if (src == kContig)
+    hipLaunchKernelGGL((down_partial_kernel<LPR, CPL, kContig, DQ, D>), dim3(blocks),
+                       dim3(kThreads), 0, stream, a);
+  else if (src == kGather)
+    hipLaunchKernelGGL((down_partial_kernel<LPR, CPL, kGather, DQ, D>), dim3(blocks),
+                       dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((down_partial_kernel<LPR, CPL, kDual, DQ, D>), dim3(blocks),
+                       dim3(kThreads), 0, stream, a);
+}
+
+template <int LPR, int CPL>
+void launch_partial(int src, const DownArgs& a, int blocks, hipStream_t stream) {
+  const int dq = tuning(DIP_TUNE_DOWN_DEQUANT);
+  const int d = tuning(DIP_TUNE_DOWN_UNROLL);
+  if (dq == 1) {
+    if (d == 4) launch_partial4<LPR, CPL, 1, 4>(src, a, blocks, stream);
+    else if (d == 8) launch_partial4<LPR, CPL, 1, 8>(src, a, blocks, stream);
+    else launch_partial4<LPR, CPL, 1, 2>(src, a, blocks, stream);
+  } else {
+    launch_partial4<LPR, CPL, 0, 2>(src, a, blocks, stream);
+  }
+}
+
+}  // namespace
+
+size_t down_workspace_bytes(int64_t k, int64_t out_features) {
+  // row_blocks <= max(DOWN_BLOCKS / col_blocks, ceil(k / 256)): a row block
+  // never holds more than 256 rows (one prefetched batch per slot).
+  if (out_features <= 0) return 256;
+  int64_t blocks = tuning(DIP_TUNE_DOWN_BLOCKS);
+  const int64_t by_k = (k + 255) / 256;
+  if (by_k > blocks) blocks = by_k;
+  return (size_t)(blocks > 0 ? blocks : 1) * (size_t)out_features * sizeof(float);
+}
+
+int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
+             const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
+             const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
+             uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (!qw_a || !sc_a || !y) return DIP_ERR_NULL;
+  if (out_features <= 0 || out_features % kGroupSize != 0 || out_features > (1 << 20))
+    return DIP_ERR_SHAPE;
+  if (k < 0 || k > INT32_MAX || rows_a < 0 || rows_a > INT32_MAX || rows_b > INT32_MAX)
+    return DIP_ERR_SHAPE;
+  if (!aligned16(qw_a) || (qw_b && !aligned16(qw_b))) return DIP_ERR_ALIGN;
+  if (k > 0 && !h) return DIP_ERR_NULL;
+  const unsigned red_blocks = (unsigned)((out_features + kRedOut - 1) / kRedOut);
+  if (k == 0) {
+    // y = bf16(0) for every output: the reduce over zero row blocks.
+    hipLaunchKernelGGL(down_reduce_kernel, dim3(red_blocks), dim3(kRedOut * kRedSplit), 0, stream,
+                       (const float*)nullptr, 0, (int)out_features, y);
+    return hip_status(hipGetLastError());
+  }
+  const DownPlan p = plan_down(k, out_features);
+  if (!p.lpr) return DIP_ERR_UNSUPPORTED;
+  if (!workspace || ws_bytes < down_workspace_bytes(k, out_features)) return DIP_ERR_WORKSPACE;
+  if ((size_t)p.row_blocks * (size_t)out_features * sizeof(float) > ws_bytes)
+    return DIP_ERR_WORKSPACE;
+  DownArgs a{};
+  a.qw_a = qw_a;
+  a.sc_a = sc_a;
+  a.qw_b = qw_b;
+  a.sc_b = sc_b;
+  a.h = h;
+  a.sel = sel;
+  a.sel2 = sel2;
+  a.partial = reinterpret_cast<float*>(workspace);
+  a.rows_a = (int)rows_a;
+  a.rows_b = (int)rows_b;
+  a.k = (int)k;
+  a.out_features = (int)out_features;
+  a.rows_per_block = p.rows_per_block;
+  a.col_blocks = p.col_blocks;
+  const int blocks = p.row_blocks * p.col_blocks;
+  if (p.cpl == 2) {
+    switch (p.lpr) {
+      case 32: launch_partial<32, 2>(src, a, blocks, stream); break;
+      case 16: launch_partial<16, 2>(src, a, blocks, stream); break;
+      case 8: launch_partial<8, 2>(src, a, blocks, stream); break;
+      default: launch_partial<4, 2>(src, a, blocks, stream); break;
+    }
+  } else {
+    switch (p.lpr) {
+      case 32: launch_partial<32, 1>(src, a, blocks, stream); break;
+      case 16: launch_partial<16, 1>(src, a, blocks, stream); break;
+      case 8: launch_partial<8, 1>(src, a, blocks, stream); break;
+      default: launch_partial<4, 1>(src, a, blocks, stream); break;
+    }
+  }
+  int st = hip_status(hipGetLastError());
+  if (st) return st;
+  hipLaunchKernelGGL(down_reduce_kernel, dim3(red_blocks), dim3(kRedOut * kRedSplit), 0, stream,
+                     (const float*)a.partial, p.row_blocks, (int)out_features, y);
+  return hip_status(hipGetLastError());
+}
+
+}  // namespace dip
+
+using namespace dip;
+
+extern "C" size_t dip_gather_down_workspace_size(int64_t k, int64_t out_features) {
+  return down_workspace_bytes(k, out_features);
+}
+
+extern "C" int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales,
+                                    const uint16_t* h, const int32_t* indices, uint16_t* y,
+                                    int64_t rows, int64_t out_features, int64_t k,
+                                    void* workspace, size_t ws_bytes, void* stream) {
+  if (!indices && k > rows) return DIP_ERR_SHAPE;
+  return run_down(indices ? kGather : kContig, down_t, scales, rows, nullptr, nullptr, 0, h,
+                  indices, nullptr, k, out_features, y, workspace, ws_bytes,
+                  (hipStream_t)stream);
+}
+
+extern "C" int dip_ca_down(const int8_t* res_qw, const uint16_t* res_sc, const int8_t* str_qw,
+                           const uint16_t* str_sc, const uint16_t* h, const int32_t* src,
+                           const int32_t* row, uint16_t* y, int64_t res_rows, int64_t str_rows,
+                           int64_t out_features, int64_t k, void* workspace, size_t ws_bytes,
+                           void* stream) {
+  if (!str_qw || !str_sc) return DIP_ERR_NULL;
+  if (k > 0 && (!src || !row)) return DIP_ERR_NULL;
+  return run_down(kDual, res_qw, res_sc, res_rows, str_qw, str_sc, str_rows, h, src, row, k,
+                  out_features, y, workspace, ws_bytes, (hipStream_t)stream);
+}

@@ -1,0 +1,95 @@
+// dip_internal.h — host-side declarations shared by the DIP translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/dip_hip.h"
+
+namespace dip {
+
+// Row source for the row-dot and down kernels.
+enum RowSrc : int {
+  kContig = 0,  // output j reads row j of matrix A
+  kGather = 1,  // output j reads row sel[j] of matrix A
+  kDual = 2,    // output j reads row sel2[j] of A (sel[j]==0) or of B (sel[j]!=0)
+};
+
+// Epilogue of the row-dot kernel.
+enum Epi : int {
+  kRaw = 0,       // out[j] = bf16(dot)
+  kSilu = 1,      // out[j] = bf16(silu(bf16(dot)))
+  kH = 3,         // out[j] = bf16(g[gid[j]] * bf16(dot))
+};
+
+struct RowdotArgs {
+  const int8_t* qw_a;
+  const uint16_t* sc_a;
+  const int8_t* qw_b;
+  const uint16_t* sc_b;
+  const uint16_t* x;
+  const int32_t* sel;
+  const int32_t* sel2;
+  const int32_t* gid;
+  const uint16_t* g;
+  uint16_t* out;
+  int nrows;
+  int in_features;
+  int rows_a;  // rows of matrix A (row ids outside [0, rows_a) yield NaN)
+  int rows_b;  // rows of matrix B (kDual)
+};
+
+struct DownArgs {
+  const int8_t* qw_a;
+  const uint16_t* sc_a;
+  const int8_t* qw_b;
+  const uint16_t* sc_b;
+  const uint16_t* h;
+  const int32_t* sel;
+  const int32_t* sel2;
+  float* partial;     // [row_blocks, out_features]
+  int rows_a;
+  int rows_b;
+  int k;
+  int out_features;
+  int rows_per_block;
+  int col_blocks;
+};
+
+// Top-k: one histogram bin per 15-bit |s| key, held in LDS.
+constexpr int kFineBins = 32768;
+constexpr int kTopkMaxN = 65536;
+
+struct TopkMeta {
+  float lo;
+  float hi;
+  int32_t count_a;
+  int32_t count_b;
+  uint32_t key_a;   // (k+1)-th largest key, 0xFFFFFFFF if fewer than k+1 values
+  uint32_t key_max;
+  int32_t n_valid;
+  int32_t pad;
+  uint64_t stamp[6];  // wall_clock64() at the top-k's phase boundaries (diagnostics)
+};
+
+// Launchers (return hipSuccess or a DIP_ERR_* code).
+int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
+int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
+             const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
+             const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
+             uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream);
+size_t down_workspace_bytes(int64_t k, int64_t out_features);
+int launch_topk(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
+                hipStream_t stream);
+
+// Launch tuning (process-wide, host side): see DIP_TUNE_* in dip_hip.h.
+int tuning(int knob);
+// Compute units of the current device (cached per device).
+int device_cus();
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? DIP_OK : (int)e; }
+
+}  // namespace dip

@@ -1,0 +1,300 @@
+// dip_misc.hip — cache-aware hit/miss assembly, row dequantisation, the
+// host-side miss gather, the one-call resident MLP decode step and the
+// library's status helpers.
+#include <algorithm>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "dip_common.h"
+#include "dip_internal.h"
+
+namespace dip {
+
+// ---------------------------------------------------------------------------
+// Cache-aware assembly (dip_ca.py:137-171).  One workgroup: each thread owns a
+// contiguous segment of idx, counts its hits, a block scan gives every
+// element its place in [hits in idx order, misses in idx order].
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kAsmThreads = 1024;
+constexpr int kAsmWaves = kAsmThreads / 64;
+
+DIP_DEV uint32_t wave_prefix32(uint32_t v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+}  // namespace
+
+__global__ __launch_bounds__(kAsmThreads) void ca_assemble_kernel(
+    const int64_t* __restrict__ id2slot, const int32_t* __restrict__ idx, int inter, int k,
+    int32_t* __restrict__ combined, int32_t* __restrict__ src, int32_t* __restrict__ row,
+    int32_t* __restrict__ miss_ids, int32_t* __restrict__ counts) {
+  __shared__ uint32_t wave_excl[kAsmWaves];
+  __shared__ uint32_t total_hits;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int per = (k + kAsmThreads - 1) / kAsmThreads;
+  const int beg = min(k, tid * per);
+  const int end = min(k, beg + per);
+
+  uint32_t hits = 0;
+  for (int j = beg; j < end; ++j) {
+    const int c = idx[j];
+    const int64_t s = ((unsigned)c < (unsigned)inter) ? id2slot[c] : -1;
+    hits += s >= 0 ? 1u : 0u;
+  }
+  const uint32_t incl = wave_prefix32(hits, lane);
+  if (lane == 63) wave_excl[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t v = lane < kAsmWaves ? wave_excl[lane] : 0u;
+    const uint32_t p = wave_prefix32(v, lane);
+    if (lane < kAsmWaves) wave_excl[lane] = p - v;
+    const uint32_t tot = __shfl(p, kAsmWaves - 1, 64);
+    if (lane == 0) total_hits = tot;
+  }
+  __syncthreads();
+  const uint32_t n_hit = total_hits;
+  uint32_t hit_pos = wave_excl[wave] + incl - hits;  // hits before this segment
+  for (int j = beg; j < end; ++j) {
+    const int c = idx[j];
+    const int64_t s = ((unsigned)c < (unsigned)inter) ? id2slot[c] : -1;
+    if (s >= 0) {
+      combined[hit_pos] = c;
+      src[hit_pos] = 0;
+      row[hit_pos] = (int32_t)s;
+      ++hit_pos;
+    } else {
+      const uint32_t miss_rank = (uint32_t)j - hit_pos;  // misses before j
+      const uint32_t pos = n_hit + miss_rank;
+      combined[pos] = c;
+      src[pos] = 1;
+      row[pos] = (int32_t)miss_rank;
+      miss_ids[miss_rank] = c;
+    }
+  }
+  if (tid == 0) {
+    counts[0] = (int32_t)n_hit;
+    counts[1] = k - (int32_t)n_hit;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row dequantisation (bit-exact dequant check).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dequant_rows_kernel(
+    const int8_t* __restrict__ qw, const uint16_t* __restrict__ sc,
+    const int32_t* __restrict__ indices, void* __restrict__ out, int n_out_rows, int rows,
+    int cols, int mode) {
+  const int half = cols >> 1;
+  const int ngroups = cols >> 7;
+  const size_t total = (size_t)n_out_rows * half;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total;
+       e += (size_t)gridDim.x * 256) {
+    const int i = (int)(e / half);
+    const int b = (int)(e % half);
+    const int r = indices ? indices[i] : i;
+    float v0, v1;
+    if ((unsigned)r < (unsigned)rows) {
+      const uint32_t byte = (uint8_t)qw[(size_t)r * half + b];
+      const int q0 = (int)(byte & 0xFu) - (int)((byte & 0x8u) << 1);
+      const int q1 = (int)(byte >> 4) - (int)((byte & 0x80u) >> 3);
+      const float s = bf16_to_f32(sc[(size_t)r * ngroups + (2 * b) / kGroupSize]);
+      v0 = (float)q0 * s;
+      v1 = (float)q1 * s;
+    } else {
+      v0 = v1 = __builtin_nanf("");
+    }
+    const size_t o = (size_t)i * cols + 2 * (size_t)b;
+    if (mode == 0) {
+      reinterpret_cast<float*>(out)[o] = v0;
+      reinterpret_cast<float*>(out)[o + 1] = v1;
+    } else {
+      reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16(v0);
+      reinterpret_cast<uint16_t*>(out)[o + 1] = (uint16_t)f32_to_bf16(v1);
+    }
+  }
+}
+
+}  // namespace dip
+
+using namespace dip;
+
+extern "C" const char* dip_status_string(int status) {
+  switch (status) {
+    case DIP_OK: return "ok";
+    case DIP_ERR_NULL: return "a required pointer is NULL";
+    case DIP_ERR_SHAPE: return "invalid or unsupported size";
+    case DIP_ERR_ALIGN: return "pointer is not 16-byte aligned";
+    case DIP_ERR_UNSUPPORTED: return "no kernel instantiation for this shape";
+    case DIP_ERR_WORKSPACE: return "workspace missing or too small";
+    case DIP_ERR_ARG: return "invalid argument";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown status";
+}
+
+extern "C" int dip_version(void) { return 100; }
+
+// ---------------------------------------------------------------------------
+// Tuning table and device facts.
+// ---------------------------------------------------------------------------
+namespace {
+int g_tune[DIP_TUNE_COUNT] = {2, 0, 1024, 1, 2, 1, 3, 2};
+}  // namespace
+
+int dip::tuning(int knob) { return g_tune[knob]; }
+
+int dip::device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+extern "C" int dip_set_tuning(int knob, int value) {
+  switch (knob) {
+    case DIP_TUNE_ROWDOT_WGS_PER_CU:
+      if (value < 1 || value > 16) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_DOWN_LPR:
+      if (value != 0 && value != 4 && value != 8 && value != 16 && value != 32) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_DOWN_BLOCKS:
+      if (value < 1 || value > 65536) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_DOWN_DEQUANT:
+      if (value != 0 && value != 1) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_DOWN_UNROLL:
+      if (value != 2 && value != 4 && value != 8) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_ROWDOT_X_LDS:
+      if (value != 0 && value != 1) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_ROWDOT_DEPTH:
+      if (value < 2 || value > 4) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_DOWN_CPL:
+      if (value != 1 && value != 2) return DIP_ERR_ARG;
+      break;
+    default:
+      return DIP_ERR_ARG;
+  }
+  g_tune[knob] = value;
+  return DIP_OK;
+}
+
+extern "C" int dip_get_tuning(int knob) {
+  if (knob < 0 || knob >= DIP_TUNE_COUNT) return DIP_ERR_ARG;
+  return g_tune[knob];
+}
+
+extern "C" int dip_ca_assemble(const int64_t* id2slot, const int32_t* idx, int32_t* combined,
+                               int32_t* src, int32_t* row, int32_t* miss_ids, int32_t* counts,
+                               int64_t inter, int64_t k, void* stream) {
+  if (inter < 0 || k < 0 || inter > INT32_MAX || k > INT32_MAX) return DIP_ERR_SHAPE;
+  if (!counts || !id2slot) return DIP_ERR_NULL;
+  if (k > 0 && (!idx || !combined || !src || !row || !miss_ids)) return DIP_ERR_NULL;
+  hipLaunchKernelGGL(ca_assemble_kernel, dim3(1), dim3(kAsmThreads), 0, (hipStream_t)stream,
+                     id2slot, idx, (int)inter, (int)k, combined, src, row, miss_ids, counts);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" int dip_dequant_rows(const int8_t* qweight, const uint16_t* scales,
+                                const int32_t* indices, void* out, int64_t n_out_rows,
+                                int64_t rows, int64_t cols, int mode, void* stream) {
+  if (!qweight || !scales || !out) return DIP_ERR_NULL;
+  if (cols <= 0 || cols % kGroupSize != 0 || rows < 0 || n_out_rows < 0 ||
+      rows > INT32_MAX || n_out_rows > INT32_MAX)
+    return DIP_ERR_SHAPE;
+  if (!indices && n_out_rows > rows) return DIP_ERR_SHAPE;
+  if (mode != 0 && mode != 1) return DIP_ERR_ARG;
+  if (n_out_rows == 0) return DIP_OK;
+  const size_t total = (size_t)n_out_rows * (size_t)(cols / 2);
+  const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(dequant_rows_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     qweight, scales, indices, out, (int)n_out_rows, (int)rows, (int)cols, mode);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t n,
+                                    int64_t row_bytes, int64_t src_rows, int threads) {
+  if (n < 0 || row_bytes < 0 || src_rows < 0) return DIP_ERR_SHAPE;
+  if (n == 0 || row_bytes == 0) return DIP_OK;
+  if (!src || !ids || !dst) return DIP_ERR_NULL;
+  for (int64_t i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= src_rows) return DIP_ERR_SHAPE;
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  auto work = [&](int64_t b, int64_t e) {
+    for (int64_t i = b; i < e; ++i)
+      std::memcpy(d + i * row_bytes, s + (int64_t)ids[i] * row_bytes, (size_t)row_bytes);
+  };
+  int nt = std::max(1, threads);
+  if ((int64_t)nt > n) nt = (int)n;
+  if (nt == 1) {
+    work(0, n);
+    return DIP_OK;
+  }
+  std::vector<std::thread> pool;
+  pool.reserve(nt - 1);
+  const int64_t per = (n + nt - 1) / nt;
+  for (int t = 1; t < nt; ++t) {
+    const int64_t b = t * per, e = std::min(n, b + per);
+    if (b < e) pool.emplace_back(work, b, e);
+  }
+  work(0, std::min(n, per));
+  for (auto& th : pool) th.join();
+  return DIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// One resident DIP MLP decode step.
+// ---------------------------------------------------------------------------
+namespace {
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+}  // namespace
+
+extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k) {
+  return align256(dip_topk_workspace_size(inter)) + align256(down_workspace_bytes(k, hidden));
+}
+
+extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
+                              const int8_t* up_qw, const uint16_t* up_sc,
+                              const int8_t* down_t_qw, const uint16_t* down_t_sc,
+                              const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
+                              uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
+                              void* workspace, size_t ws_bytes, void* stream) {
+  if (!g_out || !y || !x) return DIP_ERR_NULL;
+  if (k < 0 || k > inter) return DIP_ERR_SHAPE;
+  if (k > 0 && (!idx_out || !h_out)) return DIP_ERR_NULL;
+  if (!workspace || ws_bytes < dip_mlp_workspace_size(hidden, inter, k)) return DIP_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  const size_t topk_bytes = align256(dip_topk_workspace_size(inter));
+  void* ws_topk = ws;
+  void* ws_down = ws + topk_bytes;
+  const size_t down_bytes = ws_bytes - topk_bytes;
+  int st = dip_int4_gemv(gate_qw, gate_sc, x, g_out, inter, hidden, DIP_ACT_SILU, stream);
+  if (st) return st;
+  st = dip_topk_select(g_out, idx_out, inter, k, ws_topk, topk_bytes, stream);
+  if (st) return st;
+  st = dip_up_gather_h(up_qw, up_sc, x, idx_out, g_out, h_out, inter, hidden, k, stream);
+  if (st) return st;
+  return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k, ws_down,
+                              down_bytes, stream);
+}

@@ -1,0 +1,191 @@
+"""Cache-aware DIP (drop-in for the reference's dip_ca.py:58-196, 300-309).
+
+The most frequently selected channels of each layer keep their up/down rows
+resident in HBM; each decode token splits its k selected channels into hits
+(resident) and misses (streamed from a pinned host copy).  Per token:
+
+    GPU : gate GEMV + SiLU + top-k (bit-exact reference order)
+          -> hit/miss assembly through id2slot            (dip_ca_assemble)
+    host: read n_hit/n_miss and the miss ids (the one sync the reference also
+          has, dip_ca.py:139-146); gather the miss rows into pinned staging
+          with native threads
+    GPU : hits' up GEMV + h runs while the misses cross PCIe on a side stream
+          -> misses' up GEMV + h -> dual-source transposed-down gather
+
+The combined order is [hits in idx order, misses in idx order] with
+src 0 = hit / 1 = miss and row = resident slot / staging row, exactly as the
+reference builds it (dip_ca.py:158-171).  The hot set is ordered by
+key = count * I - id, descending (dip_ca.py:300-308); resident slots follow
+ascending channel id (dip_ca.py:107-113).
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import _dip_hip as K
+from qlinear import GROUP_SIZE, dequantize
+from dip_stream_predispatch import _transpose_down_to_int4, _use_gather, _use_down  # noqa: F401
+
+_use_ca_fused = True
+
+
+def hot_ids_from_counts(counts: torch.Tensor) -> torch.Tensor:
+    """Channels ordered by (selection count desc, id asc) via the single key
+    count * I - id (dip_ca.py:305-307)."""
+    cnt = counts.to(torch.long)
+    inter = cnt.numel()
+    key = cnt * inter - torch.arange(inter, dtype=torch.long, device=cnt.device)
+    return key.argsort(descending=True)
+
+
+class CABuffers:
+    """Staging for the streamed misses, sized for the worst case of k misses
+    (dip_ca.py:58-70), plus the per-token intermediates."""
+
+    def __init__(self, k, up_in_packed, up_ngroups, down_out, down_ngroups, device):
+        self.device = torch.device(device)
+        self.k = int(k)
+        dev = self.device
+        self.gpu_up_qw = torch.empty(k, up_in_packed, dtype=torch.int8, device=dev)
+        self.gpu_up_sc = torch.empty(k, up_ngroups, dtype=torch.bfloat16, device=dev)
+        self.pin_up_qw = torch.empty(k, up_in_packed, dtype=torch.int8).pin_memory()
+        self.pin_up_sc = torch.empty(k, up_ngroups, dtype=torch.bfloat16).pin_memory()
+        self.gpu_dn_qw = torch.empty(k, down_out // 2, dtype=torch.int8, device=dev)
+        self.gpu_dn_sc = torch.empty(k, down_ngroups, dtype=torch.bfloat16, device=dev)
+        self.pin_dn_qw = torch.empty(k, down_out // 2, dtype=torch.int8).pin_memory()
+        self.pin_dn_sc = torch.empty(k, down_ngroups, dtype=torch.bfloat16).pin_memory()
+        self.copy_stream = torch.cuda.Stream(device=dev)
+        self.h = torch.empty(k, dtype=torch.bfloat16, device=dev)
+        self._g = {}
+        self.host_threads = int(os.environ.get("DIP_HOST_THREADS", "8"))
+        # statistics of the last forward (hit rate, bytes streamed)
+        self.last_n_hit = 0
+        self.last_n_miss = 0
+
+    def g(self, inter: int) -> torch.Tensor:
+        t = self._g.get(inter)
+        if t is None:
+            t = self._g[inter] = torch.empty(inter, dtype=torch.bfloat16, device=self.device)
+        return t
+
+
+class CADIPMlp(nn.Module):
+    """MLP with a resident channel cache (dip_ca.py:73-196)."""
+
+    def __init__(self, gate_qw, gate_sc, up_qw, up_sc, down_qw, down_sc, buf,
+                 keep_ratio=0.6, cache_frac=0.3, device="cuda:0", down_transposed=False):
+        super().__init__()
+        self.device = torch.device(device)
+        self.keep_ratio = keep_ratio
+        self.buf = buf
+
+        self.gate_qw = gate_qw.to(self.device).contiguous()
+        self.gate_sc = gate_sc.to(self.device).contiguous()
+
+        # full up / down_t pinned on the host: the source of streamed misses
+        self.up_qw = up_qw.cpu().contiguous().pin_memory()
+        self.up_sc = up_sc.cpu().contiguous().pin_memory()
+        self.inter = up_qw.shape[0]
+        if down_transposed:
+            dn_t_qw, dn_t_sc = down_qw, down_sc
+        else:
+            dn_t_qw, dn_t_sc = _transpose_down_to_int4(down_qw.to(self.device),
+                                                       down_sc.to(self.device))
+        self.down_t_qw = dn_t_qw.cpu().contiguous().pin_memory()
+        self.down_t_sc = dn_t_sc.cpu().contiguous().pin_memory()
+        self.out_features = self.down_t_qw.shape[1] * 2
+
+        self.k = int(round(self.inter * keep_ratio))
+        self.cache_n = int(round(self.inter * cache_frac))
+
+        self.register_buffer("cache_ids", torch.empty(0, dtype=torch.long), persistent=False)
+        self.register_buffer("id2slot", torch.full((self.inter,), -1, dtype=torch.long),
+                             persistent=False)
+        self._res_up_qw = None
+        self._res_up_sc = None
+        self._res_dn_qw = None
+        self._res_dn_sc = None
+
+    def set_cache(self, hot_ids):
+        """Make the first cache_n of `hot_ids` resident (dip_ca.py:107-117)."""
+        hot_ids = hot_ids[: self.cache_n].cpu().sort().values
+        self.cache_ids = hot_ids.to(self.device)
+        id2 = torch.full((self.inter,), -1, dtype=torch.long)
+        id2[hot_ids] = torch.arange(len(hot_ids))
+        self.id2slot = id2.to(self.device)
+        self._res_up_qw = self.up_qw[hot_ids].to(self.device)
+        self._res_up_sc = self.up_sc[hot_ids].to(self.device)
+        self._res_dn_qw = self.down_t_qw[hot_ids].to(self.device)
+        self._res_dn_sc = self.down_t_sc[hot_ids].to(self.device)
+
+    def _gate(self, x):
+        if x.dim() == 3 and x.shape[1] == 1:
+            out = torch.stack([K.int4_gemv(self.gate_qw, self.gate_sc, x[b, 0].to(torch.bfloat16))
+                               for b in range(x.shape[0])])
+            return out.reshape(x.shape[0], 1, -1)
+        w = dequantize(self.gate_qw, self.gate_sc).to(x.dtype)
+        return F.linear(x, w)
+
+    def _stream_misses(self, miss_ids_cpu: torch.Tensor, n_miss: int):
+        """Pinned row gather of the misses (native threads) + async H2D on the
+        copy stream (dip_ca.py:146-156)."""
+        b = self.buf
+        t = b.host_threads
+        K.host_gather_rows(self.up_qw, miss_ids_cpu, b.pin_up_qw, t)
+        K.host_gather_rows(self.up_sc, miss_ids_cpu, b.pin_up_sc, t)
+        K.host_gather_rows(self.down_t_qw, miss_ids_cpu, b.pin_dn_qw, t)
+        K.host_gather_rows(self.down_t_sc, miss_ids_cpu, b.pin_dn_sc, t)
+        main = torch.cuda.current_stream(self.device)
+        b.copy_stream.wait_stream(main)
+        with torch.cuda.stream(b.copy_stream):
+            b.gpu_up_qw[:n_miss].copy_(b.pin_up_qw[:n_miss], non_blocking=True)
+            b.gpu_up_sc[:n_miss].copy_(b.pin_up_sc[:n_miss], non_blocking=True)
+            b.gpu_dn_qw[:n_miss].copy_(b.pin_dn_qw[:n_miss], non_blocking=True)
+            b.gpu_dn_sc[:n_miss].copy_(b.pin_dn_sc[:n_miss], non_blocking=True)
+
+    def _decode_one(self, xv: torch.Tensor) -> torch.Tensor:
+        b = self.buf
+        g, idx = K.gate_silu_topk(self.gate_qw, self.gate_sc, xv, self.k, g=b.g(self.inter))
+        combined, src, row, miss, counts = K.ca_assemble(self.id2slot, idx)
+        n_hit, n_miss = (int(v) for v in counts.cpu())   # host sync, as the reference
+        b.last_n_hit, b.last_n_miss = n_hit, n_miss
+        h = b.h[: self.k]
+        if n_hit:
+            K.ca_fused_gemv(self._res_up_qw, self._res_up_sc, b.gpu_up_qw, b.gpu_up_sc, xv,
+                            src[:n_hit], row[:n_hit], g=g, gid=combined[:n_hit], out=h[:n_hit])
+        if n_miss:
+            miss_cpu = miss[:n_miss].cpu()
+            self._stream_misses(miss_cpu, n_miss)
+            torch.cuda.current_stream(self.device).wait_stream(b.copy_stream)
+            K.ca_fused_gemv(self._res_up_qw, self._res_up_sc, b.gpu_up_qw, b.gpu_up_sc, xv,
+                            src[n_hit:], row[n_hit:], g=g, gid=combined[n_hit:], out=h[n_hit:])
+        return K.ca_down(self._res_dn_qw, self._res_dn_sc, b.gpu_dn_qw, b.gpu_dn_sc, h, src, row)
+
+    def forward(self, x):
+        if x.dim() != 3 or x.shape[1] != 1 or self.keep_ratio >= 0.999 or self._res_up_qw is None:
+            return self._dense(x)
+        xdt = x.dtype
+        ys = [self._decode_one(x[i, 0].to(torch.bfloat16)) for i in range(x.shape[0])]
+        return torch.stack(ys).to(xdt).reshape(x.shape[0], 1, -1)
+
+    def _dense(self, x):
+        """dip_ca.py:190-196."""
+        g = F.silu(self._gate(x))
+        up_w = dequantize(self.up_qw.to(self.device), self.up_sc.to(self.device)).to(x.dtype)
+        u = F.linear(x, up_w)
+        del up_w
+        h = g * u
+        dn_t = dequantize(self.down_t_qw.to(self.device),
+                          self.down_t_sc.to(self.device)).to(x.dtype)
+        return h @ dn_t
+
+
+def calibrate_cache_from_counts(cas, counts):
+    """Apply the reference's hot-set rule (dip_ca.py:300-308) to per-layer
+    selection counts gathered by any calibration pass."""
+    for c, cnt in zip(cas, counts):
+        c.set_cache(hot_ids_from_counts(cnt))

@@ -1,0 +1,169 @@
+"""A resident stack of DIP MLP layers decoding one token at a time.
+
+This is the MLP half of the reference's decode loop (64 x StreamingDIPMlp
+inside Qwen3DecoderLayer, gen_utils.py:49-93 / dip_stream_predispatch.py:
+176-204) without the attention half: every layer's int4 gate/up/down_t stays
+in HBM, the per-token intermediates (g, idx, h) and the kernels' workspace are
+shared by all layers (they run in stream order), and one token through all
+layers can be captured as a single HIP graph.
+
+Synthetic weights follow the benchmark configs: N(0, 0.02) draws quantized
+with the reference quantizer rule, drawn and quantized on the GPU.  Down is
+quantized directly in the transposed layout [inter, hidden] (same format as
+the reference's dequant -> transpose -> requant route, which the tests pin
+separately) so building a 64-layer Qwen3-32B stack takes seconds.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+import _dip_hip as K
+from quantize import quantize_tensor_int4_groupwise
+
+SHAPES = {
+    "qwen3-32b": dict(hidden=5120, inter=25600, layers=64),
+    "qwen3-8b": dict(hidden=4096, inter=12288, layers=36),
+}
+
+
+def keep_count(inter: int, keep_ratio: float) -> int:
+    """k = max(1, int(round(I * keep))) (dip_stream_predispatch.py:248)."""
+    return max(1, int(round(inter * keep_ratio)))
+
+
+def bytes_per_layer(hidden: int, inter: int, k: int) -> int:
+    """Algorithmic HBM bytes of one decode step of one layer: the gate is read
+    in full, up and down_t only on the k selected rows; one row is hidden/2
+    packed bytes + hidden/128 bf16 scales."""
+    row = hidden // 2 + 2 * (hidden // 128)
+    return inter * row + 2 * k * row
+
+
+class DIPStack:
+    def __init__(self, hidden: int, inter: int, layers: int, keep_ratio: float = 0.6,
+                 device="cuda:0", seed: int = 0):
+        self.hidden, self.inter, self.layers = hidden, inter, layers
+        self.keep_ratio = keep_ratio
+        self.k = keep_count(inter, keep_ratio)
+        self.device = torch.device(device)
+        dev = self.device
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        self.w = []
+        for _ in range(layers):
+            lw = {}
+            for name in ("gate", "up", "down_t"):
+                q, s = quantize_tensor_int4_groupwise(
+                    torch.randn(inter, hidden, device=dev, generator=gen) * 0.02)
+                lw[name + "_qw"], lw[name + "_sc"] = q, s
+            self.w.append(lw)
+        self.x = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
+        self.y = [torch.empty(hidden, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+        self.g = torch.empty(inter, dtype=torch.bfloat16, device=dev)
+        self.idx = torch.empty(self.k, dtype=torch.int32, device=dev)
+        self.h = torch.empty(self.k, dtype=torch.bfloat16, device=dev)
+        self.ws = torch.zeros(K.mlp_workspace_bytes(hidden, inter, self.k), dtype=torch.uint8,
+                              device=dev)
+        self.graph = None
+
+    @property
+    def bytes_per_token(self) -> int:
+        return self.layers * bytes_per_layer(self.hidden, self.inter, self.k)
+
+    def run_token(self):
+        """All layers on self.x, in stream order (one dip_mlp_decode each)."""
+        for lw, y in zip(self.w, self.y):
+            K.mlp_decode(lw["gate_qw"], lw["gate_sc"], lw["up_qw"], lw["up_sc"],
+                         lw["down_t_qw"], lw["down_t_sc"], self.x, self.k, y=y, g=self.g,
+                         idx=self.idx, h=self.h, ws=self.ws)
+
+    def capture(self):
+        """Capture run_token() as one HIP graph (after an eager warm-up)."""
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            self.run_token()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.run_token()
+        torch.cuda.synchronize(self.device)
+
+    def step(self, x_t: torch.Tensor):
+        """Decode one token: feed x_t into the captured graph's input buffer
+        and replay all layers."""
+        self.x.copy_(x_t, non_blocking=True)
+        self.graph.replay()
+
+    # -- per-stage timing --------------------------------------------------
+    def stage_graphs(self):
+        """One HIP graph per kernel stage, each launching that stage for every
+        layer back to back (on the intermediates the last token left)."""
+        lib = K.lib
+        H, I, k = self.hidden, self.inter, self.k
+        topk_bytes = (lib.dip_topk_workspace_size(I) + 255) // 256 * 256
+        ws_ptr = self.ws.data_ptr()
+        ws_n = self.ws.numel()
+        x = self.x.data_ptr()
+
+        def gate(st):
+            for lw in self.w:
+                K._check(lib.dip_int4_gemv(lw["gate_qw"].data_ptr(), lw["gate_sc"].data_ptr(), x,
+                                           self.g.data_ptr(), I, H, 1, st), "gate")
+
+        def topk(st):
+            for _ in self.w:
+                K._check(lib.dip_topk_select(self.g.data_ptr(), self.idx.data_ptr(), I, k,
+                                             ws_ptr, topk_bytes, st), "topk")
+
+        def up(st):
+            for lw in self.w:
+                K._check(lib.dip_up_gather_h(lw["up_qw"].data_ptr(), lw["up_sc"].data_ptr(), x,
+                                             self.idx.data_ptr(), self.g.data_ptr(),
+                                             self.h.data_ptr(), I, H, k, st), "up")
+
+        def down(st):
+            for lw, y in zip(self.w, self.y):
+                K._check(lib.dip_int4_gather_down(lw["down_t_qw"].data_ptr(),
+                                                  lw["down_t_sc"].data_ptr(), self.h.data_ptr(),
+                                                  self.idx.data_ptr(), y.data_ptr(), I, H, k,
+                                                  ctypes.c_void_p(ws_ptr + topk_bytes),
+                                                  ws_n - topk_bytes, st), "down")
+
+        graphs = {}
+        for name, fn in (("gate_silu", gate), ("topk", topk), ("up_gather_h", up),
+                         ("down_gather", down)):
+            s = torch.cuda.Stream(device=self.device)
+            s.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(s):
+                fn(s.cuda_stream)
+            torch.cuda.current_stream(self.device).wait_stream(s)
+            torch.cuda.synchronize(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn(torch.cuda.current_stream(self.device).cuda_stream)
+            graphs[name] = g
+        return graphs
+
+    def stage_times_ms(self, reps: int = 3):
+        """Average duration of one launch of each kernel stage: each stage's
+        graph (one launch per layer, back to back) is replayed between two
+        HIP events on the replaying stream; time / (layers * reps)."""
+        self.run_token()
+        torch.cuda.synchronize(self.device)
+        graphs = self.stage_graphs()
+        stream = torch.cuda.current_stream(self.device)
+        out = {}
+        for name, g in graphs.items():
+            g.replay()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize(self.device)
+            out[name] = e0.elapsed_time(e1) / (reps * self.layers)
+        return out

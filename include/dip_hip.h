@@ -1,0 +1,239 @@
+/*
+ * dip_hip.h — C ABI of libdip_hip.so, the MI355X (gfx950) decode path of
+ * Dynamic Input Pruning (DIP) for an int4 g128 SwiGLU MLP.
+ *
+ * Conventions for every entry point:
+ *   - All tensor arguments are DEVICE pointers to contiguous, caller-owned
+ *     memory; weight/activation pointers must be 16-byte aligned.
+ *   - bf16 values travel as uint16_t bit patterns; packed int4 weights as
+ *     int8_t [rows, cols/2] (low nibble = even column, high nibble = odd
+ *     column, two's complement), scales as bf16 [rows, cols/128].
+ *   - `stream` is a hipStream_t (NULL = legacy default stream).  Calls only
+ *     enqueue work: none synchronises the host and none allocates memory.
+ *   - Return value: DIP_OK (0), a negative DIP_ERR_* code for an argument
+ *     rejected before any launch, or a positive hipError_t from the launch.
+ *   - Workspaces are caller-owned device buffers of the size the matching
+ *     *_workspace_size() reports.  They must be zero-filled once before their
+ *     first use; the kernels leave them zeroed again after every call.
+ *     Calls that share a workspace must be ordered on one stream.
+ *
+ * Reference interfaces each entry point replaces are cited as
+ * <file>:<line> of rohitpotluri/dynamic-input-pruning.
+ */
+#ifndef DIP_HIP_H_
+#define DIP_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  DIP_OK = 0,
+  DIP_ERR_NULL = -1,        /* a required pointer is NULL */
+  DIP_ERR_SHAPE = -2,       /* a size is negative / inconsistent / too large */
+  DIP_ERR_ALIGN = -3,       /* a pointer is not 16-byte aligned */
+  DIP_ERR_UNSUPPORTED = -4, /* the shape has no kernel instantiation */
+  DIP_ERR_WORKSPACE = -5,   /* workspace missing or smaller than required */
+  DIP_ERR_ARG = -6          /* any other invalid argument */
+};
+
+enum { DIP_ACT_NONE = 0, DIP_ACT_SILU = 1 };
+
+/* Human-readable text for a status returned by this library. */
+const char* dip_status_string(int status);
+
+/* Library version as an integer (major * 10000 + minor * 100 + patch). */
+int dip_version(void);
+
+/* Highest row count the top-k supports (its keys are staged in LDS). */
+int64_t dip_topk_max_n(void);
+
+/*
+ * out[r] = bf16( sum_c (q*s)[r,c] * x[c] ), or with act = DIP_ACT_SILU
+ * out[r] = bf16( silu( float( bf16(dot) ) ) ).
+ * Replaces int4_ops::int4_gemv (kernels/int4_gemv/int4_gemv.cu:89-115,
+ * gate_kernel.py:29-33); DIP_ACT_SILU also fuses the separate F.silu of
+ * dip_stream_predispatch.py:182.
+ */
+int dip_int4_gemv(const int8_t* qweight, const uint16_t* scales, const uint16_t* x,
+                  uint16_t* out, int64_t out_features, int64_t in_features, int act,
+                  void* stream);
+
+/*
+ * idx[0:k] int32 = the reference's threshold top-k of |s| (bisection of 25
+ * fp32 steps on max|s|, then tier |s| > t_strict in ascending index followed
+ * by tier t_lo < |s| <= t_strict in ascending index, unfilled slots 0).
+ * Bit-exact with topk_ops::topk_select (kernels/topk_select/topk_select.cu:
+ * 134-171, topk_kernel.py:29-40).  n <= dip_topk_max_n(); s 16-byte aligned.
+ * One workgroup, no host round trips; the workspace only receives the last
+ * call's thresholds (dip_topk_meta).
+ */
+size_t dip_topk_workspace_size(int64_t n);
+int dip_topk_select(const uint16_t* s, int32_t* idx, int64_t n, int64_t k,
+                    void* workspace, size_t ws_bytes, void* stream);
+/* Copy the last top-k's thresholds (fp32 t_lo, t_strict) and tier sizes
+ * (int32 count_a, count_b) from the workspace into `meta` (device, 16 B). */
+int dip_topk_meta(const void* workspace, void* meta_out, void* stream);
+
+/*
+ * out[j] = bf16( sum_c (q*s)[indices[j], c] * x[c] ), j < k.
+ * Replaces int4_gather_ops::int4_gather_gemv
+ * (kernels/int4_gather/int4_gather_gemv.cu:87-115).
+ */
+int dip_int4_gather_gemv(const int8_t* qweight, const uint16_t* scales, const uint16_t* x,
+                         const int32_t* indices, uint16_t* out, int64_t rows,
+                         int64_t in_features, int64_t k, void* stream);
+
+/*
+ * Up-row gather GEMV fused with h: h[j] = bf16( float(g[indices[j]]) *
+ * float( bf16( sum_c (q*s)[indices[j], c] * x[c] ) ) ).
+ * Replaces int4_gather_gemv + `(g[idx] * up_sel).to(bf16)` at
+ * dip_stream_predispatch.py:199-201.
+ */
+int dip_up_gather_h(const int8_t* qweight, const uint16_t* scales, const uint16_t* x,
+                    const int32_t* indices, const uint16_t* g, uint16_t* h, int64_t rows,
+                    int64_t in_features, int64_t k, void* stream);
+
+/*
+ * y[o] = bf16( sum_{j<k} float(h[j]) * (q*s)[row_j, o] ) over rows of the
+ * transposed down matrix down_t [rows, out_features/2]; row_j = indices[j],
+ * or j when indices == NULL (the staged-copy layout of the reference).
+ * Deterministic: fp32 partial sums over fixed row blocks reduced in a fixed
+ * order, no float atomics.
+ * Replaces int4_down_ops::int4_gather_down
+ * (kernels/int4_down/int4_gather_down.cu:77-102).
+ */
+size_t dip_gather_down_workspace_size(int64_t k, int64_t out_features);
+int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uint16_t* h,
+                         const int32_t* indices, uint16_t* y, int64_t rows,
+                         int64_t out_features, int64_t k, void* workspace, size_t ws_bytes,
+                         void* stream);
+
+/*
+ * Launch tuning, no counterpart in the reference (process-wide, host side;
+ * speed only):
+ *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 2)
+ *   DIP_TUNE_DOWN_LPR           lanes per row segment in the down kernel:
+ *                               32/16/8/4, 0 = widest that divides (default)
+ *   DIP_TUNE_DOWN_BLOCKS        target workgroups of the down kernel (640)
+ *   DIP_TUNE_DOWN_DEQUANT       0: v_cvt_f32_ubyte + bias removal,
+ *                               1: v_cvt_off_f32_i4 via SDWA (default 1)
+ *   DIP_TUNE_DOWN_UNROLL        rows in flight per lane in the down kernel (4)
+ *   DIP_TUNE_ROWDOT_X_LDS       gate/up keep x in LDS (1) or in VGPRs (0) (1)
+ *   DIP_TUNE_ROWDOT_DEPTH       rows of loads in flight per row group, 2..4 (3)
+ *   DIP_TUNE_DOWN_CPL           16-byte chunks per lane per row in the down
+ *                               kernel, 1 or 2 (2)
+ * The down tiling fixes the fp32 summation order, so changing it may move y
+ * by an ulp; for a fixed setting results are identical run to run.
+ * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
+ */
+enum {
+  DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
+  DIP_TUNE_DOWN_LPR = 1,
+  DIP_TUNE_DOWN_BLOCKS = 2,
+  DIP_TUNE_DOWN_DEQUANT = 3,
+  DIP_TUNE_DOWN_UNROLL = 4,
+  DIP_TUNE_ROWDOT_X_LDS = 5,
+  DIP_TUNE_ROWDOT_DEPTH = 6,
+  DIP_TUNE_DOWN_CPL = 7,
+  DIP_TUNE_COUNT = 8
+};
+int dip_set_tuning(int knob, int value);
+int dip_get_tuning(int knob);
+
+/*
+ * Cache-aware dual-source up GEMV: row j comes from the resident cache
+ * (src[j] == 0, row res[row[j]]) or the streamed staging buffer
+ * (src[j] != 0, row str[row[j]]).  Replaces ca_fused_ops::ca_fused_gemv
+ * (kernels/ca_fused/ca_fused_gemv.cu:87-112).  If g != NULL the output is
+ * h[j] = bf16(g[gid[j]] * bf16(dot)) instead (dip_ca.py:185-186).
+ */
+int dip_ca_fused_gemv(const int8_t* res_qw, const uint16_t* res_sc, const int8_t* str_qw,
+                      const uint16_t* str_sc, const uint16_t* x, const int32_t* src,
+                      const int32_t* row, const uint16_t* g, const int32_t* gid,
+                      uint16_t* out, int64_t res_rows, int64_t str_rows,
+                      int64_t in_features, int64_t k, void* stream);
+
+/*
+ * Cache-aware dual-source down: like dip_int4_gather_down with row j read
+ * from the resident cache (src[j] == 0) or the staging buffer (src[j] != 0),
+ * replacing the torch.cat assembly + int4_gather_down of dip_ca.py:175-187.
+ */
+int dip_ca_down(const int8_t* res_qw, const uint16_t* res_sc, const int8_t* str_qw,
+                const uint16_t* str_sc, const uint16_t* h, const int32_t* src,
+                const int32_t* row, uint16_t* y, int64_t res_rows, int64_t str_rows,
+                int64_t out_features, int64_t k, void* workspace, size_t ws_bytes,
+                void* stream);
+
+/*
+ * Cache-aware hit/miss assembly (dip_ca.py:137-171): from idx[k] and
+ * id2slot[inter] (int64, -1 = not resident) write, in the order
+ * [hits in idx order, misses in idx order]:
+ *   combined[k] channel ids, src[k] (0 hit / 1 miss), row[k] (slot for hits,
+ *   0..n_miss-1 for misses), miss_ids[0:n_miss], counts[0] = n_hit,
+ *   counts[1] = n_miss.
+ */
+int dip_ca_assemble(const int64_t* id2slot, const int32_t* idx, int32_t* combined,
+                    int32_t* src, int32_t* row, int32_t* miss_ids, int32_t* counts,
+                    int64_t inter, int64_t k, void* stream);
+
+/*
+ * Dequantize rows: mode 0 -> out float32 [rows, cols] = float(q) * float(s)
+ * (the value the reference kernels multiply with, int4_gemv.cu:71-72);
+ * mode 1 -> out bf16 [rows, cols] = bf16(q*s) (qlinear.dequantize,
+ * qlinear.py:53-64).  Rows are indices[i] (or i when indices == NULL).
+ */
+int dip_dequant_rows(const int8_t* qweight, const uint16_t* scales, const int32_t* indices,
+                     void* out, int64_t n_out_rows, int64_t rows, int64_t cols, int mode,
+                     void* stream);
+
+/*
+ * Quantize w [rows, cols] (fp32, or bf16 when w_is_bf16) to int4 g128:
+ * s = max(max|w_group| / 7, 1e-8) in fp32, q = clamp(round_half_even(w / s),
+ * -8, 7), scales = bf16(s).  Bit-exact with quantize_tensor_int4_groupwise
+ * (scripts/quantize.py:32-64) run on the CPU.  w 8-byte aligned.
+ */
+int dip_quantize_int4(const void* w, int w_is_bf16, int8_t* qweight, uint16_t* scales,
+                      int64_t rows, int64_t cols, void* stream);
+
+/*
+ * down [out_features, inter] int4 -> down_t [inter, out_features] int4 via
+ * bf16 dequantize, transpose and re-quantization along out_features; bit-exact
+ * with _transpose_down_to_int4 (dip_stream_predispatch.py:100-120).
+ */
+int dip_transpose_down_int4(const int8_t* down_qw, const uint16_t* down_sc, int8_t* down_t_qw,
+                            uint16_t* down_t_sc, int64_t out_features, int64_t inter,
+                            void* stream);
+
+/*
+ * One resident-weight DIP MLP decode step (batch 1, seq 1):
+ *   g = silu(gate(x)); idx = topk(|g|, k); h = g[idx] * up[idx](x);
+ *   y = h @ down_t[idx]
+ * i.e. StreamingDIPMlp.forward (dip_stream_predispatch.py:176-204) with all
+ * weights resident in HBM.  g_out [inter], idx_out [k], h_out [k] receive
+ * the intermediates; y [hidden].  workspace: dip_mlp_workspace_size().
+ */
+size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k);
+int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
+                   const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
+                   const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
+                   uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
+                   void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Host-side row gather for the cache-aware miss path: copies rows
+ * src + ids[i] * row_bytes -> dst + i * row_bytes for i < n using up to
+ * `threads` host threads (the pinned index_select of dip_ca.py:148-153).
+ * Host pointers; returns DIP_OK or a DIP_ERR_* code.
+ */
+int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t n,
+                         int64_t row_bytes, int64_t src_rows, int threads);
+
+#ifdef __cplusplus
+}  // extern "C"
+#endif
+
+#endif  /* DIP_HIP_H_ */

@@ -1,0 +1,115 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/dip_hip.h declares, rejects bad arguments before any launch, and its
+host-side row gather is correct."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import _dip_hip as K
+
+
+def _declared():
+    text = K.HEADER_PATH.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    names = _declared()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(K.lib, n), n
+    assert set(names) == set(K._SIGS), set(names) ^ set(K._SIGS)
+
+
+def test_status_strings():
+    assert K.status_string(0) == "ok"
+    for code in (-1, -2, -3, -4, -5, -6):
+        assert K.status_string(code) not in ("ok", "unknown status")
+    assert K.lib.dip_version() >= 100
+    assert K.lib.dip_topk_max_n() == 65536
+
+
+def _fake(n=16):
+    """An aligned host pointer that is never dereferenced by a rejected call."""
+    buf = (ctypes.c_uint8 * (n + 16))()
+    addr = ctypes.addressof(buf)
+    return buf, addr + (-addr % 16)
+
+
+def test_argument_rejection_before_launch():
+    keep, p = _fake()
+    L = K.lib
+    # NULL weights
+    assert L.dip_int4_gemv(None, p, p, p, 8, 128, 0, None) == -1
+    # in_features not a multiple of 128
+    assert L.dip_int4_gemv(p, p, p, p, 8, 100, 0, None) == -2
+    # misaligned weights
+    assert L.dip_int4_gemv(p + 1, p, p, p, 8, 128, 0, None) == -3
+    # unsupported width (no instantiation): 384 = 12 chunks
+    # (validated by launch dispatch, which runs no kernel for unknown shapes)
+    # bad activation
+    assert L.dip_int4_gemv(p, p, p, p, 8, 128, 5, None) == -6
+    # top-k: n too large, workspace missing/small
+    assert L.dip_topk_select(p, p, 1 << 20, 5, p, 1 << 20, None) == -2
+    assert L.dip_topk_select(p, p, 100, 5, None, 0, None) == -5
+    assert L.dip_topk_select(p, p, 100, 5, p, 16, None) == -5
+    # down: workspace too small
+    need = L.dip_gather_down_workspace_size(15360, 5120)
+    assert need > 0
+    assert L.dip_int4_gather_down(p, p, p, None, p, 15360, 5120, 15360, p, need - 1, None) == -5
+    # contiguous down with k > rows
+    assert L.dip_int4_gather_down(p, p, p, None, p, 10, 5120, 11, p, need, None) == -2
+    # mlp: k > inter, missing outputs
+    ws = L.dip_mlp_workspace_size(5120, 25600, 15360)
+    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 30000, p, ws, None) == -2
+    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, None, p, p, 5120, 25600, 100, p, ws, None) == -1
+    assert L.dip_set_tuning(3, 7) == -6
+    assert L.dip_set_tuning(99, 1) == -6
+    assert L.dip_get_tuning(99) == -6
+    assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
+    assert L.dip_ca_assemble(None, p, p, p, p, p, p, 10, 5, None) == -1
+    del keep
+
+
+def test_workspace_sizes():
+    L = K.lib
+    assert L.dip_topk_workspace_size(25600) >= 16
+    # down partials: at most DOWN_BLOCKS rows of out fp32, independent of k
+    need = L.dip_gather_down_workspace_size(15360, 5120)
+    assert need % (5120 * 4) == 0
+    assert need == L.dip_gather_down_workspace_size(25600, 5120)
+    assert L.dip_mlp_workspace_size(5120, 25600, 15360) >= need
+
+
+def test_host_gather_rows():
+    rng = np.random.default_rng(0)
+    src = torch.from_numpy(rng.integers(-128, 128, size=(300, 2560), dtype=np.int8))
+    ids = torch.from_numpy(rng.permutation(300)[:111].astype(np.int32))
+    for threads in (1, 3, 8):
+        dst = torch.zeros(200, 2560, dtype=torch.int8)
+        K.host_gather_rows(src, ids, dst, threads=threads)
+        assert torch.equal(dst[:111], src[ids.long()])
+        assert torch.all(dst[111:] == 0)
+    sc = torch.from_numpy(rng.standard_normal((300, 40)).astype(np.float32)).to(torch.bfloat16)
+    dst = torch.zeros(111, 40, dtype=torch.bfloat16)
+    K.host_gather_rows(sc, ids, dst, threads=4)
+    assert torch.equal(dst, sc[ids.long()])
+    bad = torch.tensor([5, 300], dtype=torch.int32)
+    with pytest.raises(RuntimeError):
+        K.host_gather_rows(src, bad, torch.zeros(2, 2560, dtype=torch.int8))
+
+
+def test_python_layer_rejects_host_tensors():
+    qw = torch.zeros(8, 64, dtype=torch.int8)
+    sc = torch.zeros(8, 1, dtype=torch.bfloat16)
+    x = torch.zeros(128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        K.int4_gemv(qw, sc, x)
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        K.int4_gemv(torch.zeros(8, 50, dtype=torch.int8), sc, x)
+    with pytest.raises(RuntimeError, match="must be torch.bfloat16"):
+        K.int4_gemv(qw, sc.float(), x)
