@@ -412,7 +412,8 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
 
 
 TUNE = {"rowdot_wgs_per_cu": 0, "down_lpr": 1, "down_blocks": 2, "down_dequant": 3,
-        "down_unroll": 4, "rowdot_x_lds": 5, "rowdot_depth": 6, "down_cpl": 7}
+        "down_unroll": 4, "rowdot_x_lds": 5, "rowdot_depth": 6, "down_cpl": 7,
+        "topk_stamps": 8}
 
 
 def set_tuning(name: str, value: int) -> None:

@@ -125,13 +125,32 @@ DIP_DEV float cvt_nibble_div16(uint32_t v) {
 
 // Sum over aligned groups of W lanes (W a power of two <= 64), every lane of
 // the group receiving the total: DPP within rows of 16 lanes (xor 1, xor 2,
-// half-row mirror, row mirror), then v_permlane16_swap / a 32-lane swap to
+// half-row mirror, row mirror), then v_permlane16_swap / v_permlane32_swap to
 // combine rows.  All VALU, no LDS round trips.
 template <int CTRL>
 DIP_DEV float dpp_mov(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
                                                             0xF, 0xF, true));
 }
+
+// v_permlane{16,32}_swap_b32 a, b swaps the odd rows (of 16 / 32 lanes) of a
+// with the even rows of b.  With a = b = v every lane then holds its own row
+// in one register and the partner row in the other, so a + b is the sum of
+// the row pair in every lane.  Written as inline asm with two distinct
+// read-write registers: this toolchain's optimiser folds the second result
+// of __builtin_amdgcn_permlane16_swap into the first (both read element 0).
+// The s_nop covers the VALU-write -> permlane read hazard.
+DIP_DEV float row_pair_sum16(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+DIP_DEV float row_pair_sum32(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 template <int W>
 DIP_DEV float group_sum(float v) {
   static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "W");
@@ -139,17 +158,8 @@ DIP_DEV float group_sum(float v) {
   if (W >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
   if (W >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror: the other quad of 8
   if (W >= 16) v += dpp_mov<0x140>(v); // row_mirror: the other half of 16
-  if (W >= 32) {
-    // rows (0,1) and (2,3) exchange: r[0] + r[1] = sum of the two rows
-    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
-                                                    __builtin_bit_cast(uint32_t, v), false, false);
-    v = __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-  }
-  if (W >= 64) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
-                                                    __builtin_bit_cast(uint32_t, v), false, false);
-    v = __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-  }
+  if (W >= 32) v = row_pair_sum16(v);  // rows (0,1) and (2,3)
+  if (W >= 64) v = row_pair_sum32(v);  // lanes 0-31 and 32-63
   return v;
 }
 

@@ -70,7 +70,8 @@ struct TopkMeta {
   uint32_t key_max;
   int32_t n_valid;
   int32_t pad;
-  uint64_t stamp[6];  // wall_clock64() at the top-k's phase boundaries (diagnostics)
+  uint64_t stamp[6];   // wall_clock64() at the top-k's phase boundaries (diagnostics)
+  uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
 };
 
 // Launchers (return hipSuccess or a DIP_ERR_* code).

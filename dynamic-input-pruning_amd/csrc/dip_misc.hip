@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 0, 1024, 1, 2, 1, 3, 2};
+int g_tune[DIP_TUNE_COUNT] = {2, 0, 1024, 1, 2, 1, 3, 2, 0};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -191,6 +191,9 @@ extern "C" int dip_set_tuning(int knob, int value) {
       break;
     case DIP_TUNE_DOWN_CPL:
       if (value != 1 && value != 2) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_TOPK_STAMPS:
+      if (value != 0 && value != 1) return DIP_ERR_ARG;
       break;
     default:
       return DIP_ERR_ARG;

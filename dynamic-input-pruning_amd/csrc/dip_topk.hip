@@ -8,17 +8,26 @@
 //     #{|s| > t} > k   <=>   a_{k+1} > t
 // where a_{k+1} is the (k+1)-th largest |s| (NaN never counts, fewer than k+1
 // values means "never").  So the whole bisection is a function of two
-// numbers, max|s| and a_{k+1}, which a 32768-bin histogram of the 15-bit |s|
-// keys gives exactly.  The steps are then replayed in registers with the same
-// fp32 arithmetic, and the compaction runs once over keys staged in LDS.
+// numbers, max|s| and a_{k+1}, which a 32768-bin histogram of the 15-bit
+// magnitudes gives exactly; the steps are then replayed with the same fp32
+// arithmetic.
 //
-//   pass 1 (many workgroups, or fused into the gate GEMV epilogue):
-//       fine[key]++, coarse[key >> 7]++ with device-scope atomics
-//   pass 2 (one workgroup of 1024 threads):
-//       coarse suffix scan -> bin of a_{k+1} and of max; fine scan inside
-//       those bins -> exact keys; 25 bisection steps -> (lo, hi); per-thread
-//       tier counts -> block scan -> scatter of ascending ids; zero the
-//       histogram bins it used so the workspace is clean for the next call.
+// Launch: kBlocks workgroups of 1024 threads (16 waves).  Every workgroup
+// loads all n values and repeats the analysis (histogram, a_{k+1}, max,
+// bisection, per-wave tier counts) on identical data, so all of them agree on
+// every threshold and position; workgroup b then writes only the ids of the
+// keys its wave b holds.  This spreads the per-key scatter, the costliest
+// part, over 16 CUs without any inter-workgroup communication.
+//
+// Data layout: wave w holds the R*512 consecutive values [w*512R, (w+1)*512R)
+// as raw bf16 bits in VGPRs (lane L, round r: the 8 values of chunk
+// w*64R + 64r + L), so loads are coalesced and each wave's keys form one
+// contiguous index range.
+//
+// Magnitudes are used unflushed: bf16 subnormals (|bits| 1..0x7F) are 0 under
+// the reference's --use_fast_math, so histogram bins below 0x80 all mean 0
+// and both cuts are clamped to >= 0x80; NaN and padding (0xFFFF) land in bins
+// above 0x7F80, which the search ignores and the tier ranges exclude.
 #include "dip_common.h"
 #include "dip_internal.h"
 
@@ -28,171 +37,211 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
+constexpr int kBlocks = kWaves;  // workgroup b writes the ids held by its wave b
 constexpr uint32_t kNoKey = 0xFFFFFFFFu;
+constexpr uint32_t kMaxValidKey = kKeyInf;  // 0x7F80: +inf
+constexpr uint32_t kMinNormalKey = 0x0080u;
 
-// Inclusive suffix sum across the 64 lanes of a wave: lane L gets
-// sum_{L' >= L} v_{L'}.
-DIP_DEV uint32_t wave_suffix(uint32_t v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    uint32_t t = __shfl_down(v, d, 64);
-    if (lane + d < 64) v += t;
-  }
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// DPP move with zero fill: lanes whose source is outside the row (or whose
+// row is masked off) read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+DIP_DEV uint32_t dpp_zero(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, true);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: Hillis-Steele within
+// rows of 16 (row_shr 1, 2, 4, 8), then row_bcast:15 / row_bcast:31 carry
+// the row totals into the later rows.
+DIP_DEV uint32_t wave_prefix(uint32_t v) {
+  v += dpp_zero<0x111>(v);        // row_shr:1
+  v += dpp_zero<0x112>(v);        // row_shr:2
+  v += dpp_zero<0x114>(v);        // row_shr:4
+  v += dpp_zero<0x118>(v);        // row_shr:8
+  v += dpp_zero<0x142, 0xA>(v);   // row_bcast:15 -> rows 1, 3
+  v += dpp_zero<0x143, 0xC>(v);   // row_bcast:31 -> rows 2, 3
   return v;
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave (64-bit payload).
-DIP_DEV uint64_t wave_prefix64(uint64_t v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    uint64_t t = __shfl_up(v, d, 64);
-    if (lane >= d) v += t;
-  }
-  return v;
+DIP_DEV uint32_t lane63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
+
+// Per 16-bit half: 1 if d < span1 (unsigned), else 0.  Saturating packed
+// subtract then min with 1, as two VOP3P instructions (written as asm so the
+// compiler keeps them packed instead of splitting into per-half compares).
+DIP_DEV uint32_t in_span2(uint32_t d, uint32_t span1_2, uint32_t ones) {
+  uint32_t r;
+  asm("v_pk_sub_u16 %0, %1, %2 clamp\n\tv_pk_min_u16 %0, %0, %3"
+      : "=&v"(r)
+      : "v"(span1_2), "v"(d), "v"(ones));
+  return r;
 }
 
-// Highest lane whose predicate holds, or -1.
-DIP_DEV int highest_lane(bool p) {
-  const unsigned long long m = __ballot(p);
-  return m ? 63 - __clzll(m) : -1;
+DIP_DEV uint32_t pk_sub(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) - __builtin_bit_cast(u16x2, b));
+}
+DIP_DEV uint32_t pk_add(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) + __builtin_bit_cast(u16x2, b));
+}
+
+// Elements [base, n) of a chunk that straddles n, 2 per dword; the rest read
+// 0xFFFF.
+DIP_DEV void load_tail8(const uint16_t* __restrict__ s, int n, int base, uint32_t out[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = base + 2 * i < n ? s[base + 2 * i] : 0xFFFFu;
+    const uint32_t hi = base + 2 * i + 1 < n ? s[base + 2 * i + 1] : 0xFFFFu;
+    out[i] = lo | (hi << 16);
+  }
 }
 
 }  // namespace
 
-// Keys of 8 consecutive bf16 values from one 128-bit load, packed 2 per
-// dword; positions past n get 0xFFFF (never counted, never selected).
-DIP_DEV void load_keys8(const uint16_t* __restrict__ s, int n, int c, uint32_t out[4]) {
-  const int base = c * 8;
-  uint32_t w[4];
-  if (base + 8 <= n) {
-    const uint4 v = *reinterpret_cast<const uint4*>(s + base);
-    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = base + 2 * i < n ? s[base + 2 * i] : 0xFFFFu;
-      const uint32_t hi = base + 2 * i + 1 < n ? s[base + 2 * i + 1] : 0xFFFFu;
-      w[i] = lo | (hi << 16);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = w[i] & 0xFFFFu, hi = w[i] >> 16;
-    const uint32_t klo = lo == 0xFFFFu && base + 2 * i >= n ? 0xFFFFu : topk_key(lo);
-    const uint32_t khi = hi == 0xFFFFu && base + 2 * i + 1 >= n ? 0xFFFFu : topk_key(hi);
-    out[i] = klo | (khi << 16);
-  }
-}
-
-// One workgroup of 1024 threads; dynamic LDS = 32768 u32 histogram bins.
-// Thread t owns 8-element chunks t, t+1024, ... (kRounds of them, n <=
-// kRounds * 8192) in registers, and histogram bins [32t, 32t+32).
-template <int kRounds>
+// R rounds of 8 values per lane: n <= 16 waves * 64 lanes * 8R.
+template <int R>
 __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restrict__ s, int n,
                                                         int k, int32_t* __restrict__ idx,
-                                                        TopkMeta* __restrict__ meta) {
-  extern __shared__ uint32_t hist[];
-  __shared__ uint32_t wsum[kWaves];
-  __shared__ uint32_t wround[kWaves][kRounds];
-  __shared__ int wmax[kWaves];
-  __shared__ uint32_t sh_a, sh_max, sh_nvalid, sh_cut_a, sh_cut_b, sh_tot_a;
+                                                        TopkMeta* __restrict__ meta,
+                                                        int stamps) {
+  // Tier counts packed 16|16 while block totals stay below 2^16.
+  constexpr bool kPack = R * 8 * kThreads <= 32768;
+  extern __shared__ uint32_t hist[];  // kFineBins bins
+  __shared__ uint32_t wtot[kWaves];
+  __shared__ uint32_t wtot_b[kWaves];
+  __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b;
   __shared__ float sh_lo, sh_hi;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int nchunks = (n + 7) >> 3;
-  if (tid == 0 && meta) meta->stamp[0] = wall_clock64();
+  const bool lead = blockIdx.x == 0;
+  // Phase stamps (diagnostics, off by default: each store makes the storing
+  // wave wait for its completion at the next vmcnt wait).
+  const bool stamp = stamps && lead && tid == 0;
+  if (stamp) {
+    meta->stamp[0] = wall_clock64();
+    meta->cycles[0] = clock64();
+  }
 
-  // ---- keys into registers (loads issued before the LDS clear) ----------
-  uint32_t key[kRounds][4];
+  // ---- 1. values into registers; clear the histogram meanwhile -----------
+  // Whole chunks are fetched with predicated 128-bit loads (no else branch,
+  // so all R loads stay in flight together); the one chunk that straddles n
+  // is filled element by element afterwards.
+  uint32_t key[R][4];
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    const int c = tid + r * kThreads;
-    if (c < nchunks) {
-      load_keys8(s, n, c, key[r]);
-    } else {
+  for (int r = 0; r < R; ++r) {
+    const int base = (wave * 64 * R + 64 * r + lane) * 8;
+    uint4 v = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+    if (base + 8 <= n) v = *reinterpret_cast<const uint4*>(s + base);
+    key[r][0] = v.x;
+    key[r][1] = v.y;
+    key[r][2] = v.z;
+    key[r][3] = v.w;
+  }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) key[r][i] = 0xFFFFFFFFu;
-    }
+  for (int r = 0; r < R; ++r) {
+    const int base = (wave * 64 * R + 64 * r + lane) * 8;
+    if (base < n && base + 8 > n) load_tail8(s, n, base, key[r]);
   }
   {
     uint4* h4 = reinterpret_cast<uint4*>(hist);
 #pragma unroll
-    for (int i = 0; i < kFineBins / 4 / kThreads; ++i) h4[tid + i * kThreads] = make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < kFineBins / 4 / kThreads; ++i)
+      h4[tid + i * kThreads] = make_uint4(0, 0, 0, 0);
   }
   if (tid == 0) {
     sh_a = kNoKey;
     sh_max = kNoKey;
   }
   __syncthreads();
-  if (tid == 0 && meta) meta->stamp[1] = wall_clock64();
+  if (stamp) meta->stamp[1] = wall_clock64();
 
-  // ---- LDS histogram of valid keys ---------------------------------------
+  // ---- 2. histogram of every magnitude (NaN / padding bins ignored later) --
+  // (rounds wholly past n are skipped: their padding would pile onto one bin)
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
+  for (int r = 0; r < R; ++r) {
+    if ((wave * 64 * R + 64 * r + lane) * 8 < n) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = key[r][i] & 0xFFFFu, hi = key[r][i] >> 16;
-      if (lo <= kKeyInf) atomicAdd(&hist[lo], 1u);
-      if (hi <= kKeyInf) atomicAdd(&hist[hi], 1u);
+      for (int i = 0; i < 4; ++i) {
+        atomicAdd(&hist[key[r][i] & 0x7FFFu], 1u);
+        atomicAdd(&hist[(key[r][i] >> 16) & 0x7FFFu], 1u);
+      }
     }
   }
   __syncthreads();
-  if (tid == 0 && meta) meta->stamp[2] = wall_clock64();
+  if (stamp) meta->stamp[2] = wall_clock64();
 
-  // ---- block suffix scan of my 32 bins' sums -----------------------------
-  const uint4* my_bins = reinterpret_cast<const uint4*>(hist) + tid * 8;
-  uint32_t tsum = 0;
-  int top = -1;  // highest nonempty bin of mine
+  // ---- 3. max and a_{k+1} from a scan of the bins, from the top ----------
+  // Wave w reads its 2048 bins as eight 256-bin rows j; lane L holds bins
+  // 2048w + 256j + 4L .. +3 (consecutive lanes, consecutive 16 B: no bank
+  // conflicts).
+  uint32_t nvalid = 0;
+  {
+    const uint4* h4 = reinterpret_cast<const uint4*>(hist);
+    uint4 v[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint4 v = my_bins[i];
-    tsum += v.x + v.y + v.z + v.w;
-    if (v.x) top = 4 * i;
-    if (v.y) top = 4 * i + 1;
-    if (v.z) top = 4 * i + 2;
-    if (v.w) top = 4 * i + 3;
-  }
-  const uint32_t wincl = wave_suffix(tsum, lane);      // within the wave, from my lane up
-  int wtop = top >= 0 ? tid * 32 + top : -1;
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) wtop = max(wtop, __shfl_xor(wtop, d, 64));
-  if (lane == 0) {
-    wsum[wave] = wincl;   // lane 0 holds the whole wave's sum
-    wmax[wave] = wtop;
-  }
-  __syncthreads();
-  uint32_t above_waves = 0;
-  int gmax = -1;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    if (w > wave) above_waves += wsum[w];
-    gmax = max(gmax, wmax[w]);
-  }
-  const uint32_t suf_me = wincl + above_waves;   // valid keys in bins >= 32*tid
-  const uint32_t suf_next = suf_me - tsum;       // valid keys in bins >= 32*(tid+1)
-  const uint32_t need = (uint32_t)k + 1u;
-  if (suf_me >= need && suf_next < need) {
-    // a_{k+1} lies in my bins: walk them from the top
-    uint32_t run = suf_next;
-    uint32_t a = kNoKey;
-    for (int b = 31; b >= 0 && a == kNoKey; --b) {
-      run += hist[tid * 32 + b];
-      if (run >= need) a = tid * 32 + b;
+    for (int j = 0; j < 8; ++j) v[j] = h4[512 * wave + 64 * j + lane];
+    if (wave == kWaves - 1) {
+      // bins above +inf (NaN magnitudes, padding) do not exist
+      const uint32_t b0 = 2048u * wave + 256u * 7 + 4u * lane;
+      if (b0 + 0 > kMaxValidKey) v[7].x = 0;
+      if (b0 + 1 > kMaxValidKey) v[7].y = 0;
+      if (b0 + 2 > kMaxValidKey) v[7].z = 0;
+      if (b0 + 3 > kMaxValidKey) v[7].w = 0;
     }
-    sh_a = a;
-  }
-  if (tid == 0) {
-    sh_max = gmax < 0 ? kNoKey : (uint32_t)gmax;
-    sh_nvalid = suf_me;
+    uint32_t sum4[8], suf[8];
+    uint32_t carry = 0;
+#pragma unroll
+    for (int j = 7; j >= 0; --j) {
+      sum4[j] = v[j].x + v[j].y + v[j].z + v[j].w;
+      const uint32_t p = wave_prefix(sum4[j]);
+      const uint32_t t = lane63(p);
+      suf[j] = carry + t - p + sum4[j];  // values in bins >= my first bin of row j (in this wave)
+      carry += t;
+    }
+    if (lane == 0) wtot[wave] = carry;
+    __syncthreads();
+    uint32_t above = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      above += w > wave ? wtot[w] : 0u;
+      nvalid += wtot[w];
+    }
+    const uint32_t need = (uint32_t)k + 1u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t ge = above + suf[j];  // valid values in bins >= b0
+      const uint32_t gt = ge - sum4[j];    // valid values in bins >= b0 + 4
+      const uint32_t b0 = 2048u * wave + 256u * j + 4u * lane;
+      const uint32_t cnt[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      if (gt < 1u && ge >= 1u) {  // the largest value is in these 4 bins
+        uint32_t run = gt, b = kNoKey;
+#pragma unroll
+        for (int e = 3; e >= 0; --e) {
+          run += cnt[e];
+          if (b == kNoKey && run >= 1u) b = b0 + e;
+        }
+        sh_max = b;
+      }
+      if (gt < need && ge >= need) {  // the (k+1)-th largest is in these 4 bins
+        uint32_t run = gt, b = kNoKey;
+#pragma unroll
+        for (int e = 3; e >= 0; --e) {
+          run += cnt[e];
+          if (b == kNoKey && run >= need) b = b0 + e;
+        }
+        sh_a = b;
+      }
+    }
   }
   __syncthreads();
+  if (stamp) meta->stamp[3] = wall_clock64();
 
-  // ---- replay the 25 fp32 bisection steps (topk_select.cu:141-158) --------
+  // ---- 4. replay the 25 fp32 bisection steps (topk_select.cu:141-158) -----
   if (tid == 0) {
-    if (meta) meta->stamp[3] = wall_clock64();
-    const uint32_t ka = sh_a, km = sh_max;
+    uint32_t ka = sh_a, km = sh_max;
+    if (ka != kNoKey && ka < kMinNormalKey) ka = 0;  // subnormal -> 0
+    if (km != kNoKey && km < kMinNormalKey) km = 0;
     const float a = ka == kNoKey ? 0.f : bf16_to_f32(ka);
     float hi = km == kNoKey ? 0.f : bf16_to_f32(km);
     float lo = 0.f;
@@ -202,96 +251,106 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
       if (ka != kNoKey && a > t) lo = t; else hi = t;
       t = 0.5f * (lo + hi);
     }
-    // |s| > v for a bf16 key b  <=>  b >= (bits(v) >> 16) + 1   (v >= 0)
-    sh_cut_a = (__float_as_uint(hi) >> 16) + 1u;
-    sh_cut_b = (__float_as_uint(lo) >> 16) + 1u;
+    // |s| > v for a bf16 magnitude b  <=>  b >= (bits(v) >> 16) + 1  (v >= 0);
+    // subnormal magnitudes never qualify, so the cuts start at 0x80.
+    sh_cut_a = max((__float_as_uint(hi) >> 16) + 1u, kMinNormalKey);
+    sh_cut_b = max((__float_as_uint(lo) >> 16) + 1u, kMinNormalKey);
     sh_lo = lo;
     sh_hi = hi;
-    sh_tot_a = 0;
+    sh_a = ka;
+    sh_max = km;
   }
   __syncthreads();
-  if (tid == 0 && meta) meta->stamp[4] = wall_clock64();
-  const uint32_t cut_a = sh_cut_a, cut_b = sh_cut_b;
-  // tier-A size from the histogram: valid keys >= cut_a
-  if (cut_a >= 32u * tid && cut_a < 32u * (tid + 1)) {
-    uint32_t c = suf_next;
-    for (uint32_t b = cut_a; b < 32u * (tid + 1); ++b) c += hist[b];
-    sh_tot_a = c;
-  }
+  if (stamp) meta->stamp[4] = wall_clock64();
 
-  // ---- compaction: per-round block scans of (tier A, tier B) counts -------
-  uint32_t cnt[kRounds];
+  // ---- 5. tier counts, positions, ids -------------------------------------
+  // tier A: cut_a <= b <= 0x7F80;  tier B: cut_b <= b < cut_a   (b = |bits|)
+  const uint32_t cut_a = sh_cut_a, cut_b = sh_cut_b;
+  const uint32_t span_a = kMaxValidKey + 1u - cut_a;  // b - cut_a < span_a
+  const uint32_t span_b = cut_a - cut_b;              // b - cut_b < span_b
+  const uint32_t ones = 0x00010001u;
+  uint32_t ca[R], cb[R];
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    uint32_t ca = 0, cb = 0;
+  for (int r = 0; r < R; ++r) {
+    uint32_t acc_a = 0, acc_b = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = key[r][i] & 0xFFFFu, hi = key[r][i] >> 16;
-      ca += (lo <= kKeyInf && lo >= cut_a) + (hi <= kKeyInf && hi >= cut_a);
-      cb += (lo <= kKeyInf && lo >= cut_b && lo < cut_a) + (hi <= kKeyInf && hi >= cut_b && hi < cut_a);
+      const uint32_t k2 = key[r][i] & 0x7FFF7FFFu;
+      acc_a = pk_add(acc_a, in_span2(pk_sub(k2, cut_a * 0x10001u), span_a * 0x10001u, ones));
+      acc_b = pk_add(acc_b, in_span2(pk_sub(k2, cut_b * 0x10001u), span_b * 0x10001u, ones));
     }
-    cnt[r] = ca | (cb << 16);
+    ca[r] = (acc_a & 0xFFFFu) + (acc_a >> 16);
+    cb[r] = (acc_b & 0xFFFFu) + (acc_b >> 16);
   }
-  uint32_t incl[kRounds];
+  uint32_t la = 0, lb = 0;
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    uint32_t v = cnt[r];
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t t = __shfl_up(v, d, 64);
-      if (lane >= d) v += t;
+  for (int r = 0; r < R; ++r) {
+    la += ca[r];
+    lb += cb[r];
+  }
+  if (kPack) {
+    const uint32_t t = lane63(wave_prefix(la | (lb << 16)));
+    if (lane == 0) wtot[wave] = t;
+  } else {
+    const uint32_t ta = lane63(wave_prefix(la));
+    const uint32_t tb = lane63(wave_prefix(lb));
+    if (lane == 0) {
+      wtot[wave] = ta;
+      wtot_b[wave] = tb;
     }
-    incl[r] = v;
-    if (lane == 63) wround[wave][r] = v;
   }
   __syncthreads();
-  const uint32_t tot_a = sh_tot_a;
-  uint32_t base_a = 0, base_b = 0;   // counts before this round
-  uint32_t pos_a[kRounds], pos_b[kRounds];
+  uint32_t tot_a = 0, tot_b = 0, base_a = 0, base_b = 0;
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    uint32_t before = 0, round_tot = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const uint32_t v = wround[w][r];
-      if (w < wave) before += v;
-      round_tot += v;
-    }
-    const uint32_t ex = before + incl[r] - cnt[r];
-    pos_a[r] = base_a + (ex & 0xFFFFu);
-    pos_b[r] = tot_a + base_b + (ex >> 16);
-    base_a += round_tot & 0xFFFFu;
-    base_b += round_tot >> 16;
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t x = wtot[w];
+    const uint32_t xa = kPack ? (x & 0xFFFFu) : x;
+    const uint32_t xb = kPack ? (x >> 16) : wtot_b[w];
+    tot_a += xa;
+    tot_b += xb;
+    base_a += w < wave ? xa : 0u;
+    base_b += w < wave ? xb : 0u;
   }
   const uint32_t uk = (uint32_t)k;
+  if (wave == (int)blockIdx.x) {
+    // my wave's ids: tier A at base_a.., tier B at tot_a + base_b.. (capped at k)
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    uint32_t pa = pos_a[r], pb = pos_b[r];
-    const int c = tid + r * kThreads;
+    for (int r = 0; r < R; ++r) {
+      const uint32_t pa_incl = wave_prefix(ca[r]);
+      const uint32_t pb_incl = wave_prefix(cb[r]);
+      uint32_t pa = base_a + pa_incl - ca[r];
+      uint32_t pb = tot_a + base_b + pb_incl - cb[r];
+      base_a += lane63(pa_incl);
+      base_b += lane63(pb_incl);
+      const uint32_t id0 = (uint32_t)(wave * 64 * R + 64 * r + lane) * 8u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t kv = (key[r][i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-      if (kv > kKeyInf) continue;
-      if (kv >= cut_a) {
-        if (pa < uk) idx[pa] = c * 8 + i;
-        ++pa;
-      } else if (kv >= cut_b) {
-        if (pb < uk) idx[pb] = c * 8 + i;
-        ++pb;
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t b = (key[r][i >> 1] >> (16 * (i & 1))) & 0x7FFFu;
+        const bool in_a = b - cut_a < span_a;
+        const bool in_b = b - cut_b < span_b;
+        const uint32_t pos = in_a ? pa : (in_b ? pb : uk);
+        pa += in_a;
+        pb += in_b;
+        if (pos < uk) idx[pos] = (int32_t)(id0 + i);
       }
     }
   }
-  const uint32_t filled = min(uk, tot_a + base_b);
-  for (uint32_t p = filled + tid; p < uk; p += kThreads) idx[p] = 0;
-  if (tid == 0 && meta) {
-    meta->stamp[5] = wall_clock64();
+  // unfilled slots (fewer than k values qualify) are 0, as in the reference
+  const uint32_t filled = min(uk, tot_a + tot_b);
+  for (uint32_t p = filled + blockIdx.x * kThreads + tid; p < uk; p += kBlocks * kThreads)
+    idx[p] = 0;
+  if (lead && tid == 0) {
+    if (stamps) {
+      meta->stamp[5] = wall_clock64();
+      meta->cycles[1] = clock64();
+    }
+    meta->n_valid = (int32_t)nvalid;
+    meta->key_a = sh_a;
+    meta->key_max = sh_max;
     meta->lo = sh_lo;
     meta->hi = sh_hi;
     meta->count_a = (int32_t)tot_a;
-    meta->count_b = (int32_t)base_b;
-    meta->key_a = sh_a;
-    meta->key_max = sh_max;
-    meta->n_valid = (int32_t)sh_nvalid;
+    meta->count_b = (int32_t)tot_b;
   }
 }
 
@@ -304,15 +363,15 @@ int launch_topk_r(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMet
                                kFineBins * (int)sizeof(uint32_t)) == hipSuccess;
   }();
   if (!lds_ok) return hip_status(hipGetLastError());
-  hipLaunchKernelGGL(topk_kernel<R>, dim3(1), dim3(kThreads), kFineBins * sizeof(uint32_t),
-                     stream, s, (int)n, (int)k, idx, meta);
+  hipLaunchKernelGGL((topk_kernel<R>), dim3(kBlocks), dim3(kThreads),
+                     kFineBins * sizeof(uint32_t), stream, s, (int)n, (int)k, idx, meta,
+                     tuning(DIP_TUNE_TOPK_STAMPS));
   return hip_status(hipGetLastError());
 }
 
 int launch_topk(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
                 hipStream_t stream) {
-  if (n <= 2 * kThreads * 8) return launch_topk_r<2>(s, n, k, idx, meta, stream);
-  if (n <= 4 * kThreads * 8) return launch_topk_r<4>(s, n, k, idx, meta, stream);
+  if (n <= 4 * 8 * kThreads) return launch_topk_r<4>(s, n, k, idx, meta, stream);
   return launch_topk_r<8>(s, n, k, idx, meta, stream);
 }
 
@@ -335,6 +394,8 @@ int check_topk(const uint16_t* s, int32_t* idx, int64_t n, int64_t k, void* ws,
 }
 
 }  // namespace
+
+static_assert(sizeof(TopkMeta) <= 256, "TopkMeta must fit the top-k workspace");
 
 extern "C" size_t dip_topk_workspace_size(int64_t n) {
   (void)n;
