@@ -115,17 +115,18 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
 /*
  * Launch tuning, no counterpart in the reference (process-wide, host side;
  * speed only):
- *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 2)
+ *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 4)
  *   DIP_TUNE_DOWN_LPR           lanes per row segment in the down kernel:
- *                               32/16/8/4, 0 = widest that divides (default)
+ *                               32/16/8/4, 0 = widest that divides (8)
  *   DIP_TUNE_DOWN_BLOCKS        target workgroups of the down kernel (1024)
  *   DIP_TUNE_DOWN_DEQUANT       0: v_cvt_f32_ubyte + bias removal,
  *                               1: v_cvt_off_f32_i4 via SDWA (default 1)
- *   DIP_TUNE_DOWN_UNROLL        rows in flight per lane in the down kernel (4)
+ *   DIP_TUNE_DOWN_UNROLL        rows in flight per lane in the down kernel,
+ *                               2/4/8 (4)
  *   DIP_TUNE_ROWDOT_X_LDS       gate/up keep x in LDS (1) or in VGPRs (0) (1)
- *   DIP_TUNE_ROWDOT_DEPTH       rows of loads in flight per row group, 2..4 (3)
+ *   DIP_TUNE_ROWDOT_DEPTH       rows of loads in flight per row group, 2..4 (2)
  *   DIP_TUNE_DOWN_CPL           16-byte chunks per lane per row in the down
- *                               kernel, 1 or 2 (2)
+ *                               kernel, 1 or 2 (1)
  *   DIP_TUNE_TOPK_STAMPS        1: the top-k records wall-clock phase stamps
  *                               in its workspace (diagnostics, slower) (0)
  * The down tiling fixes the fp32 summation order, so changing it may move y
