@@ -4,15 +4,17 @@
 // selected channel is one contiguous row.  The work is tiled two ways:
 //   * column block cb: LPR lanes each own CPL 16-byte chunks (32*CPL outputs)
 //     of every row, i.e. LPR*CPL*16 contiguous bytes per row per block;
-//   * row block rb: a contiguous range of selected positions j.
-// A block of 256 threads holds 256/LPR "row slots"; slot s walks rows
-// j = j0+s, j0+s+slots, ...  Lane l of a slot prefetches the row id and h of
-// the slot's l-th row; each row's id and h are then shuffled to the slot and
-// D rows of 128-bit loads are kept in flight.  Each lane keeps 32*CPL fp32
-// accumulators (its outputs).  Slots are reduced through LDS in a fixed
-// order and the block writes one fp32 partial row segment; the reduce kernel
-// sums the row-block partials in a fixed order and rounds to bf16.  No float
-// atomics, so results are identical run to run for a given tiling.
+//   * row block rb: 256 consecutive selected positions j.
+// A block of 256 threads holds 256/LPR "slots" of LPR lanes; slot s walks the
+// LPR rows j = 256*rb + s + i*(256/LPR), i < LPR.  Lane l of a slot fetches
+// the id and h of the slot's l-th row; each row's id and h are shuffled to
+// the slot when it comes up.  The row loop is straight-line code (LPR is a
+// compile-time constant; positions past k are clamped and contribute 0), so
+// every load is unconditional and D rows of loads stay in flight.  Each lane
+// keeps 32*CPL fp32 accumulators (its outputs).  Slots are reduced through
+// LDS in a fixed order and the block writes one fp32 partial row segment; the
+// reduce kernel sums the row-block partials in a fixed order and rounds to
+// bf16.  No float atomics, so results are identical run to run.
 //
 // Tiling knobs: LPR lanes per row segment, CPL chunks per lane, D rows in
 // flight per slot (DIP_TUNE_DOWN_LPR / _CPL / _UNROLL).
@@ -31,12 +33,15 @@ namespace dip {
 
 namespace {
 constexpr int kThreads = 256;
-constexpr uint32_t kBadRow = 0xFFFFFFFFu;
+constexpr int kRowsPerBlock = kThreads;  // 256/LPR slots x LPR rows each
+constexpr uint32_t kBadRow = 0xFFFFFFFFu;  // out-of-range id: poisons y with NaN
+constexpr uint32_t kPadRow = 0xFFFFFFFEu;  // position past k: contributes 0
 constexpr uint32_t kSrcB = 0x80000000u;
 constexpr int kRedOut = 32;    // outputs per reduce block
 constexpr int kRedSplit = 8;   // partial subsets per output
 }  // namespace
 
+// Row id for position j (j < k); kBadRow if out of range.  Branch-free.
 template <int SRC>
 DIP_DEV uint32_t down_row(const DownArgs& a, int j) {
   if (SRC == kContig) return (unsigned)j < (unsigned)a.rows_a ? (uint32_t)j : kBadRow;
@@ -45,47 +50,39 @@ DIP_DEV uint32_t down_row(const DownArgs& a, int j) {
     return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
   }
   const int r = a.sel2[j];
-  if (a.sel[j] != 0) return (unsigned)r < (unsigned)a.rows_b ? ((uint32_t)r | kSrcB) : kBadRow;
-  return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
+  const bool b = a.sel[j] != 0;
+  const bool ok = b ? (unsigned)r < (unsigned)a.rows_b : (unsigned)r < (unsigned)a.rows_a;
+  return ok ? ((uint32_t)r | (b ? kSrcB : 0u)) : kBadRow;
 }
 
 template <int CPL>
 struct DownRow {
   uint4 w[CPL];
   uint32_t s;  // bf16 scale of the lane's group
-  uint32_t h;  // bf16 h of the row
-  uint32_t rid;
 };
 
+// Unconditional loads of a lane's CPL chunks and scale of one row (bad and
+// padding ids read row 0 of the safe matrix).
 template <int CPL, int SRC>
-DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, uint32_t hb, int cc0,
-                           size_t row_bytes, int ngroups, DownRow<CPL>& R) {
-  R.rid = rid;
-  R.h = hb;
-  if (rid == kBadRow) return;
-  const int8_t* qw = a.qw_a;
-  const uint16_t* sc = a.sc_a;
-  if (SRC == kDual && (rid & kSrcB)) {
-    qw = a.qw_b;
-    sc = a.sc_b;
-  }
-  const uint32_t r = rid & ~kSrcB;
+DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, int cc0, size_t row_bytes,
+                           int ngroups, DownRow<CPL>& R) {
+  const bool bad = rid >= kPadRow;
+  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
+  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
+  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
+  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
   const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes) + cc0;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) R.w[c] = ldg_nt(wr + c);
   R.s = sc[(size_t)r * ngroups + cc0 / kChunksPerGroup];
 }
 
-// Slot = LPR lanes; lane l of a slot owns CPL consecutive 16-byte chunks
-// (32*CPL outputs, inside one 128-column group) of every row the slot walks.
-// The slot's rows j = j0 + i*slots, i < cnt <= LPR: lane l prefetches the id
-// and h of row l, rows are shuffled in turn, and D rows of loads stay in
-// flight through a ring refilled right after each row is consumed.
 template <int LPR, int CPL, int SRC, int DQ, int D>
 __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
   constexpr int kSlots = kThreads / LPR;
   constexpr int kAcc = CPL * kChunkCols;
-  __shared__ float red[kSlots][kAcc][LPR];
+  constexpr int kStride = kAcc + 1;  // padded LDS rows: conflict-free both ways
+  __shared__ float red[kSlots * LPR * kStride];
 
   const int cb = blockIdx.x % a.col_blocks;
   const int rb = blockIdx.x / a.col_blocks;
@@ -95,82 +92,76 @@ __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
   const int cc0 = (cb * LPR + l) * CPL;  // first chunk of mine within a row
   const size_t row_bytes = (size_t)(a.out_features >> 1);
   const int ngroups = a.out_features >> 7;
-  const int j0 = rb * a.rows_per_block + slot;
-  const int j1 = min(a.k, rb * a.rows_per_block + a.rows_per_block);
-  const int cnt = j0 < j1 ? (j1 - 1 - j0) / kSlots + 1 : 0;  // <= LPR
+  const int j0 = rb * kRowsPerBlock + slot;
 
-  uint32_t rid_l = kBadRow, h_l = 0;
-  if (l < cnt) {
-    const int j = j0 + l * kSlots;
-    rid_l = down_row<SRC>(a, j);
-    h_l = a.h[j];
-  }
+  // lane l: id and h of the slot's row l (position clamped; past k -> kPadRow)
+  const int jl = j0 + l * kSlots;
+  const int jc = min(jl, a.k - 1);
+  const uint32_t rid_c = down_row<SRC>(a, jc);
+  const uint32_t rid_l = jl < a.k ? rid_c : kPadRow;
+  const uint32_t h_l = a.h[jc];
+
   DownRow<CPL> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (d < cnt)
-      load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + d, 64), __shfl(h_l, gbase + d, 64), cc0,
-                              row_bytes, ngroups, ring[d]);
+    load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ngroups, ring[d]);
 
   float acc[kAcc];
 #pragma unroll
   for (int m = 0; m < kAcc; ++m) acc[m] = 0.f;
   float hsum = 0.f;
 
-  for (int i0 = 0; i0 < cnt; i0 += D) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int i = i0 + d;
-      if (i < cnt) {
-        const DownRow<CPL>& R = ring[d];
-        float f = R.rid == kBadRow ? __builtin_nanf("")
-                                   : bf16_to_f32(R.h) * bf16_to_f32(R.s);
+  for (int i = 0; i < LPR; ++i) {
+    DownRow<CPL>& R = ring[i % D];
+    const uint32_t rid = __shfl(rid_l, gbase + i, 64);
+    const uint32_t hb = __shfl(h_l, gbase + i, 64);
+    const float f = rid == kBadRow   ? __builtin_nanf("")
+                    : rid == kPadRow ? 0.f
+                                     : bf16_to_f32(hb) * bf16_to_f32(R.s);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const uint32_t wv[4] = {R.w[c].x, R.w[c].y, R.w[c].z, R.w[c].w};
-          float* ac = acc + c * kChunkCols;
-          if (DQ == 0) {
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t wv[4] = {R.w[c].x, R.w[c].y, R.w[c].z, R.w[c].w};
+      float* ac = acc + c * kChunkCols;
+      if (DQ == 0) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t lo = (wv[q] & 0x0F0F0F0Fu) ^ 0x08080808u;
-              const uint32_t hi = ((wv[q] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-              ac[8 * q + 0] = fmaf(cvt_ubyte<0>(lo), f, ac[8 * q + 0]);
-              ac[8 * q + 1] = fmaf(cvt_ubyte<0>(hi), f, ac[8 * q + 1]);
-              ac[8 * q + 2] = fmaf(cvt_ubyte<1>(lo), f, ac[8 * q + 2]);
-              ac[8 * q + 3] = fmaf(cvt_ubyte<1>(hi), f, ac[8 * q + 3]);
-              ac[8 * q + 4] = fmaf(cvt_ubyte<2>(lo), f, ac[8 * q + 4]);
-              ac[8 * q + 5] = fmaf(cvt_ubyte<2>(hi), f, ac[8 * q + 5]);
-              ac[8 * q + 6] = fmaf(cvt_ubyte<3>(lo), f, ac[8 * q + 6]);
-              ac[8 * q + 7] = fmaf(cvt_ubyte<3>(hi), f, ac[8 * q + 7]);
-            }
-          } else {
-            const float f16 = f * 16.0f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t hi = wv[q] >> 4;
-              ac[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, ac[8 * q + 0]);
-              ac[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, ac[8 * q + 1]);
-              ac[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, ac[8 * q + 2]);
-              ac[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, ac[8 * q + 3]);
-              ac[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, ac[8 * q + 4]);
-              ac[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, ac[8 * q + 5]);
-              ac[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, ac[8 * q + 6]);
-              ac[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, ac[8 * q + 7]);
-            }
-          }
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = (wv[q] & 0x0F0F0F0Fu) ^ 0x08080808u;
+          const uint32_t hi = ((wv[q] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+          ac[8 * q + 0] = fmaf(cvt_ubyte<0>(lo), f, ac[8 * q + 0]);
+          ac[8 * q + 1] = fmaf(cvt_ubyte<0>(hi), f, ac[8 * q + 1]);
+          ac[8 * q + 2] = fmaf(cvt_ubyte<1>(lo), f, ac[8 * q + 2]);
+          ac[8 * q + 3] = fmaf(cvt_ubyte<1>(hi), f, ac[8 * q + 3]);
+          ac[8 * q + 4] = fmaf(cvt_ubyte<2>(lo), f, ac[8 * q + 4]);
+          ac[8 * q + 5] = fmaf(cvt_ubyte<2>(hi), f, ac[8 * q + 5]);
+          ac[8 * q + 6] = fmaf(cvt_ubyte<3>(lo), f, ac[8 * q + 6]);
+          ac[8 * q + 7] = fmaf(cvt_ubyte<3>(hi), f, ac[8 * q + 7]);
         }
-        if (DQ == 0) hsum += f;
-        if (i + D < cnt)
-          load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + i + D, 64),
-                                  __shfl(h_l, gbase + i + D, 64), cc0, row_bytes, ngroups,
-                                  ring[d]);
+      } else {
+        const float f16 = f * 16.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t hi = wv[q] >> 4;
+          ac[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, ac[8 * q + 0]);
+          ac[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, ac[8 * q + 1]);
+          ac[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, ac[8 * q + 2]);
+          ac[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, ac[8 * q + 3]);
+          ac[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, ac[8 * q + 4]);
+          ac[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, ac[8 * q + 5]);
+          ac[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, ac[8 * q + 6]);
+          ac[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, ac[8 * q + 7]);
+        }
       }
     }
+    if (DQ == 0) hsum += f;
+    if (i + D < LPR)
+      load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + i + D, 64), cc0, row_bytes, ngroups, R);
   }
 
+  // slot-major LDS rows of kStride floats: red[(slot*LPR + l)*kStride + m]
+  float* mine = red + (slot * LPR + l) * kStride;
 #pragma unroll
-  for (int m = 0; m < kAcc; ++m)
-    red[slot][m][l] = DQ == 0 ? fmaf(-8.0f, hsum, acc[m]) : acc[m];
+  for (int m = 0; m < kAcc; ++m) mine[m] = DQ == 0 ? fmaf(-8.0f, hsum, acc[m]) : acc[m];
   __syncthreads();
 
   // Sum the slots in a fixed order.  Block columns: lane l's CPL chunks are
@@ -182,40 +173,45 @@ __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
     const int m = col % kAcc;
     float s = 0.f;
 #pragma unroll 8
-    for (int sl = 0; sl < kSlots; ++sl) s += red[sl][m][ln];
+    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
     out[col] = s;
   }
 }
 
 // y[o] = bf16(sum over row blocks of partial[rb][o]): split p of an output
-// sums row blocks p, p+8, p+16, ... in ascending order with its loads issued
-// 16 at a time; the 8 splits are then added in order 0..7.
+// sums row blocks p, p+8, p+16, ... (NB of them, the ones past row_blocks
+// read a clamped address and add 0) in ascending order; the 8 splits are then
+// added in order 0..7.  All NB loads are unconditional and issued together.
+template <int NB>
 __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
     const float* __restrict__ partial, int row_blocks, int out_features, uint16_t* __restrict__ y) {
   __shared__ float part[kRedSplit][kRedOut];
   const int oo = threadIdx.x % kRedOut;
   const int p = threadIdx.x / kRedOut;
-  const int o = blockIdx.x * kRedOut + oo;
-  float s = 0.f;
-  if (o < out_features) {
-    int rb = p;
-    for (; rb + 15 * kRedSplit < row_blocks; rb += 16 * kRedSplit) {
-      float v[16];
+  const int o = min(blockIdx.x * kRedOut + oo, out_features - 1);
+  float v[NB];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = partial[(size_t)(rb + u * kRedSplit) * out_features + o];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) s += v[u];
-    }
-    for (; rb < row_blocks; rb += kRedSplit) s += partial[(size_t)rb * out_features + o];
+  for (int u = 0; u < NB; ++u) {
+    const int rb = min(p + u * kRedSplit, row_blocks - 1);
+    v[u] = partial[(size_t)rb * out_features + o];
   }
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < NB; ++u) s += p + u * kRedSplit < row_blocks ? v[u] : 0.f;
   part[p][oo] = s;
   __syncthreads();
-  if (p == 0 && o < out_features) {
+  if (p == 0 && blockIdx.x * kRedOut + oo < out_features) {
     float t = part[0][oo];
 #pragma unroll
     for (int q = 1; q < kRedSplit; ++q) t += part[q][oo];
-    y[o] = (uint16_t)f32_to_bf16(t);
+    y[blockIdx.x * kRedOut + oo] = (uint16_t)f32_to_bf16(t);
   }
+}
+
+// k == 0: y = bf16(0).
+__global__ void down_zero_kernel(int out_features, uint16_t* __restrict__ y) {
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o < out_features) y[o] = 0;
 }
 
 namespace {
@@ -225,7 +221,6 @@ struct DownPlan {
   int cpl;
   int col_blocks;
   int row_blocks;
-  int rows_per_block;
 };
 
 DownPlan plan_down(int64_t k, int64_t out_features) {
@@ -245,15 +240,7 @@ DownPlan plan_down(int64_t k, int64_t out_features) {
   }
   if (!p.lpr || k <= 0) return p;
   p.col_blocks = (int)(chunks / ((int64_t)p.lpr * p.cpl));
-  int rb = tuning(DIP_TUNE_DOWN_BLOCKS) / p.col_blocks;
-  if (rb < 1) rb = 1;
-  const int slots = kThreads / p.lpr;
-  int per = (int)((k + rb - 1) / rb);
-  per = ((per + slots - 1) / slots) * slots;  // whole rounds of slots
-  // a slot walks at most LPR rows (one prefetched batch of row ids)
-  if (per > slots * p.lpr) per = slots * p.lpr;
-  p.rows_per_block = per;
-  p.row_blocks = (int)((k + per - 1) / per);
+  p.row_blocks = (int)((k + kRowsPerBlock - 1) / kRowsPerBlock);
   return p;
 }
 
@@ -273,27 +260,46 @@ void launch_partial4(int src, const DownArgs& a, int blocks, hipStream_t stream)
 template <int LPR, int CPL>
 void launch_partial(int src, const DownArgs& a, int blocks, hipStream_t stream) {
   const int dq = tuning(DIP_TUNE_DOWN_DEQUANT);
-  const int d = tuning(DIP_TUNE_DOWN_UNROLL);
+  const int d = min(tuning(DIP_TUNE_DOWN_UNROLL), LPR);
   if (dq == 1) {
-    if (d == 4) launch_partial4<LPR, CPL, 1, 4>(src, a, blocks, stream);
-    else if (d == 8) launch_partial4<LPR, CPL, 1, 8>(src, a, blocks, stream);
+    if (d >= 8) launch_partial4<LPR, CPL, 1, (LPR >= 8 ? 8 : LPR)>(src, a, blocks, stream);
+    else if (d >= 4) launch_partial4<LPR, CPL, 1, 4>(src, a, blocks, stream);
     else launch_partial4<LPR, CPL, 1, 2>(src, a, blocks, stream);
   } else {
     launch_partial4<LPR, CPL, 0, 2>(src, a, blocks, stream);
   }
 }
 
+template <int NB>
+void launch_reduce(const float* partial, int row_blocks, int out_features, uint16_t* y,
+                   hipStream_t stream) {
+  const unsigned blocks = (unsigned)((out_features + kRedOut - 1) / kRedOut);
+  hipLaunchKernelGGL((down_reduce_kernel<NB>), dim3(blocks), dim3(kRedOut * kRedSplit), 0,
+                     stream, partial, row_blocks, out_features, y);
+}
+
+void launch_reduce_any(const float* partial, int row_blocks, int out_features, uint16_t* y,
+                       hipStream_t stream) {
+  const int nb = (row_blocks + kRedSplit - 1) / kRedSplit;
+  if (nb <= 1) launch_reduce<1>(partial, row_blocks, out_features, y, stream);
+  else if (nb <= 2) launch_reduce<2>(partial, row_blocks, out_features, y, stream);
+  else if (nb <= 4) launch_reduce<4>(partial, row_blocks, out_features, y, stream);
+  else if (nb <= 8) launch_reduce<8>(partial, row_blocks, out_features, y, stream);
+  else if (nb <= 16) launch_reduce<16>(partial, row_blocks, out_features, y, stream);
+  else if (nb <= 32) launch_reduce<32>(partial, row_blocks, out_features, y, stream);
+  else launch_reduce<64>(partial, row_blocks, out_features, y, stream);
+}
+
 }  // namespace
 
 size_t down_workspace_bytes(int64_t k, int64_t out_features) {
-  // row_blocks <= max(DOWN_BLOCKS / col_blocks, ceil(k / 256)): a row block
-  // never holds more than 256 rows (one prefetched batch per slot).
+  // one fp32 partial row per block of 256 selected positions
   if (out_features <= 0) return 256;
-  int64_t blocks = tuning(DIP_TUNE_DOWN_BLOCKS);
-  const int64_t by_k = (k + 255) / 256;
-  if (by_k > blocks) blocks = by_k;
-  return (size_t)(blocks > 0 ? blocks : 1) * (size_t)out_features * sizeof(float);
+  const int64_t blocks = k > 0 ? (k + kRowsPerBlock - 1) / kRowsPerBlock : 1;
+  return (size_t)blocks * (size_t)out_features * sizeof(float);
 }
+
+int64_t down_max_k() { return (int64_t)64 * kRedSplit * kRowsPerBlock; }
 
 int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
@@ -302,27 +308,28 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   if (!qw_a || !sc_a || !y) return DIP_ERR_NULL;
   if (out_features <= 0 || out_features % kGroupSize != 0 || out_features > (1 << 20))
     return DIP_ERR_SHAPE;
-  if (k < 0 || k > INT32_MAX || rows_a < 0 || rows_a > INT32_MAX || rows_b > INT32_MAX)
+  // row ids stay below 2^31 - 2 so that B-tagged ids never reach kPadRow
+  if (k < 0 || k > down_max_k() || rows_a < 0 || rows_a >= INT32_MAX - 1 ||
+      rows_b >= INT32_MAX - 1)
     return DIP_ERR_SHAPE;
   if (!aligned16(qw_a) || (qw_b && !aligned16(qw_b))) return DIP_ERR_ALIGN;
   if (k > 0 && !h) return DIP_ERR_NULL;
-  const unsigned red_blocks = (unsigned)((out_features + kRedOut - 1) / kRedOut);
   if (k == 0) {
-    // y = bf16(0) for every output: the reduce over zero row blocks.
-    hipLaunchKernelGGL(down_reduce_kernel, dim3(red_blocks), dim3(kRedOut * kRedSplit), 0, stream,
-                       (const float*)nullptr, 0, (int)out_features, y);
+    hipLaunchKernelGGL(down_zero_kernel, dim3((unsigned)((out_features + 255) / 256)), dim3(256),
+                       0, stream, (int)out_features, y);
     return hip_status(hipGetLastError());
   }
+  if (rows_a == 0 && (src != kDual || rows_b <= 0)) return DIP_ERR_SHAPE;
   const DownPlan p = plan_down(k, out_features);
   if (!p.lpr) return DIP_ERR_UNSUPPORTED;
   if (!workspace || ws_bytes < down_workspace_bytes(k, out_features)) return DIP_ERR_WORKSPACE;
-  if ((size_t)p.row_blocks * (size_t)out_features * sizeof(float) > ws_bytes)
-    return DIP_ERR_WORKSPACE;
   DownArgs a{};
   a.qw_a = qw_a;
   a.sc_a = sc_a;
   a.qw_b = qw_b;
   a.sc_b = sc_b;
+  a.qw_safe = rows_a > 0 ? qw_a : qw_b;
+  a.sc_safe = rows_a > 0 ? sc_a : sc_b;
   a.h = h;
   a.sel = sel;
   a.sel2 = sel2;
@@ -331,7 +338,6 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.rows_b = (int)rows_b;
   a.k = (int)k;
   a.out_features = (int)out_features;
-  a.rows_per_block = p.rows_per_block;
   a.col_blocks = p.col_blocks;
   const int blocks = p.row_blocks * p.col_blocks;
   if (p.cpl == 2) {
@@ -351,8 +357,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   }
   int st = hip_status(hipGetLastError());
   if (st) return st;
-  hipLaunchKernelGGL(down_reduce_kernel, dim3(red_blocks), dim3(kRedOut * kRedSplit), 0, stream,
-                     (const float*)a.partial, p.row_blocks, (int)out_features, y);
+  launch_reduce_any(a.partial, p.row_blocks, (int)out_features, y, stream);
   return hip_status(hipGetLastError());
 }
 

@@ -34,10 +34,13 @@ struct RowdotArgs {
   const int32_t* gid;
   const uint16_t* g;
   uint16_t* out;
+  const int8_t* qw_safe;   // a matrix with at least one row: read in place of bad rows
+  const uint16_t* sc_safe;
   int nrows;
   int in_features;
   int rows_a;  // rows of matrix A (row ids outside [0, rows_a) yield NaN)
   int rows_b;  // rows of matrix B (kDual)
+  int ngrp;    // row groups (set by the launcher)
 };
 
 struct DownArgs {
@@ -48,12 +51,13 @@ struct DownArgs {
   const uint16_t* h;
   const int32_t* sel;
   const int32_t* sel2;
+  const int8_t* qw_safe;   // a matrix with at least one row: read in place of bad rows
+  const uint16_t* sc_safe;
   float* partial;     // [row_blocks, out_features]
   int rows_a;
   int rows_b;
   int k;
   int out_features;
-  int rows_per_block;
   int col_blocks;
 };
 
@@ -66,13 +70,24 @@ struct TopkMeta {
   float hi;
   int32_t count_a;
   int32_t count_b;
-  uint32_t key_a;   // (k+1)-th largest key, 0xFFFFFFFF if fewer than k+1 values
+  uint32_t key_a;   // (k+1)-th largest magnitude key, 0xFFFFFFFF if fewer than k+1 values
   uint32_t key_max;
   int32_t n_valid;
   int32_t pad;
   uint64_t stamp[6];   // wall_clock64() at the top-k's phase boundaries (diagnostics)
   uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
 };
+
+// Handed from the top-k's analysis kernel to its scatter kernel: the key cuts
+// and each 16th of the input's tier counts (in index order).
+constexpr int kTopkSlices = 16;
+struct TopkShare {
+  uint32_t cut_a;  // tier A: cut_a <= |bits| <= 0x7F80
+  uint32_t cut_b;  // tier B: cut_b <= |bits| < cut_a
+  uint32_t slice_a[kTopkSlices];
+  uint32_t slice_b[kTopkSlices];
+};
+constexpr size_t kTopkShareOffset = 128;  // TopkMeta first, TopkShare at this byte offset
 
 // Launchers (return hipSuccess or a DIP_ERR_* code).
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
@@ -81,6 +96,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
              uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t down_workspace_bytes(int64_t k, int64_t out_features);
+int64_t down_max_k();  // largest k the down path accepts
 int launch_topk(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
                 hipStream_t stream);
 

@@ -1,5 +1,5 @@
-// dip_rowdot.hip — int4 g128 row-dot kernels: gate GEMV (+SiLU), up-row gather GEMV (+ fused h = g[idx] * u) and the cache-aware
-// dual-source variant.
+// dip_rowdot.hip — int4 g128 row-dot kernels: gate GEMV (+SiLU), up-row gather
+// GEMV (+ fused h = g[idx] * u) and the cache-aware dual-source variant.
 //
 // Mapping (one design for every row source):
 //   * LPR lanes ("a row group", a power of two dividing 64) own one row at a
@@ -7,13 +7,18 @@
 //     row, so a row of in_features/2 bytes = LPR*CH*16 bytes is read with CH
 //     128-bit loads per lane, each instruction covering LPR*16 contiguous
 //     bytes per group (fully coalesced).
-//   * Because a lane always sees the same columns, its slice of x lives in
-//     VGPRs for the whole kernel, pre-paired for v_dot2_f32_bf16, together
-//     with the per-chunk bias term (see dip_common.h).
-//   * Row groups stride over the outputs; U rows per group are in flight per
-//     iteration to keep HBM busy.
-//   * The group reduction is an xor-butterfly; lane 0 of the group applies the
-//     epilogue and stores one bf16.
+//   * A group handles ROWS outputs j = grp + i*ngrp (i < ROWS), ROWS a
+//     compile-time constant, so the row loop is straight-line code: every
+//     load is unconditional (row indices past the end are clamped, bad row
+//     ids read a designated safe row and are poisoned in the epilogue) and
+//     the compiler can wait for exactly the row it consumes (s_waitcnt
+//     vmcnt(N) with N > 0) while the next D-1 rows stay in flight.  Loads
+//     under data-dependent branches would make it wait for everything.
+//   * x is pre-paired for v_dot2_f32_bf16 with the per-chunk bias term (see
+//     dip_common.h), held in VGPRs (XL=0) or staged once per workgroup in LDS
+//     (XL=1); its loads are issued before the row loads.
+//   * The group reduction is DPP + permlane swaps (group_sum); lane l keeps
+//     the sum of row l and runs the epilogue for it.
 #include "dip_common.h"
 #include "dip_internal.h"
 
@@ -24,7 +29,8 @@ namespace {
 constexpr uint32_t kBadRow = 0xFFFFFFFFu;
 constexpr uint32_t kSrcB = 0x80000000u;
 
-// Row id for output j: bit 31 selects matrix B (kDual); kBadRow if out of range.
+// Row id for output j (j < nrows): bit 31 selects matrix B (kDual); kBadRow
+// if the id is out of range.  Branch-free (the id loads are unconditional).
 template <int SRC>
 DIP_DEV uint32_t resolve_row(const RowdotArgs& a, int j) {
   if (SRC == kContig) return (uint32_t)j;
@@ -33,27 +39,27 @@ DIP_DEV uint32_t resolve_row(const RowdotArgs& a, int j) {
     return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
   }
   const int r = a.sel2[j];
-  if (a.sel[j] != 0) return (unsigned)r < (unsigned)a.rows_b ? ((uint32_t)r | kSrcB) : kBadRow;
-  return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
+  const bool b = a.sel[j] != 0;
+  const bool ok = b ? (unsigned)r < (unsigned)a.rows_b : (unsigned)r < (unsigned)a.rows_a;
+  return ok ? ((uint32_t)r | (b ? kSrcB : 0u)) : kBadRow;
 }
 
-template <int LPR, int CH>
+template <int CH>
 struct RowRegs {
   uint4 w[CH];
   uint32_t s[CH];
 };
 
+// Unconditional loads of one row's CH chunks and scales (a bad id reads row
+// 0 of the safe matrix).
 template <int LPR, int CH, int SRC>
 DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes, int ngroups,
-                      RowRegs<LPR, CH>& R) {
-  if (rid == kBadRow) return;
-  const int8_t* qw = a.qw_a;
-  const uint16_t* sc = a.sc_a;
-  if (SRC == kDual && (rid & kSrcB)) {
-    qw = a.qw_b;
-    sc = a.sc_b;
-  }
-  const uint32_t r = rid & ~kSrcB;
+                      RowRegs<CH>& R) {
+  const bool bad = rid == kBadRow;
+  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
+  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
+  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
+  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
   const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes);
   const uint16_t* sr = sc + (size_t)r * ngroups;
 #pragma unroll
@@ -64,37 +70,30 @@ DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes
   }
 }
 
-}  // namespace
-
-// x pairs + bias for one chunk (32 columns starting at 32*chunk).
-DIP_DEV void chunk_pairs(const uint16_t* __restrict__ x, int chunk, uint32_t xp[4][4],
-                         float& bias) {
-  const uint4* xs = reinterpret_cast<const uint4*>(x) + chunk * 4;
+// x pairs + bias for one chunk (32 columns starting at 32*chunk), from the
+// four 128-bit words of x that cover it.
+DIP_DEV void pairs_of(const uint4 X[4], uint32_t xp[4][4], float& bias) {
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint4 X = xs[i];
-    make_xpairs(X.x, X.y, X.z, X.w, xp[i]);
-    s += bf16_to_f32(X.x & 0xFFFFu) + bf16_to_f32(X.x >> 16) + bf16_to_f32(X.y & 0xFFFFu) +
-         bf16_to_f32(X.y >> 16) + bf16_to_f32(X.z & 0xFFFFu) + bf16_to_f32(X.z >> 16) +
-         bf16_to_f32(X.w & 0xFFFFu) + bf16_to_f32(X.w >> 16);
+    make_xpairs(X[i].x, X[i].y, X[i].z, X[i].w, xp[i]);
+    s += bf16_to_f32(X[i].x & 0xFFFFu) + bf16_to_f32(X[i].x >> 16) +
+         bf16_to_f32(X[i].y & 0xFFFFu) + bf16_to_f32(X[i].y >> 16) +
+         bf16_to_f32(X[i].z & 0xFFFFu) + bf16_to_f32(X[i].z >> 16) +
+         bf16_to_f32(X[i].w & 0xFFFFu) + bf16_to_f32(X[i].w >> 16);
   }
   bias = -kPairBias * s;
 }
 
-// Row group = LPR lanes; group g handles outputs j = g + i*ngrp for
-// i < cnt <= LPR (the launcher sizes the grid so).  Lane l of the group
-// fetches the id of the group's l-th row once; each row's id is shuffled to
-// the group when it comes up.  D rows of loads stay in flight: the loads of
-// row i+D are issued into the ring slot of row i right after row i's dot
-// product.  Lane l keeps the reduced sum of row l, and the epilogue (bf16
-// round, SiLU or h) runs once at the end with every lane finishing one row.
-// XL = 0: each lane keeps its x pairs in VGPRs;
-// XL = 1: the workgroup stages all x pairs in LDS once and lanes read their
-//         chunk's 64 bytes per row (fewer VGPRs, more waves per SIMD).
-template <int LPR, int CH, int SRC, int EPI, int XL, int D>
+}  // namespace
+
+// XL = 1: the workgroup stages x pairs in LDS ([chunks][16] pairs, then
+// [chunks] biases; needs chunks <= 256); XL = 0: each lane keeps its CH
+// chunks' pairs in VGPRs.
+template <int LPR, int CH, int SRC, int EPI, int XL, int D, int ROWS>
 __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
-  extern __shared__ uint32_t xlds[];  // XL: [chunks][16] pairs, then [chunks] bias
+  static_assert(ROWS <= LPR && D >= 1 && D <= ROWS, "rows per group");
+  extern __shared__ uint32_t xlds[];
   const int l = threadIdx.x % LPR;
   const int lane = threadIdx.x & 63;
   const int gbase = lane - l;  // first lane of my group within the wave
@@ -102,82 +101,94 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   const int ngroups = a.in_features >> 7;
   const int nchunks = a.in_features / kChunkCols;
   const int grp = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
-  const int ngrp = gridDim.x * (256 / LPR);
-  const int cnt = grp < a.nrows ? (a.nrows - 1 - grp) / ngrp + 1 : 0;  // <= LPR
+  const int ngrp = a.ngrp;
 
-  const uint32_t rid_lane = l < cnt ? resolve_row<SRC>(a, grp + l * ngrp) : kBadRow;
-  RowRegs<LPR, CH> ring[D];
+  // 1. x loads first (XL: one chunk per thread, index clamped)
+  uint4 xs[XL ? 4 : CH * 4];
+  if (XL) {
+    const int c = min((int)threadIdx.x, nchunks - 1);
+    const uint4* src = reinterpret_cast<const uint4*>(a.x) + c * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[i] = src[i];
+  } else {
+#pragma unroll
+    for (int c = 0; c < (XL ? 1 : CH); ++c) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.x) + (l + LPR * c) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[4 * c + i] = src[i];
+    }
+  }
+
+  // 2. row ids: lane l resolves row l of the group (clamped, unconditional)
+  const long long jl = grp + (long long)l * ngrp;
+  const bool valid_l = l < ROWS && jl < a.nrows;
+  const uint32_t rid_lane = resolve_row<SRC>(a, (int)min(jl, (long long)a.nrows - 1));
+
+  // 3. first D rows of loads
+  RowRegs<CH> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (d < cnt) load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups,
-                                        ring[d]);
+    load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups, ring[d]);
 
+  // 4. x pairs
   uint32_t xp[XL ? 1 : CH][4][4];
   float bias[XL ? 1 : CH];
   if (XL) {
-    float* lbias = reinterpret_cast<float*>(xlds + nchunks * 16);
-    for (int c = threadIdx.x; c < nchunks; c += 256) {
+    if ((int)threadIdx.x < nchunks) {
       uint32_t p[4][4];
       float b;
-      chunk_pairs(a.x, c, p, b);
-      uint4* dst = reinterpret_cast<uint4*>(xlds + c * 16);
+      pairs_of(xs, p, b);
+      uint4* dst = reinterpret_cast<uint4*>(xlds + threadIdx.x * 16);
 #pragma unroll
       for (int i = 0; i < 4; ++i) dst[i] = make_uint4(p[i][0], p[i][1], p[i][2], p[i][3]);
-      lbias[c] = b;
+      reinterpret_cast<float*>(xlds + nchunks * 16)[threadIdx.x] = b;
     }
     __syncthreads();
   } else {
 #pragma unroll
-    for (int c = 0; c < (XL ? 1 : CH); ++c) chunk_pairs(a.x, l + LPR * c, xp[c], bias[c]);
+    for (int c = 0; c < (XL ? 1 : CH); ++c) pairs_of(&xs[4 * c], xp[c], bias[c]);
   }
 
+  // 5. rows
   float mine = 0.f;  // reduced dot product of row l
-  for (int i0 = 0; i0 < cnt; i0 += D) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int i = i0 + d;
-      if (i < cnt) {
-        const uint32_t rid = __shfl(rid_lane, gbase + i, 64);
-        float acc = 0.f;
-        if (rid != kBadRow) {
+  for (int i = 0; i < ROWS; ++i) {
+    RowRegs<CH>& R = ring[i % D];
+    float acc = 0.f;
 #pragma unroll
-          for (int c = 0; c < CH; ++c) {
-            float t;
-            if (XL) {
-              const int chunk = l + LPR * c;
-              const uint4* src = reinterpret_cast<const uint4*>(xlds + chunk * 16);
-              uint32_t p[4][4];
+    for (int c = 0; c < CH; ++c) {
+      float t;
+      if (XL) {
+        const int chunk = l + LPR * c;
+        const uint4* src = reinterpret_cast<const uint4*>(xlds + chunk * 16);
+        uint32_t p[4][4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const uint4 v = src[q];
-                p[q][0] = v.x; p[q][1] = v.y; p[q][2] = v.z; p[q][3] = v.w;
-              }
-              t = reinterpret_cast<const float*>(xlds + nchunks * 16)[chunk];
-              t = dot8_nibbles(ring[d].w[c].x, p[0], t);
-              t = dot8_nibbles(ring[d].w[c].y, p[1], t);
-              t = dot8_nibbles(ring[d].w[c].z, p[2], t);
-              t = dot8_nibbles(ring[d].w[c].w, p[3], t);
-            } else {
-              t = bias[XL ? 0 : c];
-              t = dot8_nibbles(ring[d].w[c].x, xp[XL ? 0 : c][0], t);
-              t = dot8_nibbles(ring[d].w[c].y, xp[XL ? 0 : c][1], t);
-              t = dot8_nibbles(ring[d].w[c].z, xp[XL ? 0 : c][2], t);
-              t = dot8_nibbles(ring[d].w[c].w, xp[XL ? 0 : c][3], t);
-            }
-            acc = fmaf(bf16_to_f32(ring[d].s[c]), kPairScale * t, acc);
-          }
+        for (int q = 0; q < 4; ++q) {
+          const uint4 v = src[q];
+          p[q][0] = v.x; p[q][1] = v.y; p[q][2] = v.z; p[q][3] = v.w;
         }
-        acc = group_sum<LPR>(acc);
-        if (l == i) mine = acc;
-        if (i + D < cnt)
-          load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + i + D, 64), l, row_bytes, ngroups,
-                                 ring[d]);
+        t = reinterpret_cast<const float*>(xlds + nchunks * 16)[chunk];
+        t = dot8_nibbles(R.w[c].x, p[0], t);
+        t = dot8_nibbles(R.w[c].y, p[1], t);
+        t = dot8_nibbles(R.w[c].z, p[2], t);
+        t = dot8_nibbles(R.w[c].w, p[3], t);
+      } else {
+        t = bias[XL ? 0 : c];
+        t = dot8_nibbles(R.w[c].x, xp[XL ? 0 : c][0], t);
+        t = dot8_nibbles(R.w[c].y, xp[XL ? 0 : c][1], t);
+        t = dot8_nibbles(R.w[c].z, xp[XL ? 0 : c][2], t);
+        t = dot8_nibbles(R.w[c].w, xp[XL ? 0 : c][3], t);
       }
+      acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
     }
+    acc = group_sum<LPR>(acc);
+    mine = l == i ? acc : mine;
+    if (i + D < ROWS)
+      load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + i + D, 64), l, row_bytes, ngroups, R);
   }
 
-  if (l < cnt) {
-    const int j = grp + l * ngrp;
+  // 6. epilogue: lane l finishes row l
+  if (valid_l) {
     uint32_t v;
     if (rid_lane == kBadRow) {
       v = 0x7FC0u;
@@ -187,11 +198,11 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
         const float f = bf16_to_f32(v);
         v = f32_to_bf16(f / (1.0f + expf(-f)));
       } else if (EPI == kH) {
-        const int ch = (SRC == kGather) ? (int)rid_lane : a.gid[j];
+        const int ch = (SRC == kGather) ? (int)rid_lane : a.gid[(int)jl];
         v = f32_to_bf16(bf16_to_f32(a.g[ch]) * bf16_to_f32(v));
       }
     }
-    a.out[j] = (uint16_t)v;
+    a.out[(int)jl] = (uint16_t)v;
   }
 }
 
@@ -200,38 +211,44 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-template <int LPR, int CH, int SRC, int EPI, int XL, int D>
-void launch_variant(const RowdotArgs& a, int blocks, hipStream_t stream) {
+template <int LPR, int CH, int SRC, int EPI, int XL, int D, int ROWS>
+void launch_variant(RowdotArgs a, hipStream_t stream) {
+  a.ngrp = (a.nrows + ROWS - 1) / ROWS;
+  const int gpb = 256 / LPR;
+  const int blocks = (a.ngrp + gpb - 1) / gpb;
   const size_t lds = XL ? (size_t)(a.in_features / kChunkCols) * 17 * sizeof(uint32_t) : 0;
-  hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XL, D>), dim3(blocks), dim3(256), lds,
-                     stream, a);
+  hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XL, D, ROWS>), dim3(blocks), dim3(256),
+                     lds, stream, a);
+}
+
+// Rows per group: the fewest (from 1, 2, 4, 8, capped at LPR) that keep the
+// grid at about wgs_per_cu workgroups per CU.
+int rows_per_group(int nrows, int lpr) {
+  const int target_groups = device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU) * (256 / lpr);
+  int rows = 1;
+  while (rows < 8 && rows < lpr && (long long)rows * target_groups < nrows) rows *= 2;
+  return rows;
 }
 
 template <int LPR, int CH, int SRC, int EPI>
 int launch_one(const RowdotArgs& a, hipStream_t stream) {
-  // Every row group gets the same number of rows (within one), at most LPR,
-  // and the grid aims at ~`wgs_per_cu` workgroups per CU.
-  const int groups_per_block = 256 / LPR;
-  const int target = device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
-  int per = (a.nrows + target * groups_per_block - 1) / (target * groups_per_block);
-  if (per > LPR) per = LPR;
-  if (per < 1) per = 1;
-  int blocks = (a.nrows + per * groups_per_block - 1) / (per * groups_per_block);
-  if (blocks < 1) blocks = 1;
-  const int xl = tuning(DIP_TUNE_ROWDOT_X_LDS);
-  const int depth = tuning(DIP_TUNE_ROWDOT_DEPTH);
+  const int rows = rows_per_group(a.nrows, LPR);
+  const int depth = tuning(DIP_TUNE_ROWDOT_DEPTH) >= 4 ? 4 : 2;
   constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5);
   if constexpr (hot) {
-    if (xl) {
-      if (depth == 2) launch_variant<LPR, CH, SRC, EPI, 1, 2>(a, blocks, stream);
-      else if (depth == 4) launch_variant<LPR, CH, SRC, EPI, 1, 4>(a, blocks, stream);
-      else launch_variant<LPR, CH, SRC, EPI, 1, 3>(a, blocks, stream);
+    if (tuning(DIP_TUNE_ROWDOT_X_LDS)) {
+      if (rows == 1) launch_variant<LPR, CH, SRC, EPI, 1, 1, 1>(a, stream);
+      else if (rows == 2) launch_variant<LPR, CH, SRC, EPI, 1, 2, 2>(a, stream);
+      else if (rows == 4 && depth == 4) launch_variant<LPR, CH, SRC, EPI, 1, 4, 4>(a, stream);
+      else if (rows == 4) launch_variant<LPR, CH, SRC, EPI, 1, 2, 4>(a, stream);
+      else if (depth == 4) launch_variant<LPR, CH, SRC, EPI, 1, 4, 8>(a, stream);
+      else launch_variant<LPR, CH, SRC, EPI, 1, 2, 8>(a, stream);
     } else {
-      if (depth == 3) launch_variant<LPR, CH, SRC, EPI, 0, 3>(a, blocks, stream);
-      else launch_variant<LPR, CH, SRC, EPI, 0, 2>(a, blocks, stream);
+      if (rows <= 2) launch_variant<LPR, CH, SRC, EPI, 0, 2, 2>(a, stream);
+      else launch_variant<LPR, CH, SRC, EPI, 0, 2, 4>(a, stream);
     }
   } else {
-    launch_variant<LPR, CH, SRC, EPI, 0, 2>(a, blocks, stream);
+    if (LPR >= 4) launch_variant<LPR, CH, SRC, EPI, 0, 2, 4>(a, stream);
   }
   return hip_status(hipGetLastError());
 }
@@ -295,6 +312,8 @@ RowdotArgs base_args(const int8_t* qw, const uint16_t* sc, const uint16_t* x, ui
   RowdotArgs a{};
   a.qw_a = qw;
   a.sc_a = sc;
+  a.qw_safe = qw;
+  a.sc_safe = sc;
   a.x = x;
   a.out = out;
   a.nrows = (int)n;
@@ -327,6 +346,7 @@ extern "C" int dip_int4_gather_gemv(const int8_t* qweight, const uint16_t* scale
   if (k == 0) return DIP_OK;
   if (!x || !out || !indices) return DIP_ERR_NULL;
   if (!aligned16(x)) return DIP_ERR_ALIGN;
+  if (rows == 0) return DIP_ERR_SHAPE;  // every index would be out of range
   RowdotArgs a = base_args(qweight, scales, x, out, k, in_features);
   a.sel = indices;
   a.rows_a = (int)rows;
@@ -342,6 +362,7 @@ extern "C" int dip_up_gather_h(const int8_t* qweight, const uint16_t* scales, co
   if (k == 0) return DIP_OK;
   if (!x || !h || !indices || !g) return DIP_ERR_NULL;
   if (!aligned16(x)) return DIP_ERR_ALIGN;
+  if (rows == 0) return DIP_ERR_SHAPE;  // every index would be out of range
   RowdotArgs a = base_args(qweight, scales, x, h, k, in_features);
   a.sel = indices;
   a.g = g;
@@ -364,9 +385,14 @@ extern "C" int dip_ca_fused_gemv(const int8_t* res_qw, const uint16_t* res_sc,
   if (!x || !out || !src || !row) return DIP_ERR_NULL;
   if (g && !gid) return DIP_ERR_NULL;
   if (!aligned16(x)) return DIP_ERR_ALIGN;
+  if (res_rows == 0 && str_rows == 0) return DIP_ERR_SHAPE;
   RowdotArgs a = base_args(res_qw, res_sc, x, out, k, in_features);
   a.qw_b = str_qw;
   a.sc_b = str_sc;
+  if (res_rows == 0) {
+    a.qw_safe = str_qw;
+    a.sc_safe = str_sc;
+  }
   a.sel = src;
   a.sel2 = row;
   a.g = g;

@@ -12,17 +12,16 @@
 // magnitudes gives exactly; the steps are then replayed with the same fp32
 // arithmetic.
 //
-// Launch: kBlocks workgroups of 1024 threads (16 waves).  Every workgroup
-// loads all n values and repeats the analysis (histogram, a_{k+1}, max,
-// bisection, per-wave tier counts) on identical data, so all of them agree on
-// every threshold and position; workgroup b then writes only the ids of the
-// keys its wave b holds.  This spreads the per-key scatter, the costliest
-// part, over 16 CUs without any inter-workgroup communication.
-//
-// Data layout: wave w holds the R*512 consecutive values [w*512R, (w+1)*512R)
-// as raw bf16 bits in VGPRs (lane L, round r: the 8 values of chunk
-// w*64R + 64r + L), so loads are coalesced and each wave's keys form one
-// contiguous index range.
+// Two kernels:
+//   analysis (one workgroup of 1024 threads): all n values into VGPRs
+//     (wave w holds the R*512 consecutive values [w*512R, (w+1)*512R)),
+//     LDS histogram, max and a_{k+1} (only the waves holding those ranks
+//     search their bins), the 25 bisection steps, then per-wave tier counts
+//     -> TopkShare in the workspace;
+//   scatter (kTopkSlices workgroups of 256 threads): workgroup w re-reads
+//     slice w (the values wave w held), takes its starting positions from
+//     the earlier slices' counts, runs one block scan and writes its ids
+//     through LDS with coalesced stores.
 //
 // Magnitudes are used unflushed: bf16 subnormals (|bits| 1..0x7F) are 0 under
 // the reference's --use_fast_math, so histogram bins below 0x80 all mean 0
@@ -37,7 +36,8 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
-constexpr int kBlocks = kWaves;  // workgroup b writes the ids held by its wave b
+static_assert(kWaves == kTopkSlices, "one scatter slice per analysis wave");
+constexpr int kScatterThreads = 256;
 constexpr uint32_t kNoKey = 0xFFFFFFFFu;
 constexpr uint32_t kMaxValidKey = kKeyInf;  // 0x7F80: +inf
 constexpr uint32_t kMinNormalKey = 0x0080u;
@@ -84,6 +84,21 @@ DIP_DEV uint32_t pk_add(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) + __builtin_bit_cast(u16x2, b));
 }
 
+// Tier counts of 8 raw values (4 dwords): returns (count A) | (count B) << 16.
+// tier A: cut_a <= b <= 0x7F80;  tier B: cut_b <= b < cut_a   (b = |bits|)
+DIP_DEV uint32_t tier_counts8(const uint32_t w[4], uint32_t cut_a2, uint32_t span_a2,
+                              uint32_t cut_b2, uint32_t span_b2) {
+  const uint32_t ones = 0x00010001u;
+  uint32_t acc_a = 0, acc_b = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t k2 = w[i] & 0x7FFF7FFFu;
+    acc_a = pk_add(acc_a, in_span2(pk_sub(k2, cut_a2), span_a2, ones));
+    acc_b = pk_add(acc_b, in_span2(pk_sub(k2, cut_b2), span_b2, ones));
+  }
+  return ((acc_a & 0xFFFFu) + (acc_a >> 16)) | (((acc_b & 0xFFFFu) + (acc_b >> 16)) << 16);
+}
+
 // Elements [base, n) of a chunk that straddles n, 2 per dword; the rest read
 // 0xFFFF.
 DIP_DEV void load_tail8(const uint16_t* __restrict__ s, int n, int base, uint32_t out[4]) {
@@ -95,49 +110,45 @@ DIP_DEV void load_tail8(const uint16_t* __restrict__ s, int n, int base, uint32_
   }
 }
 
+// 8 raw values at [base, base+8): whole chunks by a predicated 128-bit load
+// (no else branch), a chunk straddling n element by element, past n 0xFFFF.
+DIP_DEV void load_chunk8(const uint16_t* __restrict__ s, int n, int base, uint32_t out[4]) {
+  uint4 v = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+  if (base + 8 <= n) v = *reinterpret_cast<const uint4*>(s + base);
+  out[0] = v.x;
+  out[1] = v.y;
+  out[2] = v.z;
+  out[3] = v.w;
+}
+
 }  // namespace
 
-// R rounds of 8 values per lane: n <= 16 waves * 64 lanes * 8R.
+// ---------------------------------------------------------------------------
+// Analysis: R rounds of 8 values per lane, n <= 16 waves * 64 lanes * 8R.
+// ---------------------------------------------------------------------------
 template <int R>
-__global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restrict__ s, int n,
-                                                        int k, int32_t* __restrict__ idx,
-                                                        TopkMeta* __restrict__ meta,
-                                                        int stamps) {
-  // Tier counts packed 16|16 while block totals stay below 2^16.
-  constexpr bool kPack = R * 8 * kThreads <= 32768;
+__global__ __launch_bounds__(kThreads) void topk_analysis_kernel(
+    const uint16_t* __restrict__ s, int n, int k, TopkMeta* __restrict__ meta,
+    TopkShare* __restrict__ share, int stamps) {
   extern __shared__ uint32_t hist[];  // kFineBins bins
   __shared__ uint32_t wtot[kWaves];
-  __shared__ uint32_t wtot_b[kWaves];
   __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b;
-  __shared__ float sh_lo, sh_hi;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const bool lead = blockIdx.x == 0;
   // Phase stamps (diagnostics, off by default: each store makes the storing
   // wave wait for its completion at the next vmcnt wait).
-  const bool stamp = stamps && lead && tid == 0;
+  const bool stamp = stamps && tid == 0;
   if (stamp) {
     meta->stamp[0] = wall_clock64();
     meta->cycles[0] = clock64();
   }
 
   // ---- 1. values into registers; clear the histogram meanwhile -----------
-  // Whole chunks are fetched with predicated 128-bit loads (no else branch,
-  // so all R loads stay in flight together); the one chunk that straddles n
-  // is filled element by element afterwards.
   uint32_t key[R][4];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int base = (wave * 64 * R + 64 * r + lane) * 8;
-    uint4 v = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
-    if (base + 8 <= n) v = *reinterpret_cast<const uint4*>(s + base);
-    key[r][0] = v.x;
-    key[r][1] = v.y;
-    key[r][2] = v.z;
-    key[r][3] = v.w;
-  }
+  for (int r = 0; r < R; ++r) load_chunk8(s, n, (wave * 64 * R + 64 * r + lane) * 8, key[r]);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int base = (wave * 64 * R + 64 * r + lane) * 8;
@@ -171,10 +182,11 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
   __syncthreads();
   if (stamp) meta->stamp[2] = wall_clock64();
 
-  // ---- 3. max and a_{k+1} from a scan of the bins, from the top ----------
+  // ---- 3. max and a_{k+1} ------------------------------------------------
   // Wave w reads its 2048 bins as eight 256-bin rows j; lane L holds bins
   // 2048w + 256j + 4L .. +3 (consecutive lanes, consecutive 16 B: no bank
-  // conflicts).
+  // conflicts).  Wave totals first; only a wave that holds rank 1 or rank
+  // k+1 (counting from the top bin) scans its rows.
   uint32_t nvalid = 0;
   {
     const uint4* h4 = reinterpret_cast<const uint4*>(hist);
@@ -189,17 +201,15 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
       if (b0 + 2 > kMaxValidKey) v[7].z = 0;
       if (b0 + 3 > kMaxValidKey) v[7].w = 0;
     }
-    uint32_t sum4[8], suf[8];
-    uint32_t carry = 0;
+    uint32_t sum4[8];
+    uint32_t lsum = 0;
 #pragma unroll
-    for (int j = 7; j >= 0; --j) {
+    for (int j = 0; j < 8; ++j) {
       sum4[j] = v[j].x + v[j].y + v[j].z + v[j].w;
-      const uint32_t p = wave_prefix(sum4[j]);
-      const uint32_t t = lane63(p);
-      suf[j] = carry + t - p + sum4[j];  // values in bins >= my first bin of row j (in this wave)
-      carry += t;
+      lsum += sum4[j];
     }
-    if (lane == 0) wtot[wave] = carry;
+    const uint32_t wsum = lane63(wave_prefix(lsum));
+    if (lane == 0) wtot[wave] = wsum;
     __syncthreads();
     uint32_t above = 0;
 #pragma unroll
@@ -208,29 +218,37 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
       nvalid += wtot[w];
     }
     const uint32_t need = (uint32_t)k + 1u;
+    const bool own1 = above < 1u && wsum >= 1u;
+    const bool ownk = above < need && above + wsum >= need;
+    if (own1 || ownk) {  // wave-uniform
+      uint32_t carry = above;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t ge = above + suf[j];  // valid values in bins >= b0
-      const uint32_t gt = ge - sum4[j];    // valid values in bins >= b0 + 4
-      const uint32_t b0 = 2048u * wave + 256u * j + 4u * lane;
-      const uint32_t cnt[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-      if (gt < 1u && ge >= 1u) {  // the largest value is in these 4 bins
-        uint32_t run = gt, b = kNoKey;
+      for (int j = 7; j >= 0; --j) {
+        const uint32_t p = wave_prefix(sum4[j]);
+        const uint32_t t = lane63(p);
+        const uint32_t ge = carry + t - p + sum4[j];  // valid values in bins >= my first bin
+        const uint32_t gt = ge - sum4[j];             // ... in bins >= my first bin + 4
+        carry += t;
+        const uint32_t b0 = 2048u * wave + 256u * j + 4u * lane;
+        const uint32_t cnt[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        if (own1 && gt < 1u && ge >= 1u) {
+          uint32_t run = gt, b = kNoKey;
 #pragma unroll
-        for (int e = 3; e >= 0; --e) {
-          run += cnt[e];
-          if (b == kNoKey && run >= 1u) b = b0 + e;
+          for (int e = 3; e >= 0; --e) {
+            run += cnt[e];
+            if (b == kNoKey && run >= 1u) b = b0 + e;
+          }
+          sh_max = b;
         }
-        sh_max = b;
-      }
-      if (gt < need && ge >= need) {  // the (k+1)-th largest is in these 4 bins
-        uint32_t run = gt, b = kNoKey;
+        if (ownk && gt < need && ge >= need) {
+          uint32_t run = gt, b = kNoKey;
 #pragma unroll
-        for (int e = 3; e >= 0; --e) {
-          run += cnt[e];
-          if (b == kNoKey && run >= need) b = b0 + e;
+          for (int e = 3; e >= 0; --e) {
+            run += cnt[e];
+            if (b == kNoKey && run >= need) b = b0 + e;
+          }
+          sh_a = b;
         }
-        sh_a = b;
       }
     }
   }
@@ -255,100 +273,125 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
     // subnormal magnitudes never qualify, so the cuts start at 0x80.
     sh_cut_a = max((__float_as_uint(hi) >> 16) + 1u, kMinNormalKey);
     sh_cut_b = max((__float_as_uint(lo) >> 16) + 1u, kMinNormalKey);
-    sh_lo = lo;
-    sh_hi = hi;
-    sh_a = ka;
-    sh_max = km;
+    meta->lo = lo;
+    meta->hi = hi;
+    meta->key_a = ka;
+    meta->key_max = km;
+    meta->n_valid = (int32_t)nvalid;
   }
   __syncthreads();
   if (stamp) meta->stamp[4] = wall_clock64();
 
-  // ---- 5. tier counts, positions, ids -------------------------------------
-  // tier A: cut_a <= b <= 0x7F80;  tier B: cut_b <= b < cut_a   (b = |bits|)
+  // ---- 5. tier counts of each wave's values -------------------------------
   const uint32_t cut_a = sh_cut_a, cut_b = sh_cut_b;
-  const uint32_t span_a = kMaxValidKey + 1u - cut_a;  // b - cut_a < span_a
-  const uint32_t span_b = cut_a - cut_b;              // b - cut_b < span_b
-  const uint32_t ones = 0x00010001u;
-  uint32_t ca[R], cb[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    uint32_t acc_a = 0, acc_b = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t k2 = key[r][i] & 0x7FFF7FFFu;
-      acc_a = pk_add(acc_a, in_span2(pk_sub(k2, cut_a * 0x10001u), span_a * 0x10001u, ones));
-      acc_b = pk_add(acc_b, in_span2(pk_sub(k2, cut_b * 0x10001u), span_b * 0x10001u, ones));
-    }
-    ca[r] = (acc_a & 0xFFFFu) + (acc_a >> 16);
-    cb[r] = (acc_b & 0xFFFFu) + (acc_b >> 16);
-  }
+  const uint32_t cut_a2 = cut_a * 0x10001u, cut_b2 = cut_b * 0x10001u;
+  const uint32_t span_a2 = (kMaxValidKey + 1u - cut_a) * 0x10001u;  // b - cut_a < span_a
+  const uint32_t span_b2 = (cut_a - cut_b) * 0x10001u;              // b - cut_b < span_b
   uint32_t la = 0, lb = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    la += ca[r];
-    lb += cb[r];
+    const uint32_t c = tier_counts8(key[r], cut_a2, span_a2, cut_b2, span_b2);
+    la += c & 0xFFFFu;
+    lb += c >> 16;
   }
-  if (kPack) {
-    const uint32_t t = lane63(wave_prefix(la | (lb << 16)));
-    if (lane == 0) wtot[wave] = t;
-  } else {
-    const uint32_t ta = lane63(wave_prefix(la));
-    const uint32_t tb = lane63(wave_prefix(lb));
-    if (lane == 0) {
-      wtot[wave] = ta;
-      wtot_b[wave] = tb;
-    }
+  // packed: a wave's counts stay below 2^16 (at most 512R values)
+  const uint32_t wt = lane63(wave_prefix(la | (lb << 16)));
+  if (lane == 0) {
+    share->slice_a[wave] = wt & 0xFFFFu;
+    share->slice_b[wave] = wt >> 16;
   }
-  __syncthreads();
-  uint32_t tot_a = 0, tot_b = 0, base_a = 0, base_b = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const uint32_t x = wtot[w];
-    const uint32_t xa = kPack ? (x & 0xFFFFu) : x;
-    const uint32_t xb = kPack ? (x >> 16) : wtot_b[w];
-    tot_a += xa;
-    tot_b += xb;
-    base_a += w < wave ? xa : 0u;
-    base_b += w < wave ? xb : 0u;
-  }
-  const uint32_t uk = (uint32_t)k;
-  if (wave == (int)blockIdx.x) {
-    // my wave's ids: tier A at base_a.., tier B at tot_a + base_b.. (capped at k)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t pa_incl = wave_prefix(ca[r]);
-      const uint32_t pb_incl = wave_prefix(cb[r]);
-      uint32_t pa = base_a + pa_incl - ca[r];
-      uint32_t pb = tot_a + base_b + pb_incl - cb[r];
-      base_a += lane63(pa_incl);
-      base_b += lane63(pb_incl);
-      const uint32_t id0 = (uint32_t)(wave * 64 * R + 64 * r + lane) * 8u;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t b = (key[r][i >> 1] >> (16 * (i & 1))) & 0x7FFFu;
-        const bool in_a = b - cut_a < span_a;
-        const bool in_b = b - cut_b < span_b;
-        const uint32_t pos = in_a ? pa : (in_b ? pb : uk);
-        pa += in_a;
-        pb += in_b;
-        if (pos < uk) idx[pos] = (int32_t)(id0 + i);
-      }
-    }
-  }
-  // unfilled slots (fewer than k values qualify) are 0, as in the reference
-  const uint32_t filled = min(uk, tot_a + tot_b);
-  for (uint32_t p = filled + blockIdx.x * kThreads + tid; p < uk; p += kBlocks * kThreads)
-    idx[p] = 0;
-  if (lead && tid == 0) {
+  if (tid == 0) {
+    share->cut_a = cut_a;
+    share->cut_b = cut_b;
     if (stamps) {
       meta->stamp[5] = wall_clock64();
       meta->cycles[1] = clock64();
     }
-    meta->n_valid = (int32_t)nvalid;
-    meta->key_a = sh_a;
-    meta->key_max = sh_max;
-    meta->lo = sh_lo;
-    meta->hi = sh_hi;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Scatter: workgroup w handles slice w = values [w*512R, (w+1)*512R); thread t
+// holds the 2R consecutive values at w*512R + 2R*t.
+// ---------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(kScatterThreads) void topk_scatter_kernel(
+    const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
+    const TopkShare* __restrict__ share, TopkMeta* __restrict__ meta) {
+  constexpr int kPer = 2 * R;           // values per thread
+  constexpr int kSlice = 512 * R;       // values per slice
+  __shared__ uint32_t stage[kSlice];
+  __shared__ uint32_t wsum[kScatterThreads / 64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int w = blockIdx.x;
+  const int base = w * kSlice + tid * kPer;
+
+  uint32_t key[kPer / 8][4];
+#pragma unroll
+  for (int c = 0; c < kPer / 8; ++c) load_chunk8(s, n, base + 8 * c, key[c]);
+#pragma unroll
+  for (int c = 0; c < kPer / 8; ++c)
+    if (base + 8 * c < n && base + 8 * c + 8 > n) load_tail8(s, n, base + 8 * c, key[c]);
+
+  const uint32_t cut_a = share->cut_a, cut_b = share->cut_b;
+  uint32_t pre_a = 0, pre_b = 0, tot_a = 0, tot_b = 0;
+#pragma unroll
+  for (int q = 0; q < kTopkSlices; ++q) {
+    const uint32_t xa = share->slice_a[q], xb = share->slice_b[q];
+    pre_a += q < w ? xa : 0u;
+    pre_b += q < w ? xb : 0u;
+    tot_a += xa;
+    tot_b += xb;
+  }
+  const uint32_t my_a = share->slice_a[w];
+
+  const uint32_t cut_a2 = cut_a * 0x10001u, cut_b2 = cut_b * 0x10001u;
+  const uint32_t span_a = kMaxValidKey + 1u - cut_a, span_b = cut_a - cut_b;
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int c = 0; c < kPer / 8; ++c)
+    cnt += tier_counts8(key[c], cut_a2, span_a * 0x10001u, cut_b2, span_b * 0x10001u);
+  // block exclusive scan of the packed (A | B << 16) counts (slice totals < 2^16)
+  const uint32_t incl = wave_prefix(cnt);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0;
+#pragma unroll
+  for (int q = 0; q < kScatterThreads / 64; ++q) before += q < wave ? wsum[q] : 0u;
+  const uint32_t ex = before + incl - cnt;
+  // stage: the slice's tier-A ids at [0, my_a), its tier-B ids after them
+  uint32_t pa = ex & 0xFFFFu;
+  uint32_t pb = my_a + (ex >> 16);
+#pragma unroll
+  for (int c = 0; c < kPer / 8; ++c) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t b = (key[c][i >> 1] >> (16 * (i & 1))) & 0x7FFFu;
+      const bool in_a = b - cut_a < span_a;
+      const bool in_b = b - cut_b < span_b;
+      if (in_a | in_b) stage[in_a ? pa : pb] = (uint32_t)(base + 8 * c + i);
+      pa += in_a;
+      pb += in_b;
+    }
+  }
+  __syncthreads();
+  // copy out: tier A to [pre_a, pre_a + my_a), tier B to tot_a + pre_b + ...,
+  // both capped at k
+  const uint32_t uk = (uint32_t)k;
+  const uint32_t my_b = share->slice_b[w];
+  for (uint32_t i = tid; i < my_a + my_b; i += kScatterThreads) {
+    const uint32_t pos = i < my_a ? pre_a + i : tot_a + pre_b + (i - my_a);
+    if (pos < uk) idx[pos] = (int32_t)stage[i];
+  }
+  // unfilled slots (fewer than k values qualify) are 0, as in the reference
+  const uint32_t filled = min(uk, tot_a + tot_b);
+  for (uint32_t p = filled + (uint32_t)(w * kScatterThreads + tid); p < uk;
+       p += kTopkSlices * kScatterThreads)
+    idx[p] = 0;
+  if (w == 0 && tid == 0) {
     meta->count_a = (int32_t)tot_a;
     meta->count_b = (int32_t)tot_b;
   }
@@ -358,14 +401,20 @@ template <int R>
 int launch_topk_r(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
                   hipStream_t stream) {
   static const bool lds_ok = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel<R>),
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_analysis_kernel<R>),
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                kFineBins * (int)sizeof(uint32_t)) == hipSuccess;
   }();
   if (!lds_ok) return hip_status(hipGetLastError());
-  hipLaunchKernelGGL((topk_kernel<R>), dim3(kBlocks), dim3(kThreads),
-                     kFineBins * sizeof(uint32_t), stream, s, (int)n, (int)k, idx, meta,
+  TopkShare* share =
+      reinterpret_cast<TopkShare*>(reinterpret_cast<char*>(meta) + kTopkShareOffset);
+  hipLaunchKernelGGL((topk_analysis_kernel<R>), dim3(1), dim3(kThreads),
+                     kFineBins * sizeof(uint32_t), stream, s, (int)n, (int)k, meta, share,
                      tuning(DIP_TUNE_TOPK_STAMPS));
+  int st = hip_status(hipGetLastError());
+  if (st) return st;
+  hipLaunchKernelGGL((topk_scatter_kernel<R>), dim3(kTopkSlices), dim3(kScatterThreads), 0,
+                     stream, s, (int)n, (int)k, idx, share, meta);
   return hip_status(hipGetLastError());
 }
 
@@ -395,11 +444,12 @@ int check_topk(const uint16_t* s, int32_t* idx, int64_t n, int64_t k, void* ws,
 
 }  // namespace
 
-static_assert(sizeof(TopkMeta) <= 256, "TopkMeta must fit the top-k workspace");
+static_assert(sizeof(TopkMeta) <= kTopkShareOffset, "TopkMeta overlaps TopkShare");
+static_assert(kTopkShareOffset + sizeof(TopkShare) <= 512, "top-k workspace");
 
 extern "C" size_t dip_topk_workspace_size(int64_t n) {
   (void)n;
-  return 256;  // holds the last call's thresholds (TopkMeta)
+  return 512;  // the last call's thresholds (TopkMeta) and cuts / tier counts (TopkShare)
 }
 
 extern "C" int64_t dip_topk_max_n(void) { return kTopkMaxN; }

@@ -101,8 +101,9 @@ int dip_up_gather_h(const int8_t* qweight, const uint16_t* scales, const uint16_
  * y[o] = bf16( sum_{j<k} float(h[j]) * (q*s)[row_j, o] ) over rows of the
  * transposed down matrix down_t [rows, out_features/2]; row_j = indices[j],
  * or j when indices == NULL (the staged-copy layout of the reference).
- * Deterministic: fp32 partial sums over fixed row blocks reduced in a fixed
- * order, no float atomics.
+ * Deterministic: fp32 partial sums over fixed blocks of 256 positions
+ * reduced in a fixed order, no float atomics.  k <= 131072; the workspace
+ * holds ceil(k/256) * out_features fp32 partials.
  * Replaces int4_down_ops::int4_gather_down
  * (kernels/int4_down/int4_gather_down.cu:77-102).
  */
@@ -118,7 +119,8 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 4)
  *   DIP_TUNE_DOWN_LPR           lanes per row segment in the down kernel:
  *                               32/16/8/4, 0 = widest that divides (8)
- *   DIP_TUNE_DOWN_BLOCKS        target workgroups of the down kernel (1024)
+ *   DIP_TUNE_DOWN_BLOCKS        reserved: accepted, no effect (the down
+ *                               kernel's row blocks are 256 positions)
  *   DIP_TUNE_DOWN_DEQUANT       0: v_cvt_f32_ubyte + bias removal,
  *                               1: v_cvt_off_f32_i4 via SDWA (default 1)
  *   DIP_TUNE_DOWN_UNROLL        rows in flight per lane in the down kernel,

@@ -78,10 +78,11 @@ def test_argument_rejection_before_launch():
 def test_workspace_sizes():
     L = K.lib
     assert L.dip_topk_workspace_size(25600) >= 16
-    # down partials: at most DOWN_BLOCKS rows of out fp32, independent of k
+    # down partials: one fp32 row of `out` per block of 256 selected positions
     need = L.dip_gather_down_workspace_size(15360, 5120)
-    assert need % (5120 * 4) == 0
-    assert need == L.dip_gather_down_workspace_size(25600, 5120)
+    assert need == 60 * 5120 * 4
+    assert L.dip_gather_down_workspace_size(15361, 5120) == 61 * 5120 * 4
+    assert L.dip_gather_down_workspace_size(1, 128) == 128 * 4
     assert L.dip_mlp_workspace_size(5120, 25600, 15360) >= need
 
 
