@@ -73,6 +73,28 @@ def cpu_baseline(stack, seconds: float):
     }
 
 
+def measured_traffic(shape: str, keep: float, stage: str, K):
+    """HBM bytes per launch of `stage` from the committed counter summary
+    (profiles/hbm_traffic_<shape>_keep<keep>.md: FETCH_SIZE / WRITE_SIZE
+    passes scaled against a device copy), or None when there is none for this
+    workload or it was measured under other launch tuning."""
+    path = ROOT / "profiles" / f"hbm_traffic_{shape}_keep{keep:g}.md"
+    if not path.exists():
+        return None
+    tuning, table = None, {}
+    for line in path.read_text().splitlines():
+        if line.startswith("tuning:"):
+            tuning = [int(v) for v in line.split(":", 1)[1].split(",")]
+        elif line.startswith("traffic_bytes_per_launch:"):
+            for item in line.split(":", 1)[1].split():
+                name, val = item.split("=")
+                table[name] = int(val)
+    live = [K.lib.dip_get_tuning(i) for i in range(len(tuning or []))]
+    if tuning != live:
+        return None
+    return table.get(stage)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,6 +106,12 @@ def main(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--down-mode", type=int, default=None)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel eagerly instead of replaying the captured graph "
+                         "(for counter collection, which profiles each dispatch)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after the timed run, copy a buffer of this many MiB device to device "
+                         "(the reference transfer for scaling HBM byte counters)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -107,11 +135,17 @@ def main(argv=None):
     gen = torch.Generator(device=dev).manual_seed(1)
     n_tok = args.warmup + args.steps
     xs = (torch.randn(n_tok, shape["hidden"], device=dev, generator=gen)).to(torch.bfloat16)
-    stack.capture()
-    print("[bench] graph captured", file=sys.stderr, flush=True)
+    if args.eager:
+        def run(x_t):
+            stack.x.copy_(x_t, non_blocking=True)
+            stack.run_token()
+    else:
+        stack.capture()
+        print("[bench] graph captured", file=sys.stderr, flush=True)
+        run = stack.step
 
     for i in range(args.warmup):
-        stack.step(xs[i])
+        run(xs[i])
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -119,7 +153,7 @@ def main(argv=None):
     w0 = time.perf_counter()
     e0.record(stream)
     for i in range(args.warmup, n_tok):
-        stack.step(xs[i])
+        run(xs[i])
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
@@ -130,18 +164,34 @@ def main(argv=None):
     print(f"[bench] {args.steps} tokens: {ms_step:.4f} ms/token (wall {wall:.3f} s)",
           file=sys.stderr, flush=True)
 
+    if args.copy_mib:
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    if args.eager:
+        # counter-collection runs: every dispatch above was eager; no graph
+        # replays and no CPU baseline follow
+        print(json.dumps({"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s",
+                          "eager": True, "ms_per_step": round(ms_step, 5)}), flush=True)
+        return 0
+
     # per-stage kernel durations: HIP events around graph replays of each
     # stage's launches (one per layer, back to back)
     stages = stack.stage_times_ms(reps=3)
     H, I, k = stack.hidden, stack.inter, stack.k
     row = H // 2 + 2 * (H // 128)
-    stage_bytes = {"gate_silu": I * row, "topk": 2 * I,
+    stage_bytes = {"gate_silu": I * row, "topk": 2 * I + 4 * k,
                    "up_gather_h": k * row, "down_gather": k * row}
     dom = max(stages, key=stages.get)
     ach = stage_bytes[dom] / (stages[dom] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
-                "bytes_per_launch": stage_bytes[dom],
+                "frac": round(ach / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.shape, args.keep, dom, K),
+                "kernel": dom, "bytes_per_launch": stage_bytes[dom],
                 "avg_launch_ms": round(stages[dom], 5)}
     print(f"[bench] stages (ms): {json.dumps({k_: round(v, 5) for k_, v in stages.items()})}",
           file=sys.stderr, flush=True)

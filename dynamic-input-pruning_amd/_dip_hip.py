@@ -6,9 +6,9 @@ declared in include/dip_hip.h, and raises ``RuntimeError`` on any non-zero
 status.  There is no fallback: if the library is not built, importing this
 module raises ``ImportError``.
 
-Workspaces are cached per (device, tag) as zero-filled byte tensors; the
-kernels leave them zeroed again after every call, and every call that shares
-one is ordered on the same stream (the module layer runs layers one after the
+Workspaces are cached per (device, tag) as zero-filled byte tensors; every
+call returns the parts that must start at zero (arrival counters) to zero
+before it ends, and every call that shares one is ordered on the same stream (the module layer runs layers one after the
 other, like the reference's SharedBuffers, dip_stream_predispatch.py:123-138).
 """
 from __future__ import annotations

@@ -34,6 +34,7 @@ namespace dip {
 namespace {
 constexpr int kThreads = 256;
 constexpr int kRowsPerBlock = kThreads;  // 256/LPR slots x LPR rows each
+constexpr int kXcds = 8;                 // MI355X: 8 XCDs, workgroups dispatched round-robin
 constexpr uint32_t kBadRow = 0xFFFFFFFFu;  // out-of-range id: poisons y with NaN
 constexpr uint32_t kPadRow = 0xFFFFFFFEu;  // position past k: contributes 0
 constexpr uint32_t kSrcB = 0x80000000u;
@@ -84,8 +85,15 @@ __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
   constexpr int kStride = kAcc + 1;  // padded LDS rows: conflict-free both ways
   __shared__ float red[kSlots * LPR * kStride];
 
-  const int cb = blockIdx.x % a.col_blocks;
-  const int rb = blockIdx.x / a.col_blocks;
+  // XCD-aware tile order: workgroups go to the 8 XCDs round-robin, so tile
+  // (rb, cb) runs as workgroup b with b % 8 == rb % 8.  All column blocks of
+  // a row block then share one XCD's L2, which serves the scale lines, ids
+  // and h of those rows once instead of once per column block.
+  const int xcd = blockIdx.x % kXcds;
+  const int w = blockIdx.x / kXcds;
+  const int rb = xcd + kXcds * (w / a.col_blocks);
+  const int cb = w % a.col_blocks;
+  if (rb >= a.row_blocks) return;  // padding tile (row blocks rounded up to 8)
   const int l = threadIdx.x % LPR;
   const int slot = threadIdx.x / LPR;
   const int gbase = (threadIdx.x & 63) - l;
@@ -116,9 +124,13 @@ __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
     DownRow<CPL>& R = ring[i % D];
     const uint32_t rid = __shfl(rid_l, gbase + i, 64);
     const uint32_t hb = __shfl(h_l, gbase + i, 64);
-    const float f = rid == kBadRow   ? __builtin_nanf("")
-                    : rid == kPadRow ? 0.f
-                                     : bf16_to_f32(hb) * bf16_to_f32(R.s);
+    // f = h*s, 0 for padding, NaN for a bad id: integer selects on the bits
+    // keep this branch-free (a branch here sinks the scale load into it and
+    // costs a full vmcnt(0) wait)
+    uint32_t fb = __float_as_uint(bf16_to_f32(hb) * bf16_to_f32(R.s));
+    fb = rid == kPadRow ? 0u : fb;
+    fb = rid == kBadRow ? 0x7FC00000u : fb;
+    const float f = __uint_as_float(fb);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const uint32_t wv[4] = {R.w[c].x, R.w[c].y, R.w[c].z, R.w[c].w};
@@ -339,7 +351,8 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.k = (int)k;
   a.out_features = (int)out_features;
   a.col_blocks = p.col_blocks;
-  const int blocks = p.row_blocks * p.col_blocks;
+  a.row_blocks = p.row_blocks;
+  const int blocks = (p.row_blocks + kXcds - 1) / kXcds * kXcds * p.col_blocks;
   if (p.cpl == 2) {
     switch (p.lpr) {
       case 32: launch_partial<32, 2>(src, a, blocks, stream); break;

@@ -59,6 +59,7 @@ struct DownArgs {
   int k;
   int out_features;
   int col_blocks;
+  int row_blocks;
 };
 
 // Top-k: one histogram bin per 15-bit |s| key, held in LDS.

@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {4, 8, 1024, 1, 4, 1, 2, 1, 0};
+int g_tune[DIP_TUNE_COUNT] = {2, 8, 1024, 1, 8, 1, 2, 1, 0};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }

@@ -14,8 +14,10 @@
  *     rejected before any launch, or a positive hipError_t from the launch.
  *   - Workspaces are caller-owned device buffers of the size the matching
  *     *_workspace_size() reports.  They must be zero-filled once before their
- *     first use; the kernels leave them zeroed again after every call.
- *     Calls that share a workspace must be ordered on one stream.
+ *     first use; every call returns the parts that must start at zero
+ *     (arrival counters) to zero before it ends, so no clearing is needed
+ *     between calls (and none is recorded into a captured graph).  Calls
+ *     that share a workspace must be ordered on one stream.
  *
  * Reference interfaces each entry point replaces are cited as
  * <file>:<line> of rohitpotluri/dynamic-input-pruning.
@@ -68,8 +70,11 @@ int dip_int4_gemv(const int8_t* qweight, const uint16_t* scales, const uint16_t*
  * by tier t_lo < |s| <= t_strict in ascending index, unfilled slots 0).
  * Bit-exact with topk_ops::topk_select (kernels/topk_select/topk_select.cu:
  * 134-171, topk_kernel.py:29-40).  n <= dip_topk_max_n(); s 16-byte aligned.
- * One workgroup, no host round trips; the workspace only receives the last
- * call's thresholds (dip_topk_meta).
+ * No host round trips: an analysis kernel (one workgroup: LDS histogram of
+ * the 15-bit magnitudes, a_{k+1} and max, the 25 bisection steps replayed)
+ * hands the cuts and per-slice tier counts through the workspace to a
+ * scatter kernel (16 workgroups) that writes idx.  The workspace (512 B)
+ * keeps the last call's thresholds (dip_topk_meta).
  */
 size_t dip_topk_workspace_size(int64_t n);
 int dip_topk_select(const uint16_t* s, int32_t* idx, int64_t n, int64_t k,
@@ -116,7 +121,7 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
 /*
  * Launch tuning, no counterpart in the reference (process-wide, host side;
  * speed only):
- *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 4)
+ *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 2)
  *   DIP_TUNE_DOWN_LPR           lanes per row segment in the down kernel:
  *                               32/16/8/4, 0 = widest that divides (8)
  *   DIP_TUNE_DOWN_BLOCKS        reserved: accepted, no effect (the down
@@ -124,7 +129,7 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_DOWN_DEQUANT       0: v_cvt_f32_ubyte + bias removal,
  *                               1: v_cvt_off_f32_i4 via SDWA (default 1)
  *   DIP_TUNE_DOWN_UNROLL        rows in flight per lane in the down kernel,
- *                               2/4/8 (4)
+ *                               2/4/8 (8)
  *   DIP_TUNE_ROWDOT_X_LDS       gate/up keep x in LDS (1) or in VGPRs (0) (1)
  *   DIP_TUNE_ROWDOT_DEPTH       rows of loads in flight per row group, 2..4 (2)
  *   DIP_TUNE_DOWN_CPL           16-byte chunks per lane per row in the down
