@@ -87,9 +87,12 @@ DIP_DEV void pairs_of(const uint4 X[4], uint32_t xp[4][4], float& bias) {
 
 }  // namespace
 
-// XL = 1: the workgroup stages x pairs in LDS ([chunks][16] pairs, then
-// [chunks] biases; needs chunks <= 256); XL = 0: each lane keeps its CH
-// chunks' pairs in VGPRs.
+// XL = 1: the workgroup stages x pairs in LDS (needs chunks <= 256): the
+// four 128-bit pair words of chunk l + LPR*c sit at 16-byte slot
+// (c*4 + q)*LPR + l, so the LPR lanes of a group read consecutive 16 B (no
+// bank conflicts; the other groups of the wave read the same addresses, a
+// broadcast); then [chunks] biases.  XL = 0: each lane keeps its CH chunks'
+// pairs in VGPRs.
 template <int LPR, int CH, int SRC, int EPI, int XL, int D, int ROWS>
 __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   static_assert(ROWS <= LPR && D >= 1 && D <= ROWS, "rows per group");
@@ -138,9 +141,11 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
       uint32_t p[4][4];
       float b;
       pairs_of(xs, p, b);
-      uint4* dst = reinterpret_cast<uint4*>(xlds + threadIdx.x * 16);
+      const int lc = threadIdx.x % LPR, cc = threadIdx.x / LPR;
+      uint4* dst = reinterpret_cast<uint4*>(xlds);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(p[i][0], p[i][1], p[i][2], p[i][3]);
+      for (int i = 0; i < 4; ++i)
+        dst[(cc * 4 + i) * LPR + lc] = make_uint4(p[i][0], p[i][1], p[i][2], p[i][3]);
       reinterpret_cast<float*>(xlds + nchunks * 16)[threadIdx.x] = b;
     }
     __syncthreads();
@@ -160,11 +165,11 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
       float t;
       if (XL) {
         const int chunk = l + LPR * c;
-        const uint4* src = reinterpret_cast<const uint4*>(xlds + chunk * 16);
+        const uint4* src = reinterpret_cast<const uint4*>(xlds);
         uint32_t p[4][4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const uint4 v = src[q];
+          const uint4 v = src[(c * 4 + q) * LPR + l];
           p[q][0] = v.x; p[q][1] = v.y; p[q][2] = v.z; p[q][3] = v.w;
         }
         t = reinterpret_cast<const float*>(xlds + nchunks * 16)[chunk];
