@@ -44,6 +44,7 @@ _SIGS = {
     "dip_topk_workspace_size": ([_i64], _sz),
     "dip_topk_select": ([_p, _p, _i64, _i64, _p, _sz, _p], _i32),
     "dip_topk_meta": ([_p, _p, _p], _i32),
+    "dip_gate_silu_topk": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p], _i32),
     "dip_int4_gather_gemv": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dip_up_gather_h": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dip_gather_down_workspace_size": ([_i64, _i64], _sz),
@@ -204,12 +205,9 @@ def gate_silu_topk(qweight, scales, x, k, g=None, idx=None):
     if idx is None:
         idx = torch.empty(k, dtype=torch.int32, device=dev)
     ws = workspace(dev, lib.dip_topk_workspace_size(rows), "topk")
-    st = _stream(dev)
-    _check(lib.dip_int4_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(g), rows, cols, 1, st),
-           "dip_int4_gemv")
-    if k:
-        _check(lib.dip_topk_select(_ptr(g), _ptr(idx), rows, k, _ptr(ws), ws.numel(), st),
-               "dip_topk_select")
+    _check(lib.dip_gate_silu_topk(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(g), _ptr(idx), rows,
+                                  cols, k, _ptr(ws), ws.numel(), _stream(dev)),
+           "dip_gate_silu_topk")
     return g, idx
 
 

@@ -75,20 +75,12 @@ struct TopkMeta {
   uint32_t key_max;
   int32_t n_valid;
   int32_t pad;
-  uint64_t stamp[6];   // wall_clock64() at the top-k's phase boundaries (diagnostics)
+  uint64_t stamp[6];   // wall_clock64() at the select kernel's phase boundaries (diagnostics)
   uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
 };
 
-// Handed from the top-k's analysis kernel to its scatter kernel: the key cuts
-// and each 16th of the input's tier counts (in index order).
-constexpr int kTopkSlices = 16;
-struct TopkShare {
-  uint32_t cut_a;  // tier A: cut_a <= |bits| <= 0x7F80
-  uint32_t cut_b;  // tier B: cut_b <= |bits| < cut_a
-  uint32_t slice_a[kTopkSlices];
-  uint32_t slice_b[kTopkSlices];
-};
-constexpr size_t kTopkShareOffset = 128;  // TopkMeta first, TopkShare at this byte offset
+// The top-k workspace holds the last call's TopkMeta.
+constexpr size_t kTopkWorkspace = 512;
 
 // Launchers (return hipSuccess or a DIP_ERR_* code).
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
@@ -98,8 +90,9 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t down_workspace_bytes(int64_t k, int64_t out_features);
 int64_t down_max_k();  // largest k the down path accepts
-int launch_topk(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
-                hipStream_t stream);
+// The top-k select kernel: idx from s (TopkMeta into the workspace).
+int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
+                       hipStream_t stream);
 
 // Launch tuning (process-wide, host side): see DIP_TUNE_* in dip_hip.h.
 int tuning(int knob);

@@ -292,9 +292,8 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
   void* ws_topk = ws;
   void* ws_down = ws + topk_bytes;
   const size_t down_bytes = ws_bytes - topk_bytes;
-  int st = dip_int4_gemv(gate_qw, gate_sc, x, g_out, inter, hidden, DIP_ACT_SILU, stream);
-  if (st) return st;
-  st = dip_topk_select(g_out, idx_out, inter, k, ws_topk, topk_bytes, stream);
+  int st = dip_gate_silu_topk(gate_qw, gate_sc, x, g_out, idx_out, inter, hidden, k, ws_topk,
+                              topk_bytes, stream);
   if (st) return st;
   st = dip_up_gather_h(up_qw, up_sc, x, idx_out, g_out, h_out, inter, hidden, k, stream);
   if (st) return st;

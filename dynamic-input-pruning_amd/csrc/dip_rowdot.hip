@@ -341,6 +341,24 @@ extern "C" int dip_int4_gemv(const int8_t* qweight, const uint16_t* scales, cons
   return launch_rowdot(kContig, act == DIP_ACT_SILU ? kSilu : kRaw, a, (hipStream_t)stream);
 }
 
+extern "C" int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc,
+                                  const uint16_t* x, uint16_t* g, int32_t* idx, int64_t inter,
+                                  int64_t hidden, int64_t k, void* workspace, size_t ws_bytes,
+                                  void* stream) {
+  int st = check_matrix(gate_qw, gate_sc, inter, hidden);
+  if (st) return st;
+  if (!x || !g) return DIP_ERR_NULL;
+  if (!aligned16(x) || !aligned16(g)) return DIP_ERR_ALIGN;
+  if (inter > kTopkMaxN || k < 0 || k > INT32_MAX) return DIP_ERR_SHAPE;
+  if (k > 0 && !idx) return DIP_ERR_NULL;
+  if (!workspace || ws_bytes < dip_topk_workspace_size(inter)) return DIP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DIP_ERR_ALIGN;
+  RowdotArgs a = base_args(gate_qw, gate_sc, x, g, inter, hidden);
+  st = launch_rowdot(kContig, kSilu, a, (hipStream_t)stream);
+  if (st || k == 0) return st;
+  return launch_topk_select(g, inter, k, idx, workspace, (hipStream_t)stream);
+}
+
 extern "C" int dip_int4_gather_gemv(const int8_t* qweight, const uint16_t* scales,
                                     const uint16_t* x, const int32_t* indices, uint16_t* out,
                                     int64_t rows, int64_t in_features, int64_t k,

@@ -12,16 +12,19 @@
 // magnitudes gives exactly; the steps are then replayed with the same fp32
 // arithmetic.
 //
-// Two kernels:
-//   analysis (one workgroup of 1024 threads): all n values into VGPRs
-//     (wave w holds the R*512 consecutive values [w*512R, (w+1)*512R)),
-//     LDS histogram, max and a_{k+1} (only the waves holding those ranks
-//     search their bins), the 25 bisection steps, then per-wave tier counts
-//     -> TopkShare in the workspace;
-//   scatter (kTopkSlices workgroups of 256 threads): workgroup w re-reads
-//     slice w (the values wave w held), takes its starting positions from
-//     the earlier slices' counts, runs one block scan and writes its ids
-//     through LDS with coalesced stores.
+// One launch of ceil(n / 2048) workgroups of 1024 threads writes idx.  Every
+// workgroup redundantly
+//   1. loads all n values into registers and builds the histogram in its LDS
+//      (a global histogram would need device-scope atomics, and the many
+//      channels that share a bf16 magnitude serialise those);
+//   2. finds max|s| and a_{k+1} (only the waves holding rank 1 / rank k+1
+//      search their bins);
+//   3. replays the 25 bisection steps on one lane -> the two key cuts;
+//   4. takes the tier totals from the histogram and counts the tiers of the
+//      values on the shorter side of its slice (before or after it);
+// and then places the ids of its own slice of 2048 values (2 per thread, one
+// block scan) at their final positions in idx.  The workgroups never wait for
+// each other.
 //
 // Magnitudes are used unflushed: bf16 subnormals (|bits| 1..0x7F) are 0 under
 // the reference's --use_fast_math, so histogram bins below 0x80 all mean 0
@@ -36,8 +39,7 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
-static_assert(kWaves == kTopkSlices, "one scatter slice per analysis wave");
-constexpr int kScatterThreads = 256;
+constexpr int kSlice = 2 * kThreads;  // values placed per select workgroup
 constexpr uint32_t kNoKey = 0xFFFFFFFFu;
 constexpr uint32_t kMaxValidKey = kKeyInf;  // 0x7F80: +inf
 constexpr uint32_t kMinNormalKey = 0x0080u;
@@ -121,39 +123,66 @@ DIP_DEV void load_chunk8(const uint16_t* __restrict__ s, int n, int base, uint32
   out[3] = v.w;
 }
 
+
+// Tier ranges of the 15-bit keys b = |bits|:
+//   tier A: cut_a <= b <= 0x7F80      tier B: cut_b <= b < cut_a
+struct Cuts {
+  uint32_t cut_a2, span_a2, cut_b2, span_b2;  // packed in both 16-bit halves
+  uint32_t cut_a, span_a, cut_b, span_b;
+};
+
+DIP_DEV Cuts make_cuts(uint32_t cut_a, uint32_t cut_b) {
+  Cuts c;
+  c.cut_a = cut_a;
+  c.cut_b = cut_b;
+  c.span_a = kMaxValidKey + 1u - cut_a;
+  c.span_b = cut_a - cut_b;
+  c.cut_a2 = cut_a * 0x10001u;
+  c.cut_b2 = cut_b * 0x10001u;
+  c.span_a2 = c.span_a * 0x10001u;
+  c.span_b2 = c.span_b * 0x10001u;
+  return c;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Analysis: R rounds of 8 values per lane, n <= 16 waves * 64 lanes * 8R.
+// Select: R rounds of one 8-value chunk per thread cover n <= 8192 R values;
+// workgroup w places values [2048 w, 2048 (w + 1)).
 // ---------------------------------------------------------------------------
 template <int R>
-__global__ __launch_bounds__(kThreads) void topk_analysis_kernel(
-    const uint16_t* __restrict__ s, int n, int k, TopkMeta* __restrict__ meta,
-    TopkShare* __restrict__ share, int stamps) {
+__global__ __launch_bounds__(kThreads) void topk_select_kernel(
+    const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
+    TopkMeta* __restrict__ meta, int stamps) {
   extern __shared__ uint32_t hist[];  // kFineBins bins
   __shared__ uint32_t wtot[kWaves];
+  __shared__ uint32_t wsum_a[kWaves], wsum_b[kWaves], wside[kWaves], wown[kWaves];
   __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // Phase stamps (diagnostics, off by default: each store makes the storing
-  // wave wait for its completion at the next vmcnt wait).
-  const bool stamp = stamps && tid == 0;
+  const int slice0 = blockIdx.x * kSlice;
+  const bool stamp = stamps && blockIdx.x == 0 && tid == 0;
   if (stamp) {
     meta->stamp[0] = wall_clock64();
     meta->cycles[0] = clock64();
   }
 
   // ---- 1. values into registers; clear the histogram meanwhile -----------
+  // thread t holds chunks t, t + 1024, ... (8 values each)
   uint32_t key[R][4];
 #pragma unroll
-  for (int r = 0; r < R; ++r) load_chunk8(s, n, (wave * 64 * R + 64 * r + lane) * 8, key[r]);
+  for (int r = 0; r < R; ++r) load_chunk8(s, n, (tid + kThreads * r) * 8, key[r]);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int base = (wave * 64 * R + 64 * r + lane) * 8;
+    const int base = (tid + kThreads * r) * 8;
     if (base < n && base + 8 > n) load_tail8(s, n, base, key[r]);
   }
+  const int my = slice0 + 2 * tid;  // my two values to place (even index: one aligned dword)
+  uint32_t mine = 0xFFFFFFFFu;
+  if (my + 1 < n) mine = *reinterpret_cast<const uint32_t*>(s + my);
+  else if (my < n) mine = (uint32_t)s[my] | 0xFFFF0000u;
   {
     uint4* h4 = reinterpret_cast<uint4*>(hist);
 #pragma unroll
@@ -165,13 +194,11 @@ __global__ __launch_bounds__(kThreads) void topk_analysis_kernel(
     sh_max = kNoKey;
   }
   __syncthreads();
-  if (stamp) meta->stamp[1] = wall_clock64();
 
   // ---- 2. histogram of every magnitude (NaN / padding bins ignored later) --
-  // (rounds wholly past n are skipped: their padding would pile onto one bin)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    if ((wave * 64 * R + 64 * r + lane) * 8 < n) {
+    if ((tid + kThreads * r) * 8 < n) {  // chunks wholly past n would pile onto one bin
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         atomicAdd(&hist[key[r][i] & 0x7FFFu], 1u);
@@ -180,28 +207,28 @@ __global__ __launch_bounds__(kThreads) void topk_analysis_kernel(
     }
   }
   __syncthreads();
-  if (stamp) meta->stamp[2] = wall_clock64();
+  if (stamp) meta->stamp[1] = wall_clock64();
 
-  // ---- 3. max and a_{k+1} ------------------------------------------------
+  // ---- 3. max and a_{k+1} --------------------------------------------------
   // Wave w reads its 2048 bins as eight 256-bin rows j; lane L holds bins
   // 2048w + 256j + 4L .. +3 (consecutive lanes, consecutive 16 B: no bank
   // conflicts).  Wave totals first; only a wave that holds rank 1 or rank
   // k+1 (counting from the top bin) scans its rows.
   uint32_t nvalid = 0;
+  uint32_t sum4[8];
   {
     const uint4* h4 = reinterpret_cast<const uint4*>(hist);
     uint4 v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = h4[512 * wave + 64 * j + lane];
     if (wave == kWaves - 1) {
-      // bins above +inf (NaN magnitudes, padding) do not exist
+      // bins above +inf (NaN magnitudes, padding) never count
       const uint32_t b0 = 2048u * wave + 256u * 7 + 4u * lane;
       if (b0 + 0 > kMaxValidKey) v[7].x = 0;
       if (b0 + 1 > kMaxValidKey) v[7].y = 0;
       if (b0 + 2 > kMaxValidKey) v[7].z = 0;
       if (b0 + 3 > kMaxValidKey) v[7].w = 0;
     }
-    uint32_t sum4[8];
     uint32_t lsum = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -253,175 +280,160 @@ __global__ __launch_bounds__(kThreads) void topk_analysis_kernel(
     }
   }
   __syncthreads();
-  if (stamp) meta->stamp[3] = wall_clock64();
+  if (stamp) meta->stamp[2] = wall_clock64();
 
   // ---- 4. replay the 25 fp32 bisection steps (topk_select.cu:141-158) -----
   if (tid == 0) {
     uint32_t ka = sh_a, km = sh_max;
     if (ka != kNoKey && ka < kMinNormalKey) ka = 0;  // subnormal -> 0
     if (km != kNoKey && km < kMinNormalKey) km = 0;
+    // with fewer than k+1 values "c > k" never holds: a = 0 never exceeds t >= 0
     const float a = ka == kNoKey ? 0.f : bf16_to_f32(ka);
     float hi = km == kNoKey ? 0.f : bf16_to_f32(km);
     float lo = 0.f;
     float t = 0.5f * (lo + hi);
-#pragma unroll 1
+#pragma unroll
     for (int step = 0; step < 25; ++step) {
-      if (ka != kNoKey && a > t) lo = t; else hi = t;
+      const bool gt = a > t;
+      lo = gt ? t : lo;
+      hi = gt ? hi : t;
       t = 0.5f * (lo + hi);
     }
     // |s| > v for a bf16 magnitude b  <=>  b >= (bits(v) >> 16) + 1  (v >= 0);
     // subnormal magnitudes never qualify, so the cuts start at 0x80.
     sh_cut_a = max((__float_as_uint(hi) >> 16) + 1u, kMinNormalKey);
     sh_cut_b = max((__float_as_uint(lo) >> 16) + 1u, kMinNormalKey);
-    meta->lo = lo;
-    meta->hi = hi;
-    meta->key_a = ka;
-    meta->key_max = km;
-    meta->n_valid = (int32_t)nvalid;
+    if (blockIdx.x == 0) {
+      meta->lo = lo;
+      meta->hi = hi;
+      meta->key_a = ka;
+      meta->key_max = km;
+      meta->n_valid = (int32_t)nvalid;
+    }
+  }
+  __syncthreads();
+  if (stamp) meta->stamp[3] = wall_clock64();
+  const Cuts c = make_cuts(sh_cut_a, sh_cut_b);
+
+  // ---- 5. tier totals from the histogram, tier counts of one side ----------
+  // Totals: #{b >= cut} summed per 4-bin group; the one group a cut splits
+  // is summed bin by bin (bins above +inf were zeroed in sum4).
+  uint32_t ge_a = 0, ge_b = 0;
+  {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t b0 = 2048u * wave + 256u * j + 4u * lane;
+      ge_a += b0 >= c.cut_a ? sum4[j] : 0u;
+      ge_b += b0 >= c.cut_b ? sum4[j] : 0u;
+      const bool split_a = b0 < c.cut_a && b0 + 3 >= c.cut_a;
+      const bool split_b = b0 < c.cut_b && b0 + 3 >= c.cut_b;
+      if (split_a | split_b) {
+        const uint4 v = reinterpret_cast<const uint4*>(hist)[512 * wave + 64 * j + lane];
+        const uint32_t cnt[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 1; e < 4; ++e) {
+          const uint32_t ce = b0 + e <= kMaxValidKey ? cnt[e] : 0u;
+          ge_a += split_a && b0 + e >= c.cut_a ? ce : 0u;
+          ge_b += split_b && b0 + e >= c.cut_b ? ce : 0u;
+        }
+      }
+    }
+  }
+  // The tier counts before my slice: count whichever side of the slice is
+  // shorter (values before it, or after it) and derive the other.
+  const int slice1 = min(slice0 + kSlice, n);
+  const bool count_before = slice0 <= n - slice1;
+  uint32_t side = 0;  // packed (A | B << 16); at most 8R values per thread
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int base = (tid + kThreads * r) * 8;
+    const bool in_side = count_before ? base < slice0 : (base >= slice1 && base < n);
+    if (in_side) side += tier_counts8(key[r], c.cut_a2, c.span_a2, c.cut_b2, c.span_b2);
+  }
+  // my two values: tier flags, counts packed (A | B << 16)
+  const uint32_t b0 = mine & 0x7FFFu, b1 = (mine >> 16) & 0x7FFFu;
+  const uint32_t a0 = b0 - c.cut_a < c.span_a, a1 = b1 - c.cut_a < c.span_a;
+  const uint32_t q0 = b0 - c.cut_b < c.span_b, q1 = b1 - c.cut_b < c.span_b;
+  const uint32_t own = (a0 + a1) | ((q0 + q1) << 16);
+  const uint32_t incl = wave_prefix(own);
+  {
+    const uint32_t ta = lane63(wave_prefix(ge_a));
+    const uint32_t tb = lane63(wave_prefix(ge_b));
+    const uint32_t ts = lane63(wave_prefix(side));
+    if (lane == 63) wown[wave] = incl;
+    if (lane == 0) {
+      wsum_a[wave] = ta;
+      wsum_b[wave] = tb;
+      wside[wave] = ts;
+    }
   }
   __syncthreads();
   if (stamp) meta->stamp[4] = wall_clock64();
 
-  // ---- 5. tier counts of each wave's values -------------------------------
-  const uint32_t cut_a = sh_cut_a, cut_b = sh_cut_b;
-  const uint32_t cut_a2 = cut_a * 0x10001u, cut_b2 = cut_b * 0x10001u;
-  const uint32_t span_a2 = (kMaxValidKey + 1u - cut_a) * 0x10001u;  // b - cut_a < span_a
-  const uint32_t span_b2 = (cut_a - cut_b) * 0x10001u;              // b - cut_b < span_b
-  uint32_t la = 0, lb = 0;
+  uint32_t tot_a = 0, tot_ge_b = 0, side_a = 0, side_b = 0, own_tot = 0, before = 0;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint32_t c = tier_counts8(key[r], cut_a2, span_a2, cut_b2, span_b2);
-    la += c & 0xFFFFu;
-    lb += c >> 16;
+  for (int w = 0; w < kWaves; ++w) {
+    tot_a += wsum_a[w];
+    tot_ge_b += wsum_b[w];
+    side_a += wside[w] & 0xFFFFu;
+    side_b += wside[w] >> 16;
+    own_tot += wown[w];   // packed: a slice holds at most 2048 values
+    before += w < wave ? wown[w] : 0u;
   }
-  // packed: a wave's counts stay below 2^16 (at most 512R values)
-  const uint32_t wt = lane63(wave_prefix(la | (lb << 16)));
-  if (lane == 0) {
-    share->slice_a[wave] = wt & 0xFFFFu;
-    share->slice_b[wave] = wt >> 16;
-  }
-  if (tid == 0) {
-    share->cut_a = cut_a;
-    share->cut_b = cut_b;
-    if (stamps) {
-      meta->stamp[5] = wall_clock64();
-      meta->cycles[1] = clock64();
-    }
-  }
-}
+  const uint32_t tot_b = tot_ge_b - tot_a;
+  // tier counts of the values before my slice
+  const uint32_t pre_a = count_before ? side_a : tot_a - side_a - (own_tot & 0xFFFFu);
+  const uint32_t pre_b = count_before ? side_b : tot_b - side_b - (own_tot >> 16);
 
-// ---------------------------------------------------------------------------
-// Scatter: workgroup w handles slice w = values [w*512R, (w+1)*512R); thread t
-// holds the 2R consecutive values at w*512R + 2R*t.
-// ---------------------------------------------------------------------------
-template <int R>
-__global__ __launch_bounds__(kScatterThreads) void topk_scatter_kernel(
-    const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
-    const TopkShare* __restrict__ share, TopkMeta* __restrict__ meta) {
-  constexpr int kPer = 2 * R;           // values per thread
-  constexpr int kSlice = 512 * R;       // values per slice
-  __shared__ uint32_t stage[kSlice];
-  __shared__ uint32_t wsum[kScatterThreads / 64];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int w = blockIdx.x;
-  const int base = w * kSlice + tid * kPer;
-
-  uint32_t key[kPer / 8][4];
-#pragma unroll
-  for (int c = 0; c < kPer / 8; ++c) load_chunk8(s, n, base + 8 * c, key[c]);
-#pragma unroll
-  for (int c = 0; c < kPer / 8; ++c)
-    if (base + 8 * c < n && base + 8 * c + 8 > n) load_tail8(s, n, base + 8 * c, key[c]);
-
-  const uint32_t cut_a = share->cut_a, cut_b = share->cut_b;
-  uint32_t pre_a = 0, pre_b = 0, tot_a = 0, tot_b = 0;
-#pragma unroll
-  for (int q = 0; q < kTopkSlices; ++q) {
-    const uint32_t xa = share->slice_a[q], xb = share->slice_b[q];
-    pre_a += q < w ? xa : 0u;
-    pre_b += q < w ? xb : 0u;
-    tot_a += xa;
-    tot_b += xb;
-  }
-  const uint32_t my_a = share->slice_a[w];
-
-  const uint32_t cut_a2 = cut_a * 0x10001u, cut_b2 = cut_b * 0x10001u;
-  const uint32_t span_a = kMaxValidKey + 1u - cut_a, span_b = cut_a - cut_b;
-  uint32_t cnt = 0;
-#pragma unroll
-  for (int c = 0; c < kPer / 8; ++c)
-    cnt += tier_counts8(key[c], cut_a2, span_a * 0x10001u, cut_b2, span_b * 0x10001u);
-  // block exclusive scan of the packed (A | B << 16) counts (slice totals < 2^16)
-  const uint32_t incl = wave_prefix(cnt);
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  uint32_t before = 0;
-#pragma unroll
-  for (int q = 0; q < kScatterThreads / 64; ++q) before += q < wave ? wsum[q] : 0u;
-  const uint32_t ex = before + incl - cnt;
-  // stage: the slice's tier-A ids at [0, my_a), its tier-B ids after them
-  uint32_t pa = ex & 0xFFFFu;
-  uint32_t pb = my_a + (ex >> 16);
-#pragma unroll
-  for (int c = 0; c < kPer / 8; ++c) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t b = (key[c][i >> 1] >> (16 * (i & 1))) & 0x7FFFu;
-      const bool in_a = b - cut_a < span_a;
-      const bool in_b = b - cut_b < span_b;
-      if (in_a | in_b) stage[in_a ? pa : pb] = (uint32_t)(base + 8 * c + i);
-      pa += in_a;
-      pb += in_b;
-    }
-  }
-  __syncthreads();
-  // copy out: tier A to [pre_a, pre_a + my_a), tier B to tot_a + pre_b + ...,
-  // both capped at k
+  // ---- 6. place my slice ---------------------------------------------------
+  const uint32_t ex = before + incl - own;
   const uint32_t uk = (uint32_t)k;
-  const uint32_t my_b = share->slice_b[w];
-  for (uint32_t i = tid; i < my_a + my_b; i += kScatterThreads) {
-    const uint32_t pos = i < my_a ? pre_a + i : tot_a + pre_b + (i - my_a);
-    if (pos < uk) idx[pos] = (int32_t)stage[i];
+  const uint32_t pa0 = pre_a + (ex & 0xFFFFu);
+  const uint32_t pb0 = tot_a + pre_b + (ex >> 16);
+  if (a0 | q0) {
+    const uint32_t pos = a0 ? pa0 : pb0;
+    if (pos < uk) idx[pos] = my;
+  }
+  if (a1 | q1) {
+    const uint32_t pos = a1 ? pa0 + a0 : pb0 + q0;
+    if (pos < uk) idx[pos] = my + 1;
   }
   // unfilled slots (fewer than k values qualify) are 0, as in the reference
   const uint32_t filled = min(uk, tot_a + tot_b);
-  for (uint32_t p = filled + (uint32_t)(w * kScatterThreads + tid); p < uk;
-       p += kTopkSlices * kScatterThreads)
+  for (uint32_t p = filled + (uint32_t)(blockIdx.x * kThreads + tid); p < uk;
+       p += gridDim.x * kThreads)
     idx[p] = 0;
-  if (w == 0 && tid == 0) {
+  if (blockIdx.x == 0 && tid == 0) {
     meta->count_a = (int32_t)tot_a;
     meta->count_b = (int32_t)tot_b;
   }
+  if (stamp) {
+    meta->stamp[5] = wall_clock64();
+    meta->cycles[1] = clock64();
+  }
 }
 
-template <int R>
-int launch_topk_r(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
-                  hipStream_t stream) {
+int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
+                       hipStream_t stream) {
   static const bool lds_ok = [] {
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_analysis_kernel<R>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               kFineBins * (int)sizeof(uint32_t)) == hipSuccess;
+    const int bytes = kFineBins * (int)sizeof(uint32_t);
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_select_kernel<4>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess &&
+           hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_select_kernel<8>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
   }();
   if (!lds_ok) return hip_status(hipGetLastError());
-  TopkShare* share =
-      reinterpret_cast<TopkShare*>(reinterpret_cast<char*>(meta) + kTopkShareOffset);
-  hipLaunchKernelGGL((topk_analysis_kernel<R>), dim3(1), dim3(kThreads),
-                     kFineBins * sizeof(uint32_t), stream, s, (int)n, (int)k, meta, share,
-                     tuning(DIP_TUNE_TOPK_STAMPS));
-  int st = hip_status(hipGetLastError());
-  if (st) return st;
-  hipLaunchKernelGGL((topk_scatter_kernel<R>), dim3(kTopkSlices), dim3(kScatterThreads), 0,
-                     stream, s, (int)n, (int)k, idx, share, meta);
+  TopkMeta* meta = reinterpret_cast<TopkMeta*>(ws);
+  const unsigned blocks = (unsigned)(n > 0 ? (n + kSlice - 1) / kSlice : 1);
+  const int stamps = tuning(DIP_TUNE_TOPK_STAMPS);
+  const size_t lds = kFineBins * sizeof(uint32_t);
+  if (n <= 4 * 8 * kThreads)
+    hipLaunchKernelGGL((topk_select_kernel<4>), dim3(blocks), dim3(kThreads), lds, stream, s,
+                       (int)n, (int)k, idx, meta, stamps);
+  else
+    hipLaunchKernelGGL((topk_select_kernel<8>), dim3(blocks), dim3(kThreads), lds, stream, s,
+                       (int)n, (int)k, idx, meta, stamps);
   return hip_status(hipGetLastError());
-}
-
-int launch_topk(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, TopkMeta* meta,
-                hipStream_t stream) {
-  if (n <= 4 * 8 * kThreads) return launch_topk_r<4>(s, n, k, idx, meta, stream);
-  return launch_topk_r<8>(s, n, k, idx, meta, stream);
 }
 
 }  // namespace dip
@@ -430,8 +442,6 @@ using namespace dip;
 
 namespace {
 
-TopkMeta* meta_of(void* ws) { return reinterpret_cast<TopkMeta*>(ws); }
-
 int check_topk(const uint16_t* s, int32_t* idx, int64_t n, int64_t k, void* ws,
                size_t ws_bytes) {
   if (n < 0 || k < 0 || n > kTopkMaxN || k > INT32_MAX) return DIP_ERR_SHAPE;
@@ -439,17 +449,17 @@ int check_topk(const uint16_t* s, int32_t* idx, int64_t n, int64_t k, void* ws,
   if (n > 0 && !s) return DIP_ERR_NULL;
   if (n > 0 && (reinterpret_cast<uintptr_t>(s) & 15u)) return DIP_ERR_ALIGN;
   if (!ws || ws_bytes < dip_topk_workspace_size(n)) return DIP_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) & 15u) return DIP_ERR_ALIGN;
   return DIP_OK;
 }
 
 }  // namespace
 
-static_assert(sizeof(TopkMeta) <= kTopkShareOffset, "TopkMeta overlaps TopkShare");
-static_assert(kTopkShareOffset + sizeof(TopkShare) <= 512, "top-k workspace");
+static_assert(sizeof(TopkMeta) <= kTopkWorkspace, "top-k workspace");
 
 extern "C" size_t dip_topk_workspace_size(int64_t n) {
   (void)n;
-  return 512;  // the last call's thresholds (TopkMeta) and cuts / tier counts (TopkShare)
+  return kTopkWorkspace;  // the last call's thresholds and tier sizes (TopkMeta)
 }
 
 extern "C" int64_t dip_topk_max_n(void) { return kTopkMaxN; }
@@ -459,7 +469,7 @@ extern "C" int dip_topk_select(const uint16_t* s, int32_t* idx, int64_t n, int64
   int st = check_topk(s, idx, n, k, workspace, ws_bytes);
   if (st) return st;
   if (k == 0) return DIP_OK;
-  return launch_topk(s, n, k, idx, meta_of(workspace), (hipStream_t)stream);
+  return launch_topk_select(s, n, k, idx, workspace, (hipStream_t)stream);
 }
 
 extern "C" int dip_topk_meta(const void* workspace, void* meta_out, void* stream) {

@@ -113,10 +113,14 @@ class DIPStack:
                 K._check(lib.dip_int4_gemv(lw["gate_qw"].data_ptr(), lw["gate_sc"].data_ptr(), x,
                                            self.g.data_ptr(), I, H, 1, st), "gate")
 
-        def topk(st):
-            for _ in self.w:
-                K._check(lib.dip_topk_select(self.g.data_ptr(), self.idx.data_ptr(), I, k,
-                                             ws_ptr, topk_bytes, st), "topk")
+        def gate_topk(st):
+            # the decode step's first half: gate GEMV + SiLU building the
+            # top-k histogram, then the top-k select
+            for lw in self.w:
+                K._check(lib.dip_gate_silu_topk(lw["gate_qw"].data_ptr(),
+                                                lw["gate_sc"].data_ptr(), x, self.g.data_ptr(),
+                                                self.idx.data_ptr(), I, H, k, ws_ptr, topk_bytes,
+                                                st), "gate_topk")
 
         def up(st):
             for lw in self.w:
@@ -133,7 +137,7 @@ class DIPStack:
                                                   ws_n - topk_bytes, st), "down")
 
         graphs = {}
-        for name, fn in (("gate_silu", gate), ("topk", topk), ("up_gather_h", up),
+        for name, fn in (("gate_silu", gate), ("gate_topk", gate_topk), ("up_gather_h", up),
                          ("down_gather", down)):
             s = torch.cuda.Stream(device=self.device)
             s.wait_stream(torch.cuda.current_stream(self.device))
@@ -150,7 +154,9 @@ class DIPStack:
     def stage_times_ms(self, reps: int = 3):
         """Average duration of one launch of each kernel stage: each stage's
         graph (one launch per layer, back to back) is replayed between two
-        HIP events on the replaying stream; time / (layers * reps)."""
+        HIP events on the replaying stream; time / (layers * reps).  The
+        top-k runs on the histogram the gate launch builds, so its time is
+        that of gate + top-k minus that of the gate alone."""
         self.run_token()
         torch.cuda.synchronize(self.device)
         graphs = self.stage_graphs()
@@ -166,4 +172,5 @@ class DIPStack:
             e1.record(stream)
             torch.cuda.synchronize(self.device)
             out[name] = e0.elapsed_time(e1) / (reps * self.layers)
-        return out
+        out["topk"] = max(out.pop("gate_topk") - out["gate_silu"], 0.0)
+        return {name: out[name] for name in ("gate_silu", "topk", "up_gather_h", "down_gather")}

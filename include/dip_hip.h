@@ -70,11 +70,11 @@ int dip_int4_gemv(const int8_t* qweight, const uint16_t* scales, const uint16_t*
  * by tier t_lo < |s| <= t_strict in ascending index, unfilled slots 0).
  * Bit-exact with topk_ops::topk_select (kernels/topk_select/topk_select.cu:
  * 134-171, topk_kernel.py:29-40).  n <= dip_topk_max_n(); s 16-byte aligned.
- * No host round trips: an analysis kernel (one workgroup: LDS histogram of
- * the 15-bit magnitudes, a_{k+1} and max, the 25 bisection steps replayed)
- * hands the cuts and per-slice tier counts through the workspace to a
- * scatter kernel (16 workgroups) that writes idx.  The workspace (512 B)
- * keeps the last call's thresholds (dip_topk_meta).
+ * No host round trips: one launch of one workgroup per 2048 values; each
+ * builds an LDS histogram of the 15-bit magnitudes, finds max|s| and
+ * a_{k+1}, replays the 25 bisection steps and writes its 2048-value slice
+ * of idx.  The workspace (512 B) keeps the last call's thresholds
+ * (dip_topk_meta).
  */
 size_t dip_topk_workspace_size(int64_t n);
 int dip_topk_select(const uint16_t* s, int32_t* idx, int64_t n, int64_t k,
@@ -82,6 +82,17 @@ int dip_topk_select(const uint16_t* s, int32_t* idx, int64_t n, int64_t k,
 /* Copy the last top-k's thresholds (fp32 t_lo, t_strict) and tier sizes
  * (int32 count_a, count_b) from the workspace into `meta` (device, 16 B). */
 int dip_topk_meta(const void* workspace, void* meta_out, void* stream);
+
+/*
+ * Gate GEMV + SiLU + top-k in one call: g = bf16(silu(bf16(gate @ x))) as
+ * dip_int4_gemv with DIP_ACT_SILU, then idx[0:k] = dip_topk_select(g).
+ * inter <= dip_topk_max_n(); workspace: dip_topk_workspace_size(inter).
+ * Replaces gate_gemv + F.silu + select_topk (gate_kernel.py:29-33,
+ * dip_stream_predispatch.py:181-185, topk_kernel.py:29-40).
+ */
+int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc, const uint16_t* x,
+                       uint16_t* g, int32_t* idx, int64_t inter, int64_t hidden, int64_t k,
+                       void* workspace, size_t ws_bytes, void* stream);
 
 /*
  * out[j] = bf16( sum_c (q*s)[indices[j], c] * x[c] ), j < k.

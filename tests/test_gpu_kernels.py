@@ -247,6 +247,27 @@ def test_gate_silu_topk_fused_matches_unfused(K):
         assert np.array_equal(idx.cpu().numpy(), O.topk_select(host_bf16(g), k))
 
 
+def test_gate_silu_topk_across_shapes(K):
+    """The fused gate + top-k and the standalone top-k, alternating on one
+    workspace over shapes whose select grids have 1 to 13 workgroups."""
+    rng = np.random.default_rng(24)
+    layers = []
+    for rows, cols in ((25600, 5120), (3072, 1024), (12288, 4096), (100 * 128, 128)):
+        qw, sc = random_int4(rng, rows, cols)
+        layers.append((dev(qw), dev_bf16(sc), dev_bf16(random_bf16(rng, cols))))
+    for rep in range(2):
+        for i, (qd, sd, xd) in enumerate(layers):
+            rows = qd.shape[0]
+            for k in (rows * 3 // 5, 1, rows):
+                print(f"rep {rep} layer {i} rows={rows} k={k}", flush=True)
+                g, idx = K.gate_silu_topk(qd, sd, xd, k)
+                want = O.topk_select(host_bf16(g), k)
+                assert np.array_equal(idx.cpu().numpy(), want), (rep, i, k)
+                s = dev_bf16(random_bf16(rng, rows))
+                got = K.topk_select(s, k).cpu().numpy()
+                assert np.array_equal(got, O.topk_select(host_bf16(s), k)), (rep, i, k)
+
+
 def test_ca_assemble(K):
     rng = np.random.default_rng(23)
     inter, k, cache_n = 25600, 15360, 7680
