@@ -105,7 +105,6 @@ def main(argv=None):
     ap.add_argument("--keep", type=float, default=0.6)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--down-mode", type=int, default=None)
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel eagerly instead of replaying the captured graph "
                          "(for counter collection, which profiles each dispatch)")
@@ -123,8 +122,6 @@ def main(argv=None):
     import _dip_hip as K
     from dip_stack import SHAPES, DIPStack
 
-    if args.down_mode is not None:
-        K.set_down_dequant_mode(args.down_mode)
     shape = dict(SHAPES[args.shape])
     if args.layers:
         shape["layers"] = args.layers

@@ -409,9 +409,7 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
     return y, g, idx, h
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "down_lpr": 1, "down_blocks": 2, "down_dequant": 3,
-        "down_unroll": 4, "rowdot_x_lds": 5, "rowdot_depth": 6, "down_cpl": 7,
-        "topk_stamps": 8}
+TUNE = {"rowdot_wgs_per_cu": 0, "rowdot_x_lds": 1, "rowdot_depth": 2, "topk_stamps": 3}
 
 
 def set_tuning(name: str, value: int) -> None:
@@ -421,10 +419,6 @@ def set_tuning(name: str, value: int) -> None:
 
 def get_tuning(name: str) -> int:
     return lib.dip_get_tuning(TUNE[name])
-
-
-def set_down_dequant_mode(mode: int) -> None:
-    set_tuning("down_dequant", mode)
 
 
 # DIP_TUNE="knob=value,knob=value" applies launch tuning at import (profiling

@@ -2,30 +2,30 @@
 //
 // down_t is [rows, out/2] packed int4 (row = one intermediate channel), so a
 // selected channel is one contiguous row.  The work is tiled two ways:
-//   * column block cb: LPR lanes each own CPL 16-byte chunks (32*CPL outputs)
-//     of every row, i.e. LPR*CPL*16 contiguous bytes per row per block;
+//   * column block cb: LPR lanes each own one 16-byte chunk (32 outputs) of
+//     every row, i.e. 16*LPR contiguous bytes per row per block;
 //   * row block rb: 256 consecutive selected positions j.
 // A block of 256 threads holds 256/LPR "slots" of LPR lanes; slot s walks the
 // LPR rows j = 256*rb + s + i*(256/LPR), i < LPR.  Lane l of a slot fetches
 // the id and h of the slot's l-th row; each row's id and h are shuffled to
 // the slot when it comes up.  The row loop is straight-line code (LPR is a
 // compile-time constant; positions past k are clamped and contribute 0), so
-// every load is unconditional and D rows of loads stay in flight.  Each lane
-// keeps 32*CPL fp32 accumulators (its outputs).  Slots are reduced through
-// LDS in a fixed order and the block writes one fp32 partial row segment; the
-// reduce kernel sums the row-block partials in a fixed order and rounds to
-// bf16.  No float atomics, so results are identical run to run.
+// every load is unconditional and all of a slot's rows are in flight at once.
+// Each lane keeps 32 fp32 accumulators (its outputs).
 //
-// Tiling knobs: LPR lanes per row segment, CPL chunks per lane, D rows in
-// flight per slot (DIP_TUNE_DOWN_LPR / _CPL / _UNROLL).
+// Dequant: v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for
+// the low nibble of any byte (high nibbles after one shift), so each weight
+// costs one convert and one FMA: acc += (q/16) * (16*h*s).
 //
-// Dequant per weight, two interchangeable forms (DQ):
-//   DQ = 0: nibbles flipped to u = q + 8 in [0, 15] per byte and converted
-//           with v_cvt_f32_ubyte{0..3}; acc += u * (h*s), and the accumulated
-//           bias 8 * sum(h*s) is removed once at the end;
-//   DQ = 1: v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for
-//           the low nibble of any byte (high nibbles after one shift);
-//           acc += (q/16) * (16*h*s).  No bias, ~2.1 VALU ops per weight.
+// Reduction, deterministic and without float atomics:
+//   1. the slots of a block are summed through LDS in a fixed order (two
+//      halves of 16 accumulators, to keep the LDS footprint small) and the
+//      block stores its fp32 partial row segment;
+//   2. a reduce kernel sums the row blocks' partials of every output in a
+//      fixed order and rounds to bf16.
+// (A last-arriving-block reduce inside the partial kernel was measured and
+// dropped: the 64 arrivals on each column block's device-scope counter
+// serialise and cost more than the second launch.)
 #include "dip_common.h"
 #include "dip_internal.h"
 
@@ -38,8 +38,10 @@ constexpr int kXcds = 8;                 // MI355X: 8 XCDs, workgroups dispatche
 constexpr uint32_t kBadRow = 0xFFFFFFFFu;  // out-of-range id: poisons y with NaN
 constexpr uint32_t kPadRow = 0xFFFFFFFEu;  // position past k: contributes 0
 constexpr uint32_t kSrcB = 0x80000000u;
-constexpr int kRedOut = 32;    // outputs per reduce block
-constexpr int kRedSplit = 8;   // partial subsets per output
+constexpr int kAcc = kChunkCols;         // outputs per lane: one 16-byte chunk
+constexpr int kMaxRowBlocks = 512;       // k <= 131072
+constexpr int kRedOut = 64;              // outputs per reduce block
+constexpr int kRedSplit = 4;             // interleaved row-block splits per output
 }  // namespace
 
 // Row id for position j (j < k); kBadRow if out of range.  Branch-free.
@@ -78,11 +80,13 @@ DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, int cc0, size_t row_
   R.s = sc[(size_t)r * ngroups + cc0 / kChunksPerGroup];
 }
 
-template <int LPR, int CPL, int SRC, int DQ, int D>
-__global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
+template <int LPR, int SRC>
+__global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
+  constexpr int D = LPR;                // every row of a slot in flight at once
   constexpr int kSlots = kThreads / LPR;
-  constexpr int kAcc = CPL * kChunkCols;
-  constexpr int kStride = kAcc + 1;  // padded LDS rows: conflict-free both ways
+  constexpr int kHalf = kAcc / 2;
+  constexpr int kStride = kHalf + 1;    // padded LDS rows: conflict-free both ways
+  constexpr int kCols = LPR * kAcc;     // outputs per column block
   __shared__ float red[kSlots * LPR * kStride];
 
   // XCD-aware tile order: workgroups go to the 8 XCDs round-robin, so tile
@@ -97,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
   const int l = threadIdx.x % LPR;
   const int slot = threadIdx.x / LPR;
   const int gbase = (threadIdx.x & 63) - l;
-  const int cc0 = (cb * LPR + l) * CPL;  // first chunk of mine within a row
+  const int cc0 = cb * LPR + l;  // my chunk within a row
   const size_t row_bytes = (size_t)(a.out_features >> 1);
   const int ngroups = a.out_features >> 7;
   const int j0 = rb * kRowsPerBlock + slot;
@@ -109,91 +113,79 @@ __global__ __launch_bounds__(kThreads) void down_partial_kernel(DownArgs a) {
   const uint32_t rid_l = jl < a.k ? rid_c : kPadRow;
   const uint32_t h_l = a.h[jc];
 
-  DownRow<CPL> ring[D];
+  DownRow<1> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ngroups, ring[d]);
+    load_down_row<1, SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ngroups, ring[d]);
 
   float acc[kAcc];
 #pragma unroll
   for (int m = 0; m < kAcc; ++m) acc[m] = 0.f;
-  float hsum = 0.f;
 
 #pragma unroll
   for (int i = 0; i < LPR; ++i) {
-    DownRow<CPL>& R = ring[i % D];
+    const DownRow<1>& R = ring[i];
     const uint32_t rid = __shfl(rid_l, gbase + i, 64);
     const uint32_t hb = __shfl(h_l, gbase + i, 64);
-    // f = h*s, 0 for padding, NaN for a bad id: integer selects on the bits
-    // keep this branch-free (a branch here sinks the scale load into it and
-    // costs a full vmcnt(0) wait)
-    uint32_t fb = __float_as_uint(bf16_to_f32(hb) * bf16_to_f32(R.s));
+    // f = 16*h*s, 0 for padding, NaN for a bad id: integer selects on the
+    // bits keep this branch-free (a branch here sinks the scale load into it
+    // and costs a full vmcnt(0) wait)
+    uint32_t fb = __float_as_uint(bf16_to_f32(hb) * bf16_to_f32(R.s) * 16.0f);
     fb = rid == kPadRow ? 0u : fb;
     fb = rid == kBadRow ? 0x7FC00000u : fb;
-    const float f = __uint_as_float(fb);
+    const float f16 = __uint_as_float(fb);
+    const uint32_t wv[4] = {R.w[0].x, R.w[0].y, R.w[0].z, R.w[0].w};
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const uint32_t wv[4] = {R.w[c].x, R.w[c].y, R.w[c].z, R.w[c].w};
-      float* ac = acc + c * kChunkCols;
-      if (DQ == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t lo = (wv[q] & 0x0F0F0F0Fu) ^ 0x08080808u;
-          const uint32_t hi = ((wv[q] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-          ac[8 * q + 0] = fmaf(cvt_ubyte<0>(lo), f, ac[8 * q + 0]);
-          ac[8 * q + 1] = fmaf(cvt_ubyte<0>(hi), f, ac[8 * q + 1]);
-          ac[8 * q + 2] = fmaf(cvt_ubyte<1>(lo), f, ac[8 * q + 2]);
-          ac[8 * q + 3] = fmaf(cvt_ubyte<1>(hi), f, ac[8 * q + 3]);
-          ac[8 * q + 4] = fmaf(cvt_ubyte<2>(lo), f, ac[8 * q + 4]);
-          ac[8 * q + 5] = fmaf(cvt_ubyte<2>(hi), f, ac[8 * q + 5]);
-          ac[8 * q + 6] = fmaf(cvt_ubyte<3>(lo), f, ac[8 * q + 6]);
-          ac[8 * q + 7] = fmaf(cvt_ubyte<3>(hi), f, ac[8 * q + 7]);
-        }
-      } else {
-        const float f16 = f * 16.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t hi = wv[q] >> 4;
-          ac[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, ac[8 * q + 0]);
-          ac[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, ac[8 * q + 1]);
-          ac[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, ac[8 * q + 2]);
-          ac[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, ac[8 * q + 3]);
-          ac[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, ac[8 * q + 4]);
-          ac[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, ac[8 * q + 5]);
-          ac[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, ac[8 * q + 6]);
-          ac[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, ac[8 * q + 7]);
-        }
-      }
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t hi = wv[q] >> 4;
+      acc[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, acc[8 * q + 0]);
+      acc[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, acc[8 * q + 1]);
+      acc[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, acc[8 * q + 2]);
+      acc[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, acc[8 * q + 3]);
+      acc[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, acc[8 * q + 4]);
+      acc[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, acc[8 * q + 5]);
+      acc[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, acc[8 * q + 6]);
+      acc[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, acc[8 * q + 7]);
     }
-    if (DQ == 0) hsum += f;
-    if (i + D < LPR)
-      load_down_row<CPL, SRC>(a, __shfl(rid_l, gbase + i + D, 64), cc0, row_bytes, ngroups, R);
+    // Keep each row's conversions next to their FMAs: left free, the
+    // scheduler hoists every row's conversions ahead of the FMAs and needs
+    // over 140 VGPRs (three blocks per CU instead of five).
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  // slot-major LDS rows of kStride floats: red[(slot*LPR + l)*kStride + m]
+  // Slots summed in a fixed order, 16 accumulators at a time (written out
+  // twice: as a loop over the halves the compiler keeps both halves' sums in
+  // flight and needs 170 VGPRs); column l*32 + m of the block sits at
+  // red[(slot*LPR + l)*kStride + m - half]
+  float* out = a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols;
   float* mine = red + (slot * LPR + l) * kStride;
 #pragma unroll
-  for (int m = 0; m < kAcc; ++m) mine[m] = DQ == 0 ? fmaf(-8.0f, hsum, acc[m]) : acc[m];
+  for (int m = 0; m < kHalf; ++m) mine[m] = acc[m];
   __syncthreads();
-
-  // Sum the slots in a fixed order.  Block columns: lane l's CPL chunks are
-  // consecutive, so column = (l*CPL + c)*32 + m = l*kAcc + (c*32 + m).
-  constexpr int kCols = LPR * kAcc;
-  float* out = a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols;
-  for (int col = threadIdx.x; col < kCols; col += kThreads) {
-    const int ln = col / kAcc;
-    const int m = col % kAcc;
+  for (int e = threadIdx.x; e < LPR * kHalf; e += kThreads) {
+    const int ln = e / kHalf, m = e % kHalf;
     float s = 0.f;
 #pragma unroll 8
     for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
-    out[col] = s;
+    out[ln * kAcc + m] = s;
+  }
+  __syncthreads();  // the first half's reads are done
+#pragma unroll
+  for (int m = 0; m < kHalf; ++m) mine[m] = acc[kHalf + m];
+  __syncthreads();
+  for (int e = threadIdx.x; e < LPR * kHalf; e += kThreads) {
+    const int ln = e / kHalf, m = e % kHalf;
+    float s = 0.f;
+#pragma unroll 8
+    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
+    out[ln * kAcc + kHalf + m] = s;
   }
 }
 
-// y[o] = bf16(sum over row blocks of partial[rb][o]): split p of an output
-// sums row blocks p, p+8, p+16, ... (NB of them, the ones past row_blocks
-// read a clamped address and add 0) in ascending order; the 8 splits are then
-// added in order 0..7.  All NB loads are unconditional and issued together.
+// y[o] = bf16(sum over row blocks rb of partial[rb][o]), rb ascending in four
+// interleaved splits (split p sums rb = p, p+4, ...), the splits then added
+// in order 0..3.  A thread issues all its loads at once (NB per split; row
+// blocks past row_blocks read a clamped address and are skipped).
 template <int NB>
 __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
     const float* __restrict__ partial, int row_blocks, int out_features, uint16_t* __restrict__ y) {
@@ -201,15 +193,17 @@ __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
   const int oo = threadIdx.x % kRedOut;
   const int p = threadIdx.x / kRedOut;
   const int o = min(blockIdx.x * kRedOut + oo, out_features - 1);
-  float v[NB];
-#pragma unroll
-  for (int u = 0; u < NB; ++u) {
-    const int rb = min(p + u * kRedSplit, row_blocks - 1);
-    v[u] = partial[(size_t)rb * out_features + o];
-  }
   float s = 0.f;
+  for (int r0 = p; r0 < row_blocks; r0 += NB * kRedSplit) {
+    float v[NB];
 #pragma unroll
-  for (int u = 0; u < NB; ++u) s += p + u * kRedSplit < row_blocks ? v[u] : 0.f;
+    for (int u = 0; u < NB; ++u) {
+      const int rb = min(r0 + u * kRedSplit, row_blocks - 1);
+      v[u] = partial[(size_t)rb * out_features + o];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) s = r0 + u * kRedSplit < row_blocks ? s + v[u] : s;
+  }
   part[p][oo] = s;
   __syncthreads();
   if (p == 0 && blockIdx.x * kRedOut + oo < out_features) {
@@ -228,90 +222,48 @@ __global__ void down_zero_kernel(int out_features, uint16_t* __restrict__ y) {
 
 namespace {
 
-struct DownPlan {
-  int lpr;
-  int cpl;
-  int col_blocks;
-  int row_blocks;
-};
-
-DownPlan plan_down(int64_t k, int64_t out_features) {
-  DownPlan p{};
+// Lanes per row segment: 8 (128 B per row, 256 outputs per column block)
+// wherever the width allows, else 4.
+int down_lpr(int64_t out_features) {
   const int64_t chunks = out_features / kChunkCols;
-  const int want = tuning(DIP_TUNE_DOWN_LPR);
-  for (int cpl : {tuning(DIP_TUNE_DOWN_CPL), 1}) {
-    for (int lpr : {32, 16, 8, 4}) {
-      if (want && lpr > want) continue;
-      if (chunks % ((int64_t)lpr * cpl) == 0) {
-        p.lpr = lpr;
-        p.cpl = cpl;
-        break;
-      }
-    }
-    if (p.lpr) break;
-  }
-  if (!p.lpr || k <= 0) return p;
-  p.col_blocks = (int)(chunks / ((int64_t)p.lpr * p.cpl));
-  p.row_blocks = (int)((k + kRowsPerBlock - 1) / kRowsPerBlock);
-  return p;
+  if (chunks % 8 == 0) return 8;
+  if (chunks % 4 == 0) return 4;
+  return 0;
 }
 
-template <int LPR, int CPL, int DQ, int D>
-void launch_partial4(int src, const DownArgs& a, int blocks, hipStream_t stream) {
-  if (src == kContig)
-    hipLaunchKernelGGL((down_partial_kernel<LPR, CPL, kContig, DQ, D>), dim3(blocks),
-                       dim3(kThreads), 0, stream, a);
-  else if (src == kGather)
-    hipLaunchKernelGGL((down_partial_kernel<LPR, CPL, kGather, DQ, D>), dim3(blocks),
-                       dim3(kThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL((down_partial_kernel<LPR, CPL, kDual, DQ, D>), dim3(blocks),
-                       dim3(kThreads), 0, stream, a);
-}
-
-template <int LPR, int CPL>
-void launch_partial(int src, const DownArgs& a, int blocks, hipStream_t stream) {
-  const int dq = tuning(DIP_TUNE_DOWN_DEQUANT);
-  const int d = min(tuning(DIP_TUNE_DOWN_UNROLL), LPR);
-  if (dq == 1) {
-    if (d >= 8) launch_partial4<LPR, CPL, 1, (LPR >= 8 ? 8 : LPR)>(src, a, blocks, stream);
-    else if (d >= 4) launch_partial4<LPR, CPL, 1, 4>(src, a, blocks, stream);
-    else launch_partial4<LPR, CPL, 1, 2>(src, a, blocks, stream);
-  } else {
-    launch_partial4<LPR, CPL, 0, 2>(src, a, blocks, stream);
-  }
-}
-
-template <int NB>
 void launch_reduce(const float* partial, int row_blocks, int out_features, uint16_t* y,
                    hipStream_t stream) {
   const unsigned blocks = (unsigned)((out_features + kRedOut - 1) / kRedOut);
-  hipLaunchKernelGGL((down_reduce_kernel<NB>), dim3(blocks), dim3(kRedOut * kRedSplit), 0,
-                     stream, partial, row_blocks, out_features, y);
+  const dim3 threads(kRedOut * kRedSplit);
+  const int per = (row_blocks + kRedSplit - 1) / kRedSplit;  // row blocks per split
+  if (per <= 4)
+    hipLaunchKernelGGL((down_reduce_kernel<4>), dim3(blocks), threads, 0, stream, partial,
+                       row_blocks, out_features, y);
+  else
+    hipLaunchKernelGGL((down_reduce_kernel<16>), dim3(blocks), threads, 0, stream, partial,
+                       row_blocks, out_features, y);
 }
 
-void launch_reduce_any(const float* partial, int row_blocks, int out_features, uint16_t* y,
-                       hipStream_t stream) {
-  const int nb = (row_blocks + kRedSplit - 1) / kRedSplit;
-  if (nb <= 1) launch_reduce<1>(partial, row_blocks, out_features, y, stream);
-  else if (nb <= 2) launch_reduce<2>(partial, row_blocks, out_features, y, stream);
-  else if (nb <= 4) launch_reduce<4>(partial, row_blocks, out_features, y, stream);
-  else if (nb <= 8) launch_reduce<8>(partial, row_blocks, out_features, y, stream);
-  else if (nb <= 16) launch_reduce<16>(partial, row_blocks, out_features, y, stream);
-  else if (nb <= 32) launch_reduce<32>(partial, row_blocks, out_features, y, stream);
-  else launch_reduce<64>(partial, row_blocks, out_features, y, stream);
+template <int LPR>
+void launch_down(int src, const DownArgs& a, int blocks, hipStream_t stream) {
+  if (src == kContig)
+    hipLaunchKernelGGL((down_kernel<LPR, kContig>), dim3(blocks), dim3(kThreads), 0, stream, a);
+  else if (src == kGather)
+    hipLaunchKernelGGL((down_kernel<LPR, kGather>), dim3(blocks), dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((down_kernel<LPR, kDual>), dim3(blocks), dim3(kThreads), 0, stream, a);
 }
 
 }  // namespace
 
 size_t down_workspace_bytes(int64_t k, int64_t out_features) {
-  // one fp32 partial row per block of 256 selected positions
+  // one fp32 partial row of out_features per block of 256 selected positions
   if (out_features <= 0) return 256;
   const int64_t blocks = k > 0 ? (k + kRowsPerBlock - 1) / kRowsPerBlock : 1;
   return (size_t)blocks * (size_t)out_features * sizeof(float);
 }
 
-int64_t down_max_k() { return (int64_t)64 * kRedSplit * kRowsPerBlock; }
+int64_t down_max_k() { return (int64_t)kMaxRowBlocks * kRowsPerBlock; }
 
 int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
@@ -332,9 +284,10 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
     return hip_status(hipGetLastError());
   }
   if (rows_a == 0 && (src != kDual || rows_b <= 0)) return DIP_ERR_SHAPE;
-  const DownPlan p = plan_down(k, out_features);
-  if (!p.lpr) return DIP_ERR_UNSUPPORTED;
+  const int lpr = down_lpr(out_features);
+  if (!lpr) return DIP_ERR_UNSUPPORTED;
   if (!workspace || ws_bytes < down_workspace_bytes(k, out_features)) return DIP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DIP_ERR_ALIGN;
   DownArgs a{};
   a.qw_a = qw_a;
   a.sc_a = sc_a;
@@ -350,27 +303,14 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.rows_b = (int)rows_b;
   a.k = (int)k;
   a.out_features = (int)out_features;
-  a.col_blocks = p.col_blocks;
-  a.row_blocks = p.row_blocks;
-  const int blocks = (p.row_blocks + kXcds - 1) / kXcds * kXcds * p.col_blocks;
-  if (p.cpl == 2) {
-    switch (p.lpr) {
-      case 32: launch_partial<32, 2>(src, a, blocks, stream); break;
-      case 16: launch_partial<16, 2>(src, a, blocks, stream); break;
-      case 8: launch_partial<8, 2>(src, a, blocks, stream); break;
-      default: launch_partial<4, 2>(src, a, blocks, stream); break;
-    }
-  } else {
-    switch (p.lpr) {
-      case 32: launch_partial<32, 1>(src, a, blocks, stream); break;
-      case 16: launch_partial<16, 1>(src, a, blocks, stream); break;
-      case 8: launch_partial<8, 1>(src, a, blocks, stream); break;
-      default: launch_partial<4, 1>(src, a, blocks, stream); break;
-    }
-  }
+  a.col_blocks = (int)(out_features / (kChunkCols * lpr));
+  a.row_blocks = (int)((k + kRowsPerBlock - 1) / kRowsPerBlock);
+  const int blocks = (a.row_blocks + kXcds - 1) / kXcds * kXcds * a.col_blocks;
+  if (lpr == 8) launch_down<8>(src, a, blocks, stream);
+  else launch_down<4>(src, a, blocks, stream);
   int st = hip_status(hipGetLastError());
   if (st) return st;
-  launch_reduce_any(a.partial, p.row_blocks, (int)out_features, y, stream);
+  launch_reduce(a.partial, a.row_blocks, (int)out_features, y, stream);
   return hip_status(hipGetLastError());
 }
 

@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 8, 1024, 1, 8, 1, 2, 1, 0};
+int g_tune[DIP_TUNE_COUNT] = {2, 2, 2, 0};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -171,26 +171,11 @@ extern "C" int dip_set_tuning(int knob, int value) {
     case DIP_TUNE_ROWDOT_WGS_PER_CU:
       if (value < 1 || value > 16) return DIP_ERR_ARG;
       break;
-    case DIP_TUNE_DOWN_LPR:
-      if (value != 0 && value != 4 && value != 8 && value != 16 && value != 32) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_DOWN_BLOCKS:
-      if (value < 1 || value > 65536) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_DOWN_DEQUANT:
-      if (value != 0 && value != 1) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_DOWN_UNROLL:
-      if (value != 2 && value != 4 && value != 8) return DIP_ERR_ARG;
-      break;
     case DIP_TUNE_ROWDOT_X_LDS:
-      if (value != 0 && value != 1) return DIP_ERR_ARG;
+      if (value < 0 || value > 2) return DIP_ERR_ARG;
       break;
     case DIP_TUNE_ROWDOT_DEPTH:
       if (value < 2 || value > 4) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_DOWN_CPL:
-      if (value != 1 && value != 2) return DIP_ERR_ARG;
       break;
     case DIP_TUNE_TOPK_STAMPS:
       if (value != 0 && value != 1) return DIP_ERR_ARG;

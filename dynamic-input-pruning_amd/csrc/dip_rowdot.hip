@@ -15,8 +15,11 @@
 //     vmcnt(N) with N > 0) while the next D-1 rows stay in flight.  Loads
 //     under data-dependent branches would make it wait for everything.
 //   * x is pre-paired for v_dot2_f32_bf16 with the per-chunk bias term (see
-//     dip_common.h), held in VGPRs (XL=0) or staged once per workgroup in LDS
-//     (XL=1); its loads are issued before the row loads.
+//     dip_common.h) and its loads are issued before the row loads.  XL=0:
+//     each lane builds its CH chunks' pairs in VGPRs from global memory;
+//     XL=1: the workgroup stages all pairs once in LDS and every row re-reads
+//     them from LDS; XL=2: staged in LDS once, then each lane copies its CH
+//     chunks' pairs into VGPRs, so the row loop touches no LDS.
 //   * The group reduction is DPP + permlane swaps (group_sum); lane l keeps
 //     the sum of row l and runs the epilogue for it.
 #include "dip_common.h"
@@ -87,12 +90,12 @@ DIP_DEV void pairs_of(const uint4 X[4], uint32_t xp[4][4], float& bias) {
 
 }  // namespace
 
-// XL = 1: the workgroup stages x pairs in LDS (needs chunks <= 256): the
+// XL >= 1: the workgroup stages x pairs in LDS (needs chunks <= 256): the
 // four 128-bit pair words of chunk l + LPR*c sit at 16-byte slot
 // (c*4 + q)*LPR + l, so the LPR lanes of a group read consecutive 16 B (no
 // bank conflicts; the other groups of the wave read the same addresses, a
-// broadcast); then [chunks] biases.  XL = 0: each lane keeps its CH chunks'
-// pairs in VGPRs.
+// broadcast); then [chunks] biases.  XL = 0 and XL = 2: each lane keeps its
+// CH chunks' pairs in VGPRs.
 template <int LPR, int CH, int SRC, int EPI, int XL, int D, int ROWS>
 __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   static_assert(ROWS <= LPR && D >= 1 && D <= ROWS, "rows per group");
@@ -134,8 +137,9 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
     load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups, ring[d]);
 
   // 4. x pairs
-  uint32_t xp[XL ? 1 : CH][4][4];
-  float bias[XL ? 1 : CH];
+  constexpr bool kXRegs = XL != 1;
+  uint32_t xp[kXRegs ? CH : 1][4][4];
+  float bias[kXRegs ? CH : 1];
   if (XL) {
     if ((int)threadIdx.x < nchunks) {
       uint32_t p[4][4];
@@ -149,9 +153,24 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
       reinterpret_cast<float*>(xlds + nchunks * 16)[threadIdx.x] = b;
     }
     __syncthreads();
+    if (XL == 2) {
+      const uint4* src = reinterpret_cast<const uint4*>(xlds);
+#pragma unroll
+      for (int c = 0; c < (kXRegs ? CH : 1); ++c) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint4 v = src[(c * 4 + q) * LPR + l];
+          xp[c][q][0] = v.x;
+          xp[c][q][1] = v.y;
+          xp[c][q][2] = v.z;
+          xp[c][q][3] = v.w;
+        }
+        bias[c] = reinterpret_cast<const float*>(xlds + nchunks * 16)[l + LPR * c];
+      }
+    }
   } else {
 #pragma unroll
-    for (int c = 0; c < (XL ? 1 : CH); ++c) pairs_of(&xs[4 * c], xp[c], bias[c]);
+    for (int c = 0; c < (XL ? 1 : CH); ++c) pairs_of(&xs[4 * c], xp[kXRegs ? c : 0], bias[kXRegs ? c : 0]);
   }
 
   // 5. rows
@@ -163,7 +182,7 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       float t;
-      if (XL) {
+      if (!kXRegs) {
         const int chunk = l + LPR * c;
         const uint4* src = reinterpret_cast<const uint4*>(xlds);
         uint32_t p[4][4];
@@ -178,11 +197,12 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
         t = dot8_nibbles(R.w[c].z, p[2], t);
         t = dot8_nibbles(R.w[c].w, p[3], t);
       } else {
-        t = bias[XL ? 0 : c];
-        t = dot8_nibbles(R.w[c].x, xp[XL ? 0 : c][0], t);
-        t = dot8_nibbles(R.w[c].y, xp[XL ? 0 : c][1], t);
-        t = dot8_nibbles(R.w[c].z, xp[XL ? 0 : c][2], t);
-        t = dot8_nibbles(R.w[c].w, xp[XL ? 0 : c][3], t);
+        const int cr = kXRegs ? c : 0;
+        t = bias[cr];
+        t = dot8_nibbles(R.w[c].x, xp[cr][0], t);
+        t = dot8_nibbles(R.w[c].y, xp[cr][1], t);
+        t = dot8_nibbles(R.w[c].z, xp[cr][2], t);
+        t = dot8_nibbles(R.w[c].w, xp[cr][3], t);
       }
       acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
     }
@@ -241,7 +261,15 @@ int launch_one(const RowdotArgs& a, hipStream_t stream) {
   const int depth = tuning(DIP_TUNE_ROWDOT_DEPTH) >= 4 ? 4 : 2;
   constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5);
   if constexpr (hot) {
-    if (tuning(DIP_TUNE_ROWDOT_X_LDS)) {
+    const int xl = tuning(DIP_TUNE_ROWDOT_X_LDS);
+    if (xl == 2) {
+      if (rows == 1) launch_variant<LPR, CH, SRC, EPI, 2, 1, 1>(a, stream);
+      else if (rows == 2) launch_variant<LPR, CH, SRC, EPI, 2, 2, 2>(a, stream);
+      else if (rows == 4 && depth == 4) launch_variant<LPR, CH, SRC, EPI, 2, 4, 4>(a, stream);
+      else if (rows == 4) launch_variant<LPR, CH, SRC, EPI, 2, 2, 4>(a, stream);
+      else if (depth == 4) launch_variant<LPR, CH, SRC, EPI, 2, 4, 8>(a, stream);
+      else launch_variant<LPR, CH, SRC, EPI, 2, 2, 8>(a, stream);
+    } else if (xl == 1) {
       if (rows == 1) launch_variant<LPR, CH, SRC, EPI, 1, 1, 1>(a, stream);
       else if (rows == 2) launch_variant<LPR, CH, SRC, EPI, 1, 2, 2>(a, stream);
       else if (rows == 4 && depth == 4) launch_variant<LPR, CH, SRC, EPI, 1, 4, 4>(a, stream);

@@ -118,8 +118,8 @@ int dip_up_gather_h(const int8_t* qweight, const uint16_t* scales, const uint16_
  * transposed down matrix down_t [rows, out_features/2]; row_j = indices[j],
  * or j when indices == NULL (the staged-copy layout of the reference).
  * Deterministic: fp32 partial sums over fixed blocks of 256 positions
- * reduced in a fixed order, no float atomics.  k <= 131072; the workspace
- * holds ceil(k/256) * out_features fp32 partials.
+ * reduced in a fixed order by a second launch, no float atomics.
+ * k <= 131072; the workspace holds ceil(k/256) * out_features fp32 partials.
  * Replaces int4_down_ops::int4_gather_down
  * (kernels/int4_down/int4_gather_down.cu:77-102).
  */
@@ -133,35 +133,20 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  * Launch tuning, no counterpart in the reference (process-wide, host side;
  * speed only):
  *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 2)
- *   DIP_TUNE_DOWN_LPR           lanes per row segment in the down kernel:
- *                               32/16/8/4, 0 = widest that divides (8)
- *   DIP_TUNE_DOWN_BLOCKS        reserved: accepted, no effect (the down
- *                               kernel's row blocks are 256 positions)
- *   DIP_TUNE_DOWN_DEQUANT       0: v_cvt_f32_ubyte + bias removal,
- *                               1: v_cvt_off_f32_i4 via SDWA (default 1)
- *   DIP_TUNE_DOWN_UNROLL        rows in flight per lane in the down kernel,
- *                               2/4/8 (8)
- *   DIP_TUNE_ROWDOT_X_LDS       gate/up keep x in LDS (1) or in VGPRs (0) (1)
+ *   DIP_TUNE_ROWDOT_X_LDS       gate/up x pairs: 0 built per lane in VGPRs, 1 staged
+ *                               in LDS and re-read per row, 2 staged in LDS then
+ *                               held in VGPRs (2)
  *   DIP_TUNE_ROWDOT_DEPTH       rows of loads in flight per row group, 2..4 (2)
- *   DIP_TUNE_DOWN_CPL           16-byte chunks per lane per row in the down
- *                               kernel, 1 or 2 (1)
  *   DIP_TUNE_TOPK_STAMPS        1: the top-k records wall-clock phase stamps
  *                               in its workspace (diagnostics, slower) (0)
- * The down tiling fixes the fp32 summation order, so changing it may move y
- * by an ulp; for a fixed setting results are identical run to run.
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
-  DIP_TUNE_DOWN_LPR = 1,
-  DIP_TUNE_DOWN_BLOCKS = 2,
-  DIP_TUNE_DOWN_DEQUANT = 3,
-  DIP_TUNE_DOWN_UNROLL = 4,
-  DIP_TUNE_ROWDOT_X_LDS = 5,
-  DIP_TUNE_ROWDOT_DEPTH = 6,
-  DIP_TUNE_DOWN_CPL = 7,
-  DIP_TUNE_TOPK_STAMPS = 8,
-  DIP_TUNE_COUNT = 9
+  DIP_TUNE_ROWDOT_X_LDS = 1,
+  DIP_TUNE_ROWDOT_DEPTH = 2,
+  DIP_TUNE_TOPK_STAMPS = 3,
+  DIP_TUNE_COUNT = 4
 };
 int dip_set_tuning(int knob, int value);
 int dip_get_tuning(int knob);

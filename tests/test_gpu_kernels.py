@@ -126,41 +126,30 @@ def test_up_gather_h_is_bf16_of_g_times_u(K):
     assert np.array_equal(h, O.h_bf16(g[idx], u))
 
 
-@pytest.mark.parametrize("mode", [0, 1])
-def test_gather_down_reference_shape(K, mode):
+def test_gather_down_reference_shape(K):
     """kernels/int4_down/test_down.py:31-54 shape: k=15360 rows, out=5120."""
-    old = K.get_tuning("down_dequant")
-    K.set_down_dequant_mode(mode)
-    try:
-        rng = np.random.default_rng(2)
-        k, out_f = 15360, 5120
-        qw, sc = random_int4(rng, k, out_f)
-        h = random_bf16(rng, k)
-        y = host_bf16(K.int4_gather_down(dev(qw), dev_bf16(sc), dev_bf16(h)))
-        ref = O.down_f64(qw, sc, h)
-        assert rel_err(y, ref) < 1e-2
-        assert_fp32_close(y, ref, down_abs_terms(qw, sc, h))
-    finally:
-        K.set_down_dequant_mode(old)
+    rng = np.random.default_rng(2)
+    k, out_f = 15360, 5120
+    qw, sc = random_int4(rng, k, out_f)
+    h = random_bf16(rng, k)
+    y = host_bf16(K.int4_gather_down(dev(qw), dev_bf16(sc), dev_bf16(h)))
+    ref = O.down_f64(qw, sc, h)
+    assert rel_err(y, ref) < 1e-2
+    assert_fp32_close(y, ref, down_abs_terms(qw, sc, h))
 
 
-@pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("rows,k,out_f", [(25600, 15360, 5120), (12288, 7373, 4096),
-                                          (1024, 100, 2560), (300, 3, 128), (64, 64, 256)])
-def test_gather_down_indexed(K, mode, rows, k, out_f):
-    old = K.get_tuning("down_dequant")
-    K.set_down_dequant_mode(mode)
-    try:
-        rng = np.random.default_rng(rows + k)
-        qw, sc = random_int4(rng, rows, out_f)
-        idx = rng.permutation(rows)[:k].astype(np.int32)
-        h = random_bf16(rng, k)
-        y = host_bf16(K.int4_gather_down(dev(qw), dev_bf16(sc), dev_bf16(h), dev(idx)))
-        ref = O.down_f64(qw, sc, h, rows=idx)
-        assert rel_err(y, ref) < 1e-2
-        assert_fp32_close(y, ref, down_abs_terms(qw, sc, h, rows=idx))
-    finally:
-        K.set_down_dequant_mode(old)
+                                          (1024, 100, 2560), (300, 3, 128), (64, 64, 256),
+                                          (40000, 33000, 384)])
+def test_gather_down_indexed(K, rows, k, out_f):
+    rng = np.random.default_rng(rows + k)
+    qw, sc = random_int4(rng, rows, out_f)
+    idx = rng.permutation(rows)[:k].astype(np.int32)
+    h = random_bf16(rng, k)
+    y = host_bf16(K.int4_gather_down(dev(qw), dev_bf16(sc), dev_bf16(h), dev(idx)))
+    ref = O.down_f64(qw, sc, h, rows=idx)
+    assert rel_err(y, ref) < 1e-2
+    assert_fp32_close(y, ref, down_abs_terms(qw, sc, h, rows=idx))
 
 
 def test_down_deterministic(K):
