@@ -26,68 +26,24 @@
 // (A last-arriving-block reduce inside the partial kernel was measured and
 // dropped: the 64 arrivals on each column block's device-scope counter
 // serialise and cost more than the second launch.)
-#include "dip_common.h"
-#include "dip_internal.h"
+#include "dip_tiles.h"
 
 namespace dip {
 
 namespace {
-constexpr int kThreads = 256;
+constexpr int kThreads = kDownThreads;
 constexpr int kRowsPerBlock = kThreads;  // 256/LPR slots x LPR rows each
 constexpr int kXcds = 8;                 // MI355X: 8 XCDs, workgroups dispatched round-robin
-constexpr uint32_t kBadRow = 0xFFFFFFFFu;  // out-of-range id: poisons y with NaN
-constexpr uint32_t kPadRow = 0xFFFFFFFEu;  // position past k: contributes 0
-constexpr uint32_t kSrcB = 0x80000000u;
-constexpr int kAcc = kChunkCols;         // outputs per lane: one 16-byte chunk
 constexpr int kMaxRowBlocks = 512;       // k <= 131072
 constexpr int kRedOut = 64;              // outputs per reduce block
 constexpr int kRedSplit = 4;             // interleaved row-block splits per output
 }  // namespace
 
-// Row id for position j (j < k); kBadRow if out of range.  Branch-free.
-template <int SRC>
-DIP_DEV uint32_t down_row(const DownArgs& a, int j) {
-  if (SRC == kContig) return (unsigned)j < (unsigned)a.rows_a ? (uint32_t)j : kBadRow;
-  if (SRC == kGather) {
-    const int r = a.sel[j];
-    return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
-  }
-  const int r = a.sel2[j];
-  const bool b = a.sel[j] != 0;
-  const bool ok = b ? (unsigned)r < (unsigned)a.rows_b : (unsigned)r < (unsigned)a.rows_a;
-  return ok ? ((uint32_t)r | (b ? kSrcB : 0u)) : kBadRow;
-}
-
-template <int CPL>
-struct DownRow {
-  uint4 w[CPL];
-  uint32_t s;  // bf16 scale of the lane's group
-};
-
-// Unconditional loads of a lane's CPL chunks and scale of one row (bad and
-// padding ids read row 0 of the safe matrix).
-template <int CPL, int SRC>
-DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, int cc0, size_t row_bytes,
-                           int ngroups, DownRow<CPL>& R) {
-  const bool bad = rid >= kPadRow;
-  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
-  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
-  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
-  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
-  const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes) + cc0;
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) R.w[c] = ldg_nt(wr + c);
-  R.s = sc[(size_t)r * ngroups + cc0 / kChunksPerGroup];
-}
-
 template <int LPR, int SRC>
 __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
-  constexpr int D = LPR;                // every row of a slot in flight at once
   constexpr int kSlots = kThreads / LPR;
-  constexpr int kHalf = kAcc / 2;
-  constexpr int kStride = kHalf + 1;    // padded LDS rows: conflict-free both ways
-  constexpr int kCols = LPR * kAcc;     // outputs per column block
-  __shared__ float red[kSlots * LPR * kStride];
+  constexpr int kCols = LPR * kDownAcc;  // outputs per column block
+  __shared__ float red[down_red_floats<LPR>()];
 
   // XCD-aware tile order: workgroups go to the 8 XCDs round-robin, so tile
   // (rb, cb) runs as workgroup b with b % 8 == rb % 8.  All column blocks of
@@ -104,82 +60,25 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   const int cc0 = cb * LPR + l;  // my chunk within a row
   const size_t row_bytes = (size_t)(a.out_features >> 1);
   const int ngroups = a.out_features >> 7;
-  const int j0 = rb * kRowsPerBlock + slot;
 
   // lane l: id and h of the slot's row l (position clamped; past k -> kPadRow)
-  const int jl = j0 + l * kSlots;
+  const int jl = rb * kRowsPerBlock + slot + l * kSlots;
   const int jc = min(jl, a.k - 1);
   const uint32_t rid_c = down_row<SRC>(a, jc);
   const uint32_t rid_l = jl < a.k ? rid_c : kPadRow;
   const uint32_t h_l = a.h[jc];
 
-  DownRow<1> ring[D];
+  DownRow ring[LPR];
 #pragma unroll
-  for (int d = 0; d < D; ++d)
-    load_down_row<1, SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ngroups, ring[d]);
+  for (int d = 0; d < LPR; ++d)
+    load_down_row<SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ngroups, ring[d]);
 
-  float acc[kAcc];
+  float acc[kDownAcc];
 #pragma unroll
-  for (int m = 0; m < kAcc; ++m) acc[m] = 0.f;
-
-#pragma unroll
-  for (int i = 0; i < LPR; ++i) {
-    const DownRow<1>& R = ring[i];
-    const uint32_t rid = __shfl(rid_l, gbase + i, 64);
-    const uint32_t hb = __shfl(h_l, gbase + i, 64);
-    // f = 16*h*s, 0 for padding, NaN for a bad id: integer selects on the
-    // bits keep this branch-free (a branch here sinks the scale load into it
-    // and costs a full vmcnt(0) wait)
-    uint32_t fb = __float_as_uint(bf16_to_f32(hb) * bf16_to_f32(R.s) * 16.0f);
-    fb = rid == kPadRow ? 0u : fb;
-    fb = rid == kBadRow ? 0x7FC00000u : fb;
-    const float f16 = __uint_as_float(fb);
-    const uint32_t wv[4] = {R.w[0].x, R.w[0].y, R.w[0].z, R.w[0].w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t hi = wv[q] >> 4;
-      acc[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, acc[8 * q + 0]);
-      acc[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, acc[8 * q + 1]);
-      acc[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, acc[8 * q + 2]);
-      acc[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, acc[8 * q + 3]);
-      acc[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, acc[8 * q + 4]);
-      acc[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, acc[8 * q + 5]);
-      acc[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, acc[8 * q + 6]);
-      acc[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, acc[8 * q + 7]);
-    }
-    // Keep each row's conversions next to their FMAs: left free, the
-    // scheduler hoists every row's conversions ahead of the FMAs and needs
-    // over 140 VGPRs (three blocks per CU instead of five).
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  // Slots summed in a fixed order, 16 accumulators at a time (written out
-  // twice: as a loop over the halves the compiler keeps both halves' sums in
-  // flight and needs 170 VGPRs); column l*32 + m of the block sits at
-  // red[(slot*LPR + l)*kStride + m - half]
-  float* out = a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols;
-  float* mine = red + (slot * LPR + l) * kStride;
-#pragma unroll
-  for (int m = 0; m < kHalf; ++m) mine[m] = acc[m];
-  __syncthreads();
-  for (int e = threadIdx.x; e < LPR * kHalf; e += kThreads) {
-    const int ln = e / kHalf, m = e % kHalf;
-    float s = 0.f;
-#pragma unroll 8
-    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
-    out[ln * kAcc + m] = s;
-  }
-  __syncthreads();  // the first half's reads are done
-#pragma unroll
-  for (int m = 0; m < kHalf; ++m) mine[m] = acc[kHalf + m];
-  __syncthreads();
-  for (int e = threadIdx.x; e < LPR * kHalf; e += kThreads) {
-    const int ln = e / kHalf, m = e % kHalf;
-    float s = 0.f;
-#pragma unroll 8
-    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
-    out[ln * kAcc + kHalf + m] = s;
-  }
+  for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
+  down_accumulate<LPR>(ring, rid_l, h_l, gbase, acc);
+  down_block_partial<LPR, false>(acc, red, a.partial + (size_t)rb * a.out_features +
+                                               (size_t)cb * kCols, slot, l);
 }
 
 // y[o] = bf16(sum over row blocks rb of partial[rb][o]), rb ascending in four

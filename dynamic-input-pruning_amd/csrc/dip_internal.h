@@ -94,6 +94,7 @@ int64_t down_max_k();  // largest k the down path accepts
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
                        hipStream_t stream);
 
+
 // Launch tuning (process-wide, host side): see DIP_TUNE_* in dip_hip.h.
 int tuning(int knob);
 // Compute units of the current device (cached per device).

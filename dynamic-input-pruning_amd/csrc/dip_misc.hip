@@ -253,13 +253,17 @@ extern "C" int dip_host_gather_rows(const void* src, const int32_t* ids, void* d
 
 // ---------------------------------------------------------------------------
 // One resident DIP MLP decode step.
+//   workspace: [0, 512) top-k state | down partials
 // ---------------------------------------------------------------------------
 namespace {
+constexpr size_t kMlpTopkBytes = 512;
+static_assert(kTopkWorkspace <= kMlpTopkBytes, "top-k state");
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
 
 extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k) {
-  return align256(dip_topk_workspace_size(inter)) + align256(down_workspace_bytes(k, hidden));
+  (void)inter;
+  return kMlpTopkBytes + align256(down_workspace_bytes(k, hidden));
 }
 
 extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
@@ -273,15 +277,13 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
   if (k > 0 && (!idx_out || !h_out)) return DIP_ERR_NULL;
   if (!workspace || ws_bytes < dip_mlp_workspace_size(hidden, inter, k)) return DIP_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
-  const size_t topk_bytes = align256(dip_topk_workspace_size(inter));
-  void* ws_topk = ws;
-  void* ws_down = ws + topk_bytes;
-  const size_t down_bytes = ws_bytes - topk_bytes;
-  int st = dip_gate_silu_topk(gate_qw, gate_sc, x, g_out, idx_out, inter, hidden, k, ws_topk,
-                              topk_bytes, stream);
+  int st = dip_gate_silu_topk(gate_qw, gate_sc, x, g_out, idx_out, inter, hidden, k, ws,
+                              kMlpTopkBytes, stream);
   if (st) return st;
-  st = dip_up_gather_h(up_qw, up_sc, x, idx_out, g_out, h_out, inter, hidden, k, stream);
-  if (st) return st;
-  return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k, ws_down,
-                              down_bytes, stream);
+  if (k > 0) {
+    st = dip_up_gather_h(up_qw, up_sc, x, idx_out, g_out, h_out, inter, hidden, k, stream);
+    if (st) return st;
+  }
+  return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k,
+                              ws + kMlpTopkBytes, ws_bytes - kMlpTopkBytes, stream);
 }

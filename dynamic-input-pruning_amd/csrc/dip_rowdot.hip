@@ -1,94 +1,25 @@
 // dip_rowdot.hip — int4 g128 row-dot kernels: gate GEMV (+SiLU), up-row gather
 // GEMV (+ fused h = g[idx] * u) and the cache-aware dual-source variant.
 //
-// Mapping (one design for every row source):
-//   * LPR lanes ("a row group", a power of two dividing 64) own one row at a
-//     time; lane l of the group owns chunks l, l+LPR, ..., l+(CH-1)*LPR of the
-//     row, so a row of in_features/2 bytes = LPR*CH*16 bytes is read with CH
-//     128-bit loads per lane, each instruction covering LPR*16 contiguous
-//     bytes per group (fully coalesced).
-//   * A group handles ROWS outputs j = grp + i*ngrp (i < ROWS), ROWS a
-//     compile-time constant, so the row loop is straight-line code: every
-//     load is unconditional (row indices past the end are clamped, bad row
-//     ids read a designated safe row and are poisoned in the epilogue) and
-//     the compiler can wait for exactly the row it consumes (s_waitcnt
+// Mapping (one design for every row source; the row-group layout and the x
+// pairs are described in dip_tiles.h):
+//   * A group of LPR lanes handles ROWS outputs j = grp + i*ngrp (i < ROWS),
+//     ROWS a compile-time constant, so the row loop is straight-line code:
+//     every load is unconditional (row indices past the end are clamped, bad
+//     row ids read a designated safe row and are poisoned in the epilogue)
+//     and the compiler can wait for exactly the row it consumes (s_waitcnt
 //     vmcnt(N) with N > 0) while the next D-1 rows stay in flight.  Loads
 //     under data-dependent branches would make it wait for everything.
-//   * x is pre-paired for v_dot2_f32_bf16 with the per-chunk bias term (see
-//     dip_common.h) and its loads are issued before the row loads.  XL=0:
-//     each lane builds its CH chunks' pairs in VGPRs from global memory;
-//     XL=1: the workgroup stages all pairs once in LDS and every row re-reads
-//     them from LDS; XL=2: staged in LDS once, then each lane copies its CH
-//     chunks' pairs into VGPRs, so the row loop touches no LDS.
+//   * x pairs: XL=0: each lane builds its CH chunks' pairs in VGPRs from
+//     global memory; XL=1: the workgroup stages all pairs once in LDS and
+//     every row re-reads them from LDS; XL=2: staged in LDS once, then each
+//     lane copies its CH chunks' pairs into VGPRs, so the row loop touches no
+//     LDS.  The x loads are issued before the row loads.
 //   * The group reduction is DPP + permlane swaps (group_sum); lane l keeps
 //     the sum of row l and runs the epilogue for it.
-#include "dip_common.h"
-#include "dip_internal.h"
+#include "dip_tiles.h"
 
 namespace dip {
-
-namespace {
-
-constexpr uint32_t kBadRow = 0xFFFFFFFFu;
-constexpr uint32_t kSrcB = 0x80000000u;
-
-// Row id for output j (j < nrows): bit 31 selects matrix B (kDual); kBadRow
-// if the id is out of range.  Branch-free (the id loads are unconditional).
-template <int SRC>
-DIP_DEV uint32_t resolve_row(const RowdotArgs& a, int j) {
-  if (SRC == kContig) return (uint32_t)j;
-  if (SRC == kGather) {
-    const int r = a.sel[j];
-    return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
-  }
-  const int r = a.sel2[j];
-  const bool b = a.sel[j] != 0;
-  const bool ok = b ? (unsigned)r < (unsigned)a.rows_b : (unsigned)r < (unsigned)a.rows_a;
-  return ok ? ((uint32_t)r | (b ? kSrcB : 0u)) : kBadRow;
-}
-
-template <int CH>
-struct RowRegs {
-  uint4 w[CH];
-  uint32_t s[CH];
-};
-
-// Unconditional loads of one row's CH chunks and scales (a bad id reads row
-// 0 of the safe matrix).
-template <int LPR, int CH, int SRC>
-DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes, int ngroups,
-                      RowRegs<CH>& R) {
-  const bool bad = rid == kBadRow;
-  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
-  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
-  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
-  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
-  const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes);
-  const uint16_t* sr = sc + (size_t)r * ngroups;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int chunk = l + LPR * c;
-    R.w[c] = ldg_nt(wr + chunk);
-    R.s[c] = sr[chunk / kChunksPerGroup];
-  }
-}
-
-// x pairs + bias for one chunk (32 columns starting at 32*chunk), from the
-// four 128-bit words of x that cover it.
-DIP_DEV void pairs_of(const uint4 X[4], uint32_t xp[4][4], float& bias) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    make_xpairs(X[i].x, X[i].y, X[i].z, X[i].w, xp[i]);
-    s += bf16_to_f32(X[i].x & 0xFFFFu) + bf16_to_f32(X[i].x >> 16) +
-         bf16_to_f32(X[i].y & 0xFFFFu) + bf16_to_f32(X[i].y >> 16) +
-         bf16_to_f32(X[i].z & 0xFFFFu) + bf16_to_f32(X[i].z >> 16) +
-         bf16_to_f32(X[i].w & 0xFFFFu) + bf16_to_f32(X[i].w >> 16);
-  }
-  bias = -kPairBias * s;
-}
-
-}  // namespace
 
 // XL >= 1: the workgroup stages x pairs in LDS (needs chunks <= 256): the
 // four 128-bit pair words of chunk l + LPR*c sit at 16-byte slot
@@ -112,10 +43,7 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   // 1. x loads first (XL: one chunk per thread, index clamped)
   uint4 xs[XL ? 4 : CH * 4];
   if (XL) {
-    const int c = min((int)threadIdx.x, nchunks - 1);
-    const uint4* src = reinterpret_cast<const uint4*>(a.x) + c * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xs[i] = src[i];
+    load_x_chunk(a.x, nchunks, xs);
   } else {
 #pragma unroll
     for (int c = 0; c < (XL ? 1 : CH); ++c) {
@@ -141,36 +69,12 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   uint32_t xp[kXRegs ? CH : 1][4][4];
   float bias[kXRegs ? CH : 1];
   if (XL) {
-    if ((int)threadIdx.x < nchunks) {
-      uint32_t p[4][4];
-      float b;
-      pairs_of(xs, p, b);
-      const int lc = threadIdx.x % LPR, cc = threadIdx.x / LPR;
-      uint4* dst = reinterpret_cast<uint4*>(xlds);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dst[(cc * 4 + i) * LPR + lc] = make_uint4(p[i][0], p[i][1], p[i][2], p[i][3]);
-      reinterpret_cast<float*>(xlds + nchunks * 16)[threadIdx.x] = b;
-    }
-    __syncthreads();
-    if (XL == 2) {
-      const uint4* src = reinterpret_cast<const uint4*>(xlds);
-#pragma unroll
-      for (int c = 0; c < (kXRegs ? CH : 1); ++c) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint4 v = src[(c * 4 + q) * LPR + l];
-          xp[c][q][0] = v.x;
-          xp[c][q][1] = v.y;
-          xp[c][q][2] = v.z;
-          xp[c][q][3] = v.w;
-        }
-        bias[c] = reinterpret_cast<const float*>(xlds + nchunks * 16)[l + LPR * c];
-      }
-    }
+    stage_x_pairs<LPR>(xs, xlds, nchunks);
+    if constexpr (XL == 2) x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
   } else {
 #pragma unroll
-    for (int c = 0; c < (XL ? 1 : CH); ++c) pairs_of(&xs[4 * c], xp[kXRegs ? c : 0], bias[kXRegs ? c : 0]);
+    for (int c = 0; c < (XL ? 1 : CH); ++c)
+      pairs_of(&xs[4 * c], xp[kXRegs ? c : 0], bias[kXRegs ? c : 0]);
   }
 
   // 5. rows
@@ -178,11 +82,13 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
     RowRegs<CH>& R = ring[i % D];
-    float acc = 0.f;
+    float acc;
+    if constexpr (kXRegs) {
+      acc = row_dot_part<CH>(R, xp, bias);
+    } else {
+      acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      float t;
-      if (!kXRegs) {
+      for (int c = 0; c < CH; ++c) {
         const int chunk = l + LPR * c;
         const uint4* src = reinterpret_cast<const uint4*>(xlds);
         uint32_t p[4][4];
@@ -191,20 +97,13 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
           const uint4 v = src[(c * 4 + q) * LPR + l];
           p[q][0] = v.x; p[q][1] = v.y; p[q][2] = v.z; p[q][3] = v.w;
         }
-        t = reinterpret_cast<const float*>(xlds + nchunks * 16)[chunk];
+        float t = reinterpret_cast<const float*>(xlds + nchunks * 16)[chunk];
         t = dot8_nibbles(R.w[c].x, p[0], t);
         t = dot8_nibbles(R.w[c].y, p[1], t);
         t = dot8_nibbles(R.w[c].z, p[2], t);
         t = dot8_nibbles(R.w[c].w, p[3], t);
-      } else {
-        const int cr = kXRegs ? c : 0;
-        t = bias[cr];
-        t = dot8_nibbles(R.w[c].x, xp[cr][0], t);
-        t = dot8_nibbles(R.w[c].y, xp[cr][1], t);
-        t = dot8_nibbles(R.w[c].z, xp[cr][2], t);
-        t = dot8_nibbles(R.w[c].w, xp[cr][3], t);
+        acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
       }
-      acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
     }
     acc = group_sum<LPR>(acc);
     mine = l == i ? acc : mine;
@@ -241,7 +140,7 @@ void launch_variant(RowdotArgs a, hipStream_t stream) {
   a.ngrp = (a.nrows + ROWS - 1) / ROWS;
   const int gpb = 256 / LPR;
   const int blocks = (a.ngrp + gpb - 1) / gpb;
-  const size_t lds = XL ? (size_t)(a.in_features / kChunkCols) * 17 * sizeof(uint32_t) : 0;
+  const size_t lds = XL ? x_pairs_lds_bytes(a.in_features) : 0;
   hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XL, D, ROWS>), dim3(blocks), dim3(256),
                      lds, stream, a);
 }

@@ -1,0 +1,287 @@
+// dip_tiles.h — device building blocks shared by the row-dot kernels (gate,
+// up), the down kernels and the fused up+down launch.
+//
+// Row dot (one output per weight row, reduced across the row):
+//   LPR lanes ("a row group") own one row at a time; lane l of the group owns
+//   chunks l, l+LPR, ..., l+(CH-1)*LPR of the row (16 bytes = 32 columns
+//   each), so every load instruction covers LPR*16 contiguous bytes of the
+//   row.  x is pre-paired for v_dot2_f32_bf16 with a per-chunk bias term (see
+//   dip_common.h); a workgroup stages the pairs of all chunks in LDS once and
+//   each lane then copies its own CH chunks into VGPRs.
+//
+// Down (outputs along the row, reduced across rows):
+//   LPR lanes ("a slot") each own one 16-byte chunk (32 outputs) of every row
+//   the slot walks; a block of 256 threads holds 256/LPR slots that walk the
+//   LPR rows j = j0 + slot + i*(256/LPR).  Lane l of a slot holds the id and
+//   h of the slot's row l; each row's id and h are shuffled to the slot when
+//   it comes up.  All LPR rows of a slot are loaded before any is consumed.
+#pragma once
+
+#include "dip_common.h"
+#include "dip_internal.h"
+
+namespace dip {
+
+constexpr uint32_t kBadRow = 0xFFFFFFFFu;  // out-of-range id: the output becomes NaN
+constexpr uint32_t kPadRow = 0xFFFFFFFEu;  // down position past k: contributes 0
+constexpr uint32_t kSrcB = 0x80000000u;    // dual-source row id: bit 31 selects matrix B
+
+// ---------------------------------------------------------------------------
+// Row dot
+// ---------------------------------------------------------------------------
+
+// Row id for output j (j < nrows): bit 31 selects matrix B (kDual); kBadRow
+// if the id is out of range.  Branch-free (the id loads are unconditional).
+template <int SRC>
+DIP_DEV uint32_t resolve_row(const RowdotArgs& a, int j) {
+  if (SRC == kContig) return (uint32_t)j;
+  if (SRC == kGather) {
+    const int r = a.sel[j];
+    return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
+  }
+  const int r = a.sel2[j];
+  const bool b = a.sel[j] != 0;
+  const bool ok = b ? (unsigned)r < (unsigned)a.rows_b : (unsigned)r < (unsigned)a.rows_a;
+  return ok ? ((uint32_t)r | (b ? kSrcB : 0u)) : kBadRow;
+}
+
+template <int CH>
+struct RowRegs {
+  uint4 w[CH];
+  uint32_t s[CH];
+};
+
+// Unconditional loads of one row's CH chunks and scales (a bad id reads row
+// 0 of the safe matrix).
+template <int LPR, int CH, int SRC>
+DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes, int ngroups,
+                      RowRegs<CH>& R) {
+  const bool bad = rid == kBadRow;
+  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
+  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
+  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
+  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
+  const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes);
+  const uint16_t* sr = sc + (size_t)r * ngroups;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int chunk = l + LPR * c;
+    R.w[c] = ldg_nt(wr + chunk);
+    R.s[c] = sr[chunk / kChunksPerGroup];
+  }
+}
+
+// x pairs + bias for one chunk (32 columns starting at 32*chunk), from the
+// four 128-bit words of x that cover it.
+DIP_DEV void pairs_of(const uint4 X[4], uint32_t xp[4][4], float& bias) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    make_xpairs(X[i].x, X[i].y, X[i].z, X[i].w, xp[i]);
+    s += bf16_to_f32(X[i].x & 0xFFFFu) + bf16_to_f32(X[i].x >> 16) +
+         bf16_to_f32(X[i].y & 0xFFFFu) + bf16_to_f32(X[i].y >> 16) +
+         bf16_to_f32(X[i].z & 0xFFFFu) + bf16_to_f32(X[i].z >> 16) +
+         bf16_to_f32(X[i].w & 0xFFFFu) + bf16_to_f32(X[i].w >> 16);
+  }
+  bias = -kPairBias * s;
+}
+
+// LDS bytes for the staged x pairs of a row of `in_features` columns.
+constexpr size_t x_pairs_lds_bytes(int in_features) {
+  return (size_t)(in_features / kChunkCols) * 17 * sizeof(uint32_t);
+}
+
+// x loads for the staging step: thread t < nchunks loads chunk t (four
+// 128-bit words; the index is clamped so every thread loads).
+DIP_DEV void load_x_chunk(const uint16_t* x, int nchunks, uint4 xs[4]) {
+  const int c = min((int)threadIdx.x, nchunks - 1);
+  const uint4* src = reinterpret_cast<const uint4*>(x) + c * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xs[i] = src[i];
+}
+
+// Stage the pairs of every chunk in LDS: the four 128-bit pair words of chunk
+// l + LPR*c sit at 16-byte slot (c*4 + q)*LPR + l, so the LPR lanes of a
+// group read consecutive 16 B (no bank conflicts; the other groups of the
+// wave read the same addresses, a broadcast); then [nchunks] biases.
+// Needs nchunks <= blockDim.x; ends with a block barrier.
+template <int LPR>
+DIP_DEV void stage_x_pairs(const uint4 xs[4], uint32_t* xlds, int nchunks) {
+  if ((int)threadIdx.x < nchunks) {
+    uint32_t p[4][4];
+    float b;
+    pairs_of(xs, p, b);
+    const int lc = threadIdx.x % LPR, cc = threadIdx.x / LPR;
+    uint4* dst = reinterpret_cast<uint4*>(xlds);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dst[(cc * 4 + i) * LPR + lc] = make_uint4(p[i][0], p[i][1], p[i][2], p[i][3]);
+    reinterpret_cast<float*>(xlds + nchunks * 16)[threadIdx.x] = b;
+  }
+  __syncthreads();
+}
+
+// Lane l's CH chunks of staged pairs and biases, into VGPRs.
+template <int LPR, int CH>
+DIP_DEV void x_pairs_to_regs(const uint32_t* xlds, int nchunks, int l, uint32_t xp[CH][4][4],
+                             float bias[CH]) {
+  const uint4* src = reinterpret_cast<const uint4*>(xlds);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = src[(c * 4 + q) * LPR + l];
+      xp[c][q][0] = v.x;
+      xp[c][q][1] = v.y;
+      xp[c][q][2] = v.z;
+      xp[c][q][3] = v.w;
+    }
+    bias[c] = reinterpret_cast<const float*>(xlds + nchunks * 16)[l + LPR * c];
+  }
+}
+
+// The lane's part of one row's dot product with x pairs in VGPRs (not yet
+// reduced across the row group).
+template <int CH>
+DIP_DEV float row_dot_part(const RowRegs<CH>& R, const uint32_t xp[CH][4][4],
+                           const float bias[CH]) {
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float t = bias[c];
+    t = dot8_nibbles(R.w[c].x, xp[c][0], t);
+    t = dot8_nibbles(R.w[c].y, xp[c][1], t);
+    t = dot8_nibbles(R.w[c].z, xp[c][2], t);
+    t = dot8_nibbles(R.w[c].w, xp[c][3], t);
+    acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
+  }
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Down
+// ---------------------------------------------------------------------------
+constexpr int kDownThreads = 256;
+constexpr int kDownAcc = kChunkCols;  // outputs per lane: one 16-byte chunk
+
+// Row id for position j (j < k); kBadRow if out of range.  Branch-free.
+template <int SRC>
+DIP_DEV uint32_t down_row(const DownArgs& a, int j) {
+  if (SRC == kContig) return (unsigned)j < (unsigned)a.rows_a ? (uint32_t)j : kBadRow;
+  if (SRC == kGather) {
+    const int r = a.sel[j];
+    return (unsigned)r < (unsigned)a.rows_a ? (uint32_t)r : kBadRow;
+  }
+  const int r = a.sel2[j];
+  const bool b = a.sel[j] != 0;
+  const bool ok = b ? (unsigned)r < (unsigned)a.rows_b : (unsigned)r < (unsigned)a.rows_a;
+  return ok ? ((uint32_t)r | (b ? kSrcB : 0u)) : kBadRow;
+}
+
+struct DownRow {
+  uint4 w;     // the lane's 16-byte chunk of the row
+  uint32_t s;  // bf16 scale of the chunk's group
+};
+
+// Unconditional loads of a lane's chunk cc0 and its scale for one row (bad
+// and padding ids read row 0 of the safe matrix).
+template <int SRC>
+DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, int cc0, size_t row_bytes,
+                           int ngroups, DownRow& R) {
+  const bool bad = rid >= kPadRow;
+  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
+  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
+  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
+  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
+  R.w = ldg_nt(reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes) + cc0);
+  R.s = sc[(size_t)r * ngroups + cc0 / kChunksPerGroup];
+}
+
+// acc[m] += (q/16)[row, 32*cc0 + m] * 16*h*s over the slot's LPR rows.
+// v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for the low
+// nibble of any byte (high nibbles after one shift): one convert and one FMA
+// per weight.  A padding row contributes 0, a bad id NaN.
+template <int LPR>
+DIP_DEV void down_accumulate(const DownRow ring[LPR], uint32_t rid_l, uint32_t h_l, int gbase,
+                             float acc[kDownAcc]) {
+#pragma unroll
+  for (int i = 0; i < LPR; ++i) {
+    const DownRow& R = ring[i];
+    const uint32_t rid = __shfl(rid_l, gbase + i, 64);
+    const uint32_t hb = __shfl(h_l, gbase + i, 64);
+    // integer selects on the bits keep this branch-free (a branch here sinks
+    // the scale load into it and costs a full vmcnt(0) wait)
+    uint32_t fb = __float_as_uint(bf16_to_f32(hb) * bf16_to_f32(R.s) * 16.0f);
+    fb = rid == kPadRow ? 0u : fb;
+    fb = rid == kBadRow ? 0x7FC00000u : fb;
+    const float f16 = __uint_as_float(fb);
+    const uint32_t wv[4] = {R.w.x, R.w.y, R.w.z, R.w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t hi = wv[q] >> 4;
+      acc[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, acc[8 * q + 0]);
+      acc[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, acc[8 * q + 1]);
+      acc[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, acc[8 * q + 2]);
+      acc[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, acc[8 * q + 3]);
+      acc[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, acc[8 * q + 4]);
+      acc[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, acc[8 * q + 5]);
+      acc[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, acc[8 * q + 6]);
+      acc[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, acc[8 * q + 7]);
+    }
+    // Keep each row's conversions next to their FMAs: left free, the
+    // scheduler hoists every row's conversions ahead of the FMAs and needs
+    // over 140 VGPRs (three blocks per CU instead of five).
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// LDS floats for the slot reduction of a block.
+template <int LPR>
+constexpr int down_red_floats() {
+  return (kDownThreads / LPR) * LPR * (kDownAcc / 2 + 1);
+}
+
+// Sum the block's slots in a fixed order, 16 accumulators at a time, and
+// store the block's LPR*32 partial sums to out[0 .. LPR*32) (coherent: with
+// device-scope stores that write through to memory).  Written out twice
+// rather than as a loop over the halves: as a loop the compiler keeps both
+// halves' sums in flight and needs 170 VGPRs.  Column l*32 + m of the block
+// sits at red[(slot*LPR + l)*kStride + m - half].
+template <int LPR, bool COHERENT>
+DIP_DEV void down_block_partial(const float acc[kDownAcc], float* red, float* out, int slot,
+                                int l) {
+  constexpr int kSlots = kDownThreads / LPR;
+  constexpr int kHalf = kDownAcc / 2;
+  constexpr int kStride = kHalf + 1;  // padded LDS rows: conflict-free both ways
+  float* mine = red + (slot * LPR + l) * kStride;
+#pragma unroll
+  for (int m = 0; m < kHalf; ++m) mine[m] = acc[m];
+  __syncthreads();
+  for (int e = threadIdx.x; e < LPR * kHalf; e += kDownThreads) {
+    const int ln = e / kHalf, m = e % kHalf;
+    float s = 0.f;
+#pragma unroll 8
+    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
+    if (COHERENT)
+      __hip_atomic_store(out + ln * kDownAcc + m, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      out[ln * kDownAcc + m] = s;
+  }
+  __syncthreads();  // the first half's reads are done
+#pragma unroll
+  for (int m = 0; m < kHalf; ++m) mine[m] = acc[kHalf + m];
+  __syncthreads();
+  for (int e = threadIdx.x; e < LPR * kHalf; e += kDownThreads) {
+    const int ln = e / kHalf, m = e % kHalf;
+    float s = 0.f;
+#pragma unroll 8
+    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
+    if (COHERENT)
+      __hip_atomic_store(out + ln * kDownAcc + kHalf + m, s, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    else
+      out[ln * kDownAcc + kHalf + m] = s;
+  }
+}
+
+}  // namespace dip

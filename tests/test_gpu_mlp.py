@@ -220,6 +220,15 @@ def test_hip_graph_replay_matches_eager(K):
             assert torch.equal(a, b), rep
 
 
+def test_step_qwen3_8b_shape(K):
+    """Config 2 layer shape (H=4096, I=12288, keep 0.6) against the oracle."""
+    print("building a Qwen3-8B-shape layer on the CPU oracle", flush=True)
+    L = O.make_layer(4096, 12288, seed=2)
+    D = _layer_to_dev(L)
+    x = O.make_x(4096, seed=4)
+    assert _check_step(K, L, D, x, O.keep_count(12288, 0.6)) < 1e-2
+
+
 def test_full_size_properties(K):
     """Config 3 shape on synthetic GPU-drawn weights: size-independent
     properties of the selection and determinism of y."""
