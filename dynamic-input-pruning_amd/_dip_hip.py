@@ -409,7 +409,7 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
     return y, g, idx, h
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "rowdot_x_lds": 1, "rowdot_depth": 2, "topk_stamps": 3}
+TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1}
 
 
 def set_tuning(name: str, value: int) -> None:

@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 2, 2, 0};
+int g_tune[DIP_TUNE_COUNT] = {2, 0};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -170,12 +170,6 @@ extern "C" int dip_set_tuning(int knob, int value) {
   switch (knob) {
     case DIP_TUNE_ROWDOT_WGS_PER_CU:
       if (value < 1 || value > 16) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_ROWDOT_X_LDS:
-      if (value < 0 || value > 2) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_ROWDOT_DEPTH:
-      if (value < 2 || value > 4) return DIP_ERR_ARG;
       break;
     case DIP_TUNE_TOPK_STAMPS:
       if (value != 0 && value != 1) return DIP_ERR_ARG;

@@ -3,33 +3,33 @@
 //
 // Mapping (one design for every row source; the row-group layout and the x
 // pairs are described in dip_tiles.h):
-//   * A group of LPR lanes handles ROWS outputs j = grp + i*ngrp (i < ROWS),
-//     ROWS a compile-time constant, so the row loop is straight-line code:
-//     every load is unconditional (row indices past the end are clamped, bad
-//     row ids read a designated safe row and are poisoned in the epilogue)
-//     and the compiler can wait for exactly the row it consumes (s_waitcnt
-//     vmcnt(N) with N > 0) while the next D-1 rows stay in flight.  Loads
-//     under data-dependent branches would make it wait for everything.
-//   * x pairs: XL=0: each lane builds its CH chunks' pairs in VGPRs from
-//     global memory; XL=1: the workgroup stages all pairs once in LDS and
-//     every row re-reads them from LDS; XL=2: staged in LDS once, then each
-//     lane copies its CH chunks' pairs into VGPRs, so the row loop touches no
-//     LDS.  The x loads are issued before the row loads.
+//   * A workgroup holds 256/LPR groups of LPR lanes; a group
+//     handles ROWS outputs j = grp + i*ngrp (i < ROWS), ROWS a compile-time
+//     constant, so the row loop is straight-line code: every load is
+//     unconditional (row indices past the end are clamped, bad row ids read a
+//     designated safe row and are poisoned in the epilogue) and the compiler
+//     can wait for exactly the row it consumes (s_waitcnt vmcnt(N) with N > 0)
+//     while the next row stays in flight.  Loads under data-dependent
+//     branches would make it wait for everything.
+//   * Workgroups are 256 threads; ROWS is the fewest of 1, 2, 4, 8 that keeps
+//     the grid at about 2 workgroups per CU (a Qwen3-32B gate: 400
+//     workgroups of 8 groups x 8 rows; its up gather: 480 of 8 x 4).
+//   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
+//     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
+//     touches no LDS; otherwise each lane builds its own pairs from global
+//     memory.  The x loads are issued before the row loads.
 //   * The group reduction is DPP + permlane swaps (group_sum); lane l keeps
 //     the sum of row l and runs the epilogue for it.
 #include "dip_tiles.h"
 
 namespace dip {
 
-// XL >= 1: the workgroup stages x pairs in LDS (needs chunks <= 256): the
-// four 128-bit pair words of chunk l + LPR*c sit at 16-byte slot
-// (c*4 + q)*LPR + l, so the LPR lanes of a group read consecutive 16 B (no
-// bank conflicts; the other groups of the wave read the same addresses, a
-// broadcast); then [chunks] biases.  XL = 0 and XL = 2: each lane keeps its
-// CH chunks' pairs in VGPRs.
-template <int LPR, int CH, int SRC, int EPI, int XL, int D, int ROWS>
-__global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
-  static_assert(ROWS <= LPR && D >= 1 && D <= ROWS, "rows per group");
+constexpr int kRowdotMaxThreads = 256;
+
+template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
+__global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a) {
+  constexpr int D = ROWS < 2 ? ROWS : 2;  // rows of loads in flight per group
+  static_assert(ROWS <= LPR, "rows per group");
   extern __shared__ uint32_t xlds[];
   const int l = threadIdx.x % LPR;
   const int lane = threadIdx.x & 63;
@@ -37,16 +37,16 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   const size_t row_bytes = (size_t)(a.in_features >> 1);
   const int ngroups = a.in_features >> 7;
   const int nchunks = a.in_features / kChunkCols;
-  const int grp = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  const int grp = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
   const int ngrp = a.ngrp;
 
-  // 1. x loads first (XL: one chunk per thread, index clamped)
-  uint4 xs[XL ? 4 : CH * 4];
-  if (XL) {
+  // 1. x loads first (XS: one chunk per thread, index clamped)
+  uint4 xs[XS ? 4 : CH * 4];
+  if constexpr (XS) {
     load_x_chunk(a.x, nchunks, xs);
   } else {
 #pragma unroll
-    for (int c = 0; c < (XL ? 1 : CH); ++c) {
+    for (int c = 0; c < CH; ++c) {
       const uint4* src = reinterpret_cast<const uint4*>(a.x) + (l + LPR * c) * 4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) xs[4 * c + i] = src[i];
@@ -64,17 +64,15 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
   for (int d = 0; d < D; ++d)
     load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups, ring[d]);
 
-  // 4. x pairs
-  constexpr bool kXRegs = XL != 1;
-  uint32_t xp[kXRegs ? CH : 1][4][4];
-  float bias[kXRegs ? CH : 1];
-  if (XL) {
+  // 4. x pairs into VGPRs
+  uint32_t xp[CH][4][4];
+  float bias[CH];
+  if constexpr (XS) {
     stage_x_pairs<LPR>(xs, xlds, nchunks);
-    if constexpr (XL == 2) x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
+    x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
   } else {
 #pragma unroll
-    for (int c = 0; c < (XL ? 1 : CH); ++c)
-      pairs_of(&xs[4 * c], xp[kXRegs ? c : 0], bias[kXRegs ? c : 0]);
+    for (int c = 0; c < CH; ++c) pairs_of(&xs[4 * c], xp[c], bias[c]);
   }
 
   // 5. rows
@@ -82,29 +80,7 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
     RowRegs<CH>& R = ring[i % D];
-    float acc;
-    if constexpr (kXRegs) {
-      acc = row_dot_part<CH>(R, xp, bias);
-    } else {
-      acc = 0.f;
-#pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int chunk = l + LPR * c;
-        const uint4* src = reinterpret_cast<const uint4*>(xlds);
-        uint32_t p[4][4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint4 v = src[(c * 4 + q) * LPR + l];
-          p[q][0] = v.x; p[q][1] = v.y; p[q][2] = v.z; p[q][3] = v.w;
-        }
-        float t = reinterpret_cast<const float*>(xlds + nchunks * 16)[chunk];
-        t = dot8_nibbles(R.w[c].x, p[0], t);
-        t = dot8_nibbles(R.w[c].y, p[1], t);
-        t = dot8_nibbles(R.w[c].z, p[2], t);
-        t = dot8_nibbles(R.w[c].w, p[3], t);
-        acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
-      }
-    }
+    float acc = row_dot_part<CH>(R, xp, bias);
     acc = group_sum<LPR>(acc);
     mine = l == i ? acc : mine;
     if (i + D < ROWS)
@@ -135,52 +111,51 @@ __global__ __launch_bounds__(256) void rowdot_kernel(RowdotArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-template <int LPR, int CH, int SRC, int EPI, int XL, int D, int ROWS>
-void launch_variant(RowdotArgs a, hipStream_t stream) {
-  a.ngrp = (a.nrows + ROWS - 1) / ROWS;
-  const int gpb = 256 / LPR;
-  const int blocks = (a.ngrp + gpb - 1) / gpb;
-  const size_t lds = XL ? x_pairs_lds_bytes(a.in_features) : 0;
-  hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XL, D, ROWS>), dim3(blocks), dim3(256),
-                     lds, stream, a);
+struct RowdotPlan {
+  int rows;    // per group
+  int groups;  // per workgroup
+  int blocks;
+};
+
+// Rows per group for nrows outputs: the fewest of 1, 2, 4, 8 (at most LPR)
+// that keep the grid of 256-thread workgroups at about wgs_per_cu per CU.
+// (Measured on the Qwen3-32B shapes: 256-thread workgroups with 8 rows per
+// gate group and 4 per up group beat balanced grids of 5-wave or 8-wave
+// workgroups; a 5-wave workgroup leaves one SIMD per CU with an extra wave.)
+RowdotPlan plan_rowdot(int nrows, int lpr) {
+  const int groups = 256 / lpr;
+  const long long target = (long long)device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU) * groups;
+  int rows = 1;
+  while (rows < 8 && rows < lpr && (long long)rows * target < nrows) rows *= 2;
+  return RowdotPlan{rows, groups, (nrows + rows * groups - 1) / (rows * groups)};
 }
 
-// Rows per group: the fewest (from 1, 2, 4, 8, capped at LPR) that keep the
-// grid at about wgs_per_cu workgroups per CU.
-int rows_per_group(int nrows, int lpr) {
-  const int target_groups = device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU) * (256 / lpr);
-  int rows = 1;
-  while (rows < 8 && rows < lpr && (long long)rows * target_groups < nrows) rows *= 2;
-  return rows;
+template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
+void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
+  a.ngrp = p.blocks * p.groups;
+  const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) : 0;
+  hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, ROWS>), dim3(p.blocks),
+                     dim3(p.groups * LPR), lds, stream, a);
 }
 
 template <int LPR, int CH, int SRC, int EPI>
 int launch_one(const RowdotArgs& a, hipStream_t stream) {
-  const int rows = rows_per_group(a.nrows, LPR);
-  const int depth = tuning(DIP_TUNE_ROWDOT_DEPTH) >= 4 ? 4 : 2;
+  // the widths of Qwen3-4B/8B/14B/32B stage x through LDS; every ROWS the
+  // plan can pick is instantiated
   constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5);
   if constexpr (hot) {
-    const int xl = tuning(DIP_TUNE_ROWDOT_X_LDS);
-    if (xl == 2) {
-      if (rows == 1) launch_variant<LPR, CH, SRC, EPI, 2, 1, 1>(a, stream);
-      else if (rows == 2) launch_variant<LPR, CH, SRC, EPI, 2, 2, 2>(a, stream);
-      else if (rows == 4 && depth == 4) launch_variant<LPR, CH, SRC, EPI, 2, 4, 4>(a, stream);
-      else if (rows == 4) launch_variant<LPR, CH, SRC, EPI, 2, 2, 4>(a, stream);
-      else if (depth == 4) launch_variant<LPR, CH, SRC, EPI, 2, 4, 8>(a, stream);
-      else launch_variant<LPR, CH, SRC, EPI, 2, 2, 8>(a, stream);
-    } else if (xl == 1) {
-      if (rows == 1) launch_variant<LPR, CH, SRC, EPI, 1, 1, 1>(a, stream);
-      else if (rows == 2) launch_variant<LPR, CH, SRC, EPI, 1, 2, 2>(a, stream);
-      else if (rows == 4 && depth == 4) launch_variant<LPR, CH, SRC, EPI, 1, 4, 4>(a, stream);
-      else if (rows == 4) launch_variant<LPR, CH, SRC, EPI, 1, 2, 4>(a, stream);
-      else if (depth == 4) launch_variant<LPR, CH, SRC, EPI, 1, 4, 8>(a, stream);
-      else launch_variant<LPR, CH, SRC, EPI, 1, 2, 8>(a, stream);
-    } else {
-      if (rows <= 2) launch_variant<LPR, CH, SRC, EPI, 0, 2, 2>(a, stream);
-      else launch_variant<LPR, CH, SRC, EPI, 0, 2, 4>(a, stream);
+    const RowdotPlan p = plan_rowdot(a.nrows, LPR);
+    switch (p.rows) {
+      case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
+      case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
+      case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
+      default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
     }
   } else {
-    if (LPR >= 4) launch_variant<LPR, CH, SRC, EPI, 0, 2, 4>(a, stream);
+    const int rows = LPR >= 4 ? 4 : LPR;
+    const int groups = 256 / LPR;
+    const RowdotPlan p{rows, groups, (a.nrows + rows * groups - 1) / (rows * groups)};
+    launch_variant<LPR, CH, SRC, EPI, false, (LPR >= 4 ? 4 : LPR)>(a, p, stream);
   }
   return hip_status(hipGetLastError());
 }

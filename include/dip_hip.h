@@ -132,21 +132,15 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
 /*
  * Launch tuning, no counterpart in the reference (process-wide, host side;
  * speed only):
- *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grid = CUs * this workgroups (default 2)
- *   DIP_TUNE_ROWDOT_X_LDS       gate/up x pairs: 0 built per lane in VGPRs, 1 staged
- *                               in LDS and re-read per row, 2 staged in LDS then
- *                               held in VGPRs (2)
- *   DIP_TUNE_ROWDOT_DEPTH       rows of loads in flight per row group, 2..4 (2)
+ *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grids aim at CUs * this workgroups (2)
  *   DIP_TUNE_TOPK_STAMPS        1: the top-k records wall-clock phase stamps
  *                               in its workspace (diagnostics, slower) (0)
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
-  DIP_TUNE_ROWDOT_X_LDS = 1,
-  DIP_TUNE_ROWDOT_DEPTH = 2,
-  DIP_TUNE_TOPK_STAMPS = 3,
-  DIP_TUNE_COUNT = 4
+  DIP_TUNE_TOPK_STAMPS = 1,
+  DIP_TUNE_COUNT = 2
 };
 int dip_set_tuning(int knob, int value);
 int dip_get_tuning(int knob);

@@ -67,7 +67,8 @@ def test_argument_rejection_before_launch():
     ws = L.dip_mlp_workspace_size(5120, 25600, 15360)
     assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 30000, p, ws, None) == -2
     assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, None, p, p, 5120, 25600, 100, p, ws, None) == -1
-    assert L.dip_set_tuning(3, 7) == -6
+    assert L.dip_set_tuning(1, 7) == -6
+    assert L.dip_set_tuning(0, 0) == -6
     assert L.dip_set_tuning(99, 1) == -6
     assert L.dip_get_tuning(99) == -6
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
