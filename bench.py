@@ -105,6 +105,9 @@ def main(argv=None):
     ap.add_argument("--keep", type=float, default=0.6)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-spec", action="store_true",
+                    help="run every layer stage by stage (no speculative up rows during the "
+                         "top-k); same outputs, five launches per layer instead of four")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel eagerly instead of replaying the captured graph "
                          "(for counter collection, which profiles each dispatch)")
@@ -128,7 +131,8 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     print(f"[bench] building {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
           flush=True)
-    stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0)
+    stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0,
+                     spec=not args.no_spec)
     gen = torch.Generator(device=dev).manual_seed(1)
     n_tok = args.warmup + args.steps
     xs = (torch.randn(n_tok, shape["hidden"], device=dev, generator=gen)).to(torch.bfloat16)
@@ -182,7 +186,10 @@ def main(argv=None):
     H, I, k = stack.hidden, stack.inter, stack.k
     row = H // 2 + 2 * (H // 128)
     stage_bytes = {"gate_silu": I * row, "topk": 2 * I + 4 * k,
-                   "up_gather_h": k * row, "down_gather": k * row}
+                   "up_gather_h": k * row, "down_gather": k * row,
+                   # top-k + the up rows of the k selected channels (rows
+                   # speculated on but not selected are not counted)
+                   "topk_spec_up": 2 * I + 4 * k + k * row}
     dom = max(stages, key=stages.get)
     ach = stage_bytes[dom] / (stages[dom] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -217,6 +224,7 @@ def main(argv=None):
             "hidden": H, "inter": I, "layers": stack.layers, "k": k,
             "weights": "int4 g128 symmetric, bf16 scales; N(0,0.02) draws",
             "activations": "bf16, fp32 accumulate",
+            "speculative_up": not args.no_spec,
             "bytes_per_token": stack.bytes_per_token,
         },
         "step_hbm_gbs": round(step_gbs, 1),

@@ -56,7 +56,12 @@ _SIGS = {
     "dip_dequant_rows": ([_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p], _i32),
     "dip_mlp_workspace_size": ([_i64, _i64, _i64], _sz),
     "dip_mlp_decode": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz,
-                        _p], _i32),
+                        _p, _p], _i32),
+    "dip_mlp_state_size": ([], _sz),
+    "dip_gate_silu_topk_spec": ([_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p,
+                                 _p], _i32),
+    "dip_int4_gather_down_by_channel": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p],
+                                        _i32),
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
@@ -376,9 +381,20 @@ def mlp_workspace_bytes(hidden: int, inter: int, k: int) -> int:
     return lib.dip_mlp_workspace_size(hidden, inter, k)
 
 
+def mlp_state(device) -> torch.Tensor:
+    """A zeroed per-layer decode state for mlp_decode (speculative up rows)."""
+    n = lib.dip_mlp_state_size()
+    return torch.zeros(n // 4, dtype=torch.int32, device=device)
+
+
 def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=None, g=None,
-               idx=None, h=None, ws=None):
-    """One resident DIP MLP decode step; returns (y, g, idx, h)."""
+               idx=None, h=None, ws=None, state=None):
+    """One resident DIP MLP decode step; returns (y, g, idx, h).
+
+    state: this layer's mlp_state() tensor, kept across calls.  With it the
+    step overlaps the top-k with up rows of the channels the last call ranked
+    highest (same outputs, bit for bit); without it the step runs stage by
+    stage."""
     gate_qw, gate_sc, inter, hidden = _weights(gate_qw, gate_sc, "gate")
     up_qw, up_sc, inter2, hidden2 = _weights(up_qw, up_sc, "up")
     down_t_qw, down_t_sc, inter3, hidden3 = _weights(down_t_qw, down_t_sc, "down_t")
@@ -402,14 +418,19 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
         ws = workspace(dev, nbytes, "mlp")
     elif ws.numel() < nbytes:
         raise RuntimeError("workspace too small")
+    if state is not None:
+        if (state.device != dev or state.dtype != torch.int32 or not state.is_contiguous()
+                or state.numel() * 4 < lib.dip_mlp_state_size()):
+            raise RuntimeError("state must be this device's mlp_state() tensor")
     _check(lib.dip_mlp_decode(_ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc),
                               _ptr(down_t_qw), _ptr(down_t_sc), _ptr(x), _ptr(y), _ptr(g),
                               _ptr(idx), _ptr(h), hidden, inter, k, _ptr(ws), ws.numel(),
-                              _stream(dev)), "dip_mlp_decode")
+                              None if state is None else _ptr(state), _stream(dev)),
+           "dip_mlp_decode")
     return y, g, idx, h
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1}
+TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2}
 
 
 def set_tuning(name: str, value: int) -> None:

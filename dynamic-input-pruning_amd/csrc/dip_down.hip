@@ -66,7 +66,9 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   const int jc = min(jl, a.k - 1);
   const uint32_t rid_c = down_row<SRC>(a, jc);
   const uint32_t rid_l = jl < a.k ? rid_c : kPadRow;
-  const uint32_t h_l = a.h[jc];
+  const int hix = !a.h_by_row ? jc : (rid_c < (uint32_t)a.rows_a ? (int)rid_c : 0);
+  const uint32_t h_l = a.h[hix];
+  if (a.h_out && cb == 0 && jl < a.k) a.h_out[jl] = (uint16_t)h_l;
 
   DownRow ring[LPR];
 #pragma unroll
@@ -167,7 +169,8 @@ int64_t down_max_k() { return (int64_t)kMaxRowBlocks * kRowsPerBlock; }
 int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
-             uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream) {
+             uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream, int h_by_row,
+             uint16_t* h_out) {
   if (!qw_a || !sc_a || !y) return DIP_ERR_NULL;
   if (out_features <= 0 || out_features % kGroupSize != 0 || out_features > (1 << 20))
     return DIP_ERR_SHAPE;
@@ -198,6 +201,8 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.sel = sel;
   a.sel2 = sel2;
   a.partial = reinterpret_cast<float*>(workspace);
+  a.h_out = h_out;
+  a.h_by_row = h_by_row;
   a.rows_a = (int)rows_a;
   a.rows_b = (int)rows_b;
   a.k = (int)k;
@@ -229,6 +234,16 @@ extern "C" int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales
   return run_down(indices ? kGather : kContig, down_t, scales, rows, nullptr, nullptr, 0, h,
                   indices, nullptr, k, out_features, y, workspace, ws_bytes,
                   (hipStream_t)stream);
+}
+
+extern "C" int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint16_t* scales,
+                                               const uint16_t* h_full, const int32_t* indices,
+                                               uint16_t* y, uint16_t* h_out, int64_t rows,
+                                               int64_t out_features, int64_t k, void* workspace,
+                                               size_t ws_bytes, void* stream) {
+  if (k > 0 && !indices) return DIP_ERR_NULL;
+  return run_down(kGather, down_t, scales, rows, nullptr, nullptr, 0, h_full, indices, nullptr,
+                  k, out_features, y, workspace, ws_bytes, (hipStream_t)stream, 1, h_out);
 }
 
 extern "C" int dip_ca_down(const int8_t* res_qw, const uint16_t* res_sc, const int8_t* str_qw,

@@ -41,6 +41,7 @@ struct RowdotArgs {
   int rows_a;  // rows of matrix A (row ids outside [0, rows_a) yield NaN)
   int rows_b;  // rows of matrix B (kDual)
   int ngrp;    // row groups (set by the launcher)
+  uint32_t* rotate;  // if set: workgroup 0 copies rotate[1] to rotate[0] (speculation state)
 };
 
 struct DownArgs {
@@ -54,6 +55,8 @@ struct DownArgs {
   const int8_t* qw_safe;   // a matrix with at least one row: read in place of bad rows
   const uint16_t* sc_safe;
   float* partial;     // [row_blocks, out_features]
+  uint16_t* h_out;    // if set: h_out[j] = the h used for position j
+  int h_by_row;       // h is indexed by row id (h[sel[j]]) instead of by position
   int rows_a;
   int rows_b;
   int k;
@@ -82,17 +85,39 @@ struct TopkMeta {
 // The top-k workspace holds the last call's TopkMeta.
 constexpr size_t kTopkWorkspace = 512;
 
+// Top-k + speculative up (one launch): workgroups [0, ntopk) run the select,
+// the rest compute h_full[c] = bf16(g[c] * bf16(up[c] . x)) for every channel
+// whose magnitude key is at or above state[0]; the select workgroups add the
+// selected channels below it.  state[1] receives the key at rank k + margin
+// for the next call.
+struct SpecArgs {
+  const int8_t* up_qw;
+  const uint16_t* up_sc;
+  const uint16_t* x;
+  uint16_t* h_full;   // [n] h by channel (only the selected channels are meaningful)
+  uint32_t* state;    // [0] speculation key in use, [1] the next call's key
+  int hidden;
+  int margin;         // set by the launcher (DIP_TUNE_SPEC_MARGIN)
+  int chan_per_wg;    // set by the launcher
+  int ntopk;          // set by the launcher
+};
+
 // Launchers (return hipSuccess or a DIP_ERR_* code).
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
 int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
-             uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream);
+             uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream,
+             int h_by_row = 0, uint16_t* h_out = nullptr);
 size_t down_workspace_bytes(int64_t k, int64_t out_features);
 int64_t down_max_k();  // largest k the down path accepts
 // The top-k select kernel: idx from s (TopkMeta into the workspace).
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
                        hipStream_t stream);
+// The top-k + speculative-up launch (hidden widths of topk_spec_supported).
+bool topk_spec_supported(int64_t hidden);
+int launch_topk_spec(const uint16_t* g, int64_t n, int64_t k, int32_t* idx, void* ws,
+                     SpecArgs sp, hipStream_t stream);
 
 
 // Launch tuning (process-wide, host side): see DIP_TUNE_* in dip_hip.h.

@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 0};
+int g_tune[DIP_TUNE_COUNT] = {2, 0, 32};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -173,6 +173,9 @@ extern "C" int dip_set_tuning(int knob, int value) {
       break;
     case DIP_TUNE_TOPK_STAMPS:
       if (value != 0 && value != 1) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_SPEC_MARGIN:
+      if (value < 0 || value > 1024) return DIP_ERR_ARG;
       break;
     default:
       return DIP_ERR_ARG;
@@ -247,7 +250,7 @@ extern "C" int dip_host_gather_rows(const void* src, const int32_t* ids, void* d
 
 // ---------------------------------------------------------------------------
 // One resident DIP MLP decode step.
-//   workspace: [0, 512) top-k state | down partials
+//   workspace: [0, 512) top-k state | h by channel [inter] bf16 | down partials
 // ---------------------------------------------------------------------------
 namespace {
 constexpr size_t kMlpTopkBytes = 512;
@@ -256,8 +259,8 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
 
 extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k) {
-  (void)inter;
-  return kMlpTopkBytes + align256(down_workspace_bytes(k, hidden));
+  const size_t hfull = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
+  return kMlpTopkBytes + hfull + align256(down_workspace_bytes(k, hidden));
 }
 
 extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
@@ -265,12 +268,24 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
                               const int8_t* down_t_qw, const uint16_t* down_t_sc,
                               const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
                               uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
-                              void* workspace, size_t ws_bytes, void* stream) {
+                              void* workspace, size_t ws_bytes, void* layer_state,
+                              void* stream) {
   if (!g_out || !y || !x) return DIP_ERR_NULL;
   if (k < 0 || k > inter) return DIP_ERR_SHAPE;
   if (k > 0 && (!idx_out || !h_out)) return DIP_ERR_NULL;
   if (!workspace || ws_bytes < dip_mlp_workspace_size(hidden, inter, k)) return DIP_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
+  const size_t hfull_bytes = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
+  char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
+  const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
+  if (layer_state && k > 0 && topk_spec_supported(hidden) && inter <= kTopkMaxN) {
+    uint16_t* h_full = reinterpret_cast<uint16_t*>(ws + kMlpTopkBytes);
+    int st = dip_gate_silu_topk_spec(gate_qw, gate_sc, up_qw, up_sc, x, g_out, idx_out, h_full,
+                                     inter, hidden, k, ws, kMlpTopkBytes, layer_state, stream);
+    if (st) return st;
+    return dip_int4_gather_down_by_channel(down_t_qw, down_t_sc, h_full, idx_out, y, h_out,
+                                           inter, hidden, k, down_ws, down_bytes, stream);
+  }
   int st = dip_gate_silu_topk(gate_qw, gate_sc, x, g_out, idx_out, inter, hidden, k, ws,
                               kMlpTopkBytes, stream);
   if (st) return st;
@@ -279,5 +294,5 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
     if (st) return st;
   }
   return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k,
-                              ws + kMlpTopkBytes, ws_bytes - kMlpTopkBytes, stream);
+                              down_ws, down_bytes, stream);
 }

@@ -30,7 +30,7 @@ template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
 __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a) {
   constexpr int D = ROWS < 2 ? ROWS : 2;  // rows of loads in flight per group
   static_assert(ROWS <= LPR, "rows per group");
-  extern __shared__ uint32_t xlds[];
+  extern __shared__ __align__(16) uint32_t xlds[];
   const int l = threadIdx.x % LPR;
   const int lane = threadIdx.x & 63;
   const int gbase = lane - l;  // first lane of my group within the wave
@@ -39,6 +39,7 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   const int nchunks = a.in_features / kChunkCols;
   const int grp = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
   const int ngrp = a.ngrp;
+  if (a.rotate && blockIdx.x == 0 && threadIdx.x == 0) a.rotate[0] = a.rotate[1];
 
   // 1. x loads first (XS: one chunk per thread, index clamped)
   uint4 xs[XS ? 4 : CH * 4];
@@ -259,6 +260,39 @@ extern "C" int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc
   st = launch_rowdot(kContig, kSilu, a, (hipStream_t)stream);
   if (st || k == 0) return st;
   return launch_topk_select(g, inter, k, idx, workspace, (hipStream_t)stream);
+}
+
+extern "C" size_t dip_mlp_state_size(void) { return 2 * sizeof(uint32_t); }
+
+extern "C" int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
+                                       const int8_t* up_qw, const uint16_t* up_sc,
+                                       const uint16_t* x, uint16_t* g, int32_t* idx,
+                                       uint16_t* h_full, int64_t inter, int64_t hidden,
+                                       int64_t k, void* workspace, size_t ws_bytes, void* state,
+                                       void* stream) {
+  int st = check_matrix(gate_qw, gate_sc, inter, hidden);
+  if (st) return st;
+  st = check_matrix(up_qw, up_sc, inter, hidden);
+  if (st) return st;
+  if (!x || !g || !idx || !h_full || !state) return DIP_ERR_NULL;
+  if (!aligned16(x) || !aligned16(g) || (reinterpret_cast<uintptr_t>(state) & 3u))
+    return DIP_ERR_ALIGN;
+  if (inter > kTopkMaxN || k < 1 || k > inter) return DIP_ERR_SHAPE;
+  if (!topk_spec_supported(hidden)) return DIP_ERR_UNSUPPORTED;
+  if (!workspace || ws_bytes < dip_topk_workspace_size(inter)) return DIP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DIP_ERR_ALIGN;
+  RowdotArgs a = base_args(gate_qw, gate_sc, x, g, inter, hidden);
+  a.rotate = static_cast<uint32_t*>(state);
+  st = launch_rowdot(kContig, kSilu, a, (hipStream_t)stream);
+  if (st) return st;
+  SpecArgs sp{};
+  sp.up_qw = up_qw;
+  sp.up_sc = up_sc;
+  sp.x = x;
+  sp.h_full = h_full;
+  sp.state = static_cast<uint32_t*>(state);
+  sp.hidden = (int)hidden;
+  return launch_topk_spec(g, inter, k, idx, workspace, sp, (hipStream_t)stream);
 }
 
 extern "C" int dip_int4_gather_gemv(const int8_t* qweight, const uint16_t* scales,

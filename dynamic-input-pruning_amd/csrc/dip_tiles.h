@@ -51,16 +51,11 @@ struct RowRegs {
   uint32_t s[CH];
 };
 
-// Unconditional loads of one row's CH chunks and scales (a bad id reads row
-// 0 of the safe matrix).
-template <int LPR, int CH, int SRC>
-DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes, int ngroups,
-                      RowRegs<CH>& R) {
-  const bool bad = rid == kBadRow;
-  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
-  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
-  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
-  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
+// Unconditional loads of CH chunks (lane l owns chunks l + LPR*c) and their
+// scales of row r of one matrix.
+template <int LPR, int CH>
+DIP_DEV void load_row_at(const int8_t* qw, const uint16_t* sc, uint32_t r, int l,
+                         size_t row_bytes, int ngroups, RowRegs<CH>& R) {
   const uint4* wr = reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes);
   const uint16_t* sr = sc + (size_t)r * ngroups;
 #pragma unroll
@@ -69,6 +64,17 @@ DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes
     R.w[c] = ldg_nt(wr + chunk);
     R.s[c] = sr[chunk / kChunksPerGroup];
   }
+}
+
+// The same for a resolved row id (a bad id reads row 0 of the safe matrix).
+template <int LPR, int CH, int SRC>
+DIP_DEV void load_row(const RowdotArgs& a, uint32_t rid, int l, size_t row_bytes, int ngroups,
+                      RowRegs<CH>& R) {
+  const bool bad = rid == kBadRow;
+  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
+  const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
+  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
+  load_row_at<LPR, CH>(qw, sc, bad ? 0u : (rid & ~kSrcB), l, row_bytes, ngroups, R);
 }
 
 // x pairs + bias for one chunk (32 columns starting at 32*chunk), from the
@@ -140,6 +146,17 @@ DIP_DEV void x_pairs_to_regs(const uint32_t* xlds, int nchunks, int l, uint32_t 
   }
 }
 
+// One chunk's contribution: acc + 16*s*(bias + sum of its 32 (1.5 + q/16)*x).
+DIP_DEV float chunk_dot(const uint4& w, const uint32_t xp[4][4], float bias, uint32_t s,
+                        float acc) {
+  float t = bias;
+  t = dot8_nibbles(w.x, xp[0], t);
+  t = dot8_nibbles(w.y, xp[1], t);
+  t = dot8_nibbles(w.z, xp[2], t);
+  t = dot8_nibbles(w.w, xp[3], t);
+  return fmaf(bf16_to_f32(s), kPairScale * t, acc);
+}
+
 // The lane's part of one row's dot product with x pairs in VGPRs (not yet
 // reduced across the row group).
 template <int CH>
@@ -147,15 +164,36 @@ DIP_DEV float row_dot_part(const RowRegs<CH>& R, const uint32_t xp[CH][4][4],
                            const float bias[CH]) {
   float acc = 0.f;
 #pragma unroll
+  for (int c = 0; c < CH; ++c) acc = chunk_dot(R.w[c], xp[c], bias[c], R.s[c], acc);
+  return acc;
+}
+
+// The same with the pairs read from the staged LDS copy chunk by chunk (the
+// same operations in the same order, so the result is bit-identical).
+template <int LPR, int CH>
+DIP_DEV float row_dot_lds(const RowRegs<CH>& R, const uint32_t* xlds, int nchunks, int l) {
+  const uint4* src = reinterpret_cast<const uint4*>(xlds);
+  const float* bias = reinterpret_cast<const float*>(xlds + nchunks * 16);
+  float acc = 0.f;
+#pragma unroll
   for (int c = 0; c < CH; ++c) {
-    float t = bias[c];
-    t = dot8_nibbles(R.w[c].x, xp[c][0], t);
-    t = dot8_nibbles(R.w[c].y, xp[c][1], t);
-    t = dot8_nibbles(R.w[c].z, xp[c][2], t);
-    t = dot8_nibbles(R.w[c].w, xp[c][3], t);
-    acc = fmaf(bf16_to_f32(R.s[c]), kPairScale * t, acc);
+    uint32_t xp[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = src[(c * 4 + q) * LPR + l];
+      xp[q][0] = v.x;
+      xp[q][1] = v.y;
+      xp[q][2] = v.z;
+      xp[q][3] = v.w;
+    }
+    acc = chunk_dot(R.w[c], xp, bias[l + LPR * c], R.s[c], acc);
   }
   return acc;
+}
+
+// h = bf16(g * bf16(u)) from the reduced up dot product u (dip_stream_predispatch.py:198-199).
+DIP_DEV uint32_t h_of(uint32_t g_bits, float u) {
+  return f32_to_bf16(bf16_to_f32(g_bits) * bf16_to_f32(f32_to_bf16(u)));
 }
 
 // ---------------------------------------------------------------------------

@@ -30,8 +30,9 @@
 // the reference's --use_fast_math, so histogram bins below 0x80 all mean 0
 // and both cuts are clamped to >= 0x80; NaN and padding (0xFFFF) land in bins
 // above 0x7F80, which the search ignores and the tier ranges exclude.
-#include "dip_common.h"
-#include "dip_internal.h"
+#include <algorithm>
+
+#include "dip_tiles.h"
 
 namespace dip {
 
@@ -147,23 +148,153 @@ DIP_DEV Cuts make_cuts(uint32_t cut_a, uint32_t cut_b) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Speculative up rows.  h for a channel c is bf16(g[c] * bf16(up[c] . x)),
+// computed with the same row-dot code and order as dip_up_gather_h, so every
+// h below is bit-identical to the one that entry point would produce.
+// ---------------------------------------------------------------------------
+
+// h of the residual channels of a select workgroup (list entries: channel |
+// g bits << 16): row group i takes entries i, i + groups, ... one row at a
+// time (the residual is a handful of rows in steady state).
+template <int LPR, int CH>
+DIP_DEV void residual_rows(const SpecArgs& sp, const uint32_t* rlist, int rcount,
+                           uint32_t* xlds) {
+  const int nchunks = sp.hidden / kChunkCols;
+  uint4 xs[4];
+  load_x_chunk(sp.x, nchunks, xs);
+  stage_x_pairs<LPR>(xs, xlds, nchunks);
+  const int l = threadIdx.x % LPR;
+  const size_t row_bytes = (size_t)(sp.hidden >> 1);
+  const int ngr = sp.hidden >> 7;
+  for (int e = threadIdx.x / LPR; e < rcount; e += kThreads / LPR) {
+    const uint32_t ent = rlist[e];
+    RowRegs<CH> R;
+    load_row_at<LPR, CH>(sp.up_qw, sp.up_sc, ent & 0xFFFFu, l, row_bytes, ngr, R);
+    const float u = group_sum<LPR>(row_dot_lds<LPR, CH>(R, xlds, nchunks, l));
+    if (l == 0) sp.h_full[ent & 0xFFFFu] = (uint16_t)h_of(ent >> 16, u);
+  }
+}
+
+// Speculation workgroup u: h for every channel c in [u*C, min((u+1)*C, n))
+// whose magnitude key |bits| is at or above the speculation key state[0]
+// (C = chan_per_wg <= kThreads).  The channels are compacted into an LDS
+// list (channel | g bits << 16); row group i takes entries i, i + groups, ...
+// with D rows in flight, the first D issued before x is staged.
+template <int LPR, int CH>
+DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp, int u,
+                       uint32_t* lds) {
+  constexpr int kGroups = kThreads / LPR;
+  // rows in flight per group (16-lane groups: twice the groups, and more
+  // rows in flight spill registers)
+  constexpr int D = LPR >= 32 ? 3 : 1;
+  __shared__ uint32_t wcnt[kWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nchunks = sp.hidden / kChunkCols;
+  const uint32_t sk = sp.state[0];
+  const int c0 = u * sp.chan_per_wg;
+  const int c1 = min(c0 + sp.chan_per_wg, n);
+
+  uint4 xs[4];
+  load_x_chunk(sp.x, nchunks, xs);
+  const int c = c0 + tid;
+  const uint32_t gb = c < c1 ? (uint32_t)g[c] : 0u;
+  const bool f = c < c1 && (gb & 0x7FFFu) >= sk;
+  const uint64_t m = __ballot(f);
+  if (lane == 0) wcnt[wave] = (uint32_t)__popcll(m);
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int v = (int)wcnt[w];
+    base += w < wave ? v : 0;
+    total += v;
+  }
+  if (f) lds[base + __popcll(m & ((1ull << lane) - 1ull))] = (uint32_t)c | (gb << 16);
+  __syncthreads();
+  if (total == 0) return;  // workgroup-uniform
+
+  const int grp = tid / LPR;
+  const int l = tid % LPR;
+  const size_t row_bytes = (size_t)(sp.hidden >> 1);
+  const int ngr = sp.hidden >> 7;
+  uint32_t* xlds = lds + kThreads;  // after the list
+  const int rounds = (total + kGroups - 1) / kGroups;
+  RowRegs<CH> ring[D];
+  uint32_t ent[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {  // entries past the end re-read the last row
+    ent[d] = lds[min(grp + d * kGroups, total - 1)];
+    load_row_at<LPR, CH>(sp.up_qw, sp.up_sc, ent[d] & 0xFFFFu, l, row_bytes, ngr, ring[d]);
+  }
+  stage_x_pairs<LPR>(xs, xlds, nchunks);
+  const uint4* xsrc = reinterpret_cast<const uint4*>(xlds);
+  const float* xbias = reinterpret_cast<const float*>(xlds + nchunks * 16);
+  for (int i0 = 0; i0 < rounds; i0 += D) {
+    // The D rows in flight share each chunk's x pairs (one LDS read for all
+    // of them); a group skips its rows past the end of the list.  Each row
+    // still accumulates its chunks in order, as row_dot_part does.
+    bool live[D];
+    float acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      live[d] = i0 + d < rounds && grp + (i0 + d) * kGroups < total;
+      acc[d] = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      uint32_t xp[4][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = xsrc[(c * 4 + q) * LPR + l];
+        xp[q][0] = v.x;
+        xp[q][1] = v.y;
+        xp[q][2] = v.z;
+        xp[q][3] = v.w;
+      }
+      const float b = xbias[l + LPR * c];
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (live[d]) acc[d] = chunk_dot(ring[d].w[c], xp, b, ring[d].s[c], acc[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (live[d]) {  // uniform within the group
+        const float uu = group_sum<LPR>(acc[d]);
+        if (l == 0) sp.h_full[ent[d] & 0xFFFFu] = (uint16_t)h_of(ent[d] >> 16, uu);
+      }
+      if (i0 + d + D < rounds) {  // workgroup-uniform
+        ent[d] = lds[min(grp + (i0 + d + D) * kGroups, total - 1)];
+        load_row_at<LPR, CH>(sp.up_qw, sp.up_sc, ent[d] & 0xFFFFu, l, row_bytes, ngr,
+                             ring[d]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Select: R rounds of one 8-value chunk per thread cover n <= 8192 R values;
 // workgroup w places values [2048 w, 2048 (w + 1)).
 // ---------------------------------------------------------------------------
-template <int R>
-__global__ __launch_bounds__(kThreads) void topk_select_kernel(
-    const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
-    TopkMeta* __restrict__ meta, int stamps) {
-  extern __shared__ uint32_t hist[];  // kFineBins bins
+// The select body, run by workgroups 0 .. nblk-1 of a launch.  SPEC (the
+// decode step with speculative up rows): also records the magnitude key at
+// rank k + margin for the next call and computes h for the selected channels
+// that the speculation workgroups skip (residual_rows).
+template <int R, bool SPEC, int LPR, int CH>
+DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
+                       TopkMeta* __restrict__ meta, int stamps, int nblk, const SpecArgs& sp,
+                       uint32_t* hist) {
   __shared__ uint32_t wtot[kWaves];
   __shared__ uint32_t wsum_a[kWaves], wsum_b[kWaves], wside[kWaves], wown[kWaves];
-  __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b;
+  __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b, sh_spec, sh_rcount;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int slice0 = blockIdx.x * kSlice;
   const bool stamp = stamps && blockIdx.x == 0 && tid == 0;
+  const uint32_t sk = SPEC ? sp.state[0] : 0u;  // read early: used after placement
   if (stamp) {
     meta->stamp[0] = wall_clock64();
     meta->cycles[0] = clock64();
@@ -192,6 +323,8 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   if (tid == 0) {
     sh_a = kNoKey;
     sh_max = kNoKey;
+    sh_spec = kNoKey;
+    sh_rcount = 0;
   }
   __syncthreads();
 
@@ -245,9 +378,11 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
       nvalid += wtot[w];
     }
     const uint32_t need = (uint32_t)k + 1u;
+    const uint32_t need_s = SPEC ? (uint32_t)k + (uint32_t)sp.margin : 0u;
     const bool own1 = above < 1u && wsum >= 1u;
     const bool ownk = above < need && above + wsum >= need;
-    if (own1 || ownk) {  // wave-uniform
+    const bool owns = SPEC && blockIdx.x == 0 && above < need_s && above + wsum >= need_s;
+    if (own1 || ownk || owns) {  // wave-uniform
       uint32_t carry = above;
 #pragma unroll
       for (int j = 7; j >= 0; --j) {
@@ -276,6 +411,15 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
           }
           sh_a = b;
         }
+        if (owns && gt < need_s && ge >= need_s) {
+          uint32_t run = gt, b = kNoKey;
+#pragma unroll
+          for (int e = 3; e >= 0; --e) {
+            run += cnt[e];
+            if (b == kNoKey && run >= need_s) b = b0 + e;
+          }
+          sh_spec = b;
+        }
       }
     }
   }
@@ -303,6 +447,8 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
     // subnormal magnitudes never qualify, so the cuts start at 0x80.
     sh_cut_a = max((__float_as_uint(hi) >> 16) + 1u, kMinNormalKey);
     sh_cut_b = max((__float_as_uint(lo) >> 16) + 1u, kMinNormalKey);
+    if (SPEC && blockIdx.x == 0)  // fewer than k + margin values: speculate on all
+      sp.state[1] = sh_spec == kNoKey ? 0u : sh_spec;
     if (blockIdx.x == 0) {
       meta->lo = lo;
       meta->hi = hi;
@@ -401,17 +547,66 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   // unfilled slots (fewer than k values qualify) are 0, as in the reference
   const uint32_t filled = min(uk, tot_a + tot_b);
   for (uint32_t p = filled + (uint32_t)(blockIdx.x * kThreads + tid); p < uk;
-       p += gridDim.x * kThreads)
+       p += (uint32_t)nblk * kThreads)
     idx[p] = 0;
   if (blockIdx.x == 0 && tid == 0) {
     meta->count_a = (int32_t)tot_a;
     meta->count_b = (int32_t)tot_b;
+  }
+  if constexpr (SPEC) {
+    // Residual h: selected channels whose key is below the speculation key
+    // (the speculation workgroups compute every channel at or above it), and
+    // channel 0 when unfilled slots point at it.  The histogram is no longer
+    // read: its LDS holds the list and then the x pairs.
+    const bool sel0 = (a0 | q0) && (a0 ? pa0 : pb0) < uk;
+    const bool sel1 = (a1 | q1) && (a1 ? pa0 + a0 : pb0 + q0) < uk;
+    const bool r0 = (sel0 || (my == 0 && filled < uk)) && b0 < sk;
+    const bool r1 = sel1 && b1 < sk;
+    const uint64_t m0 = __ballot(r0), m1 = __ballot(r1);
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint32_t n0 = (uint32_t)__popcll(m0), nw = n0 + (uint32_t)__popcll(m1);
+    uint32_t base = 0;
+    if (lane == 0 && nw) base = atomicAdd(&sh_rcount, nw);
+    base = (uint32_t)__shfl((int)base, 0, 64);
+    uint32_t* rlist = hist;
+    const uint32_t gpair = mine;
+    if (r0) rlist[base + __popcll(m0 & below)] = (uint32_t)my | (gpair << 16);
+    if (r1) rlist[base + n0 + __popcll(m1 & below)] = (uint32_t)(my + 1) | (gpair & 0xFFFF0000u);
+    __syncthreads();
+    const int rcount = (int)sh_rcount;
+    if (rcount > 0) residual_rows<LPR, CH>(sp, rlist, rcount, hist + kSlice);
   }
   if (stamp) {
     meta->stamp[5] = wall_clock64();
     meta->cycles[1] = clock64();
   }
 }
+
+template <int R>
+__global__ __launch_bounds__(kThreads) void topk_select_kernel(
+    const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
+    TopkMeta* __restrict__ meta, int stamps) {
+  // 16-byte aligned: the histogram is cleared and scanned with 128-bit LDS
+  // accesses, which are slow when misaligned
+  extern __shared__ __align__(16) uint32_t hist[];  // kFineBins bins
+  const SpecArgs none{};
+  topk_body<R, false, 32, 5>(s, n, k, idx, meta, stamps, (int)gridDim.x, none, hist);
+}
+
+// Top-k + speculative up rows in one launch: workgroups [0, sp.ntopk) run
+// the select (and the residual rows), the rest compute h for the channels at
+// or above the speculation key.  No workgroup waits for another.
+template <int R, int LPR, int CH>
+__global__ __launch_bounds__(kThreads) void topk_spec_kernel(
+    const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
+    TopkMeta* __restrict__ meta, int stamps, SpecArgs sp) {
+  extern __shared__ __align__(16) uint32_t lds[];  // 128-bit LDS accesses: keep aligned
+  if ((int)blockIdx.x < sp.ntopk)
+    topk_body<R, true, LPR, CH>(s, n, k, idx, meta, stamps, sp.ntopk, sp, lds);
+  else
+    spec_rows<LPR, CH>(s, n, sp, (int)blockIdx.x - sp.ntopk, lds);
+}
+
 
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
                        hipStream_t stream) {
@@ -434,6 +629,54 @@ int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, vo
     hipLaunchKernelGGL((topk_select_kernel<8>), dim3(blocks), dim3(kThreads), lds, stream, s,
                        (int)n, (int)k, idx, meta, stamps);
   return hip_status(hipGetLastError());
+}
+
+namespace {
+
+template <int R, int LPR, int CH>
+int launch_spec_variant(const uint16_t* s, int n, int k, int32_t* idx, TopkMeta* meta,
+                        const SpecArgs& sp, int blocks, hipStream_t stream) {
+  static const bool lds_ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_spec_kernel<R, LPR, CH>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kFineBins * (int)sizeof(uint32_t)) == hipSuccess;
+  if (!lds_ok) return hip_status(hipGetLastError());
+  hipLaunchKernelGGL((topk_spec_kernel<R, LPR, CH>), dim3(blocks), dim3(kThreads),
+                     kFineBins * sizeof(uint32_t), stream, s, n, k, idx, meta,
+                     tuning(DIP_TUNE_TOPK_STAMPS), sp);
+  return hip_status(hipGetLastError());
+}
+
+template <int LPR, int CH>
+int launch_spec_width(const uint16_t* s, int n, int k, int32_t* idx, TopkMeta* meta,
+                      const SpecArgs& sp, int blocks, hipStream_t stream) {
+  if (n <= 4 * 8 * kThreads) return launch_spec_variant<4, LPR, CH>(s, n, k, idx, meta, sp, blocks, stream);
+  return launch_spec_variant<8, LPR, CH>(s, n, k, idx, meta, sp, blocks, stream);
+}
+
+}  // namespace
+
+bool topk_spec_supported(int64_t hidden) {
+  const int64_t chunks = hidden / kChunkCols;
+  return hidden % kGroupSize == 0 && (chunks == 160 || chunks == 128 || chunks == 80);
+}
+
+int launch_topk_spec(const uint16_t* g, int64_t n, int64_t k, int32_t* idx, void* ws,
+                     SpecArgs sp, hipStream_t stream) {
+  if (n <= 0 || k <= 0 || k > n || n > kTopkMaxN) return DIP_ERR_SHAPE;
+  if (!topk_spec_supported(sp.hidden)) return DIP_ERR_UNSUPPORTED;
+  const int ntopk = (int)((n + kSlice - 1) / kSlice);
+  const int min_spec = (int)((n + kThreads - 1) / kThreads);
+  const int nspec = std::max(std::max(device_cus() - ntopk, min_spec), 1);
+  sp.ntopk = ntopk;
+  sp.chan_per_wg = (int)((n + nspec - 1) / nspec);
+  sp.margin = (int)(n * (int64_t)tuning(DIP_TUNE_SPEC_MARGIN) / 1024);
+  TopkMeta* meta = reinterpret_cast<TopkMeta*>(ws);
+  const int blocks = ntopk + nspec;
+  const int chunks = sp.hidden / kChunkCols;
+  if (chunks == 160) return launch_spec_width<32, 5>(g, (int)n, (int)k, idx, meta, sp, blocks, stream);
+  if (chunks == 128) return launch_spec_width<32, 4>(g, (int)n, (int)k, idx, meta, sp, blocks, stream);
+  return launch_spec_width<16, 5>(g, (int)n, (int)k, idx, meta, sp, blocks, stream);
 }
 
 }  // namespace dip

@@ -43,7 +43,7 @@ def bytes_per_layer(hidden: int, inter: int, k: int) -> int:
 
 class DIPStack:
     def __init__(self, hidden: int, inter: int, layers: int, keep_ratio: float = 0.6,
-                 device="cuda:0", seed: int = 0):
+                 device="cuda:0", seed: int = 0, spec: bool = True):
         self.hidden, self.inter, self.layers = hidden, inter, layers
         self.keep_ratio = keep_ratio
         self.k = keep_count(inter, keep_ratio)
@@ -65,6 +65,9 @@ class DIPStack:
         self.h = torch.empty(self.k, dtype=torch.bfloat16, device=dev)
         self.ws = torch.zeros(K.mlp_workspace_bytes(hidden, inter, self.k), dtype=torch.uint8,
                               device=dev)
+        # per-layer speculation state (None: every step runs stage by stage)
+        self.spec = spec
+        self.state = [K.mlp_state(dev) for _ in range(layers)] if spec else [None] * layers
         self.graph = None
 
     @property
@@ -73,10 +76,10 @@ class DIPStack:
 
     def run_token(self):
         """All layers on self.x, in stream order (one dip_mlp_decode each)."""
-        for lw, y in zip(self.w, self.y):
+        for lw, y, st in zip(self.w, self.y, self.state):
             K.mlp_decode(lw["gate_qw"], lw["gate_sc"], lw["up_qw"], lw["up_sc"],
                          lw["down_t_qw"], lw["down_t_sc"], self.x, self.k, y=y, g=self.g,
-                         idx=self.idx, h=self.h, ws=self.ws)
+                         idx=self.idx, h=self.h, ws=self.ws, state=st)
 
     def capture(self):
         """Capture run_token() as one HIP graph (after an eager warm-up)."""
@@ -100,12 +103,19 @@ class DIPStack:
     # -- per-stage timing --------------------------------------------------
     def stage_graphs(self):
         """One HIP graph per kernel stage, each launching that stage for every
-        layer back to back (on the intermediates the last token left)."""
+        layer back to back (on the intermediates the last token left).  With
+        speculation: gate_silu, gate_topk (gate + the top-k / speculative-up
+        launch) and down_gather (h by channel); without: gate_silu, gate_topk,
+        up_gather_h and down_gather."""
         lib = K.lib
         H, I, k = self.hidden, self.inter, self.k
-        topk_bytes = (lib.dip_topk_workspace_size(I) + 255) // 256 * 256
+        topk_bytes = 512
+        hfull_bytes = (2 * I + 255) // 256 * 256
         ws_ptr = self.ws.data_ptr()
         ws_n = self.ws.numel()
+        down_ws = ws_ptr + topk_bytes + hfull_bytes
+        down_n = ws_n - topk_bytes - hfull_bytes
+        h_full = ws_ptr + topk_bytes
         x = self.x.data_ptr()
 
         def gate(st):
@@ -114,13 +124,18 @@ class DIPStack:
                                            self.g.data_ptr(), I, H, 1, st), "gate")
 
         def gate_topk(st):
-            # the decode step's first half: gate GEMV + SiLU building the
-            # top-k histogram, then the top-k select
-            for lw in self.w:
-                K._check(lib.dip_gate_silu_topk(lw["gate_qw"].data_ptr(),
-                                                lw["gate_sc"].data_ptr(), x, self.g.data_ptr(),
-                                                self.idx.data_ptr(), I, H, k, ws_ptr, topk_bytes,
-                                                st), "gate_topk")
+            for lw, state in zip(self.w, self.state):
+                if self.spec:
+                    K._check(lib.dip_gate_silu_topk_spec(
+                        lw["gate_qw"].data_ptr(), lw["gate_sc"].data_ptr(),
+                        lw["up_qw"].data_ptr(), lw["up_sc"].data_ptr(), x, self.g.data_ptr(),
+                        self.idx.data_ptr(), h_full, I, H, k, ws_ptr, topk_bytes,
+                        state.data_ptr(), st), "gate_topk_spec")
+                else:
+                    K._check(lib.dip_gate_silu_topk(lw["gate_qw"].data_ptr(),
+                                                    lw["gate_sc"].data_ptr(), x,
+                                                    self.g.data_ptr(), self.idx.data_ptr(), I, H,
+                                                    k, ws_ptr, topk_bytes, st), "gate_topk")
 
         def up(st):
             for lw in self.w:
@@ -130,15 +145,25 @@ class DIPStack:
 
         def down(st):
             for lw, y in zip(self.w, self.y):
-                K._check(lib.dip_int4_gather_down(lw["down_t_qw"].data_ptr(),
-                                                  lw["down_t_sc"].data_ptr(), self.h.data_ptr(),
-                                                  self.idx.data_ptr(), y.data_ptr(), I, H, k,
-                                                  ctypes.c_void_p(ws_ptr + topk_bytes),
-                                                  ws_n - topk_bytes, st), "down")
+                if self.spec:
+                    K._check(lib.dip_int4_gather_down_by_channel(
+                        lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(), h_full,
+                        self.idx.data_ptr(), y.data_ptr(), self.h.data_ptr(), I, H, k,
+                        ctypes.c_void_p(down_ws), down_n, st), "down_by_channel")
+                else:
+                    K._check(lib.dip_int4_gather_down(lw["down_t_qw"].data_ptr(),
+                                                      lw["down_t_sc"].data_ptr(),
+                                                      self.h.data_ptr(), self.idx.data_ptr(),
+                                                      y.data_ptr(), I, H, k,
+                                                      ctypes.c_void_p(down_ws), down_n, st),
+                             "down")
 
+        stages = [("gate_silu", gate), ("gate_topk", gate_topk)]
+        if not self.spec:
+            stages.append(("up_gather_h", up))
+        stages.append(("down_gather", down))
         graphs = {}
-        for name, fn in (("gate_silu", gate), ("gate_topk", gate_topk), ("up_gather_h", up),
-                         ("down_gather", down)):
+        for name, fn in stages:
             s = torch.cuda.Stream(device=self.device)
             s.wait_stream(torch.cuda.current_stream(self.device))
             with torch.cuda.stream(s):
@@ -155,8 +180,9 @@ class DIPStack:
         """Average duration of one launch of each kernel stage: each stage's
         graph (one launch per layer, back to back) is replayed between two
         HIP events on the replaying stream; time / (layers * reps).  The
-        top-k runs on the histogram the gate launch builds, so its time is
-        that of gate + top-k minus that of the gate alone."""
+        top-k stage (with speculation: the top-k / speculative-up launch)
+        reads the g its gate launch wrote, so its time is that of gate +
+        top-k minus that of the gate alone."""
         self.run_token()
         torch.cuda.synchronize(self.device)
         graphs = self.stage_graphs()
@@ -172,5 +198,12 @@ class DIPStack:
             e1.record(stream)
             torch.cuda.synchronize(self.device)
             out[name] = e0.elapsed_time(e1) / (reps * self.layers)
-        out["topk"] = max(out.pop("gate_topk") - out["gate_silu"], 0.0)
-        return {name: out[name] for name in ("gate_silu", "topk", "up_gather_h", "down_gather")}
+        topk = max(out.pop("gate_topk") - out["gate_silu"], 0.0)
+        res = {"gate_silu": out["gate_silu"]}
+        if self.spec:
+            res["topk_spec_up"] = topk
+        else:
+            res["topk"] = topk
+            res["up_gather_h"] = out["up_gather_h"]
+        res["down_gather"] = out["down_gather"]
+        return res

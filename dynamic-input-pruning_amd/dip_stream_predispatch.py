@@ -7,10 +7,13 @@ gather kernels run.  On MI355X all MLP weights fit in HBM (a 64-layer Qwen3-32B
 MLP stack is ~13 GB of 288 GB), so this module keeps gate, up and the
 transposed down resident and runs the whole decode step on the GPU:
 
-    dip_mlp_decode:  gate GEMV + SiLU (+ top-k histogram)
-                  -> top-k finish (bit-exact reference order)
-                  -> up-row gather GEMV with h = bf16(g[idx] * u) fused
-                  -> transposed-down gather (deterministic two-stage sum)
+    dip_mlp_decode:  gate GEMV + SiLU
+                  -> one launch: the bit-exact threshold top-k, and meanwhile
+                     h = bf16(g * bf16(up . x)) for the channels this layer's
+                     previous token ranked highest (then any selected ones
+                     they missed)
+                  -> transposed-down gather of h[idx] (deterministic
+                     two-stage sum)
 
 with no host synchronisation, so consecutive layers (and HIP-graph captures of
 them) run back to back.  Constructor arguments, attributes and routing follow
@@ -135,6 +138,9 @@ class StreamingDIPMlp(nn.Module):
         self.down_t_sc = dn_t_sc.to(self.device).contiguous()
         self.out_features = self.down_t_qw.shape[1] * 2
         self.k = shared.k
+        # which channels the next token's up rows are speculated on (decides
+        # only which workgroups compute which h, never a value)
+        self._spec_state = K.mlp_state(self.device)
 
     def _gate(self, x):
         """gate_proj(x) (dip_stream_predispatch.py:166-174)."""
@@ -158,7 +164,8 @@ class StreamingDIPMlp(nn.Module):
         ws = b.workspace(hidden, self.inter, self.k)
         y, _, _, _ = K.mlp_decode(self.gate_qw, self.gate_sc, self.up_qw, self.up_sc,
                                   self.down_t_qw, self.down_t_sc, xv, self.k,
-                                  g=b.g(self.inter), idx=b.idx, h=b.h, ws=ws)
+                                  g=b.g(self.inter), idx=b.idx, h=b.h, ws=ws,
+                                  state=self._spec_state)
         return y
 
     def forward(self, x):

@@ -135,12 +135,16 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grids aim at CUs * this workgroups (2)
  *   DIP_TUNE_TOPK_STAMPS        1: the top-k records wall-clock phase stamps
  *                               in its workspace (diagnostics, slower) (0)
+ *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
+ *                               on the channels at or above the magnitude of
+ *                               rank k + inter * this / 1024 (0..1024) (32)
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
   DIP_TUNE_TOPK_STAMPS = 1,
-  DIP_TUNE_COUNT = 2
+  DIP_TUNE_SPEC_MARGIN = 2,
+  DIP_TUNE_COUNT = 3
 };
 int dip_set_tuning(int knob, int value);
 int dip_get_tuning(int knob);
@@ -210,19 +214,61 @@ int dip_transpose_down_int4(const int8_t* down_qw, const uint16_t* down_sc, int8
                             void* stream);
 
 /*
+ * The decode step's first half with speculative up rows: no counterpart in
+ * the reference (it replaces gate_kernel.py:29-33 + topk_kernel.py:29-40 +
+ * the up half of dip_stream_predispatch.py:196-199 by two launches):
+ *   1. g = bf16(silu(bf16(gate @ x))) [inter] (as dip_int4_gemv, DIP_ACT_SILU);
+ *   2. one launch: idx[0:k] as dip_topk_select(g), and meanwhile
+ *      h_full[c] = bf16(g[c] * bf16(up[c] . x)) for the channels c whose
+ *      magnitude key (|g| bits) is at or above state[0], then for the
+ *      selected channels below it (and channel 0 when slots are unfilled).
+ * h_full[idx[j]] is bit-identical to the h of dip_up_gather_h for every j;
+ * entries of unselected channels are unspecified.  state: 2 uint32 per layer
+ * (dip_mlp_state_size bytes, zero before the first call, then left to these
+ * calls): [0] the key in use, [1] the key of rank k + margin of the last call
+ * (DIP_TUNE_SPEC_MARGIN), moved to [0] by launch 1 of the next call.  The
+ * state only decides which workgroups compute which h, never a value.
+ * hidden / 32 must be 160, 128 or 80 (else DIP_ERR_UNSUPPORTED); 1 <= k <=
+ * inter <= dip_topk_max_n(); workspace: dip_topk_workspace_size(inter).
+ */
+size_t dip_mlp_state_size(void);
+int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
+                            const int8_t* up_qw, const uint16_t* up_sc, const uint16_t* x,
+                            uint16_t* g, int32_t* idx, uint16_t* h_full, int64_t inter,
+                            int64_t hidden, int64_t k, void* workspace, size_t ws_bytes,
+                            void* state, void* stream);
+
+/*
+ * dip_int4_gather_down with h indexed by channel: y = sum_j h_full[idx[j]] *
+ * down_t[idx[j]] (the down half of dip_stream_predispatch.py:196-203 after
+ * dip_gate_silu_topk_spec); h_out[j] = h_full[idx[j]] when h_out != NULL.
+ * Same workspace as dip_int4_gather_down.
+ */
+int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint16_t* scales,
+                                    const uint16_t* h_full, const int32_t* indices,
+                                    uint16_t* y, uint16_t* h_out, int64_t rows,
+                                    int64_t out_features, int64_t k, void* workspace,
+                                    size_t ws_bytes, void* stream);
+
+/*
  * One resident-weight DIP MLP decode step (batch 1, seq 1):
  *   g = silu(gate(x)); idx = topk(|g|, k); h = g[idx] * up[idx](x);
  *   y = h @ down_t[idx]
  * i.e. StreamingDIPMlp.forward (dip_stream_predispatch.py:176-204) with all
  * weights resident in HBM.  g_out [inter], idx_out [k], h_out [k] receive
  * the intermediates; y [hidden].  workspace: dip_mlp_workspace_size().
+ * layer_state (dip_mlp_state_size bytes per layer, zeroed once, or NULL):
+ * when set and the width allows, the step runs as dip_gate_silu_topk_spec +
+ * dip_int4_gather_down_by_channel (four launches); otherwise as
+ * dip_gate_silu_topk + dip_up_gather_h + dip_int4_gather_down (five).  Both
+ * give bit-identical outputs.
  */
 size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k);
 int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
                    const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
                    const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
                    uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
-                   void* workspace, size_t ws_bytes, void* stream);
+                   void* workspace, size_t ws_bytes, void* layer_state, void* stream);
 
 /*
  * Host-side row gather for the cache-aware miss path: copies rows

@@ -65,8 +65,29 @@ def test_argument_rejection_before_launch():
     assert L.dip_int4_gather_down(p, p, p, None, p, 10, 5120, 11, p, need, None) == -2
     # mlp: k > inter, missing outputs
     ws = L.dip_mlp_workspace_size(5120, 25600, 15360)
-    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 30000, p, ws, None) == -2
-    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, None, p, p, 5120, 25600, 100, p, ws, None) == -1
+    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 30000, p, ws, p,
+                            None) == -2
+    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, None, p, p, 5120, 25600, 100, p, ws, p,
+                            None) == -1
+    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 15360, p, ws - 1, p,
+                            None) == -5
+    # speculative first half: missing state, k = 0, unsupported width, misaligned state
+    tw = L.dip_topk_workspace_size(25600)
+    assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 100, p, tw, None,
+                                     None) == -1
+    assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 0, p, tw, p,
+                                     None) == -2
+    assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 1024, 100, p, tw, p,
+                                     None) == -4
+    assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 100, p, tw, p + 2,
+                                     None) == -3
+    assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 100, p, 8, p,
+                                     None) == -5
+    assert L.dip_int4_gather_down_by_channel(p, p, p, None, p, None, 25600, 5120, 10, p, need,
+                                             None) == -1
+    assert L.dip_mlp_state_size() == 8
+    assert L.dip_set_tuning(2, 1025) == -6
+    assert L.dip_set_tuning(2, -1) == -6
     assert L.dip_set_tuning(1, 7) == -6
     assert L.dip_set_tuning(0, 0) == -6
     assert L.dip_set_tuning(99, 1) == -6

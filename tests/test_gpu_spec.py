@@ -1,0 +1,175 @@
+"""GPU parity of the decode step with speculative up rows.
+
+dip_mlp_decode with a layer state runs the gate, then one launch holding the
+top-k select and the up rows of the channels the state names, then the down
+gather of h by channel.  Whatever the state holds, y, g, idx and h must be
+bit-identical to the stage-by-stage step (no state), which the other GPU
+tests pin against the oracle; the state itself must hold the magnitude key of
+rank k + margin of the last call's g.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dip_oracle as O
+from gpu_util import host_bf16
+
+pytestmark = pytest.mark.gpu
+
+MARGIN_PER_1024 = 32  # DIP_TUNE_SPEC_MARGIN default
+
+
+@pytest.fixture(scope="module")
+def K():
+    import _dip_hip
+    return _dip_hip
+
+
+def _weights(H, I, seed):
+    from quantize import quantize_tensor_int4_groupwise
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    out = []
+    for _ in range(3):
+        q, s = quantize_tensor_int4_groupwise(
+            torch.randn(I, H, device="cuda", generator=gen) * 0.02)
+        out += [q, s]
+    return out  # gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc
+
+
+def _x(H, seed):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    return torch.randn(H, device="cuda", generator=gen).to(torch.bfloat16)
+
+
+def _bits(t):
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t
+
+
+def _step(K, W, x, k, state=None):
+    return [t.clone() for t in K.mlp_decode(*W, x, k, state=state)]
+
+
+def _assert_same(a, b, what):
+    for name, u, v in zip(("y", "g", "idx", "h"), a, b):
+        assert torch.equal(_bits(u), _bits(v)), f"{what}: {name} differs"
+
+
+def _rank_key(g, r):
+    """Magnitude key (|bf16 bits|) of rank r (1 = largest) among the values
+    that are not NaN; 0 when there are fewer than r."""
+    keys = host_bf16(g).astype(np.int64) & 0x7FFF
+    keys = np.sort(keys[keys <= 0x7F80])[::-1]
+    return int(keys[r - 1]) if r <= len(keys) else 0
+
+
+@pytest.mark.parametrize("H,I,keep", [(5120, 25600, 0.6), (4096, 12288, 0.3), (2560, 9728, 0.6)])
+def test_spec_matches_stagewise(K, H, I, keep):
+    W = _weights(H, I, seed=H)
+    k = O.keep_count(I, keep)
+    state = K.mlp_state("cuda")
+    margin = I * MARGIN_PER_1024 // 1024
+    for t in range(4):
+        x = _x(H, 100 + t)
+        got = _step(K, W, x, k, state)
+        ref = _step(K, W, x, k)
+        _assert_same(got, ref, f"H={H} token {t}")
+        st = state.cpu().numpy().view(np.uint32)
+        assert st[1] == _rank_key(ref[1], k + margin), t
+        if t == 0:
+            assert st[0] == 0  # a zeroed state speculates on every channel
+
+
+def test_spec_any_state_value(K):
+    """Forced speculation keys: all channels, none (every selected channel is
+    a residual row of the select workgroups), the exact cut, half of the
+    selection, a wide margin, +inf."""
+    H, I = 4096, 12288
+    W = _weights(H, I, seed=7)
+    k = O.keep_count(I, 0.6)
+    x = _x(H, 5)
+    ref = _step(K, W, x, k)
+    g = ref[1]
+    keys = [0, 0xFFFF, _rank_key(g, k), _rank_key(g, k // 2), _rank_key(g, k + 2000), 0x7F80,
+            0x7FFF, 1]
+    for key in keys:
+        state = torch.tensor([key, key], dtype=torch.int32, device="cuda")
+        got = _step(K, W, x, k, state)
+        _assert_same(got, ref, f"key {key:#x}")
+
+
+def test_spec_unfilled_slots_use_channel_0(K):
+    """Fewer than k channels are nonzero: the unfilled slots point at channel
+    0, whose h must be computed even when it is neither selected nor
+    speculated on (including h = bf16(0 * u), which keeps u's sign)."""
+    H, I = 2560, 9728
+    W = _weights(H, I, seed=9)
+    gs = W[1].clone()
+    gs[200:] = 0            # g = silu(0) = 0 for all but 200 channels
+    gs[0] = 0               # channel 0 among the zeros
+    W0 = [W[0], gs] + W[2:]
+    k = O.keep_count(I, 0.3)
+    x = _x(H, 6)
+    ref = _step(K, W0, x, k)
+    assert (ref[2][200:] == 0).all()  # unfilled slots hold channel 0
+    for key in (0, 1, 0xFFFF, _rank_key(ref[1], 100)):
+        state = torch.tensor([key, key], dtype=torch.int32, device="cuda")
+        _assert_same(_step(K, W0, x, k, state), ref, f"key {key:#x}")
+    gs[0] = W[1][0]         # channel 0 nonzero again
+    ref = _step(K, W0, x, k)
+    for key in (0, 0xFFFF):
+        state = torch.tensor([key, key], dtype=torch.int32, device="cuda")
+        _assert_same(_step(K, W0, x, k, state), ref, f"key {key:#x}, channel 0 live")
+
+
+def test_spec_margin_knob(K):
+    H, I = 2560, 9728
+    W = _weights(H, I, seed=11)
+    k = O.keep_count(I, 0.6)
+    try:
+        for m in (0, 1024):
+            K.set_tuning("spec_margin", m)
+            state = K.mlp_state("cuda")
+            for t in range(3):
+                x = _x(H, 30 + t)
+                ref = _step(K, W, x, k)
+                _assert_same(_step(K, W, x, k, state), ref, f"margin {m} token {t}")
+                st = state.cpu().numpy().view(np.uint32)
+                assert st[1] == _rank_key(ref[1], k + I * m // 1024)
+    finally:
+        K.set_tuning("spec_margin", MARGIN_PER_1024)
+
+
+def test_spec_unsupported_width_runs_stagewise(K):
+    """A width without a speculative instantiation runs the stage-by-stage
+    step and leaves the state alone."""
+    H, I = 1024, 3072
+    W = _weights(H, I, seed=13)
+    k = O.keep_count(I, 0.6)
+    x = _x(H, 8)
+    state = K.mlp_state("cuda")
+    _assert_same(_step(K, W, x, k, state), _step(K, W, x, k), "H=1024")
+    assert (state == 0).all()
+
+
+def test_spec_stack_graph_replays(K):
+    """A 3-layer stack with speculation captured as one HIP graph: every
+    replay (new x each time, eager work and synchronisation in between)
+    equals the stage-by-stage eager run of the same weights."""
+    from dip_stack import DIPStack
+    H, I = 2560, 9728
+    spec = DIPStack(H, I, 3, 0.6, "cuda", seed=21, spec=True)
+    plain = DIPStack(H, I, 3, 0.6, "cuda", seed=21, spec=False)
+    for name in ("gate_qw", "up_qw", "down_t_qw"):
+        assert torch.equal(spec.w[2][name], plain.w[2][name])
+    spec.capture()
+    for rep in range(4):
+        x = _x(H, 50 + rep)
+        for y in spec.y:
+            y.zero_()
+        torch.randn(1000, device="cuda").sum().item()    # unrelated eager work
+        spec.step(x)
+        plain.x.copy_(x)
+        plain.run_token()
+        torch.cuda.synchronize()
+        for a, b in zip(spec.y, plain.y):
+            assert torch.equal(_bits(a), _bits(b)), rep
