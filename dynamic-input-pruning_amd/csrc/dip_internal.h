@@ -80,6 +80,9 @@ struct TopkMeta {
   int32_t pad;
   uint64_t stamp[6];   // wall_clock64() at the select kernel's phase boundaries (diagnostics)
   uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
+  // wall_clock64() in two speculation workgroups (the first and the middle
+  // one): start, list built, x staged, done (diagnostics)
+  uint64_t spec_stamp[2][4];
 };
 
 // The top-k workspace holds the last call's TopkMeta.

@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 0, 32};
+int g_tune[DIP_TUNE_COUNT] = {2, 0, 8};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }

@@ -179,10 +179,10 @@ DIP_DEV void residual_rows(const SpecArgs& sp, const uint32_t* rlist, int rcount
 // whose magnitude key |bits| is at or above the speculation key state[0]
 // (C = chan_per_wg <= kThreads).  The channels are compacted into an LDS
 // list (channel | g bits << 16); row group i takes entries i, i + groups, ...
-// with D rows in flight, the first D issued before x is staged.
+// with D rows in flight.
 template <int LPR, int CH>
 DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp, int u,
-                       uint32_t* lds) {
+                       uint32_t* lds, TopkMeta* __restrict__ meta, int stamps, int nspec) {
   constexpr int kGroups = kThreads / LPR;
   // rows in flight per group (16-lane groups: twice the groups, and more
   // rows in flight spill registers)
@@ -195,6 +195,9 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
   const uint32_t sk = sp.state[0];
   const int c0 = u * sp.chan_per_wg;
   const int c1 = min(c0 + sp.chan_per_wg, n);
+  const int sw = (u == 0) ? 0 : (u == nspec / 2 ? 1 : -1);
+  const bool stamp = stamps && sw >= 0 && tid == 0;
+  if (stamp) meta->spec_stamp[sw][0] = wall_clock64();
 
   uint4 xs[4];
   load_x_chunk(sp.x, nchunks, xs);
@@ -212,14 +215,19 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
     total += v;
   }
   if (f) lds[base + __popcll(m & ((1ull << lane) - 1ull))] = (uint32_t)c | (gb << 16);
-  __syncthreads();
+  if (stamp) meta->spec_stamp[sw][1] = wall_clock64();
+  // x pairs are staged before any row load is issued: with the whole chip
+  // streaming, issuing a wave's row loads stalls until data drains, and
+  // compute must be able to start as soon as the first rows arrive.
+  uint32_t* xlds = lds + kThreads;  // after the list
+  stage_x_pairs<LPR>(xs, xlds, nchunks);  // its barrier also publishes the list
+  if (stamp) meta->spec_stamp[sw][2] = wall_clock64();
   if (total == 0) return;  // workgroup-uniform
 
   const int grp = tid / LPR;
   const int l = tid % LPR;
   const size_t row_bytes = (size_t)(sp.hidden >> 1);
   const int ngr = sp.hidden >> 7;
-  uint32_t* xlds = lds + kThreads;  // after the list
   const int rounds = (total + kGroups - 1) / kGroups;
   RowRegs<CH> ring[D];
   uint32_t ent[D];
@@ -228,7 +236,6 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
     ent[d] = lds[min(grp + d * kGroups, total - 1)];
     load_row_at<LPR, CH>(sp.up_qw, sp.up_sc, ent[d] & 0xFFFFu, l, row_bytes, ngr, ring[d]);
   }
-  stage_x_pairs<LPR>(xs, xlds, nchunks);
   const uint4* xsrc = reinterpret_cast<const uint4*>(xlds);
   const float* xbias = reinterpret_cast<const float*>(xlds + nchunks * 16);
   for (int i0 = 0; i0 < rounds; i0 += D) {
@@ -270,6 +277,10 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
                              ring[d]);
       }
     }
+  }
+  if (stamps && sw >= 0) {  // when the last wave of the workgroup is done
+    __syncthreads();
+    if (stamp) meta->spec_stamp[sw][3] = wall_clock64();
   }
 }
 
@@ -536,16 +547,33 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
   const uint32_t uk = (uint32_t)k;
   const uint32_t pa0 = pre_a + (ex & 0xFFFFu);
   const uint32_t pb0 = tot_a + pre_b + (ex >> 16);
-  if (a0 | q0) {
-    const uint32_t pos = a0 ? pa0 : pb0;
-    if (pos < uk) idx[pos] = my;
-  }
-  if (a1 | q1) {
-    const uint32_t pos = a1 ? pa0 + a0 : pb0 + q0;
-    if (pos < uk) idx[pos] = my + 1;
-  }
+  const uint32_t pos0 = a0 ? pa0 : pb0;
+  const uint32_t pos1 = a1 ? pa0 + a0 : pb0 + q0;
   // unfilled slots (fewer than k values qualify) are 0, as in the reference
   const uint32_t filled = min(uk, tot_a + tot_b);
+  int rcount = 0;
+  if constexpr (SPEC) {
+    // Residual h: selected channels whose key is below the speculation key
+    // (the speculation workgroups compute every channel at or above it), and
+    // channel 0 when unfilled slots point at it.  The histogram is no longer
+    // read: its LDS holds the list and then the x pairs.  The list is
+    // published before the idx stores, so this barrier does not wait for them.
+    const bool r0 = (((a0 | q0) && pos0 < uk) || (my == 0 && filled < uk)) && b0 < sk;
+    const bool r1 = (a1 | q1) && pos1 < uk && b1 < sk;
+    const uint64_t m0 = __ballot(r0), m1 = __ballot(r1);
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint32_t n0 = (uint32_t)__popcll(m0), nw = n0 + (uint32_t)__popcll(m1);
+    uint32_t base = 0;
+    if (lane == 0 && nw) base = atomicAdd(&sh_rcount, nw);
+    base = (uint32_t)__shfl((int)base, 0, 64);
+    const uint32_t gpair = mine;
+    if (r0) hist[base + __popcll(m0 & below)] = (uint32_t)my | (gpair << 16);
+    if (r1) hist[base + n0 + __popcll(m1 & below)] = (uint32_t)(my + 1) | (gpair & 0xFFFF0000u);
+    __syncthreads();
+    rcount = (int)sh_rcount;
+  }
+  if ((a0 | q0) && pos0 < uk) idx[pos0] = my;
+  if ((a1 | q1) && pos1 < uk) idx[pos1] = my + 1;
   for (uint32_t p = filled + (uint32_t)(blockIdx.x * kThreads + tid); p < uk;
        p += (uint32_t)nblk * kThreads)
     idx[p] = 0;
@@ -554,27 +582,7 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
     meta->count_b = (int32_t)tot_b;
   }
   if constexpr (SPEC) {
-    // Residual h: selected channels whose key is below the speculation key
-    // (the speculation workgroups compute every channel at or above it), and
-    // channel 0 when unfilled slots point at it.  The histogram is no longer
-    // read: its LDS holds the list and then the x pairs.
-    const bool sel0 = (a0 | q0) && (a0 ? pa0 : pb0) < uk;
-    const bool sel1 = (a1 | q1) && (a1 ? pa0 + a0 : pb0 + q0) < uk;
-    const bool r0 = (sel0 || (my == 0 && filled < uk)) && b0 < sk;
-    const bool r1 = sel1 && b1 < sk;
-    const uint64_t m0 = __ballot(r0), m1 = __ballot(r1);
-    const uint64_t below = (1ull << lane) - 1ull;
-    const uint32_t n0 = (uint32_t)__popcll(m0), nw = n0 + (uint32_t)__popcll(m1);
-    uint32_t base = 0;
-    if (lane == 0 && nw) base = atomicAdd(&sh_rcount, nw);
-    base = (uint32_t)__shfl((int)base, 0, 64);
-    uint32_t* rlist = hist;
-    const uint32_t gpair = mine;
-    if (r0) rlist[base + __popcll(m0 & below)] = (uint32_t)my | (gpair << 16);
-    if (r1) rlist[base + n0 + __popcll(m1 & below)] = (uint32_t)(my + 1) | (gpair & 0xFFFF0000u);
-    __syncthreads();
-    const int rcount = (int)sh_rcount;
-    if (rcount > 0) residual_rows<LPR, CH>(sp, rlist, rcount, hist + kSlice);
+    if (rcount > 0) residual_rows<LPR, CH>(sp, hist, rcount, hist + kSlice);
   }
   if (stamp) {
     meta->stamp[5] = wall_clock64();
@@ -604,7 +612,8 @@ __global__ __launch_bounds__(kThreads) void topk_spec_kernel(
   if ((int)blockIdx.x < sp.ntopk)
     topk_body<R, true, LPR, CH>(s, n, k, idx, meta, stamps, sp.ntopk, sp, lds);
   else
-    spec_rows<LPR, CH>(s, n, sp, (int)blockIdx.x - sp.ntopk, lds);
+    spec_rows<LPR, CH>(s, n, sp, (int)blockIdx.x - sp.ntopk, lds, meta, stamps,
+                       (int)gridDim.x - sp.ntopk);
 }
 
 

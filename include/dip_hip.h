@@ -137,7 +137,7 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *                               in its workspace (diagnostics, slower) (0)
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
  *                               on the channels at or above the magnitude of
- *                               rank k + inter * this / 1024 (0..1024) (32)
+ *                               rank k + inter * this / 1024 (0..1024) (8)
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {

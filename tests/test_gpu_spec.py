@@ -16,7 +16,7 @@ from gpu_util import host_bf16
 
 pytestmark = pytest.mark.gpu
 
-MARGIN_PER_1024 = 32  # DIP_TUNE_SPEC_MARGIN default
+MARGIN_PER_1024 = 8  # DIP_TUNE_SPEC_MARGIN default
 
 
 @pytest.fixture(scope="module")
