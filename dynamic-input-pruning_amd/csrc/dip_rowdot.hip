@@ -11,15 +11,17 @@
 //     can wait for exactly the row it consumes (s_waitcnt vmcnt(N) with N > 0)
 //     while the next row stays in flight.  Loads under data-dependent
 //     branches would make it wait for everything.
-//   * Workgroups are 256 threads; ROWS is the fewest of 1, 2, 4, 8 that keeps
-//     the grid at about 2 workgroups per CU (a Qwen3-32B gate: 400
-//     workgroups of 8 groups x 8 rows; its up gather: 480 of 8 x 4).
+//   * Workgroups are 256 threads, exactly 2 per CU where 8 rows per group
+//     suffice (plan_rowdot): a Qwen3-32B gate runs 512 workgroups of 8 groups
+//     x 6-7 rows, its up gather 512 of 8 x 3-4.
 //   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
 //     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
 //     touches no LDS; otherwise each lane builds its own pairs from global
 //     memory.  The x loads are issued before the row loads.
 //   * The group reduction is DPP + permlane swaps (group_sum); lane l keeps
 //     the sum of row l and runs the epilogue for it.
+#include <algorithm>
+
 #include "dip_tiles.h"
 
 namespace dip {
@@ -118,17 +120,22 @@ struct RowdotPlan {
   int blocks;
 };
 
-// Rows per group for nrows outputs: the fewest of 1, 2, 4, 8 (at most LPR)
-// that keep the grid of 256-thread workgroups at about wgs_per_cu per CU.
-// (Measured on the Qwen3-32B shapes: 256-thread workgroups with 8 rows per
-// gate group and 4 per up group beat balanced grids of 5-wave or 8-wave
-// workgroups; a 5-wave workgroup leaves one SIMD per CU with an extra wave.)
+// The grid for nrows outputs: exactly CUs * wgs_per_cu 256-thread
+// workgroups whenever at most 8 rows per group cover the outputs, so every CU
+// gets the same number of workgroups; a group handles ROWS = ceil(rows per
+// group) outputs, the groups past nrows - (ROWS-1)*ngrp one fewer.  (On the
+// Qwen3-32B gate, 512 workgroups of 6-7 rows per group took 15.2 us against
+// 16.2 us for 400 workgroups of 8: with 1.56 workgroups per CU, 144 CUs
+// carried twice the rows of the other 112.  Three workgroups per CU of 4-5
+// rows took 15.9 us.)
 RowdotPlan plan_rowdot(int nrows, int lpr) {
   const int groups = 256 / lpr;
-  const long long target = (long long)device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU) * groups;
-  int rows = 1;
-  while (rows < 8 && rows < lpr && (long long)rows * target < nrows) rows *= 2;
-  return RowdotPlan{rows, groups, (nrows + rows * groups - 1) / (rows * groups)};
+  const long long wgs = (long long)device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
+  const long long need = (nrows + wgs * groups - 1) / (wgs * groups);
+  if (need <= 1)  // one row per group: no more workgroups than the rows fill
+    return RowdotPlan{1, groups, (int)std::max(1LL, std::min(wgs, (nrows + groups - 1LL) / groups))};
+  if (need <= 8) return RowdotPlan{(int)need, groups, (int)wgs};
+  return RowdotPlan{8, groups, (int)((nrows + 8LL * groups - 1) / (8LL * groups))};
 }
 
 template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
@@ -149,7 +156,11 @@ int launch_one(const RowdotArgs& a, hipStream_t stream) {
     switch (p.rows) {
       case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
       case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
+      case 3: launch_variant<LPR, CH, SRC, EPI, true, 3>(a, p, stream); break;
       case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
+      case 5: launch_variant<LPR, CH, SRC, EPI, true, 5>(a, p, stream); break;
+      case 6: launch_variant<LPR, CH, SRC, EPI, true, 6>(a, p, stream); break;
+      case 7: launch_variant<LPR, CH, SRC, EPI, true, 7>(a, p, stream); break;
       default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
     }
   } else {
