@@ -11,8 +11,9 @@ vector per token.  One token = one HIP-graph replay of all layers; the timed
 region covers exactly `steps` tokens, bracketed by device synchronisation.
 
 Besides the JSON line's `value` (tok/s) it reports:
-  roofline      the dominant kernel's algorithmic bytes / its average
-                duration (HIP events around each launch, on its stream);
+  roofline      the longest single-kernel stage's algorithmic bytes / its
+                average duration (HIP events around each launch, on its
+                stream);
   step_*        whole-token bytes / time against the same peak;
   cpu_baseline  the reference's forward run literally with PyTorch CPU ops
                 (oracle.torch_cpu_forward) on one layer of the same weights,
@@ -190,7 +191,11 @@ def main(argv=None):
                    # top-k + the up rows of the k selected channels (rows
                    # speculated on but not selected are not counted)
                    "topk_spec_up": 2 * I + 4 * k + k * row}
-    dom = max(stages, key=stages.get)
+    # the roofline names one kernel: the longest single-kernel stage (the down
+    # stage is two launches, the partial-sum kernel and its reduction, and is
+    # reported in stage_ms)
+    single = {name: v for name, v in stages.items() if name != "down_gather"}
+    dom = max(single, key=single.get)
     ach = stage_bytes[dom] / (stages[dom] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4),
