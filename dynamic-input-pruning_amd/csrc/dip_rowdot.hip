@@ -11,9 +11,9 @@
 //     can wait for exactly the row it consumes (s_waitcnt vmcnt(N) with N > 0)
 //     while the next row stays in flight.  Loads under data-dependent
 //     branches would make it wait for everything.
-//   * Workgroups are 256 threads, exactly 2 per CU where 8 rows per group
-//     suffice (plan_rowdot): a Qwen3-32B gate runs 512 workgroups of 8 groups
-//     x 6-7 rows, its up gather 512 of 8 x 3-4.
+//   * Workgroups are 256 threads (plan_rowdot): a Qwen3-32B gate runs exactly
+//     2 per CU, 512 workgroups of 8 groups x 6-7 rows; its up gather 480 of
+//     8 groups x 4 rows.
 //   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
 //     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
 //     touches no LDS; otherwise each lane builds its own pairs from global
@@ -120,22 +120,27 @@ struct RowdotPlan {
   int blocks;
 };
 
-// The grid for nrows outputs: exactly CUs * wgs_per_cu 256-thread
-// workgroups whenever at most 8 rows per group cover the outputs, so every CU
-// gets the same number of workgroups; a group handles ROWS = ceil(rows per
-// group) outputs, the groups past nrows - (ROWS-1)*ngrp one fewer.  (On the
-// Qwen3-32B gate, 512 workgroups of 6-7 rows per group took 15.2 us against
-// 16.2 us for 400 workgroups of 8: with 1.56 workgroups per CU, 144 CUs
-// carried twice the rows of the other 112.  Three workgroups per CU of 4-5
-// rows took 15.9 us.)
-RowdotPlan plan_rowdot(int nrows, int lpr) {
+// The grid for nrows outputs.  Contiguous rows (the gate): exactly
+// CUs * wgs_per_cu 256-thread workgroups whenever at most 8 rows per group
+// cover the outputs, so every CU gets the same number of workgroups; a group
+// handles ROWS = ceil(rows per group) outputs, the groups past
+// nrows - (ROWS-1)*ngrp one fewer.  (On the Qwen3-32B gate, 512 workgroups of
+// 6-7 rows per group took 15.2 us against 16.2 us for 400 workgroups of 8:
+// with 1.56 workgroups per CU, 144 CUs carried twice the rows of the other
+// 112.  Three workgroups per CU of 4-5 rows took 15.9 us.)  Gathered rows
+// keep the fewest of 1, 2, 4, 8 rows per group that hold the grid near
+// wgs_per_cu per CU (the 15360-row up gather: 480 x 8 x 4 rows, 9.9 us,
+// against 10.1 us for 512 x 8 x 3-4 rows).
+RowdotPlan plan_rowdot(int nrows, int lpr, bool balanced) {
   const int groups = 256 / lpr;
   const long long wgs = (long long)device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
   const long long need = (nrows + wgs * groups - 1) / (wgs * groups);
   if (need <= 1)  // one row per group: no more workgroups than the rows fill
     return RowdotPlan{1, groups, (int)std::max(1LL, std::min(wgs, (nrows + groups - 1LL) / groups))};
-  if (need <= 8) return RowdotPlan{(int)need, groups, (int)wgs};
-  return RowdotPlan{8, groups, (int)((nrows + 8LL * groups - 1) / (8LL * groups))};
+  if (balanced && need <= 8) return RowdotPlan{(int)need, groups, (int)wgs};
+  int rows = 1;
+  while (rows < 8 && rows < lpr && (long long)rows * wgs * groups < nrows) rows *= 2;
+  return RowdotPlan{rows, groups, (nrows + rows * groups - 1) / (rows * groups)};
 }
 
 template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
@@ -152,16 +157,25 @@ int launch_one(const RowdotArgs& a, hipStream_t stream) {
   // plan can pick is instantiated
   constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5);
   if constexpr (hot) {
-    const RowdotPlan p = plan_rowdot(a.nrows, LPR);
-    switch (p.rows) {
-      case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
-      case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
-      case 3: launch_variant<LPR, CH, SRC, EPI, true, 3>(a, p, stream); break;
-      case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
-      case 5: launch_variant<LPR, CH, SRC, EPI, true, 5>(a, p, stream); break;
-      case 6: launch_variant<LPR, CH, SRC, EPI, true, 6>(a, p, stream); break;
-      case 7: launch_variant<LPR, CH, SRC, EPI, true, 7>(a, p, stream); break;
-      default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
+    const RowdotPlan p = plan_rowdot(a.nrows, LPR, SRC == kContig);
+    if constexpr (SRC == kContig) {  // balanced plan: any rows per group up to 8
+      switch (p.rows) {
+        case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
+        case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
+        case 3: launch_variant<LPR, CH, SRC, EPI, true, 3>(a, p, stream); break;
+        case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
+        case 5: launch_variant<LPR, CH, SRC, EPI, true, 5>(a, p, stream); break;
+        case 6: launch_variant<LPR, CH, SRC, EPI, true, 6>(a, p, stream); break;
+        case 7: launch_variant<LPR, CH, SRC, EPI, true, 7>(a, p, stream); break;
+        default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
+      }
+    } else {  // power-of-two plan: 1, 2, 4 or 8
+      switch (p.rows) {
+        case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
+        case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
+        case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
+        default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
+      }
     }
   } else {
     const int rows = LPR >= 4 ? 4 : LPR;
