@@ -117,6 +117,9 @@ int64_t down_max_k();  // largest k the down path accepts
 // The top-k select kernel: idx from s (TopkMeta into the workspace).
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
                        hipStream_t stream);
+// The contiguous GEMV on int8 MFMA (DIP_ERR_UNSUPPORTED for shapes it does
+// not cover: the caller then runs the row-dot kernel).
+int launch_mfma_gemv(int epi, const RowdotArgs& a, hipStream_t stream);
 // The top-k + speculative-up launch (hidden widths of topk_spec_supported).
 bool topk_spec_supported(int64_t hidden);
 int launch_topk_spec(const uint16_t* g, int64_t n, int64_t k, int32_t* idx, void* ws,

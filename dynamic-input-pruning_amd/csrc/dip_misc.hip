@@ -147,7 +147,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 0, 8};
+int g_tune[DIP_TUNE_COUNT] = {2, 0, 8, 0};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -176,6 +176,9 @@ extern "C" int dip_set_tuning(int knob, int value) {
       break;
     case DIP_TUNE_SPEC_MARGIN:
       if (value < 0 || value > 1024) return DIP_ERR_ARG;
+      break;
+    case DIP_TUNE_GATE_MFMA:
+      if (value != 0 && value != 1) return DIP_ERR_ARG;
       break;
     default:
       return DIP_ERR_ARG;

@@ -211,6 +211,10 @@ int dispatch_layout(const RowdotArgs& a, hipStream_t stream) {
 
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream) {
   if (a.nrows == 0) return DIP_OK;
+  if (src == kContig && tuning(DIP_TUNE_GATE_MFMA)) {
+    const int st = launch_mfma_gemv(epi, a, stream);
+    if (st != DIP_ERR_UNSUPPORTED) return st;
+  }
 #define DIP_CASE(S, E) \
   if (src == (S) && epi == (E)) return dispatch_layout<S, E>(a, stream);
   DIP_CASE(kContig, kRaw)
