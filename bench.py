@@ -103,6 +103,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--shape", default="qwen3-32b")
     ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--checkpoint", default=None,
+                    help="bench the MLP stack of an int4 checkpoint in the reference's format "
+                         "(model_int4.safetensors + quant_config.json) instead of synthetic weights")
     ap.add_argument("--keep", type=float, default=0.6)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -126,14 +129,20 @@ def main(argv=None):
     import _dip_hip as K
     from dip_stack import SHAPES, DIPStack
 
-    shape = dict(SHAPES[args.shape])
-    if args.layers:
-        shape["layers"] = args.layers
     dev = torch.device("cuda:0")
-    print(f"[bench] building {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
-          flush=True)
-    stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0,
-                     spec=not args.no_spec)
+    if args.checkpoint:
+        print(f"[bench] loading MLPs of {args.checkpoint} keep={args.keep}", file=sys.stderr,
+              flush=True)
+        stack = DIPStack.from_checkpoint(args.checkpoint, args.keep, dev, spec=not args.no_spec)
+        shape = dict(hidden=stack.hidden, inter=stack.inter, layers=stack.layers)
+    else:
+        shape = dict(SHAPES[args.shape])
+        if args.layers:
+            shape["layers"] = args.layers
+        print(f"[bench] building {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
+              flush=True)
+        stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0,
+                         spec=not args.no_spec)
     gen = torch.Generator(device=dev).manual_seed(1)
     n_tok = args.warmup + args.steps
     xs = (torch.randn(n_tok, shape["hidden"], device=dev, generator=gen)).to(torch.bfloat16)
@@ -199,7 +208,8 @@ def main(argv=None):
     ach = stage_bytes[dom] / (stages[dom] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.shape, args.keep, dom, K),
+                "traffic": None if args.checkpoint else measured_traffic(args.shape, args.keep,
+                                                                         dom, K),
                 "kernel": dom, "bytes_per_launch": stage_bytes[dom],
                 "avg_launch_ms": round(stages[dom], 5)}
     print(f"[bench] stages (ms): {json.dumps({k_: round(v, 5) for k_, v in stages.items()})}",
@@ -222,12 +232,14 @@ def main(argv=None):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
+        "data": "synthetic" if not args.checkpoint else "checkpoint weights, synthetic x",
         "config": {
-            "workload": f"{args.shape}-shape {stack.layers}-layer int4 g128 DIP MLP decode, "
+            "workload": (f"{args.shape}-shape" if not args.checkpoint else "checkpoint") +
+                        f" {stack.layers}-layer int4 g128 DIP MLP decode, "
                         f"batch 1, keep {args.keep}, weights resident in HBM",
             "hidden": H, "inter": I, "layers": stack.layers, "k": k,
-            "weights": "int4 g128 symmetric, bf16 scales; N(0,0.02) draws",
+            "weights": ("int4 g128 symmetric, bf16 scales; " +
+                        ("N(0,0.02) draws" if not args.checkpoint else "from the checkpoint")),
             "activations": "bf16, fp32 accumulate",
             "speculative_up": not args.no_spec,
             "bytes_per_token": stack.bytes_per_token,

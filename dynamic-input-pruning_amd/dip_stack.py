@@ -43,21 +43,25 @@ def bytes_per_layer(hidden: int, inter: int, k: int) -> int:
 
 class DIPStack:
     def __init__(self, hidden: int, inter: int, layers: int, keep_ratio: float = 0.6,
-                 device="cuda:0", seed: int = 0, spec: bool = True):
+                 device="cuda:0", seed: int = 0, spec: bool = True, weights=None):
         self.hidden, self.inter, self.layers = hidden, inter, layers
         self.keep_ratio = keep_ratio
         self.k = keep_count(inter, keep_ratio)
         self.device = torch.device(device)
         dev = self.device
-        gen = torch.Generator(device=dev).manual_seed(seed)
-        self.w = []
-        for _ in range(layers):
-            lw = {}
-            for name in ("gate", "up", "down_t"):
-                q, s = quantize_tensor_int4_groupwise(
-                    torch.randn(inter, hidden, device=dev, generator=gen) * 0.02)
-                lw[name + "_qw"], lw[name + "_sc"] = q, s
-            self.w.append(lw)
+        if weights is not None:  # per layer: gate/up/down_t qweight + scales on `device`
+            self.w = [{n: lw[n] for n in ("gate_qw", "gate_sc", "up_qw", "up_sc", "down_t_qw",
+                                          "down_t_sc")} for lw in weights]
+        else:
+            gen = torch.Generator(device=dev).manual_seed(seed)
+            self.w = []
+            for _ in range(layers):
+                lw = {}
+                for name in ("gate", "up", "down_t"):
+                    q, s = quantize_tensor_int4_groupwise(
+                        torch.randn(inter, hidden, device=dev, generator=gen) * 0.02)
+                    lw[name + "_qw"], lw[name + "_sc"] = q, s
+                self.w.append(lw)
         self.x = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
         self.y = [torch.empty(hidden, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
         self.g = torch.empty(inter, dtype=torch.bfloat16, device=dev)
@@ -69,6 +73,16 @@ class DIPStack:
         self.spec = spec
         self.state = [K.mlp_state(dev) for _ in range(layers)] if spec else [None] * layers
         self.graph = None
+
+    @classmethod
+    def from_checkpoint(cls, ckpt_dir, keep_ratio: float = 0.6, device="cuda:0",
+                        spec: bool = True):
+        """Every MLP of an int4 checkpoint in the reference's format
+        (dip_checkpoint), resident on `device`, in layer order."""
+        from dip_checkpoint import load_mlp_layers
+        layers = load_mlp_layers(ckpt_dir, device)
+        inter, hidden = layers[0]["up_qw"].shape[0], layers[0]["up_qw"].shape[1] * 2
+        return cls(hidden, inter, len(layers), keep_ratio, device, spec=spec, weights=layers)
 
     @property
     def bytes_per_token(self) -> int:
