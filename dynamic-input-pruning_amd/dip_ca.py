@@ -76,6 +76,9 @@ class CABuffers:
 class CADIPMlp(nn.Module):
     """MLP with a resident channel cache (dip_ca.py:73-196)."""
 
+    # each decode token reads the hit/miss counts back to the host
+    graph_capturable = False
+
     def __init__(self, gate_qw, gate_sc, up_qw, up_sc, down_qw, down_sc, buf,
                  keep_ratio=0.6, cache_frac=0.3, device="cuda:0", down_transposed=False):
         super().__init__()
@@ -189,3 +192,84 @@ def calibrate_cache_from_counts(cas, counts):
     selection counts gathered by any calibration pass."""
     for c, cnt in zip(cas, counts):
         c.set_cache(hot_ids_from_counts(cnt))
+
+
+def load_dip_ca(ckpt_dir, gpu_mem_gib=10, cpu_mem_gib=60, keep_ratio=0.6, cache_frac=0.3,
+                device="cuda:0"):
+    """The reference's cache-aware whole-model loader (dip_ca.py:199-269):
+    the causal LM of `ckpt_dir/config.json` with QuantLinear projections and
+    every decoder MLP replaced by a CADIPMlp (one CABuffers for all), the
+    remaining tensors loaded on `device`.  The caches are empty until
+    calibrate_cache (or calibrate_cache_from_counts) fills them; until then
+    the modules take their dense route.  Returns (model, tokenizer or None,
+    list of the CADIPMlp modules).  gpu_mem_gib / cpu_mem_gib are accepted
+    for call compatibility (no offload map: the non-MLP weights are
+    resident, the MLP weights live pinned on the host by design)."""
+    from pathlib import Path
+    from dip_checkpoint import ST_NAME, iter_mlp_layers
+    from dip_model import (build_empty_model, load_tensors, load_tokenizer, mlp_module_names,
+                           swap_modules)
+    ckpt_dir = Path(ckpt_dir)
+    model = build_empty_model(ckpt_dir)
+    names = mlp_module_names(model)
+    if not names:
+        raise ValueError(f"{ckpt_dir}: the model has no gate/up/down MLP")
+    buf, cas = None, []
+    for L in iter_mlp_layers(ckpt_dir, device, names):
+        if buf is None:
+            inter = L["up_qw"].shape[0]
+            out_f = L["down_t_qw"].shape[1] * 2
+            buf = CABuffers(int(round(inter * keep_ratio)), L["up_qw"].shape[1],
+                            L["up_sc"].shape[1], out_f, out_f // GROUP_SIZE, device)
+        cas.append(CADIPMlp(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"], L["down_t_qw"],
+                            L["down_t_sc"], buf, keep_ratio, cache_frac, device,
+                            down_transposed=True))
+        del L
+    swap_modules(model, names, cas)
+    load_tensors(model, ckpt_dir / ST_NAME, device, skip_prefixes=names)
+    return model, load_tokenizer(ckpt_dir), cas
+
+
+def calibrate_cache(model, tok, cas, prompt, calib_tokens=30):
+    """Count how often each channel is selected over a short greedy
+    generation, then make each layer's most selected channels resident
+    (dip_ca.py:272-309).  `prompt` is a string (run through the tokenizer's
+    chat template, as the reference does) or a token-id tensor [1, P].
+
+    The forward hooks select with the module's own gate + SiLU + top-k
+    kernel and count on the GPU, so the pass adds no host synchronisation;
+    the hot set follows the reference's (count desc, id asc) order."""
+    counts = [torch.zeros(c.inter, dtype=torch.long, device=c.device) for c in cas]
+
+    def make_hook(lid, c):
+        def hook(module, inp, out):
+            x = inp[0]
+            if x.dim() == 3 and x.shape[1] == 1:
+                for b in range(x.shape[0]):
+                    _, idx = K.gate_silu_topk(c.gate_qw, c.gate_sc, x[b, 0].to(torch.bfloat16),
+                                              c.k)
+                    counts[lid].index_add_(0, idx.long(),
+                                           torch.ones_like(idx, dtype=torch.long))
+        return hook
+
+    handles = [c.register_forward_hook(make_hook(lid, c)) for lid, c in enumerate(cas)]
+    if isinstance(prompt, str):
+        if tok is None:
+            raise ValueError("a text prompt needs a tokenizer")
+        ids = tok.apply_chat_template([{"role": "user", "content": prompt}],
+                                      add_generation_prompt=True, return_tensors="pt")
+        if not torch.is_tensor(ids):
+            ids = ids["input_ids"]
+    else:
+        ids = torch.as_tensor(prompt).view(1, -1)
+    dev = cas[0].device
+    pad = tok.eos_token_id if tok is not None else model.config.eos_token_id
+    try:
+        with torch.no_grad():
+            model.generate(ids.to(dev), max_new_tokens=calib_tokens, do_sample=False,
+                           use_cache=True, pad_token_id=pad)
+    finally:
+        for h in handles:
+            h.remove()
+    calibrate_cache_from_counts(cas, [c.cpu() for c in counts])
+    return counts

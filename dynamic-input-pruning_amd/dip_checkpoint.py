@@ -106,10 +106,11 @@ def mlp_names(st_path) -> list:
     return sorted(found, key=_natural_key)
 
 
-def load_mlp_layers(ckpt_dir, device="cuda:0", names=None) -> list:
-    """Per MLP (layer order): {'name', 'gate_qw', 'gate_sc', 'up_qw', 'up_sc',
-    'down_t_qw', 'down_t_sc'} resident on `device`; down is transposed to
-    [inter, hidden/2] on the GPU (dip_stream_predispatch.py:100-120)."""
+def iter_mlp_layers(ckpt_dir, device="cuda:0", names=None):
+    """Per MLP (layer order) a dict {'name', 'gate_qw', 'gate_sc', 'up_qw',
+    'up_sc', 'down_t_qw', 'down_t_sc'} resident on `device`, read one layer
+    at a time; down is transposed to [inter, hidden/2] on the GPU
+    (dip_stream_predispatch.py:100-120)."""
     ckpt_dir = Path(ckpt_dir)
     read_quant_config(ckpt_dir)
     st_path = ckpt_dir / ST_NAME
@@ -117,26 +118,34 @@ def load_mlp_layers(ckpt_dir, device="cuda:0", names=None) -> list:
     if not names:
         raise ValueError(f"{st_path}: no MLP with gate/up/down qweight and scales")
     dev = torch.device(device)
-    layers = []
     with safe_open(str(st_path), framework="pt", device="cpu") as f:
+        keys = set(f.keys())
         for m in names:
+            missing = [f"{m}.{p}.{t}" for p in _PROJ for t in ("qweight", "scales")
+                       if f"{m}.{p}.{t}" not in keys]
+            if missing:
+                raise ValueError(f"{st_path}: missing {missing}")
             t = {f"{p.split('_')[0]}_{kind}": f.get_tensor(f"{m}.{p}.{full}").to(dev)
                  for p in _PROJ for kind, full in (("qw", "qweight"), ("sc", "scales"))}
             d_qw, d_sc = K.transpose_down_int4(t.pop("down_qw"), t.pop("down_sc"))
             inter, hidden = t["up_qw"].shape[0], t["up_qw"].shape[1] * 2
             if t["gate_qw"].shape != (inter, hidden // 2) or d_qw.shape != (inter, hidden // 2):
                 raise ValueError(f"{m}: gate/up/down shapes disagree")
-            layers.append(dict(name=m, down_t_qw=d_qw, down_t_sc=d_sc, **t))
-    return layers
+            yield dict(name=m, down_t_qw=d_qw, down_t_sc=d_sc, **t)
 
 
-def load_streaming_mlps(ckpt_dir, keep_ratio=0.6, device="cuda:0"):
+def load_mlp_layers(ckpt_dir, device="cuda:0", names=None) -> list:
+    """Every MLP of the checkpoint as iter_mlp_layers yields them."""
+    return list(iter_mlp_layers(ckpt_dir, device, names))
+
+
+def load_streaming_mlps(ckpt_dir, keep_ratio=0.6, device="cuda:0", names=None):
     """The MLP half of the reference's load_streaming_dip
     (dip_stream_predispatch.py:218-246): one StreamingDIPMlp per MLP of the
     checkpoint, all sharing one SharedBuffers.  Returns (names, modules,
     shared)."""
     from dip_stream_predispatch import SharedBuffers, StreamingDIPMlp
-    layers = load_mlp_layers(ckpt_dir, device)
+    layers = load_mlp_layers(ckpt_dir, device, names)
     first = layers[0]
     inter = first["up_qw"].shape[0]
     out_f = first["down_t_qw"].shape[1] * 2

@@ -1,0 +1,287 @@
+"""Whole-model integration: an HF Qwen3 built from an int4 checkpoint with
+its MLPs swapped for DIP modules, and a decode loop captured in one HIP graph.
+
+Loading follows the reference's sequence (dip_stream_predispatch.py:218-289,
+dip_ca.py:199-269, qlinear.py:109-166): build the architecture of
+`config.json` with empty weights, swap the seven projections for QuantLinear,
+swap each decoder MLP for a DIP module, then load every other tensor of
+model_int4.safetensors.  One MI355X holds the whole model in HBM, so every
+tensor goes to one device; there is no offload map.
+
+``DIPDecoder`` runs greedy decoding.  The prompt goes through the HF forward
+(the reference's prefill: the DIP modules take their dense route for
+sequences longer than one token), then its key/value cache is copied into a
+static cache and every further token runs one decode step that reads nothing
+from the host: embedding, per layer RMSNorm -> q/k/v projections (int4 GEMV)
+-> q/k RMSNorm -> rotary embedding from a precomputed table -> cache write
+at the device-side position -> attention over the static cache with a
+position mask -> o projection -> RMSNorm -> DIP MLP, then the final norm,
+lm_head and argmax.  With ``use_graph`` the step (including the argmax and
+the position update) is captured once in a HIP graph and replayed per token.
+The step uses the model's own modules, so the decode math is the HF model's
+(transformers' Qwen3DecoderLayer / Qwen3Attention forward).
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from safetensors import safe_open
+
+from qlinear import _replace_linears_with_quant
+
+# Rotary types whose inverse frequencies are fixed at construction; the
+# dynamic ones recompute them from the sequence length at run time.
+_STATIC_ROPE = ("default", "linear", "yarn", "llama3")
+
+
+def build_empty_model(ckpt_dir, dtype=torch.bfloat16):
+    """The causal LM of `ckpt_dir/config.json` with weights on the meta device
+    (buffers computed at construction, such as rotary frequencies, stay
+    real) and QuantLinear projections."""
+    from accelerate import init_empty_weights
+    from transformers import AutoConfig, AutoModelForCausalLM
+    config = AutoConfig.from_pretrained(str(ckpt_dir))
+    with init_empty_weights():
+        model = AutoModelForCausalLM.from_config(config, dtype=dtype)
+    _replace_linears_with_quant(model)
+    return model.eval()
+
+
+def mlp_module_names(model: nn.Module) -> list:
+    """Names of the modules holding gate/up/down QuantLinear projections, in
+    model order (the reference's selection, dip_stream_predispatch.py:231-233)."""
+    from qlinear import QuantLinear
+    return [n for n, m in model.named_modules()
+            if all(hasattr(m, p) for p in ("gate_proj", "up_proj", "down_proj"))
+            and isinstance(m.up_proj, QuantLinear)]
+
+
+def swap_modules(model: nn.Module, names, modules) -> None:
+    """Put each module of `modules` where `model.<name>` was."""
+    for name, mod in zip(names, modules):
+        parent_name, _, attr = name.rpartition(".")
+        setattr(model.get_submodule(parent_name) if parent_name else model, attr, mod)
+
+
+def _set_tensor(model: nn.Module, key: str, value: torch.Tensor, device) -> None:
+    mod_name, _, attr = key.rpartition(".")
+    mod = model.get_submodule(mod_name) if mod_name else model
+    if attr in mod._parameters:
+        old = mod._parameters[attr]
+    elif attr in mod._buffers:
+        old = mod._buffers[attr]
+    else:
+        raise KeyError(f"{key}: the model has no such parameter or buffer")
+    if tuple(old.shape) != tuple(value.shape):
+        raise ValueError(f"{key}: checkpoint shape {tuple(value.shape)}, model "
+                         f"{tuple(old.shape)}")
+    dt = old.dtype if old.dtype.is_floating_point and value.dtype.is_floating_point else value.dtype
+    t = value.to(device=device, dtype=dt)
+    if attr in mod._parameters:
+        mod._parameters[attr] = nn.Parameter(t, requires_grad=False)
+    else:
+        mod._buffers[attr] = t
+
+
+def load_tensors(model: nn.Module, st_path, device, skip_prefixes=()) -> None:
+    """Load every tensor of `st_path` into `model` on `device`, except those
+    under a module named in `skip_prefixes` (the swapped MLPs, whose weights
+    their DIP modules already hold).  Ties lm_head to the embedding when the
+    config says so and the checkpoint has no lm_head, moves the buffers made
+    at construction to `device`, and raises if any parameter or buffer is
+    still empty."""
+    device = torch.device(device)
+    skip = tuple(p + "." for p in skip_prefixes)
+    with safe_open(str(st_path), framework="pt", device="cpu") as f:
+        keys = list(f.keys())
+        for key in keys:
+            if key.startswith(skip):
+                continue
+            _set_tensor(model, key, f.get_tensor(key), device)
+    if getattr(model.config, "tie_word_embeddings", False) and "lm_head.weight" not in keys:
+        model.lm_head.weight = model.get_input_embeddings().weight
+    for mod in model.modules():
+        for name, buf in list(mod._buffers.items()):
+            if buf is not None and not buf.is_meta and buf.device != device:
+                mod._buffers[name] = buf.to(device)
+    empty = [n for n, t in list(model.named_parameters()) + list(model.named_buffers())
+             if t.is_meta]
+    if empty:
+        raise ValueError(f"{st_path}: no tensor for {len(empty)} model entries, e.g. "
+                         f"{empty[:4]}")
+
+
+def load_tokenizer(ckpt_dir):
+    """The checkpoint's tokenizer, or None when the directory holds none."""
+    ckpt_dir = Path(ckpt_dir)
+    if not any((ckpt_dir / f).exists() for f in ("tokenizer.json", "tokenizer_config.json")):
+        return None
+    from transformers import AutoTokenizer
+    return AutoTokenizer.from_pretrained(str(ckpt_dir))
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class DIPDecoder:
+    """Greedy decoding of a Qwen3 causal LM with a static key/value cache and
+    a HIP-graph decode step.  Batch size 1, as the reference's decode.
+
+    Args:
+      model:     a Qwen3ForCausalLM-shaped model (model.model.layers[i] with
+                 self_attn.{q,k,v,o}_proj, q_norm, k_norm, input_layernorm,
+                 post_attention_layernorm and mlp); any MLP module works.
+      max_len:   cache length (prompt + generated tokens).
+      use_graph: capture the decode step in a HIP graph (needs a GPU and MLP
+                 modules that read nothing back to the host per token; a
+                 module says it does with `graph_capturable = False`).
+    """
+
+    def __init__(self, model: nn.Module, max_len: int = 2048, use_graph: bool = True):
+        inner = model.model
+        cfg = model.config
+        self.model = model
+        self.layers = list(inner.layers)
+        emb = inner.embed_tokens.weight
+        self.device, self.dtype = emb.device, emb.dtype
+        att = self.layers[0].self_attn
+        self.hd = att.head_dim
+        self.nh = cfg.num_attention_heads
+        self.nkv = cfg.num_key_value_heads
+        if any(getattr(L.self_attn, "sliding_window", None) for L in self.layers):
+            raise ValueError("sliding-window attention layers are not supported")
+        rot = inner.rotary_emb
+        if rot.rope_type not in _STATIC_ROPE:
+            raise ValueError(f"rope type {rot.rope_type!r}: frequencies change with length")
+        self.max_len = int(max_len)
+        pos = torch.arange(self.max_len, dtype=torch.float32, device=self.device)
+        freqs = pos[:, None] * rot.inv_freq.to(self.device, torch.float32)[None, :]
+        table = torch.cat((freqs, freqs), dim=-1)
+        self.cos = (table.cos() * rot.attention_scaling).to(self.dtype)
+        self.sin = (table.sin() * rot.attention_scaling).to(self.dtype)
+        shape = (len(self.layers), self.nkv, self.max_len, self.hd)
+        self.k_cache = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        self.v_cache = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        self._cols = torch.arange(self.max_len, device=self.device)
+        self.tok = torch.zeros(1, dtype=torch.long, device=self.device)
+        self.pos = torch.zeros(1, dtype=torch.long, device=self.device)
+        self.use_graph = bool(use_graph) and self.device.type == "cuda"
+        if self.use_graph:
+            bad = [i for i, L in enumerate(self.layers)
+                   if not getattr(L.mlp, "graph_capturable", True)]
+            if bad:
+                raise ValueError(f"the MLPs of layers {bad[:4]} synchronise with the host "
+                                 "per token and cannot be captured; use use_graph=False")
+        self.graph = None
+        self._logits = None
+
+    # -- one decode step (device-side token and position) ---------------------
+    def _forward_step(self) -> torch.Tensor:
+        inner = self.model.model
+        hd = self.hd
+        h = inner.embed_tokens(self.tok).view(1, 1, -1)
+        cos = self.cos.index_select(0, self.pos).view(1, 1, 1, hd)
+        sin = self.sin.index_select(0, self.pos).view(1, 1, 1, hd)
+        mask = torch.zeros(self.max_len, dtype=self.dtype, device=self.device).masked_fill(
+            self._cols > self.pos, float("-inf")).view(1, 1, 1, self.max_len)
+        for i, layer in enumerate(self.layers):
+            a = layer.self_attn
+            x = layer.input_layernorm(h)
+            q = a.q_norm(a.q_proj(x).view(1, 1, -1, hd)).transpose(1, 2)
+            k = a.k_norm(a.k_proj(x).view(1, 1, -1, hd)).transpose(1, 2)
+            v = a.v_proj(x).view(1, 1, -1, hd).transpose(1, 2)
+            q = q * cos + _rotate_half(q) * sin
+            k = k * cos + _rotate_half(k) * sin
+            self.k_cache[i].index_copy_(1, self.pos, k[0])
+            self.v_cache[i].index_copy_(1, self.pos, v[0])
+            # query head j reads key/value head j // (nh / nkv); the one-token
+            # queries of a group are the rows of one attention call, so the
+            # cache is read once per kv head and never repeated
+            qg = q.reshape(1, self.nkv, self.nh // self.nkv, hd)
+            o = F.scaled_dot_product_attention(qg, self.k_cache[i:i + 1], self.v_cache[i:i + 1],
+                                               attn_mask=mask, scale=a.scaling)
+            h = h + a.o_proj(o.reshape(1, 1, -1))
+            h = h + layer.mlp(layer.post_attention_layernorm(h))
+        return self.model.lm_head(inner.norm(h)).view(-1)
+
+    def _step_and_advance(self) -> torch.Tensor:
+        logits = self._forward_step()
+        self.tok.copy_(logits.argmax().view(1))
+        self.pos.add_(1)
+        return logits
+
+    @torch.no_grad()
+    def step(self) -> torch.Tensor:
+        """Decode the token in `self.tok` at position `self.pos`; afterwards
+        `self.tok` holds the argmax and `self.pos` has advanced by one.
+        Returns the logits (a buffer the next step overwrites)."""
+        if not self.use_graph:
+            return self._step_and_advance()
+        if self.graph is None:
+            # the first step runs eagerly (it also makes every lazily created
+            # buffer), then the same step is captured for the later tokens
+            out = self._step_and_advance()
+            torch.cuda.synchronize(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._logits = self._step_and_advance()
+            self.graph = g
+            return out
+        self.graph.replay()
+        return self._logits
+
+    # -- prompt ---------------------------------------------------------------
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Run the prompt [1, P] through the HF forward, copy its key/value
+        cache into the static cache, set `tok` to the argmax of the last
+        logits and `pos` to P.  Returns the last logits."""
+        from transformers import DynamicCache
+        ids = input_ids.to(self.device).view(1, -1)
+        plen = ids.shape[1]
+        if plen < 1 or plen >= self.max_len:
+            raise ValueError(f"prompt length {plen} outside [1, {self.max_len})")
+        cache = DynamicCache(config=self.model.config)
+        out = self.model(input_ids=ids, past_key_values=cache, use_cache=True)
+        for i, layer in enumerate(cache.layers):
+            self.k_cache[i, :, :plen].copy_(layer.keys[0])
+            self.v_cache[i, :, :plen].copy_(layer.values[0])
+        logits = out.logits[0, -1]
+        self.tok.copy_(logits.argmax().view(1))
+        self.pos.fill_(plen)
+        return logits
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, eos_token_id=None,
+                 return_logits: bool = False):
+        """Greedy continuation of `input_ids` [1, P]: the prompt followed by up
+        to `max_new_tokens` tokens (cut after the first `eos_token_id`), as
+        HF's generate(do_sample=False) returns it for batch 1.  With
+        `return_logits` also the logits of every generated token."""
+        ids = input_ids.to(self.device).view(1, -1)
+        plen = ids.shape[1]
+        if plen + max_new_tokens > self.max_len:
+            raise ValueError(f"{plen} + {max_new_tokens} tokens exceed max_len {self.max_len}")
+        toks = torch.empty(max_new_tokens, dtype=torch.long, device=self.device)
+        logs = []
+        last = self.prefill(ids)
+        for t in range(max_new_tokens):
+            if return_logits:
+                logs.append(last.float().clone())
+            toks[t:t + 1].copy_(self.tok)
+            if t + 1 < max_new_tokens:
+                last = self.step()
+        out = toks.cpu()
+        if eos_token_id is not None:
+            eos = set(eos_token_id if isinstance(eos_token_id, (list, tuple)) else [eos_token_id])
+            for t, v in enumerate(out.tolist()):
+                if v in eos:
+                    out = out[: t + 1]
+                    break
+        seq = torch.cat([ids[0].cpu(), out]).view(1, -1)
+        return (seq, torch.stack(logs)) if return_logits else seq

@@ -188,3 +188,29 @@ class StreamingDIPMlp(nn.Module):
     # Introspection used by tests: the intermediates of the last decode call.
     def last_selection(self):
         return self.buf.idx, self.buf.h, self.buf.g(self.inter)
+
+
+def load_streaming_dip(ckpt_dir, gpu_mem_gib=10, cpu_mem_gib=60, keep_ratio=0.6,
+                       device="cuda:0"):
+    """The reference's whole-model loader (dip_stream_predispatch.py:218-289):
+    the causal LM of `ckpt_dir/config.json` with QuantLinear projections,
+    every decoder MLP replaced by a StreamingDIPMlp (one SharedBuffers for
+    all), and the remaining tensors of model_int4.safetensors loaded.
+    Returns (model, tokenizer or None, list of the StreamingDIPMlp modules).
+
+    Every tensor is resident on `device` (a whole int4 Qwen3-32B fits one
+    MI355X), so the reference's accelerate offload sizes gpu_mem_gib /
+    cpu_mem_gib are accepted for call compatibility only."""
+    from pathlib import Path
+    from dip_checkpoint import ST_NAME, load_streaming_mlps
+    from dip_model import (build_empty_model, load_tensors, load_tokenizer, mlp_module_names,
+                           swap_modules)
+    ckpt_dir = Path(ckpt_dir)
+    model = build_empty_model(ckpt_dir)
+    names = mlp_module_names(model)
+    if not names:
+        raise ValueError(f"{ckpt_dir}: the model has no gate/up/down MLP")
+    _, sdips, _ = load_streaming_mlps(ckpt_dir, keep_ratio, device, names=names)
+    swap_modules(model, names, sdips)
+    load_tensors(model, ckpt_dir / ST_NAME, device, skip_prefixes=names)
+    return model, load_tokenizer(ckpt_dir), sdips

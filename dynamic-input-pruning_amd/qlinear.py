@@ -8,16 +8,28 @@ helpers, qlinear.py:25-88).
 ``dequantize`` on device tensors runs the HIP dequant kernel (bf16(q*s), the
 same rounding as the reference); on host tensors it uses torch ops, which is
 how the reference uses it at load time (e.g. the one-time down transpose).
-``QuantLinear`` is the dense dequant + F.linear layer the reference uses for
-prefill (qlinear.py:67-88).
+``QuantLinear`` is the reference's projection layer (qlinear.py:67-88): the
+dense dequant + F.linear route for prefill, and for a single-token decode
+input on the GPU the int4 GEMV kernel, which reads the packed weight once
+instead of writing and re-reading a bf16 copy (it sums exact fp32 q*s*x
+products, so it differs from dequant + F.linear by fp32 rounding only).
+``_replace_linears_with_quant`` and ``load_quantized_qwen3`` build the
+reference's int4 baseline model (qlinear.py:91-166) with every weight
+resident on one device.
 """
 from __future__ import annotations
+
+from pathlib import Path
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
 GROUP_SIZE = 128
+_QUANT_SUBSTRINGS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+# Input widths the int4 GEMV kernel is built for (its dispatch table:
+# 32-column chunks split over 4..32 lanes per row).
+_GEMV_COLS = frozenset((128, 256, 512, 1024, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192))
 
 
 def _unpack_int4(qweight: torch.Tensor) -> torch.Tensor:
@@ -59,5 +71,44 @@ class QuantLinear(nn.Module):
         self.bias = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if (x.is_cuda and x.numel() == self.in_features and self.in_features in _GEMV_COLS
+                and self.out_features > 0):
+            from _dip_hip import int4_gemv
+            y = int4_gemv(self.qweight, self.scales, x.reshape(-1).to(torch.bfloat16))
+            return y.to(x.dtype).reshape(*x.shape[:-1], self.out_features)
         w = dequantize(self.qweight, self.scales)
         return F.linear(x, w.to(x.dtype))
+
+
+def _replace_linears_with_quant(model: nn.Module) -> list:
+    """Swap every nn.Linear whose qualified name contains one of the seven
+    projection names for an empty QuantLinear of the same shape
+    (qlinear.py:91-106); returns the swapped names.  lm_head and the
+    embeddings stay as they are."""
+    swapped = []
+    for parent_name, parent in list(model.named_modules()):
+        for child_name, child in list(parent.named_children()):
+            full = f"{parent_name}.{child_name}" if parent_name else child_name
+            if isinstance(child, nn.Linear) and any(s in full for s in _QUANT_SUBSTRINGS):
+                setattr(parent, child_name, QuantLinear(child.in_features, child.out_features))
+                swapped.append(full)
+    return swapped
+
+
+def load_quantized_qwen3(ckpt_dir, gpu_mem_gib: int = 13, cpu_mem_gib: int = 60,
+                         device="cuda:0"):
+    """The reference's int4 baseline (qlinear.py:109-166): the model of
+    `ckpt_dir/config.json` with QuantLinear projections and the weights of
+    model_int4.safetensors.  Returns (model, tokenizer or None).
+
+    The reference splits the model between a small GPU and host memory with
+    accelerate's offload hooks (gpu_mem_gib / cpu_mem_gib); one MI355X holds
+    a whole int4 Qwen3-32B in HBM, so every tensor is placed on `device` and
+    the two sizes are accepted for call compatibility only."""
+    from dip_model import build_empty_model, load_tensors, load_tokenizer
+    from dip_checkpoint import ST_NAME, read_quant_config
+    ckpt_dir = Path(ckpt_dir)
+    read_quant_config(ckpt_dir)
+    model = build_empty_model(ckpt_dir)
+    load_tensors(model, ckpt_dir / ST_NAME, device)
+    return model, load_tokenizer(ckpt_dir)
