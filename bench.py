@@ -96,6 +96,77 @@ def measured_traffic(shape: str, keep: float, stage: str, K):
     return table.get(stage)
 
 
+def whole_model(args) -> int:
+    """Greedy decode of a whole synthetic Qwen3 (int4 attention projections,
+    DIP MLPs at --keep, bf16 embedding and lm_head) through DIPDecoder's
+    HIP-graph step.  Reports decode-only tok/s (HIP events over `steps`
+    graph replays after `warmup`) and tok/s the way the reference's
+    gen_utils.benchmark_decode measures it (wall time of a greedy generate of
+    64 new tokens, prompt prefill included, mean of 3 runs after a warmup
+    run), plus the weight bytes one token reads."""
+    import torch
+    from dip_model import DIPDecoder, qwen3_config, synthetic_model
+    from qlinear import QuantLinear
+    dev = torch.device("cuda:0")
+    over = {"num_hidden_layers": args.layers} if args.layers else {}
+    cfg = qwen3_config(args.shape, **over)
+    print(f"[bench] building whole {args.shape} model ({cfg.num_hidden_layers} layers) "
+          f"keep={args.keep}", file=sys.stderr, flush=True)
+    model, mods = synthetic_model(cfg, args.keep, dev, seed=0)
+    plen, gen_new = 32, 64
+    dec = DIPDecoder(model, max_len=plen + max(args.warmup + args.steps, gen_new) + 1)
+    prompt = torch.randint(0, cfg.vocab_size, (1, plen), generator=torch.Generator().manual_seed(0))
+    print("[bench] model built; prefill + warmup", file=sys.stderr, flush=True)
+    dec.prefill(prompt)
+    for _ in range(args.warmup):
+        dec.step()
+    torch.cuda.synchronize()
+    print("[bench] timing decode steps", file=sys.stderr, flush=True)
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        dec.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    print(f"[bench] {ms_step:.3f} ms per decode step; timing generate", file=sys.stderr,
+          flush=True)
+    dec.generate(prompt, gen_new)
+    runs = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.generate(prompt, gen_new)
+        torch.cuda.synchronize()
+        runs.append(gen_new / (time.perf_counter() - t0))
+    proj = sum(m.qweight.numel() + 2 * m.scales.numel() for m in model.modules()
+               if isinstance(m, QuantLinear))
+    H, I, k = cfg.hidden_size, cfg.intermediate_size, mods[0].k
+    row = H // 2 + 2 * (H // 128)
+    mlp = len(mods) * (I + 2 * k) * row
+    head = model.lm_head.weight.numel() * 2
+    out = {
+        "metric": "whole-model greedy decode tok/s, synthetic " + args.shape +
+                  f" int4, DIP MLPs keep {args.keep}",
+        "value": round(1000.0 / ms_step, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.shape}-shape whole model, batch 1, prompt {plen}, "
+                               "HIP-graph decode step", "layers": cfg.num_hidden_layers,
+                   "keep": args.keep, "k": k},
+        "reference_method_tok_s": round(sum(runs) / len(runs), 2),
+        "reference_method": f"greedy generate of {gen_new} tokens incl. {plen}-token prefill, "
+                            "wall clock, mean of 3 after 1 warmup",
+        "weight_bytes_per_token": {"projections_int4": proj, "dip_mlps": mlp,
+                                   "lm_head_bf16": head, "total": proj + mlp + head},
+        "weight_gbs": round((proj + mlp + head) / (ms_step * 1e-3) / 1e9, 1),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,6 +186,10 @@ def main(argv=None):
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel eagerly instead of replaying the captured graph "
                          "(for counter collection, which profiles each dispatch)")
+    ap.add_argument("--whole-model", action="store_true",
+                    help="instead of the MLP stack, time greedy decode of a whole synthetic "
+                         "Qwen3 of --shape (attention, DIP MLPs, lm_head) with the HIP-graph "
+                         "decode loop; prints its own JSON line")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed run, copy a buffer of this many MiB device to device "
                          "(the reference transfer for scaling HBM byte counters)")
@@ -124,6 +199,9 @@ def main(argv=None):
         print("bench.py measures the single-GPU DIP decode path; multi-GPU runs are not "
               "part of this build (--gpus must be 1)", file=sys.stderr)
         return 2
+
+    if args.whole_model:
+        return whole_model(args)
 
     import torch
     import _dip_hip as K

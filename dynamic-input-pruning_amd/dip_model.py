@@ -16,8 +16,9 @@ from the host: embedding, per layer RMSNorm -> q/k/v projections (int4 GEMV)
 -> q/k RMSNorm -> rotary embedding from a precomputed table -> cache write
 at the device-side position -> attention over the static cache with a
 position mask -> o projection -> RMSNorm -> DIP MLP, then the final norm,
-lm_head and argmax.  With ``use_graph`` the step (including the argmax and
-the position update) is captured once in a HIP graph and replayed per token.
+lm_head and argmax.  With ``use_graph`` the step up to the final norm (and
+the position update) is captured once in a HIP graph and replayed per token;
+lm_head and argmax run after each replay on the same stream.
 The step uses the model's own modules, so the decode math is the HF model's
 (transformers' Qwen3DecoderLayer / Qwen3Attention forward).
 """
@@ -103,6 +104,12 @@ def load_tensors(model: nn.Module, st_path, device, skip_prefixes=()) -> None:
             _set_tensor(model, key, f.get_tensor(key), device)
     if getattr(model.config, "tie_word_embeddings", False) and "lm_head.weight" not in keys:
         model.lm_head.weight = model.get_input_embeddings().weight
+    _finish(model, device, st_path)
+
+
+def _finish(model: nn.Module, device, source) -> None:
+    """Move the buffers made at construction to `device`; raise if any
+    parameter or buffer is still empty."""
     for mod in model.modules():
         for name, buf in list(mod._buffers.items()):
             if buf is not None and not buf.is_meta and buf.device != device:
@@ -110,8 +117,76 @@ def load_tensors(model: nn.Module, st_path, device, skip_prefixes=()) -> None:
     empty = [n for n, t in list(model.named_parameters()) + list(model.named_buffers())
              if t.is_meta]
     if empty:
-        raise ValueError(f"{st_path}: no tensor for {len(empty)} model entries, e.g. "
+        raise ValueError(f"{source}: no tensor for {len(empty)} model entries, e.g. "
                          f"{empty[:4]}")
+
+
+# Published Qwen3 architectures (the models' config.json values).
+QWEN3_SHAPES = {
+    "qwen3-32b": dict(hidden_size=5120, intermediate_size=25600, num_hidden_layers=64,
+                      num_attention_heads=64, num_key_value_heads=8),
+    "qwen3-8b": dict(hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                     num_attention_heads=32, num_key_value_heads=8),
+}
+
+
+def qwen3_config(shape: str = "qwen3-32b", **overrides):
+    """A Qwen3Config of a published model's shape (vocabulary 151936, head
+    dim 128, rope theta 1e6, untied embeddings)."""
+    from transformers import Qwen3Config
+    kw = dict(QWEN3_SHAPES[shape], vocab_size=151936, head_dim=128, rms_norm_eps=1e-6,
+              max_position_embeddings=40960, tie_word_embeddings=False,
+              rope_parameters={"rope_type": "default", "rope_theta": 1e6})
+    kw.update(overrides)
+    return Qwen3Config(**kw)
+
+
+def synthetic_model(config, keep_ratio: float = 0.6, device="cuda:0", seed: int = 0,
+                    std: float = 0.02):
+    """A causal LM of `config` with N(0, std) weights drawn on the device, for
+    benchmarks (no checkpoint needed): every projection quantized int4 g128
+    with the reference quantizer rule (QuantLinear buffers), every MLP a
+    StreamingDIPMlp whose down is drawn and quantized directly in the
+    transposed layout, norm weights 1, embedding and lm_head bf16.
+    Returns (model, list of the StreamingDIPMlp modules)."""
+    import _dip_hip as K
+    from accelerate import init_empty_weights
+    from transformers import AutoModelForCausalLM
+    from dip_stream_predispatch import SharedBuffers, StreamingDIPMlp
+    from qlinear import QuantLinear
+    device = torch.device(device)
+    with init_empty_weights():
+        model = AutoModelForCausalLM.from_config(config, dtype=torch.bfloat16)
+    _replace_linears_with_quant(model)
+    model.eval()
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def draw(*shape):
+        return torch.randn(*shape, device=device, generator=gen) * std
+
+    H, I = config.hidden_size, config.intermediate_size
+    k = max(1, int(round(I * keep_ratio)))
+    shared = SharedBuffers(k, H // 2, H // 128, H, H // 128, device)
+    names = mlp_module_names(model)
+    mods = []
+    for _ in names:
+        w = [K.quantize_int4(draw(I, H)) for _ in range(3)]
+        mods.append(StreamingDIPMlp(*w[0], *w[1], *w[2], shared, keep_ratio, device,
+                                    down_transposed=True))
+    swap_modules(model, names, mods)
+    for name, mod in model.named_modules():
+        if isinstance(mod, QuantLinear):
+            qw, sc = K.quantize_int4(draw(mod.out_features, mod.in_features))
+            mod._buffers["qweight"], mod._buffers["scales"] = qw, sc
+    for name, p in list(model.named_parameters()):
+        if p.is_meta:
+            t = (torch.ones(p.shape, device=device) if name.endswith("norm.weight")
+                 else draw(*p.shape))
+            _set_tensor(model, name, t.to(torch.bfloat16), device)
+    if getattr(config, "tie_word_embeddings", False):
+        model.lm_head.weight = model.get_input_embeddings().weight
+    _finish(model, device, "synthetic_model")
+    return model, mods
 
 
 def load_tokenizer(ckpt_dir):
@@ -178,17 +253,19 @@ class DIPDecoder:
                 raise ValueError(f"the MLPs of layers {bad[:4]} synchronise with the host "
                                  "per token and cannot be captured; use use_graph=False")
         self.graph = None
-        self._logits = None
+        self._h = None
 
     # -- one decode step (device-side token and position) ---------------------
-    def _forward_step(self) -> torch.Tensor:
+    def _body(self) -> torch.Tensor:
+        """Embedding of `tok` at `pos` through every layer and the final norm
+        (the part the graph captures); returns the hidden state [1, 1, H]."""
         inner = self.model.model
         hd = self.hd
         h = inner.embed_tokens(self.tok).view(1, 1, -1)
         cos = self.cos.index_select(0, self.pos).view(1, 1, 1, hd)
         sin = self.sin.index_select(0, self.pos).view(1, 1, 1, hd)
-        mask = torch.zeros(self.max_len, dtype=self.dtype, device=self.device).masked_fill(
-            self._cols > self.pos, float("-inf")).view(1, 1, 1, self.max_len)
+        mask = torch.where(self._cols > self.pos, float("-inf"), 0.0).to(self.dtype).view(
+            1, 1, 1, self.max_len)
         for i, layer in enumerate(self.layers):
             a = layer.self_attn
             x = layer.input_layernorm(h)
@@ -207,33 +284,38 @@ class DIPDecoder:
                                                attn_mask=mask, scale=a.scaling)
             h = h + a.o_proj(o.reshape(1, 1, -1))
             h = h + layer.mlp(layer.post_attention_layernorm(h))
-        return self.model.lm_head(inner.norm(h)).view(-1)
+        return inner.norm(h)
 
-    def _step_and_advance(self) -> torch.Tensor:
-        logits = self._forward_step()
+    def _head(self, h: torch.Tensor) -> torch.Tensor:
+        """lm_head and the greedy choice, outside any graph: over a full
+        vocabulary both are library calls (a GEMV and a many-workgroup
+        reduction) that may clear their own scratch with a memset, which a
+        captured graph does not replay reliably."""
+        logits = self.model.lm_head(h).view(-1)
         self.tok.copy_(logits.argmax().view(1))
-        self.pos.add_(1)
         return logits
 
     @torch.no_grad()
     def step(self) -> torch.Tensor:
         """Decode the token in `self.tok` at position `self.pos`; afterwards
         `self.tok` holds the argmax and `self.pos` has advanced by one.
-        Returns the logits (a buffer the next step overwrites)."""
-        if not self.use_graph:
-            return self._step_and_advance()
-        if self.graph is None:
-            # the first step runs eagerly (it also makes every lazily created
-            # buffer), then the same step is captured for the later tokens
-            out = self._step_and_advance()
-            torch.cuda.synchronize(self.device)
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                self._logits = self._step_and_advance()
-            self.graph = g
-            return out
+        Returns the logits."""
+        if not self.use_graph or self.graph is None:
+            h = self._body()
+            self.pos.add_(1)
+            logits = self._head(h)
+            if self.use_graph:
+                # the first step ran eagerly (it also made every lazily
+                # created buffer); capture the same body for later tokens
+                torch.cuda.synchronize(self.device)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self._h = self._body()
+                    self.pos.add_(1)
+                self.graph = g
+            return logits
         self.graph.replay()
-        return self._logits
+        return self._head(self._h)
 
     # -- prompt ---------------------------------------------------------------
     @torch.no_grad()

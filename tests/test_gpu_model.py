@@ -71,6 +71,22 @@ def test_graph_decode_equals_eager(ckpt, streaming):
     assert torch.equal(log_g, log_e)
 
 
+def test_graph_decode_real_shapes_equals_eager():
+    """Two layers of the Qwen3-32B shape with its full 151936-token
+    vocabulary (synthetic weights): every graph replay's logits equal the
+    eager step's bit for bit, with the eager lm_head and argmax between
+    replays."""
+    from dip_model import DIPDecoder, qwen3_config, synthetic_model
+    print("graph vs eager decode, qwen3-32b shape, 2 layers", flush=True)
+    cfg = qwen3_config("qwen3-32b", num_hidden_layers=2)
+    model, _ = synthetic_model(cfg, 0.6, "cuda:0", seed=3)
+    prompt = torch.randint(0, cfg.vocab_size, (1, 8), generator=torch.Generator().manual_seed(1))
+    seq_g, log_g = DIPDecoder(model, 40, use_graph=True).generate(prompt, 16, return_logits=True)
+    seq_e, log_e = DIPDecoder(model, 40, use_graph=False).generate(prompt, 16, return_logits=True)
+    assert torch.equal(seq_g, seq_e)
+    assert torch.equal(log_g, log_e)
+
+
 def test_decode_matches_hf_incremental_forward(ckpt, streaming):
     """transformers' own forward, one token at a time with its DynamicCache,
     through the same StreamingDIPMlp and QuantLinear modules."""
