@@ -65,6 +65,12 @@ _SIGS = {
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
+    "dip_add_rmsnorm": ([_p, _p, _p, _p, _i64, ctypes.c_float, _p], _i32),
+    "dip_qk_norm_rope_cache": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                ctypes.c_float, _p], _i32),
+    "dip_decode_attention_workspace_size": ([_i64, _i64, _i64], _sz),
+    "dip_decode_attention": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _sz,
+                              _p], _i32),
     "dip_set_tuning": ([_i32, _i32], _i32),
     "dip_get_tuning": ([_i32], _i32),
 }
@@ -158,6 +164,10 @@ def int4_gemv(qweight, scales, x, act: int = 0, out=None):
     x = _want(x.reshape(-1), torch.bfloat16, "x", (cols,))
     if out is None:
         out = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    elif (out.dtype != torch.bfloat16 or out.numel() != rows or not out.is_contiguous()
+          or out.device != dev or out.data_ptr() % 16 != 0):
+        raise RuntimeError(f"out must be a contiguous, 16-byte aligned bf16 tensor of {rows} "
+                           "values on the weights' device")
     _check(lib.dip_int4_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(out), rows, cols,
                              int(act), _stream(dev)), "dip_int4_gemv")
     return out
@@ -428,6 +438,97 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
                               None if state is None else _ptr(state), _stream(dev)),
            "dip_mlp_decode")
     return y, g, idx, h
+
+
+# ---------------------------------------------------------------------------
+# one-token decode steps of a Qwen3 decoder layer (whole-model decode loop)
+# ---------------------------------------------------------------------------
+def _bf16_vec(t: torch.Tensor, n: int, name: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != n:
+        raise RuntimeError(f"{name} must be a contiguous bf16 tensor of {n} values")
+    return t
+
+
+def _pos_tensor(pos: torch.Tensor, dev) -> torch.Tensor:
+    if pos.dtype != torch.int64 or pos.numel() < 1 or pos.device != dev:
+        raise RuntimeError("pos must be an int64 tensor on the device")
+    return pos
+
+
+def add_rmsnorm(h, add, weight, out, eps: float):
+    """In place h = bf16(h + add) (when add is given), then
+    out = bf16(weight * bf16(h * rsqrt(mean(h^2) + eps)))."""
+    dev = _dev(h, weight, out)
+    n = h.numel()
+    _bf16_vec(h, n, "h")
+    _bf16_vec(weight, n, "weight")
+    _bf16_vec(out, n, "out")
+    if add is not None:
+        _dev(add)
+        if add.device != dev:
+            raise RuntimeError("add must be on h's device")
+        _bf16_vec(add, n, "add")
+    _check(lib.dip_add_rmsnorm(_ptr(h), _ptr(add), _ptr(weight), _ptr(out), n, float(eps),
+                               _stream(dev)), "dip_add_rmsnorm")
+    return out
+
+
+def qk_norm_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, q_out, k_cache, v_cache,
+                       n_heads: int, n_kv_heads: int, eps: float):
+    """q/k head RMSNorm + rotary embedding at `pos` for one token's q|k|v;
+    q -> q_out, k and v -> row pos of the [n_kv_heads, max_len, head_dim]
+    caches."""
+    dev = _dev(qkv, q_out, k_cache, v_cache)
+    hd = q_norm_w.numel()
+    if k_cache.dim() != 3 or k_cache.shape != v_cache.shape or k_cache.shape[0] != n_kv_heads \
+            or k_cache.shape[2] != hd:
+        raise RuntimeError("k_cache / v_cache must be [n_kv_heads, max_len, head_dim]")
+    max_len = k_cache.shape[1]
+    _bf16_vec(qkv, (n_heads + 2 * n_kv_heads) * hd, "qkv")
+    _bf16_vec(q_norm_w, hd, "q_norm_w")
+    _bf16_vec(k_norm_w, hd, "k_norm_w")
+    _bf16_vec(cos, max_len * hd, "cos")
+    _bf16_vec(sin, max_len * hd, "sin")
+    _bf16_vec(q_out, n_heads * hd, "q_out")
+    _bf16_vec(k_cache, n_kv_heads * max_len * hd, "k_cache")
+    _bf16_vec(v_cache, n_kv_heads * max_len * hd, "v_cache")
+    for t in (q_norm_w, k_norm_w, cos, sin):
+        if t.device != dev:
+            raise RuntimeError("all tensors must be on one device")
+    _pos_tensor(pos, dev)
+    _check(lib.dip_qk_norm_rope_cache(_ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos),
+                                      _ptr(sin), _ptr(pos), _ptr(q_out), _ptr(k_cache),
+                                      _ptr(v_cache), n_heads, n_kv_heads, hd, max_len,
+                                      float(eps), _stream(dev)), "dip_qk_norm_rope_cache")
+    return q_out
+
+
+def decode_attention_workspace_bytes(n_heads: int, head_dim: int, max_len: int) -> int:
+    return lib.dip_decode_attention_workspace_size(n_heads, head_dim, max_len)
+
+
+def decode_attention(q, k_cache, v_cache, pos, out, scale: float, ws=None):
+    """Grouped-query attention of one token (q [n_heads, head_dim]) over
+    rows 0..pos of the [n_kv_heads, max_len, head_dim] caches -> out."""
+    dev = _dev(q, k_cache, v_cache, out)
+    if k_cache.dim() != 3 or k_cache.shape != v_cache.shape:
+        raise RuntimeError("k_cache / v_cache must be [n_kv_heads, max_len, head_dim]")
+    nkv, max_len, hd = k_cache.shape
+    nh = q.numel() // hd
+    _bf16_vec(q, nh * hd, "q")
+    _bf16_vec(out, nh * hd, "out")
+    _bf16_vec(k_cache, nkv * max_len * hd, "k_cache")
+    _bf16_vec(v_cache, nkv * max_len * hd, "v_cache")
+    _pos_tensor(pos, dev)
+    nbytes = decode_attention_workspace_bytes(nh, hd, max_len)
+    if ws is None:
+        ws = workspace(dev, nbytes, "attention")
+    elif ws.numel() < nbytes or ws.device != dev:
+        raise RuntimeError("attention workspace too small")
+    _check(lib.dip_decode_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out),
+                                    nh, nkv, hd, max_len, float(scale), _ptr(ws), ws.numel(),
+                                    _stream(dev)), "dip_decode_attention")
+    return out
 
 
 TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "gate_mfma": 3}

@@ -1,0 +1,328 @@
+// dip_decode.hip — the one-token decode steps of a Qwen3 decoder layer around
+// the DIP MLP: residual add + RMSNorm, q/k RMSNorm + rotary embedding + key /
+// value cache write, and grouped-query attention of the token over the cache.
+//
+// The reference runs these steps through transformers' Qwen3 modules with
+// PyTorch ops (the model its loader builds, dip_stream_predispatch.py:218-289;
+// transformers' modeling_qwen3: Qwen3RMSNorm.forward, apply_rotary_pos_emb,
+// Qwen3Attention.forward, Qwen3DecoderLayer.forward).  Where those modules
+// round to bf16 these kernels round at the same points:
+//   RMSNorm   y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))  (fp32 mean)
+//   residual  h = bf16(h + a)
+//   rotary    q' = bf16(bf16(q * cos) + bf16(rotate_half(q) * sin))
+// The attention keeps scores, softmax and the weighted value sum in fp32 and
+// rounds its output once (torch's fused attention kernels round in between,
+// so the two agree to bf16 rounding, not bit for bit).
+//
+// Every kernel here is latency-bound (a few KB per token, except attention
+// over a long cache); each is one launch of a handful of workgroups.
+#include "dip_common.h"
+#include "dip_internal.h"
+
+namespace dip {
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormPerThread = 32;        // n <= 8192
+constexpr int kHeadDim = 128;
+constexpr int kAttnChunk = 64;            // cache positions per attention workgroup
+constexpr int kPartFloats = 2 + kHeadDim; // m, l, acc[128] per (kv head, chunk, query head)
+
+DIP_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+DIP_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+DIP_DEV float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// h = bf16(h + add) when add is given; out = RMSNorm(h) * w.  One workgroup.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
+    uint16_t* __restrict__ h, const uint16_t* __restrict__ add, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ out, int n, float eps) {
+  __shared__ float part[kNormThreads / 64];
+  float v[kNormPerThread];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNormPerThread; ++j) {
+    const int i = threadIdx.x + j * kNormThreads;
+    float x = 0.f;
+    if (i < n) {
+      x = bf16_to_f32(h[i]);
+      if (add) {
+        const uint32_t s = f32_to_bf16(x + bf16_to_f32(add[i]));
+        h[i] = (uint16_t)s;
+        x = bf16_to_f32(s);
+      }
+    }
+    v[j] = x;
+    ss += x * x;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
+  const float r = rsqrtf(tot * (1.0f / (float)n) + eps);
+#pragma unroll
+  for (int j = 0; j < kNormPerThread; ++j) {
+    const int i = threadIdx.x + j * kNormThreads;
+    if (i < n) out[i] = (uint16_t)f32_to_bf16(bf16_to_f32(w[i]) * round_bf16(v[j] * r));
+  }
+}
+
+// One workgroup (one wave) per head of the fused q|k|v projection output:
+// q heads [0, nh) and k heads [nh, nh + nkv) get RMSNorm over the head and
+// the rotary embedding at `pos`; q goes to q_out, k to the key cache; v heads
+// [nh + nkv, nh + 2 nkv) are copied to the value cache.  Lane l holds
+// dimensions 2l and 2l + 1; rotate_half pairs dimension d with d +- 64, which
+// lives in lane l ^ 32.  Cache writes happen only for 0 <= pos < max_len.
+__global__ __launch_bounds__(64) void qk_rope_cache_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_w,
+    const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_p,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int nh, int nkv, int max_len, float eps) {
+  const int head = blockIdx.x;
+  const int l = threadIdx.x;
+  const int64_t pos = *pos_p;
+  const bool pos_ok = pos >= 0 && pos < max_len;
+  const uint32_t pair = reinterpret_cast<const uint32_t*>(qkv)[(size_t)head * 64 + l];
+  if (head >= nh + nkv) {
+    if (pos_ok)
+      reinterpret_cast<uint32_t*>(v_cache)[((size_t)(head - nh - nkv) * max_len + pos) * 64 + l] =
+          pair;
+    return;
+  }
+  const bool is_q = head < nh;
+  const uint32_t wp = reinterpret_cast<const uint32_t*>(is_q ? q_w : k_w)[l];
+  const float x0 = bf16_to_f32(pair & 0xFFFFu), x1 = bf16_to_f32(pair >> 16);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float r = rsqrtf(ss * (1.0f / (float)kHeadDim) + eps);
+  const uint32_t y0 = f32_to_bf16(bf16_to_f32(wp & 0xFFFFu) * round_bf16(x0 * r));
+  const uint32_t y1 = f32_to_bf16(bf16_to_f32(wp >> 16) * round_bf16(x1 * r));
+  // rotate_half: dims [0, 64) take -y[d + 64], dims [64, 128) take y[d - 64]
+  float r0 = bf16_to_f32(__shfl_xor(y0, 32, 64));
+  float r1 = bf16_to_f32(__shfl_xor(y1, 32, 64));
+  if (l < 32) {
+    r0 = -r0;
+    r1 = -r1;
+  }
+  const size_t trow = (size_t)(pos_ok ? pos : 0) * 64 + l;
+  const uint32_t cs = reinterpret_cast<const uint32_t*>(cos_t)[trow];
+  const uint32_t sn = reinterpret_cast<const uint32_t*>(sin_t)[trow];
+  const uint32_t o0 = f32_to_bf16(round_bf16(bf16_to_f32(y0) * bf16_to_f32(cs & 0xFFFFu)) +
+                                  round_bf16(r0 * bf16_to_f32(sn & 0xFFFFu)));
+  const uint32_t o1 = f32_to_bf16(round_bf16(bf16_to_f32(y1) * bf16_to_f32(cs >> 16)) +
+                                  round_bf16(r1 * bf16_to_f32(sn >> 16)));
+  const uint32_t o = o0 | (o1 << 16);
+  if (is_q)
+    reinterpret_cast<uint32_t*>(q_out)[(size_t)head * 64 + l] = o;
+  else if (pos_ok)
+    reinterpret_cast<uint32_t*>(k_cache)[((size_t)(head - nh) * max_len + pos) * 64 + l] = o;
+}
+
+// Attention, pass 1: workgroup (chunk c, kv head) takes cache positions
+// [64c, 64c + 64) up to pos and the G query heads that share the kv head.
+// Lane = position for the scores, lane = dimension pair for the value sum.
+// Writes per query head the chunk's max score m, sum of exp(s - m) and the
+// unnormalised value sum.
+template <int G>
+__global__ __launch_bounds__(64) void attn_partial_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, const int64_t* __restrict__ pos_p,
+    float* __restrict__ part, int max_len, int nchunks, float scale) {
+  __shared__ __align__(16) float qs[G][kHeadDim];
+  __shared__ float ps[G][kAttnChunk];
+  const int c = blockIdx.x, kvh = blockIdx.y, l = threadIdx.x;
+  const int64_t pos = *pos_p;
+  const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
+  const int start = c * kAttnChunk;
+  if ((int64_t)start > last) return;  // no position of this chunk is attended
+  for (int i = l; i < G * kHeadDim; i += 64)
+    qs[i / kHeadDim][i % kHeadDim] = bf16_to_f32(q[(size_t)kvh * G * kHeadDim + i]);
+  __syncthreads();
+
+  const int p = start + l;
+  const bool live = (int64_t)p <= last;
+  float s[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) s[g] = 0.f;
+  if (live) {
+    const uint4* krow =
+        reinterpret_cast<const uint4*>(k_cache + ((size_t)kvh * max_len + p) * kHeadDim);
+#pragma unroll 4
+    for (int ch = 0; ch < kHeadDim / 8; ++ch) {
+      const uint4 kv = krow[ch];
+      const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float k0 = bf16_to_f32(w4[e] & 0xFFFFu), k1 = bf16_to_f32(w4[e] >> 16);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          s[g] = fmaf(qs[g][ch * 8 + 2 * e], k0, s[g]);
+          s[g] = fmaf(qs[g][ch * 8 + 2 * e + 1], k1, s[g]);
+        }
+      }
+    }
+  }
+  float m[G], lsum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float sc = live ? s[g] * scale : -INFINITY;
+    m[g] = wave_max(sc);
+    const float e = live ? expf(sc - m[g]) : 0.f;
+    ps[g][l] = e;
+    lsum[g] = wave_sum(e);
+  }
+  __syncthreads();
+
+  float a0[G], a1[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) a0[g] = a1[g] = 0.f;
+  const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
+  const uint32_t* vcol =
+      reinterpret_cast<const uint32_t*>(v_cache + ((size_t)kvh * max_len + start) * kHeadDim) + l;
+  for (int j = 0; j < npos; ++j) {
+    const uint32_t vp = vcol[(size_t)j * 64];
+    const float v0 = bf16_to_f32(vp & 0xFFFFu), v1 = bf16_to_f32(vp >> 16);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      a0[g] = fmaf(ps[g][j], v0, a0[g]);
+      a1[g] = fmaf(ps[g][j], v1, a1[g]);
+    }
+  }
+  float* out = part + ((size_t)kvh * nchunks + c) * G * kPartFloats;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float* o = out + g * kPartFloats;
+    if (l == 0) {
+      o[0] = m[g];
+      o[1] = lsum[g];
+    }
+    o[2 + 2 * l] = a0[g];
+    o[3 + 2 * l] = a1[g];
+  }
+}
+
+// Attention, pass 2: one wave per query head merges the chunks 0 .. pos/64
+// (rescaling each by exp(m_c - max m)) and writes bf16(sum / l).
+__global__ __launch_bounds__(64) void attn_combine_kernel(
+    const float* __restrict__ part, const int64_t* __restrict__ pos_p, uint16_t* __restrict__ out,
+    int G, int max_len, int nchunks) {
+  const int qh = blockIdx.x, l = threadIdx.x;
+  const int kvh = qh / G, g = qh % G;
+  const int64_t pos = *pos_p;
+  const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
+  const int nc = last < 0 ? 0 : (int)(last / kAttnChunk) + 1;
+  const float* base = part + (size_t)kvh * nchunks * G * kPartFloats + (size_t)g * kPartFloats;
+  const size_t stride = (size_t)G * kPartFloats;
+  float mx = -INFINITY;
+  for (int c = 0; c < nc; ++c) mx = fmaxf(mx, base[c * stride]);
+  float den = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    const float* pc = base + c * stride;
+    const float f = expf(pc[0] - mx);
+    den = fmaf(f, pc[1], den);
+    a0 = fmaf(f, pc[2 + 2 * l], a0);
+    a1 = fmaf(f, pc[3 + 2 * l], a1);
+  }
+  const uint32_t o0 = f32_to_bf16(a0 / den), o1 = f32_to_bf16(a1 / den);
+  reinterpret_cast<uint32_t*>(out)[(size_t)qh * 64 + l] = o0 | (o1 << 16);
+}
+
+template <int G>
+void launch_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const int64_t* pos,
+                      uint16_t* out, int nkv, int max_len, int nchunks, float scale, float* part,
+                      hipStream_t stream) {
+  hipLaunchKernelGGL((attn_partial_kernel<G>), dim3(nchunks, nkv), dim3(64), 0, stream, q, kc, vc,
+                     pos, part, max_len, nchunks, scale);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv * G), dim3(64), 0, stream, part, pos, out, G,
+                     max_len, nchunks);
+}
+
+}  // namespace
+}  // namespace dip
+
+using namespace dip;
+
+extern "C" int dip_add_rmsnorm(uint16_t* h, const uint16_t* add, const uint16_t* weight,
+                               uint16_t* out, int64_t n, float eps, void* stream) {
+  if (!h || !weight || !out) return DIP_ERR_NULL;
+  if (n <= 0 || n > (int64_t)kNormThreads * kNormPerThread) return DIP_ERR_SHAPE;
+  if (!(eps >= 0.f)) return DIP_ERR_ARG;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, (hipStream_t)stream, h,
+                     add, weight, out, (int)n, eps);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" int dip_qk_norm_rope_cache(const uint16_t* qkv, const uint16_t* q_norm_w,
+                                      const uint16_t* k_norm_w, const uint16_t* cos_table,
+                                      const uint16_t* sin_table, const int64_t* pos,
+                                      uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                      int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                      int64_t max_len, float eps, void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !pos || !q_out || !k_cache ||
+      !v_cache)
+    return DIP_ERR_NULL;
+  if (head_dim != kHeadDim) return DIP_ERR_UNSUPPORTED;
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads > 4096 || n_kv_heads > 4096 || max_len <= 0 ||
+      max_len > INT32_MAX / kHeadDim)
+    return DIP_ERR_SHAPE;
+  if (!(eps >= 0.f)) return DIP_ERR_ARG;
+  if (!aligned16(qkv) || !aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache) ||
+      !aligned16(cos_table) || !aligned16(sin_table) || !aligned16(q_norm_w) ||
+      !aligned16(k_norm_w))
+    return DIP_ERR_ALIGN;
+  hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)(n_heads + 2 * n_kv_heads)), dim3(64), 0,
+                     (hipStream_t)stream, qkv, q_norm_w, k_norm_w, cos_table, sin_table, pos,
+                     q_out, k_cache, v_cache, (int)n_heads, (int)n_kv_heads, (int)max_len, eps);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" size_t dip_decode_attention_workspace_size(int64_t n_heads, int64_t head_dim,
+                                                      int64_t max_len) {
+  if (n_heads <= 0 || head_dim != kHeadDim || max_len <= 0) return 0;
+  const size_t nchunks = (size_t)((max_len + kAttnChunk - 1) / kAttnChunk);
+  return nchunks * (size_t)n_heads * kPartFloats * sizeof(float);
+}
+
+extern "C" int dip_decode_attention(const uint16_t* q, const uint16_t* k_cache,
+                                    const uint16_t* v_cache, const int64_t* pos, uint16_t* out,
+                                    int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                    int64_t max_len, float scale, void* workspace,
+                                    size_t ws_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !pos || !out) return DIP_ERR_NULL;
+  if (head_dim != kHeadDim) return DIP_ERR_UNSUPPORTED;
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads > 4096 ||
+      max_len <= 0 || max_len > INT32_MAX / kHeadDim)
+    return DIP_ERR_SHAPE;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+    return DIP_ERR_ALIGN;
+  if (!workspace || ws_bytes < dip_decode_attention_workspace_size(n_heads, head_dim, max_len))
+    return DIP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DIP_ERR_ALIGN;
+  const int nkv = (int)n_kv_heads;
+  const int G = (int)(n_heads / n_kv_heads);
+  const int nchunks = (int)((max_len + kAttnChunk - 1) / kAttnChunk);
+  float* part = static_cast<float*>(workspace);
+  hipStream_t s = (hipStream_t)stream;
+  const int ml = (int)max_len;
+  switch (G) {
+    case 1: launch_attention<1>(q, k_cache, v_cache, pos, out, nkv, ml, nchunks, scale, part, s); break;
+    case 2: launch_attention<2>(q, k_cache, v_cache, pos, out, nkv, ml, nchunks, scale, part, s); break;
+    case 4: launch_attention<4>(q, k_cache, v_cache, pos, out, nkv, ml, nchunks, scale, part, s); break;
+    case 5: launch_attention<5>(q, k_cache, v_cache, pos, out, nkv, ml, nchunks, scale, part, s); break;
+    case 8: launch_attention<8>(q, k_cache, v_cache, pos, out, nkv, ml, nchunks, scale, part, s); break;
+    case 16: launch_attention<16>(q, k_cache, v_cache, pos, out, nkv, ml, nchunks, scale, part, s); break;
+    default: return DIP_ERR_UNSUPPORTED;
+  }
+  return hip_status(hipGetLastError());
+}

@@ -215,9 +215,16 @@ class DIPDecoder:
       use_graph: capture the decode step in a HIP graph (needs a GPU and MLP
                  modules that read nothing back to the host per token; a
                  module says it does with `graph_capturable = False`).
+      fused:     run the layer's non-MLP steps with this library's decode
+                 kernels (one fused q|k|v GEMV, q/k norm + rotary + cache
+                 write, split-position attention, residual add fused into
+                 each RMSNorm: 11 launches per layer) instead of the HF
+                 modules' PyTorch ops.  None: whenever the model fits them
+                 (GPU, bf16, head_dim 128, int4 attention projections).
     """
 
-    def __init__(self, model: nn.Module, max_len: int = 2048, use_graph: bool = True):
+    def __init__(self, model: nn.Module, max_len: int = 2048, use_graph: bool = True,
+                 fused=None):
         inner = model.model
         cfg = model.config
         self.model = model
@@ -245,6 +252,13 @@ class DIPDecoder:
         self._cols = torch.arange(self.max_len, device=self.device)
         self.tok = torch.zeros(1, dtype=torch.long, device=self.device)
         self.pos = torch.zeros(1, dtype=torch.long, device=self.device)
+        supported = self._fused_supported()
+        if fused and not supported:
+            raise ValueError("fused decode needs a GPU, bf16 weights, head_dim 128, int4 "
+                             "attention projections and a supported head grouping")
+        self.fused = supported if fused is None else bool(fused)
+        if self.fused:
+            self._setup_fused()
         self.use_graph = bool(use_graph) and self.device.type == "cuda"
         if self.use_graph:
             bad = [i for i, L in enumerate(self.layers)
@@ -253,10 +267,93 @@ class DIPDecoder:
                 raise ValueError(f"the MLPs of layers {bad[:4]} synchronise with the host "
                                  "per token and cannot be captured; use use_graph=False")
         self.graph = None
-        self._h = None
+        self._graph_out = None
+
+    # -- fused decode kernels -------------------------------------------------
+    def _fused_supported(self) -> bool:
+        from qlinear import QuantLinear, _GEMV_COLS
+        if self.device.type != "cuda" or self.dtype != torch.bfloat16 or self.hd != 128:
+            return False
+        if self.nh % self.nkv or self.nh // self.nkv not in (1, 2, 4, 5, 8, 16):
+            return False
+        hidden = self.model.config.hidden_size
+        if hidden > 8192 or hidden not in _GEMV_COLS or self.nh * self.hd not in _GEMV_COLS:
+            return False
+        for L in self.layers:
+            a = L.self_attn
+            if not all(isinstance(getattr(a, p), QuantLinear)
+                       for p in ("q_proj", "k_proj", "v_proj", "o_proj")):
+                return False
+            if a.q_norm.variance_epsilon != a.k_norm.variance_epsilon:
+                return False
+        return True
+
+    def _setup_fused(self) -> None:
+        """Concatenate each layer's q/k/v projections into one [q|k|v]
+        matrix (the projections keep views into it, so nothing is stored
+        twice) and allocate the per-token buffers of the fused step."""
+        import _dip_hip as K
+        from dip_stream_predispatch import StreamingDIPMlp
+        self._K = K
+        self.hidden = self.model.config.hidden_size
+        dev, bf = self.device, torch.bfloat16
+        self._qkv_w = []
+        for L in self.layers:
+            a = L.self_attn
+            parts = (a.q_proj, a.k_proj, a.v_proj)
+            qw = torch.cat([p.qweight for p in parts])
+            sc = torch.cat([p.scales for p in parts])
+            r = 0
+            for p in parts:
+                n = p.out_features
+                p._buffers["qweight"], p._buffers["scales"] = qw[r:r + n], sc[r:r + n]
+                r += n
+            self._qkv_w.append((qw, sc))
+        self._mlp_fns = [(lambda x, m=L.mlp: m._decode_one(x))
+                         if isinstance(L.mlp, StreamingDIPMlp) else
+                         (lambda x, m=L.mlp, H=self.hidden: m(x.view(1, 1, H)).reshape(-1))
+                         for L in self.layers]
+        self._h = torch.empty(self.hidden, dtype=bf, device=dev)
+        self._x = torch.empty(self.hidden, dtype=bf, device=dev)
+        self._a = torch.empty(self.hidden, dtype=bf, device=dev)
+        self._qkv = torch.empty((self.nh + 2 * self.nkv) * self.hd, dtype=bf, device=dev)
+        self._q = torch.empty(self.nh * self.hd, dtype=bf, device=dev)
+        self._o = torch.empty(self.nh * self.hd, dtype=bf, device=dev)
+        self._attn_ws = torch.zeros(K.decode_attention_workspace_bytes(self.nh, self.hd,
+                                                                       self.max_len),
+                                    dtype=torch.uint8, device=dev)
+
+    def _body_fused(self) -> torch.Tensor:
+        K = self._K
+        inner = self.model.model
+        H = self.hidden
+        torch.index_select(inner.embed_tokens.weight, 0, self.tok, out=self._h.view(1, H))
+        n0 = self.layers[0].input_layernorm
+        K.add_rmsnorm(self._h, None, n0.weight, self._x, n0.variance_epsilon)
+        for i, L in enumerate(self.layers):
+            a = L.self_attn
+            qw, sc = self._qkv_w[i]
+            K.int4_gemv(qw, sc, self._x, out=self._qkv)
+            K.qk_norm_rope_cache(self._qkv, a.q_norm.weight, a.k_norm.weight, self.cos, self.sin,
+                                 self.pos, self._q, self.k_cache[i], self.v_cache[i], self.nh,
+                                 self.nkv, a.q_norm.variance_epsilon)
+            K.decode_attention(self._q, self.k_cache[i], self.v_cache[i], self.pos, self._o,
+                               a.scaling, ws=self._attn_ws)
+            K.int4_gemv(a.o_proj.qweight, a.o_proj.scales, self._o, out=self._a)
+            pn = L.post_attention_layernorm
+            K.add_rmsnorm(self._h, self._a, pn.weight, self._x, pn.variance_epsilon)
+            y = self._mlp_fns[i](self._x)
+            nn_ = self.layers[i + 1].input_layernorm if i + 1 < len(self.layers) else inner.norm
+            K.add_rmsnorm(self._h, y, nn_.weight, self._x, nn_.variance_epsilon)
+        return self._x.view(1, 1, H)
 
     # -- one decode step (device-side token and position) ---------------------
     def _body(self) -> torch.Tensor:
+        if self.fused:
+            return self._body_fused()
+        return self._body_modules()
+
+    def _body_modules(self) -> torch.Tensor:
         """Embedding of `tok` at `pos` through every layer and the final norm
         (the part the graph captures); returns the hidden state [1, 1, H]."""
         inner = self.model.model
@@ -310,12 +407,12 @@ class DIPDecoder:
                 torch.cuda.synchronize(self.device)
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g):
-                    self._h = self._body()
+                    self._graph_out = self._body()
                     self.pos.add_(1)
                 self.graph = g
             return logits
         self.graph.replay()
-        return self._head(self._h)
+        return self._head(self._graph_out)
 
     # -- prompt ---------------------------------------------------------------
     @torch.no_grad()

@@ -284,6 +284,57 @@ int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t*
 int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t n,
                          int64_t row_bytes, int64_t src_rows, int threads);
 
+/*
+ * One-token decode steps of a Qwen3 decoder layer around the DIP MLP, for
+ * the whole-model decode loop.  The reference has no kernels of its own
+ * here: its decode runs these steps through transformers' Qwen3 modules
+ * with PyTorch ops (the model built by dip_stream_predispatch.py:218-289 /
+ * dip_ca.py:199-269; transformers' modeling_qwen3 Qwen3RMSNorm.forward,
+ * apply_rotary_pos_emb, Qwen3Attention.forward,
+ * Qwen3DecoderLayer.forward).  bf16 tensors as uint16_t bits; `pos` is a
+ * device int64 holding the token's position, so the launches can be
+ * captured once and replayed for every token.
+ *
+ * dip_add_rmsnorm: if `add` is non-NULL, h[i] = bf16(h[i] + add[i]) in place
+ * (the residual add); then out = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
+ * with an fp32 mean.  1 <= n <= 8192.
+ */
+int dip_add_rmsnorm(uint16_t* h, const uint16_t* add, const uint16_t* weight, uint16_t* out,
+                    int64_t n, float eps, void* stream);
+
+/*
+ * dip_qk_norm_rope_cache: `qkv` holds one token's q | k | v projections,
+ * (n_heads + 2 n_kv_heads) * head_dim values.  Each q and k head gets
+ * RMSNorm over the head (q_norm_w / k_norm_w, head_dim values), then the
+ * rotary embedding with row `pos` of the [max_len, head_dim] cos / sin
+ * tables (bf16(bf16(x cos) + bf16(rotate_half(x) sin))); q goes to q_out
+ * [n_heads, head_dim], k and v to row `pos` of k_cache / v_cache
+ * [n_kv_heads, max_len, head_dim].  Cache rows are written only when
+ * 0 <= pos < max_len.  head_dim must be 128 (else DIP_ERR_UNSUPPORTED);
+ * pointers 16-byte aligned.
+ */
+int dip_qk_norm_rope_cache(const uint16_t* qkv, const uint16_t* q_norm_w,
+                           const uint16_t* k_norm_w, const uint16_t* cos_table,
+                           const uint16_t* sin_table, const int64_t* pos, uint16_t* q_out,
+                           uint16_t* k_cache, uint16_t* v_cache, int64_t n_heads,
+                           int64_t n_kv_heads, int64_t head_dim, int64_t max_len, float eps,
+                           void* stream);
+
+/*
+ * dip_decode_attention: out[h] = softmax(scale * q[h] . K[j]) V over cache
+ * rows j = 0 .. pos of kv head h / (n_heads / n_kv_heads) (grouped-query
+ * attention of one token; fp32 scores, softmax and sums, bf16 output).
+ * Two launches: per (64-row chunk, kv head) partial sums into the workspace
+ * (dip_decode_attention_workspace_size bytes), then one merge per query
+ * head.  head_dim 128 and n_heads / n_kv_heads in {1, 2, 4, 5, 8, 16}
+ * (else DIP_ERR_UNSUPPORTED).
+ */
+size_t dip_decode_attention_workspace_size(int64_t n_heads, int64_t head_dim, int64_t max_len);
+int dip_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         const int64_t* pos, uint16_t* out, int64_t n_heads, int64_t n_kv_heads,
+                         int64_t head_dim, int64_t max_len, float scale, void* workspace,
+                         size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }  // extern "C"
 #endif

@@ -94,6 +94,22 @@ def test_argument_rejection_before_launch():
     assert L.dip_get_tuning(99) == -6
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
     assert L.dip_ca_assemble(None, p, p, p, p, p, p, 10, 5, None) == -1
+    # decode steps: NULL / size / head_dim / alignment / grouping / workspace
+    assert L.dip_add_rmsnorm(None, None, p, p, 128, 1e-6, None) == -1
+    assert L.dip_add_rmsnorm(p, None, p, p, 0, 1e-6, None) == -2
+    assert L.dip_add_rmsnorm(p, None, p, p, 8193, 1e-6, None) == -2
+    assert L.dip_add_rmsnorm(p, None, p, p, 128, -1.0, None) == -6
+    assert L.dip_qk_norm_rope_cache(p, p, p, p, p, p, p, p, None, 4, 2, 128, 16, 1e-6,
+                                    None) == -1
+    assert L.dip_qk_norm_rope_cache(p, p, p, p, p, p, p, p, p, 4, 2, 64, 16, 1e-6, None) == -4
+    assert L.dip_qk_norm_rope_cache(p, p, p, p, p, p, p, p, p, 0, 2, 128, 16, 1e-6, None) == -2
+    assert L.dip_qk_norm_rope_cache(p + 2, p, p, p, p, p, p, p, p, 4, 2, 128, 16, 1e-6,
+                                    None) == -3
+    big = 1 << 20
+    assert L.dip_decode_attention(p, p, p, p, p, 6, 4, 128, 16, 1.0, p, big, None) == -2
+    assert L.dip_decode_attention(p, p, p, p, p, 6, 2, 128, 16, 1.0, p, big, None) == -4
+    assert L.dip_decode_attention(p, p, p, p, p, 8, 2, 128, 16, 1.0, p, 16, None) == -5
+    assert L.dip_decode_attention(p, p, p, p, p, 8, 2, 96, 16, 1.0, p, big, None) == -4
     del keep
 
 
@@ -106,6 +122,9 @@ def test_workspace_sizes():
     assert L.dip_gather_down_workspace_size(15361, 5120) == 61 * 5120 * 4
     assert L.dip_gather_down_workspace_size(1, 128) == 128 * 4
     assert L.dip_mlp_workspace_size(5120, 25600, 15360) >= need
+    # attention partials: (m, l, 128 sums) per query head per 64 cache rows
+    assert L.dip_decode_attention_workspace_size(64, 128, 300) == 5 * 64 * 130 * 4
+    assert L.dip_decode_attention_workspace_size(64, 96, 300) == 0
 
 
 def test_host_gather_rows():

@@ -1,0 +1,157 @@
+"""GPU: the one-token decode kernels of a Qwen3 decoder layer
+(dip_add_rmsnorm, dip_qk_norm_rope_cache, dip_decode_attention) against the
+math of transformers' Qwen3 modules (Qwen3RMSNorm.forward,
+apply_rotary_pos_emb, scaled-dot-product attention) restated with torch ops
+on the same bf16 inputs.
+
+Bars: the residual add and the value-cache copy are bit-exact; RMSNorm and
+the rotary embedding round at the modules' points but sum the squares in a
+different order, so outputs may differ by one bf16 ulp on a few elements;
+attention is compared with an fp64 softmax at the reference's
+max|err|/max|ref| < 1e-2 and 2 bf16 ulps per element (outputs near zero:
+1e-5 of the largest)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def K():
+    import _dip_hip
+    return _dip_hip
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+
+
+def _hf_rmsnorm(x, w, eps):
+    """Qwen3RMSNorm.forward on bf16 input (last dimension)."""
+    xf = x.float()
+    var = xf.pow(2).mean(-1, keepdim=True)
+    return w * (xf * torch.rsqrt(var + eps)).to(torch.bfloat16)
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def _tables(max_len, hd=128, theta=1e6):
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    f = torch.arange(max_len, dtype=torch.float32)[:, None] * inv[None, :]
+    t = torch.cat((f, f), -1)
+    return t.cos().to(torch.bfloat16).cuda(), t.sin().to(torch.bfloat16).cuda()
+
+
+@pytest.mark.parametrize("n", [128, 1000, 2560, 4096, 5120, 8192])
+def test_add_rmsnorm(K, n):
+    print(f"add_rmsnorm n={n}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    h = (torch.randn(n, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    add = torch.randn(n, device="cuda", generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(n, device="cuda", generator=g)).to(torch.bfloat16)
+    eps = 1e-6
+    h2 = h + add
+    ref = _hf_rmsnorm(h2, w, eps)
+    hk = h.clone()
+    out = torch.empty_like(h)
+    K.add_rmsnorm(hk, add, w, out, eps)
+    assert torch.equal(hk.view(torch.int16), h2.view(torch.int16))
+    d = ulp_diff(_bits(out), _bits(ref))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    # without the add: h is left as it is
+    h3 = h.clone()
+    K.add_rmsnorm(h3, None, w, out, eps)
+    assert torch.equal(h3.view(torch.int16), h.view(torch.int16))
+    d = ulp_diff(_bits(out), _bits(_hf_rmsnorm(h, w, eps)))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("nh,nkv,pos", [(64, 8, 5), (4, 2, 0), (40, 8, 127), (16, 16, 31)])
+def test_qk_norm_rope_cache(K, nh, nkv, pos):
+    print(f"qk_norm_rope_cache nh={nh} nkv={nkv} pos={pos}", flush=True)
+    hd, max_len, eps = 128, 128, 1e-6
+    g = torch.Generator(device="cuda").manual_seed(nh * 7 + pos)
+    qkv = (torch.randn((nh + 2 * nkv) * hd, device="cuda", generator=g) * 2).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(hd, device="cuda", generator=g)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(hd, device="cuda", generator=g)).to(torch.bfloat16)
+    cos, sin = _tables(max_len)
+    kc = torch.full((nkv, max_len, hd), 0.5, dtype=torch.bfloat16, device="cuda")
+    vc = torch.full((nkv, max_len, hd), -0.25, dtype=torch.bfloat16, device="cuda")
+    kc0, vc0 = kc.clone(), vc.clone()
+    q_out = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
+    p = torch.tensor([pos], dtype=torch.long, device="cuda")
+    K.qk_norm_rope_cache(qkv, qn, kn, cos, sin, p, q_out, kc, vc, nh, nkv, eps)
+
+    q = _hf_rmsnorm(qkv[: nh * hd].view(nh, hd), qn, eps)
+    k = _hf_rmsnorm(qkv[nh * hd:(nh + nkv) * hd].view(nkv, hd), kn, eps)
+    v = qkv[(nh + nkv) * hd:].view(nkv, hd)
+    c, s = cos[pos], sin[pos]
+    q_ref = q * c + _rotate_half(q) * s
+    k_ref = k * c + _rotate_half(k) * s
+    d = ulp_diff(_bits(q_out), _bits(q_ref))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    d = ulp_diff(_bits(kc[:, pos]), _bits(k_ref))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    assert torch.equal(vc[:, pos].view(torch.int16), v.view(torch.int16))
+    others = [i for i in range(max_len) if i != pos]
+    assert torch.equal(kc[:, others], kc0[:, others])
+    assert torch.equal(vc[:, others], vc0[:, others])
+    # a position outside the cache writes no cache row
+    K.qk_norm_rope_cache(qkv, qn, kn, cos, sin, torch.tensor([max_len], device="cuda"), q_out,
+                         kc0, vc0, nh, nkv, eps)
+    assert bool((kc0 == 0.5).all()) and bool((vc0 == -0.25).all())
+
+
+def _attn_ref(q, kc, vc, pos, scale):
+    nh, hd = q.shape
+    nkv = kc.shape[0]
+    G = nh // nkv
+    qd = q.double().cpu().view(nkv, G, hd)
+    kd = kc[:, : pos + 1].double().cpu()
+    vd = vc[:, : pos + 1].double().cpu()
+    s = torch.einsum("kgd,kpd->kgp", qd, kd) * scale
+    p = torch.softmax(s, dim=-1)
+    return torch.einsum("kgp,kpd->kgd", p, vd).reshape(nh, hd)
+
+
+@pytest.mark.parametrize("nh,nkv", [(8, 8), (4, 2), (32, 8), (40, 8), (64, 8), (64, 4)])
+def test_decode_attention(K, nh, nkv):
+    hd, max_len = 128, 300
+    g = torch.Generator(device="cuda").manual_seed(nh + nkv)
+    q = torch.randn(nh, hd, device="cuda", generator=g).to(torch.bfloat16)
+    kc = torch.randn(nkv, max_len, hd, device="cuda", generator=g).to(torch.bfloat16)
+    vc = torch.randn(nkv, max_len, hd, device="cuda", generator=g).to(torch.bfloat16)
+    scale = 1 / math.sqrt(hd)
+    ws = torch.zeros(K.decode_attention_workspace_bytes(nh, hd, max_len), dtype=torch.uint8,
+                     device="cuda")
+    for pos in (0, 1, 63, 64, 65, 200, max_len - 1):
+        print(f"decode_attention nh={nh} nkv={nkv} pos={pos}", flush=True)
+        out = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
+        K.decode_attention(q.view(-1), kc, vc, torch.tensor([pos], device="cuda"), out, scale, ws)
+        ref = _attn_ref(q, kc, vc, pos, scale)
+        got = out.view(nh, hd).double().cpu()
+        assert float((got - ref).abs().max() / ref.abs().max()) < 1e-2
+        # per element: within 2 bf16 ulps of the rounded fp64 value, or (for
+        # outputs near zero, where fp32 cancellation dominates) within
+        # 1e-5 of the largest output
+        ulps = ulp_diff(_bits(out), _bits(ref.float().to(torch.bfloat16))).reshape(nh, hd)
+        err = (got - ref).abs().numpy()
+        assert not ((ulps > 2) & (err > 1e-5 * float(ref.abs().max()))).any()
+
+
+def test_decode_attention_rejects_bad_arguments(K):
+    q = torch.zeros(3 * 128, dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(RuntimeError):   # 3 query heads over 2 kv heads
+        K.decode_attention(q, kc, kc, torch.zeros(1, dtype=torch.long, device="cuda"), out, 1.0)
+    with pytest.raises(RuntimeError):   # pos on the host
+        K.decode_attention(q[:256], kc, kc, torch.zeros(1, dtype=torch.long), out[:256], 1.0)

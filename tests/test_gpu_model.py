@@ -87,14 +87,41 @@ def test_graph_decode_real_shapes_equals_eager():
     assert torch.equal(log_g, log_e)
 
 
-def test_decode_matches_hf_incremental_forward(ckpt, streaming):
-    """transformers' own forward, one token at a time with its DynamicCache,
-    through the same StreamingDIPMlp and QuantLinear modules."""
+@pytest.mark.parametrize("keep,bound", [(KEEP, 8e-2), (1.0, 2e-2)])
+def test_fused_decode_matches_module_path(ckpt, streaming, keep, bound):
+    """The fused decode kernels against the same step through the HF
+    modules' PyTorch ops (same int4 GEMVs and DIP MLPs), teacher-forced on
+    the fused path's tokens.  The two differ by bf16 rounding (sum order
+    in RMSNorm, fp32 attention); at keep 0.6 such a difference in an MLP
+    input can swap a channel at the top-k boundary, and in a random-weight
+    model each swap moves y by about 1/sqrt(k) of its size, hence the wider
+    bound there."""
+    from dip_model import DIPDecoder
+    from dip_stream_predispatch import load_streaming_dip
+    name, d, cfg = ckpt
+    model, _, prompt = streaming
+    if keep != KEEP:
+        model, _, _ = load_streaming_dip(d, keep_ratio=keep)
+    print(f"fused vs module decode {name} keep {keep}", flush=True)
+    dec = DIPDecoder(model, 32)
+    assert dec.fused
+    seq, got = dec.generate(prompt, NEW, return_logits=True)
+    ref = teacher_forced_logits(DIPDecoder(model, 32, use_graph=False, fused=False), seq, PLEN)
+    err = max_rel(got, ref)
+    print(f"  max_rel {err:.3e}", flush=True)
+    assert err < bound
+    assert (got.argmax(-1).cpu() == ref.argmax(-1)).float().mean() >= 0.8
+
+
+def test_module_decode_equals_hf_incremental_forward(ckpt, streaming):
+    """DIPDecoder's module path (fused=False) is transformers' own
+    incremental forward, one token at a time with its DynamicCache, through
+    the same StreamingDIPMlp and QuantLinear modules: bit for bit."""
     from transformers import DynamicCache
     from dip_model import DIPDecoder
     model, _, prompt = streaming
-    print(f"decode vs HF incremental forward {ckpt[0]}", flush=True)
-    seq, got = DIPDecoder(model, 32).generate(prompt, NEW, return_logits=True)
+    print(f"module decode vs HF incremental forward {ckpt[0]}", flush=True)
+    seq, got = DIPDecoder(model, 32, fused=False).generate(prompt, NEW, return_logits=True)
     seq = seq.cuda()
     ref = []
     with torch.no_grad():
@@ -104,14 +131,10 @@ def test_decode_matches_hf_incremental_forward(ckpt, streaming):
         for t in range(PLEN, PLEN + NEW - 1):
             out = model(input_ids=seq[:, t:t + 1], past_key_values=cache, use_cache=True)
             ref.append(out.logits[0, -1].float())
-    ref = torch.stack(ref)
-    err = max_rel(got, ref)
-    print(f"  max_rel {err:.3e}", flush=True)
-    assert err < 3e-2
-    assert (got.argmax(-1).cpu() == ref.argmax(-1).cpu()).float().mean() >= 0.8
+    assert torch.equal(got, torch.stack(ref))
 
 
-@pytest.mark.parametrize("keep,bound", [(KEEP, 5e-2), (1.0, 2e-2)])
+@pytest.mark.parametrize("keep,bound", [(KEEP, 8e-2), (1.0, 2e-2)])
 def test_decode_matches_cpu_oracle_model(ckpt, streaming, keep, bound):
     """The same checkpoint on the CPU with every projection and MLP from the
     oracle (fp64 GEMV sums rounded to bf16, bit-exact threshold top-k), fed
