@@ -23,9 +23,9 @@ namespace dip {
 namespace {
 
 constexpr int kNormThreads = 256;
-constexpr int kNormPerThread = 32;        // n <= 8192
+constexpr int kNormVecs = 4;              // 16-byte vectors per thread: n <= 8192
 constexpr int kHeadDim = 128;
-constexpr int kAttnChunk = 64;            // cache positions per attention workgroup
+constexpr int kAttnChunk = 32;            // cache positions per attention workgroup
 constexpr int kPartFloats = 2 + kHeadDim; // m, l, acc[128] per (kv head, chunk, query head)
 
 DIP_DEV float wave_sum(float v) {
@@ -42,27 +42,46 @@ DIP_DEV float wave_max(float v) {
 
 DIP_DEV float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-// h = bf16(h + add) when add is given; out = RMSNorm(h) * w.  One workgroup.
+// h = bf16(h + add) when add is given; out = RMSNorm(h) * w.  One workgroup;
+// thread t owns the 16-byte vectors t, t + 256, ... (8 values each), all
+// loaded before anything is stored.
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     uint16_t* __restrict__ h, const uint16_t* __restrict__ add, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ out, int n, float eps) {
   __shared__ float part[kNormThreads / 64];
-  float v[kNormPerThread];
+  const int nv = n / 8;
+  uint4 hv[kNormVecs], av[kNormVecs], wv[kNormVecs];
+#pragma unroll
+  for (int j = 0; j < kNormVecs; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    hv[j] = av[j] = wv[j] = make_uint4(0, 0, 0, 0);
+    if (c < nv) {
+      hv[j] = reinterpret_cast<const uint4*>(h)[c];
+      av[j] = add ? reinterpret_cast<const uint4*>(add)[c] : make_uint4(0, 0, 0, 0);
+      wv[j] = reinterpret_cast<const uint4*>(w)[c];
+    }
+  }
+  float x[kNormVecs][8];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kNormPerThread; ++j) {
-    const int i = threadIdx.x + j * kNormThreads;
-    float x = 0.f;
-    if (i < n) {
-      x = bf16_to_f32(h[i]);
+  for (int j = 0; j < kNormVecs; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    const uint32_t hw[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+    const uint32_t aw[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+    uint32_t nw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float lo = bf16_to_f32(hw[e] & 0xFFFFu), hi = bf16_to_f32(hw[e] >> 16);
       if (add) {
-        const uint32_t s = f32_to_bf16(x + bf16_to_f32(add[i]));
-        h[i] = (uint16_t)s;
-        x = bf16_to_f32(s);
+        lo = round_bf16(lo + bf16_to_f32(aw[e] & 0xFFFFu));
+        hi = round_bf16(hi + bf16_to_f32(aw[e] >> 16));
       }
+      nw[e] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+      x[j][2 * e] = lo;
+      x[j][2 * e + 1] = hi;
+      if (c < nv) ss += lo * lo + hi * hi;
     }
-    v[j] = x;
-    ss += x * x;
+    if (add && c < nv) reinterpret_cast<uint4*>(h)[c] = make_uint4(nw[0], nw[1], nw[2], nw[3]);
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
@@ -72,9 +91,19 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
   for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
   const float r = rsqrtf(tot * (1.0f / (float)n) + eps);
 #pragma unroll
-  for (int j = 0; j < kNormPerThread; ++j) {
-    const int i = threadIdx.x + j * kNormThreads;
-    if (i < n) out[i] = (uint16_t)f32_to_bf16(bf16_to_f32(w[i]) * round_bf16(v[j] * r));
+  for (int j = 0; j < kNormVecs; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    if (c >= nv) continue;
+    const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = f32_to_bf16(bf16_to_f32(ww[e] & 0xFFFFu) * round_bf16(x[j][2 * e] * r));
+      const uint32_t hi =
+          f32_to_bf16(bf16_to_f32(ww[e] >> 16) * round_bf16(x[j][2 * e + 1] * r));
+      ow[e] = lo | (hi << 16);
+    }
+    reinterpret_cast<uint4*>(out)[c] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
   }
 }
 
@@ -130,8 +159,10 @@ __global__ __launch_bounds__(64) void qk_rope_cache_kernel(
 }
 
 // Attention, pass 1: workgroup (chunk c, kv head) takes cache positions
-// [64c, 64c + 64) up to pos and the G query heads that share the kv head.
-// Lane = position for the scores, lane = dimension pair for the value sum.
+// [32c, 32c + 32) up to pos and the G query heads that share the kv head.
+// Scores: lanes 2j and 2j + 1 take position j, each one half of the head
+// dimensions, and add their halves.  Value sum: lane l takes dimensions 2l
+// and 2l + 1 over the chunk's positions, all value loads issued first.
 // Writes per query head the chunk's max score m, sum of exp(s - m) and the
 // unnormalised value sum.
 template <int G>
@@ -146,29 +177,42 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
   const int start = c * kAttnChunk;
   if ((int64_t)start > last) return;  // no position of this chunk is attended
+  const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
+
+  const int half = l & 1;
+  const int p = start + (l >> 1);
+  const bool live = (l >> 1) < npos;
+  uint4 kr[8];
+  if (live) {
+    const uint4* src = reinterpret_cast<const uint4*>(
+        k_cache + ((size_t)kvh * max_len + p) * kHeadDim + half * (kHeadDim / 2));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = src[i];
+  }
+  const uint32_t* vcol =
+      reinterpret_cast<const uint32_t*>(v_cache + ((size_t)kvh * max_len + start) * kHeadDim) + l;
+  uint32_t vv[kAttnChunk];
+#pragma unroll
+  for (int j = 0; j < kAttnChunk; ++j) vv[j] = j < npos ? vcol[(size_t)j * 64] : 0u;
   for (int i = l; i < G * kHeadDim; i += 64)
     qs[i / kHeadDim][i % kHeadDim] = bf16_to_f32(q[(size_t)kvh * G * kHeadDim + i]);
   __syncthreads();
 
-  const int p = start + l;
-  const bool live = (int64_t)p <= last;
   float s[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) s[g] = 0.f;
   if (live) {
-    const uint4* krow =
-        reinterpret_cast<const uint4*>(k_cache + ((size_t)kvh * max_len + p) * kHeadDim);
-#pragma unroll 4
-    for (int ch = 0; ch < kHeadDim / 8; ++ch) {
-      const uint4 kv = krow[ch];
-      const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float k0 = bf16_to_f32(w4[e] & 0xFFFFu), k1 = bf16_to_f32(w4[e] >> 16);
+        const int d = half * (kHeadDim / 2) + i * 8 + 2 * e;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          s[g] = fmaf(qs[g][ch * 8 + 2 * e], k0, s[g]);
-          s[g] = fmaf(qs[g][ch * 8 + 2 * e + 1], k1, s[g]);
+          s[g] = fmaf(qs[g][d], k0, s[g]);
+          s[g] = fmaf(qs[g][d + 1], k1, s[g]);
         }
       }
     }
@@ -176,27 +220,27 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   float m[G], lsum[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float sc = live ? s[g] * scale : -INFINITY;
+    const float full = s[g] + __shfl_xor(s[g], 1, 64);
+    const float sc = live ? full * scale : -INFINITY;
     m[g] = wave_max(sc);
     const float e = live ? expf(sc - m[g]) : 0.f;
-    ps[g][l] = e;
-    lsum[g] = wave_sum(e);
+    if (half == 0) ps[g][l >> 1] = e;
+    lsum[g] = wave_sum(half == 0 ? e : 0.f);
   }
   __syncthreads();
 
   float a0[G], a1[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) a0[g] = a1[g] = 0.f;
-  const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
-  const uint32_t* vcol =
-      reinterpret_cast<const uint32_t*>(v_cache + ((size_t)kvh * max_len + start) * kHeadDim) + l;
-  for (int j = 0; j < npos; ++j) {
-    const uint32_t vp = vcol[(size_t)j * 64];
-    const float v0 = bf16_to_f32(vp & 0xFFFFu), v1 = bf16_to_f32(vp >> 16);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      a0[g] = fmaf(ps[g][j], v0, a0[g]);
-      a1[g] = fmaf(ps[g][j], v1, a1[g]);
+  for (int j = 0; j < kAttnChunk; ++j) {
+    if (j < npos) {
+      const float v0 = bf16_to_f32(vv[j] & 0xFFFFu), v1 = bf16_to_f32(vv[j] >> 16);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        a0[g] = fmaf(ps[g][j], v0, a0[g]);
+        a1[g] = fmaf(ps[g][j], v1, a1[g]);
+      }
     }
   }
   float* out = part + ((size_t)kvh * nchunks + c) * G * kPartFloats;
@@ -212,7 +256,7 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   }
 }
 
-// Attention, pass 2: one wave per query head merges the chunks 0 .. pos/64
+// Attention, pass 2: one wave per query head merges the chunks 0 .. pos/32
 // (rescaling each by exp(m_c - max m)) and writes bf16(sum / l).
 __global__ __launch_bounds__(64) void attn_combine_kernel(
     const float* __restrict__ part, const int64_t* __restrict__ pos_p, uint16_t* __restrict__ out,
@@ -256,8 +300,10 @@ using namespace dip;
 extern "C" int dip_add_rmsnorm(uint16_t* h, const uint16_t* add, const uint16_t* weight,
                                uint16_t* out, int64_t n, float eps, void* stream) {
   if (!h || !weight || !out) return DIP_ERR_NULL;
-  if (n <= 0 || n > (int64_t)kNormThreads * kNormPerThread) return DIP_ERR_SHAPE;
+  if (n <= 0 || n % 8 != 0 || n > (int64_t)kNormThreads * kNormVecs * 8) return DIP_ERR_SHAPE;
   if (!(eps >= 0.f)) return DIP_ERR_ARG;
+  if (!aligned16(h) || !aligned16(weight) || !aligned16(out) || (add && !aligned16(add)))
+    return DIP_ERR_ALIGN;
   hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, (hipStream_t)stream, h,
                      add, weight, out, (int)n, eps);
   return hip_status(hipGetLastError());

@@ -297,7 +297,8 @@ int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t
  *
  * dip_add_rmsnorm: if `add` is non-NULL, h[i] = bf16(h[i] + add[i]) in place
  * (the residual add); then out = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
- * with an fp32 mean.  1 <= n <= 8192.
+ * with an fp32 mean.  n a multiple of 8, at most 8192; pointers 16-byte
+ * aligned.
  */
 int dip_add_rmsnorm(uint16_t* h, const uint16_t* add, const uint16_t* weight, uint16_t* out,
                     int64_t n, float eps, void* stream);
@@ -324,7 +325,7 @@ int dip_qk_norm_rope_cache(const uint16_t* qkv, const uint16_t* q_norm_w,
  * dip_decode_attention: out[h] = softmax(scale * q[h] . K[j]) V over cache
  * rows j = 0 .. pos of kv head h / (n_heads / n_kv_heads) (grouped-query
  * attention of one token; fp32 scores, softmax and sums, bf16 output).
- * Two launches: per (64-row chunk, kv head) partial sums into the workspace
+ * Two launches: per (32-row chunk, kv head) partial sums into the workspace
  * (dip_decode_attention_workspace_size bytes), then one merge per query
  * head.  head_dim 128 and n_heads / n_kv_heads in {1, 2, 4, 5, 8, 16}
  * (else DIP_ERR_UNSUPPORTED).

@@ -98,6 +98,8 @@ def test_argument_rejection_before_launch():
     assert L.dip_add_rmsnorm(None, None, p, p, 128, 1e-6, None) == -1
     assert L.dip_add_rmsnorm(p, None, p, p, 0, 1e-6, None) == -2
     assert L.dip_add_rmsnorm(p, None, p, p, 8193, 1e-6, None) == -2
+    assert L.dip_add_rmsnorm(p, None, p, p, 100, 1e-6, None) == -2
+    assert L.dip_add_rmsnorm(p + 2, None, p, p, 128, 1e-6, None) == -3
     assert L.dip_add_rmsnorm(p, None, p, p, 128, -1.0, None) == -6
     assert L.dip_qk_norm_rope_cache(p, p, p, p, p, p, p, p, None, 4, 2, 128, 16, 1e-6,
                                     None) == -1
@@ -122,8 +124,8 @@ def test_workspace_sizes():
     assert L.dip_gather_down_workspace_size(15361, 5120) == 61 * 5120 * 4
     assert L.dip_gather_down_workspace_size(1, 128) == 128 * 4
     assert L.dip_mlp_workspace_size(5120, 25600, 15360) >= need
-    # attention partials: (m, l, 128 sums) per query head per 64 cache rows
-    assert L.dip_decode_attention_workspace_size(64, 128, 300) == 5 * 64 * 130 * 4
+    # attention partials: (m, l, 128 sums) per query head per 32 cache rows
+    assert L.dip_decode_attention_workspace_size(64, 128, 300) == 10 * 64 * 130 * 4
     assert L.dip_decode_attention_workspace_size(64, 96, 300) == 0
 
 

@@ -132,7 +132,7 @@ def test_decode_attention(K, nh, nkv):
     scale = 1 / math.sqrt(hd)
     ws = torch.zeros(K.decode_attention_workspace_bytes(nh, hd, max_len), dtype=torch.uint8,
                      device="cuda")
-    for pos in (0, 1, 63, 64, 65, 200, max_len - 1):
+    for pos in (0, 1, 31, 32, 33, 63, 64, 200, max_len - 1):
         print(f"decode_attention nh={nh} nkv={nkv} pos={pos}", flush=True)
         out = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
         K.decode_attention(q.view(-1), kc, vc, torch.tensor([pos], device="cuda"), out, scale, ws)
