@@ -163,6 +163,31 @@ DIP_DEV float group_sum(float v) {
   return v;
 }
 
+// Max over aligned groups of W lanes, every lane receiving it: group_sum's
+// exchange pattern with fmaxf.
+DIP_DEV float row_pair_max16(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+DIP_DEV float row_pair_max32(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+template <int W>
+DIP_DEV float group_max(float v) {
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "W");
+  if (W >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+  if (W >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+  if (W >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+  if (W >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+  if (W >= 32) v = row_pair_max16(v);
+  if (W >= 64) v = row_pair_max32(v);
+  return v;
+}
+
 // 128-bit streaming load (weights are read once per call: non-temporal).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 DIP_DEV uint4 ldg_nt(const uint4* p) {

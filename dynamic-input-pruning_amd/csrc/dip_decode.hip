@@ -28,17 +28,9 @@ constexpr int kHeadDim = 128;
 constexpr int kAttnChunk = 32;            // cache positions per attention workgroup
 constexpr int kPartFloats = 2 + kHeadDim; // m, l, acc[128] per (kv head, chunk, query head)
 
-DIP_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-DIP_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
+// Wave-wide reductions on DPP / permlane exchanges (no LDS round trips).
+DIP_DEV float wave_sum(float v) { return group_sum<64>(v); }
+DIP_DEV float wave_max(float v) { return group_max<64>(v); }
 
 DIP_DEV float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
@@ -194,8 +186,17 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   uint32_t vv[kAttnChunk];
 #pragma unroll
   for (int j = 0; j < kAttnChunk; ++j) vv[j] = j < npos ? vcol[(size_t)j * 64] : 0u;
-  for (int i = l; i < G * kHeadDim; i += 64)
-    qs[i / kHeadDim][i % kHeadDim] = bf16_to_f32(q[(size_t)kvh * G * kHeadDim + i]);
+  const uint4* qsrc = reinterpret_cast<const uint4*>(q + (size_t)kvh * G * kHeadDim);
+  float* qflat = &qs[0][0];
+  for (int i = l; i < G * kHeadDim / 8; i += 64) {
+    const uint4 v = qsrc[i];
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      qflat[i * 8 + 2 * e] = bf16_to_f32(w4[e] & 0xFFFFu);
+      qflat[i * 8 + 2 * e + 1] = bf16_to_f32(w4[e] >> 16);
+    }
+  }
   __syncthreads();
 
   float s[G];
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   float m[G], lsum[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float full = s[g] + __shfl_xor(s[g], 1, 64);
+    const float full = s[g] + dpp_mov<0xB1>(s[g]);  // the other half of the head
     const float sc = live ? full * scale : -INFINITY;
     m[g] = wave_max(sc);
     const float e = live ? expf(sc - m[g]) : 0.f;
