@@ -65,6 +65,7 @@ _SIGS = {
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
+    "dip_int4_gemm": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dip_add_rmsnorm": ([_p, _p, _p, _p, _i64, ctypes.c_float, _p], _i32),
     "dip_qk_norm_rope_cache": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                 ctypes.c_float, _p], _i32),
@@ -171,6 +172,26 @@ def int4_gemv(qweight, scales, x, act: int = 0, out=None):
     _check(lib.dip_int4_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(out), rows, cols,
                              int(act), _stream(dev)), "dip_int4_gemv")
     return out
+
+
+def int4_gemm(qweight, scales, x, out=None):
+    """out [M, N] = bf16(x [M, K] @ (q*s)^T) on bf16 MFMA (prompt projections)."""
+    qweight, scales, rows, cols = _weights(qweight, scales, "int4_gemm")
+    dev = _dev(qweight, scales, x)
+    if x.dtype != torch.bfloat16 or x.shape[-1] != cols:
+        raise RuntimeError(f"x must be bf16 [..., {cols}]")
+    x2 = x.reshape(-1, cols)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous().clone() if x2.data_ptr() % 16 else x2.contiguous()
+    m = x2.shape[0]
+    if out is None:
+        out = torch.empty(m, rows, dtype=torch.bfloat16, device=dev)
+    elif (out.dtype != torch.bfloat16 or out.numel() != m * rows or not out.is_contiguous()
+          or out.device != dev):
+        raise RuntimeError(f"out must be a contiguous bf16 tensor of {m} x {rows} values")
+    _check(lib.dip_int4_gemm(_ptr(qweight), _ptr(scales), _ptr(x2), _ptr(out), m, rows, cols,
+                             _stream(dev)), "dip_int4_gemm")
+    return out.view(*x.shape[:-1], rows)
 
 
 def topk_select(s: torch.Tensor, k: int, out=None):

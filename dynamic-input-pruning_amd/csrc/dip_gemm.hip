@@ -1,0 +1,226 @@
+// dip_gemm.hip — int4 g128 GEMM for prompts (more than one token) on bf16
+// MFMA: out[M, N] = bf16( x[M, K] . W[N, K]^T ), W in the reference's Linear
+// layout (qweight int8 [N, K/2], scales bf16 [N, K/128]).
+//
+// The reference computes this as dequantize + F.linear (qlinear.py:86-88,
+// dip_stream_predispatch.py:206-215 for gate and up): it writes a bf16 copy
+// of W and reads it back in a GEMM.  Here each weight is read once, as
+// packed nibbles, and turned into an MFMA operand in registers:
+//   * a nibble u (two's complement q) becomes the bf16 value 136 + q, exact:
+//     0x4300 | (u ^ 8) is 128 + (q + 8), so 8 nibbles need a few bit ops;
+//   * v_mfma_f32_16x16x32_bf16 sums (136 + q) * x over one 128-column group
+//     in fp32; subtracting 136 * sum(x) of the group leaves sum(q * x),
+//     which is scaled by the group's scale and added to the fp32 total.
+// So the weights enter exactly as q * s in fp32 (the reference rounds q * s
+// to bf16 first); the output is rounded to bf16 once.
+//
+// Tiling: a workgroup is 4 waves on 16 * RT weight rows and 16 * TM tokens;
+// the 4 / RT waves of one 16-row tile split the K groups between them (wave
+// ks takes groups ks, ks + KS, ...) and add their partial sums through LDS
+// at the end, in a fixed order.  Nothing else is shared: each lane loads
+// its own 16 bytes of nibbles and 64 bytes of x per group (x is small and
+// stays in L2), weights and scales PW groups ahead and x two groups ahead,
+// so no barrier sits in the main loop.  Inside a 32-column MFMA slice the k
+// order is permuted identically for both operands (lane quarter kb holds
+// columns 32 kb .. 32 kb + 31 and slice j uses its 8 columns 8j .. 8j + 7),
+// so a lane's nibbles are one contiguous 16-byte load.  The offset term
+// 136 * sum(x) comes from the same MFMA with a constant operand.
+#include "dip_common.h"
+#include "dip_internal.h"
+
+namespace dip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmThreads = 256;
+constexpr uint32_t kOffsetPair = 0x43084308u;  // bf16 136.0, twice
+
+// 8 nibbles (element p = nibble p of w) -> the 8 bf16 values 136 + q.
+DIP_DEV bf16x8_t offset_bf16x8(uint32_t w) {
+  const uint32_t t = w ^ 0x88888888u;  // q + 8 in every nibble
+  u32x4_t p;
+  p.x = 0x43004300u | (t & 0xFu) | ((t & 0xF0u) << 12);
+  p.y = 0x43004300u | ((t >> 8) & 0xFu) | ((t & 0xF000u) << 4);
+  p.z = 0x43004300u | ((t >> 16) & 0xFu) | ((t >> 4) & 0xF0000u);
+  p.w = 0x43004300u | ((t >> 24) & 0xFu) | ((t >> 12) & 0xF0000u);
+  return __builtin_bit_cast(bf16x8_t, p);
+}
+
+DIP_DEV bf16x8_t as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
+}
+
+template <int TM, int RT, int PW>
+__global__ __launch_bounds__(kGemmThreads) void int4_gemm_kernel(
+    const int8_t* __restrict__ qw, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ out, int M, int N, int K) {
+  static_assert(PW % 2 == 0, "x ring of 2 inside the weight ring");
+  constexpr int KS = 4 / RT;  // waves per 16-row tile (K split)
+  __shared__ float red[KS > 1 ? 4 : 1][TM][4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rt = wave / KS, ks = wave % KS;
+  const int row0 = blockIdx.x * (16 * RT) + rt * 16;
+  const int tok0 = blockIdx.y * TM * 16;
+  const int ngroups = K >> 7;
+  const int ng = ngroups > ks ? (ngroups - ks + KS - 1) / KS : 0;  // this wave's groups
+  const int kb = lane >> 4, l16 = lane & 15;
+
+  // A operand: weight row l16, columns 32 kb .. 32 kb + 31 of each group
+  const uint4* wp =
+      reinterpret_cast<const uint4*>(qw + (size_t)min(row0 + l16, N - 1) * (K >> 1)) + kb;
+  // B operand: token l16 of each 16-token tile, the same columns
+  const uint4* xp[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+    xp[t] = reinterpret_cast<const uint4*>(x + (size_t)min(tok0 + t * 16 + l16, M - 1) * K) +
+            4 * kb;
+  // D: token l16, rows 4 kb + r; their scales
+  const uint16_t* sp[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sp[r] = sc + (size_t)min(row0 + 4 * kb + r, N - 1) * ngroups;
+
+  uint4 wq[PW];
+  uint32_t sq[PW][4];
+  uint4 xq[2][TM][4];
+#pragma unroll
+  for (int p = 0; p < PW; ++p) {
+    if (p < ng) {
+      const int g = ks + p * KS;
+      wq[p] = wp[4 * g];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sq[p][r] = sp[r][g];
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    if (p < ng) {
+      const int g = ks + p * KS;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xq[p][t][v] = xp[t][16 * g + v];
+    }
+  }
+
+  const bf16x8_t c136 = __builtin_bit_cast(
+      bf16x8_t, u32x4_t{kOffsetPair, kOffsetPair, kOffsetPair, kOffsetPair});
+  floatx4 acc[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int i0 = 0; i0 < ng; i0 += PW) {
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int i = i0 + p;
+      if (i < ng) {
+        const bf16x8_t a0 = offset_bf16x8(wq[p].x), a1 = offset_bf16x8(wq[p].y);
+        const bf16x8_t a2 = offset_bf16x8(wq[p].z), a3 = offset_bf16x8(wq[p].w);
+        float s4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s4[r] = bf16_to_f32(sq[p][r]);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+          const bf16x8_t b0 = as_bf16x8(xq[p & 1][t][0]), b1 = as_bf16x8(xq[p & 1][t][1]);
+          const bf16x8_t b2 = as_bf16x8(xq[p & 1][t][2]), b3 = as_bf16x8(xq[p & 1][t][3]);
+          floatx4 d = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, d, 0, 0, 0);
+          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b0, d1, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b1, d1, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2, d, 0, 0, 0);
+          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b2, d1, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b3, d, 0, 0, 0);
+          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b3, d1, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(s4[r], d[r] - d1[r], acc[t][r]);
+        }
+        if (i + PW < ng) {
+          const int g = ks + (i + PW) * KS;
+          wq[p] = wp[4 * g];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sq[p][r] = sp[r][g];
+        }
+        if (i + 2 < ng) {
+          const int g = ks + (i + 2) * KS;
+#pragma unroll
+          for (int t = 0; t < TM; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xq[p & 1][t][v] = xp[t][16 * g + v];
+        }
+      }
+    }
+  }
+
+  if constexpr (KS > 1) {
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int w = 1; w < KS; ++w)
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] += red[wave + w][t][r][lane];
+  }
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int tok = tok0 + t * 16 + l16;
+    if (tok >= M) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 4 * kb + r;
+      if (row < N) out[(size_t)tok * N + row] = (uint16_t)f32_to_bf16(acc[t][r]);
+    }
+  }
+}
+
+template <int TM, int PW>
+void launch_gemm(const int8_t* qw, const uint16_t* sc, const uint16_t* x, uint16_t* out, int M,
+                 int N, int K, hipStream_t s) {
+  // 16 * RT rows per workgroup: as many rows as keep at least two
+  // workgroups per CU, the rest of the 4 waves splitting K
+  const int cus = device_cus();
+  const unsigned gy = (unsigned)((M + 16 * TM - 1) / (16 * TM));
+  if ((long long)N >= 64LL * 2 * cus)
+    hipLaunchKernelGGL((int4_gemm_kernel<TM, 4, PW>), dim3((N + 63) / 64, gy), dim3(kGemmThreads),
+                       0, s, qw, sc, x, out, M, N, K);
+  else if ((long long)N >= 32LL * 2 * cus)
+    hipLaunchKernelGGL((int4_gemm_kernel<TM, 2, PW>), dim3((N + 31) / 32, gy), dim3(kGemmThreads),
+                       0, s, qw, sc, x, out, M, N, K);
+  else
+    hipLaunchKernelGGL((int4_gemm_kernel<TM, 1, PW>), dim3((N + 15) / 16, gy), dim3(kGemmThreads),
+                       0, s, qw, sc, x, out, M, N, K);
+}
+
+}  // namespace
+}  // namespace dip
+
+using namespace dip;
+
+extern "C" int dip_int4_gemm(const int8_t* qweight, const uint16_t* scales, const uint16_t* x,
+                             uint16_t* out, int64_t m, int64_t out_features,
+                             int64_t in_features, void* stream) {
+  if (!qweight || !scales) return DIP_ERR_NULL;
+  if (m < 0 || out_features <= 0 || in_features <= 0 || in_features % kGroupSize != 0 ||
+      out_features > INT32_MAX || in_features > (1 << 20) || m > 64 * 65535 ||
+      m * out_features > ((int64_t)1 << 40))
+    return DIP_ERR_SHAPE;
+  if (m == 0) return DIP_OK;  // x and out may be NULL then
+  if (!x || !out) return DIP_ERR_NULL;
+  if (!aligned16(qweight) || !aligned16(x)) return DIP_ERR_ALIGN;
+  const int M = (int)m, N = (int)out_features, K = (int)in_features;
+  hipStream_t s = (hipStream_t)stream;
+  if (M <= 16)
+    launch_gemm<1, 8>(qweight, scales, x, out, M, N, K, s);
+  else if (M <= 32)
+    launch_gemm<2, 8>(qweight, scales, x, out, M, N, K, s);
+  else
+    launch_gemm<4, 4>(qweight, scales, x, out, M, N, K, s);
+  return hip_status(hipGetLastError());
+}

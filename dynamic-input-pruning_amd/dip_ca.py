@@ -27,7 +27,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 import _dip_hip as K
-from qlinear import GROUP_SIZE, dequantize
+from qlinear import GROUP_SIZE, dequantize, int4_linear
 from dip_stream_predispatch import _transpose_down_to_int4, _use_gather, _use_down  # noqa: F401
 
 _use_ca_fused = True
@@ -130,8 +130,7 @@ class CADIPMlp(nn.Module):
             out = torch.stack([K.int4_gemv(self.gate_qw, self.gate_sc, x[b, 0].to(torch.bfloat16))
                                for b in range(x.shape[0])])
             return out.reshape(x.shape[0], 1, -1)
-        w = dequantize(self.gate_qw, self.gate_sc).to(x.dtype)
-        return F.linear(x, w)
+        return int4_linear(x, self.gate_qw, self.gate_sc)
 
     def _stream_misses(self, miss_ids_cpu: torch.Tensor, n_miss: int):
         """Pinned row gather of the misses (native threads) + async H2D on the
@@ -176,11 +175,9 @@ class CADIPMlp(nn.Module):
         return torch.stack(ys).to(xdt).reshape(x.shape[0], 1, -1)
 
     def _dense(self, x):
-        """dip_ca.py:190-196."""
+        """Prefill route (dip_ca.py:190-196), as StreamingDIPMlp._dense."""
         g = F.silu(self._gate(x))
-        up_w = dequantize(self.up_qw.to(self.device), self.up_sc.to(self.device)).to(x.dtype)
-        u = F.linear(x, up_w)
-        del up_w
+        u = int4_linear(x, self.up_qw.to(self.device), self.up_sc.to(self.device))
         h = g * u
         dn_t = dequantize(self.down_t_qw.to(self.device),
                           self.down_t_sc.to(self.device)).to(x.dtype)

@@ -17,8 +17,9 @@ transposed down resident and runs the whole decode step on the GPU:
 
 with no host synchronisation, so consecutive layers (and HIP-graph captures of
 them) run back to back.  Constructor arguments, attributes and routing follow
-the reference; ``forward`` of a non-decode input (prefill) uses the dense
-dequant + GEMM route of the reference's ``_dense``.
+the reference; ``forward`` of a non-decode input (prefill) takes the dense
+route of the reference's ``_dense`` (every channel), with the gate and up
+projections on the int4 MFMA GEMM for short prompts.
 """
 from __future__ import annotations
 
@@ -27,7 +28,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 import _dip_hip as K
-from qlinear import GROUP_SIZE, dequantize, _unpack_int4
+from qlinear import GROUP_SIZE, dequantize, int4_linear, _unpack_int4
 from quantize import pack_int4
 
 # The reference decides these from which kernel .so files it found; here the
@@ -148,8 +149,7 @@ class StreamingDIPMlp(nn.Module):
             out = torch.stack([K.int4_gemv(self.gate_qw, self.gate_sc, x[b, 0].to(torch.bfloat16))
                                for b in range(x.shape[0])])
             return out.reshape(x.shape[0], 1, -1)
-        w = dequantize(self.gate_qw, self.gate_sc).to(x.dtype)
-        return F.linear(x, w)
+        return int4_linear(x, self.gate_qw, self.gate_sc)
 
     def _decode_one(self, xv: torch.Tensor) -> torch.Tensor:
         b = self.buf
@@ -176,11 +176,11 @@ class StreamingDIPMlp(nn.Module):
         return torch.stack(ys).to(xdt).reshape(x.shape[0], 1, -1)
 
     def _dense(self, x):
-        """Prefill route: dense dequant + GEMM (dip_stream_predispatch.py:206-215)."""
+        """Prefill route (dip_stream_predispatch.py:206-215): every channel; the
+        gate and up projections through int4_linear (the int4 GEMM for short
+        prompts), down through its dequantized transpose."""
         g = F.silu(self._gate(x))
-        up_w = dequantize(self.up_qw, self.up_sc).to(x.dtype)
-        u = F.linear(x, up_w)
-        del up_w
+        u = int4_linear(x, self.up_qw, self.up_sc)
         h = g * u
         dn_t = dequantize(self.down_t_qw, self.down_t_sc).to(x.dtype)
         return h @ dn_t

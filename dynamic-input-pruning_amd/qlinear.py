@@ -8,11 +8,13 @@ helpers, qlinear.py:25-88).
 ``dequantize`` on device tensors runs the HIP dequant kernel (bf16(q*s), the
 same rounding as the reference); on host tensors it uses torch ops, which is
 how the reference uses it at load time (e.g. the one-time down transpose).
-``QuantLinear`` is the reference's projection layer (qlinear.py:67-88): the
-dense dequant + F.linear route for prefill, and for a single-token decode
-input on the GPU the int4 GEMV kernel, which reads the packed weight once
-instead of writing and re-reading a bf16 copy (it sums exact fp32 q*s*x
-products, so it differs from dequant + F.linear by fp32 rounding only).
+``QuantLinear`` is the reference's projection layer (qlinear.py:67-88).  On
+the GPU it reads the packed weight once instead of writing and re-reading a
+bf16 copy: the int4 GEMV for one token, the int4 MFMA GEMM for prompts of up
+to GEMM_MAX_TOKENS tokens; longer prompts take the reference's dequant +
+F.linear route.  Both kernels take the weights as exact fp32 q*s (the
+reference rounds them to bf16 first), so they differ from dequant + F.linear
+by rounding only.
 ``_replace_linears_with_quant`` and ``load_quantized_qwen3`` build the
 reference's int4 baseline model (qlinear.py:91-166) with every weight
 resident on one device.
@@ -30,6 +32,26 @@ _QUANT_SUBSTRINGS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_pr
 # Input widths the int4 GEMV kernel is built for (its dispatch table:
 # 32-column chunks split over 4..32 lanes per row).
 _GEMV_COLS = frozenset((128, 256, 512, 1024, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192))
+# Prompts of up to this many tokens run the int4 MFMA GEMM (weights read
+# once as nibbles); longer ones dequantize once and use the library GEMM,
+# which wins once the bf16 copy is amortised over enough tokens.
+GEMM_MAX_TOKENS = 64
+
+
+def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """x @ (q*s)^T for x [..., in] on the device, in x's dtype: the int4
+    GEMV for one token, the int4 MFMA GEMM for up to GEMM_MAX_TOKENS, else
+    dequantize + F.linear (the reference's route, qlinear.py:86-88)."""
+    import _dip_hip as K
+    in_f = qweight.shape[1] * 2
+    rows = x.numel() // in_f
+    if rows == 1 and in_f in _GEMV_COLS:
+        y = K.int4_gemv(qweight, scales, x.reshape(-1).to(torch.bfloat16))
+        return y.to(x.dtype).reshape(*x.shape[:-1], qweight.shape[0])
+    if 1 < rows <= GEMM_MAX_TOKENS:
+        y = K.int4_gemm(qweight, scales, x.reshape(rows, in_f).to(torch.bfloat16))
+        return y.to(x.dtype).reshape(*x.shape[:-1], qweight.shape[0])
+    return F.linear(x, dequantize(qweight, scales).to(x.dtype))
 
 
 def _unpack_int4(qweight: torch.Tensor) -> torch.Tensor:
@@ -71,11 +93,8 @@ class QuantLinear(nn.Module):
         self.bias = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if (x.is_cuda and x.numel() == self.in_features and self.in_features in _GEMV_COLS
-                and self.out_features > 0):
-            from _dip_hip import int4_gemv
-            y = int4_gemv(self.qweight, self.scales, x.reshape(-1).to(torch.bfloat16))
-            return y.to(x.dtype).reshape(*x.shape[:-1], self.out_features)
+        if x.is_cuda and self.out_features > 0:
+            return int4_linear(x, self.qweight, self.scales)
         w = dequantize(self.qweight, self.scales)
         return F.linear(x, w.to(x.dtype))
 

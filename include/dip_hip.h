@@ -285,6 +285,20 @@ int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t
                          int64_t row_bytes, int64_t src_rows, int threads);
 
 /*
+ * out[m, n] = bf16( sum_c (q*s)[n, c] * x[m, c] ) for m < M tokens: the int4
+ * projection of a prompt (more than one token) on bf16 MFMA, weights read
+ * once as packed nibbles.  x bf16 [M, in_features] row-major, out bf16
+ * [M, out_features].  Replaces dequantize + F.linear for prompts
+ * (qlinear.py:86-88; the gate and up GEMMs of StreamingDIPMlp._dense,
+ * dip_stream_predispatch.py:206-212).  The weights enter as exact fp32 q*s
+ * (the reference rounds them to bf16 first); fp32 sums, one bf16 rounding.
+ * M <= 64 * 65535; qweight and x 16-byte aligned.
+ */
+int dip_int4_gemm(const int8_t* qweight, const uint16_t* scales, const uint16_t* x,
+                  uint16_t* out, int64_t m, int64_t out_features, int64_t in_features,
+                  void* stream);
+
+/*
  * One-token decode steps of a Qwen3 decoder layer around the DIP MLP, for
  * the whole-model decode loop.  The reference has no kernels of its own
  * here: its decode runs these steps through transformers' Qwen3 modules

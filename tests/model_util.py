@@ -48,6 +48,19 @@ def max_rel(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
 
 
+def assert_confident_argmax(got: torch.Tensor, ref: torch.Tensor, bound: float) -> int:
+    """Every row whose reference top-1 logit beats its top-2 by more than
+    twice the allowed error (bound * max|ref|) must pick the same token;
+    rows with a smaller margin may flip within the tolerance.  Returns how
+    many rows were checked."""
+    got, ref = got.detach().float().cpu(), ref.detach().float().cpu()
+    tol = bound * float(ref.abs().max())
+    top2 = ref.topk(2, dim=-1).values
+    sure = (top2[:, 0] - top2[:, 1]) > 2 * tol
+    assert torch.equal(got.argmax(-1)[sure], ref.argmax(-1)[sure])
+    return int(sure.sum())
+
+
 def teacher_forced_logits(dec, seq: torch.Tensor, plen: int) -> torch.Tensor:
     """Logits the decoder gives at positions plen-1 .. len-2 of `seq` [1, L]
     when fed the tokens of `seq` (prefill of the first plen, then one step

@@ -94,6 +94,13 @@ def test_argument_rejection_before_launch():
     assert L.dip_get_tuning(99) == -6
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
     assert L.dip_ca_assemble(None, p, p, p, p, p, p, 10, 5, None) == -1
+    # prompt GEMM: NULL weights, width not a multiple of 128, no tokens (no
+    # buffers needed), misaligned x
+    assert L.dip_int4_gemm(None, p, p, p, 4, 64, 128, None) == -1
+    assert L.dip_int4_gemm(p, p, p, p, 4, 64, 100, None) == -2
+    assert L.dip_int4_gemm(p, p, None, None, 0, 64, 128, None) == 0
+    assert L.dip_int4_gemm(p, p, None, p, 4, 64, 128, None) == -1
+    assert L.dip_int4_gemm(p, p, p + 2, p, 4, 64, 128, None) == -3
     # decode steps: NULL / size / head_dim / alignment / grouping / workspace
     assert L.dip_add_rmsnorm(None, None, p, p, 128, 1e-6, None) == -1
     assert L.dip_add_rmsnorm(p, None, p, p, 0, 1e-6, None) == -2
