@@ -15,7 +15,9 @@ from gpu_util import (assert_fp32_close, dev, dev_bf16, down_abs_terms, gemv_abs
 pytestmark = pytest.mark.gpu
 
 GEMV_SHAPES = [(4096, 5120), (512, 4096), (300, 2560), (100, 128), (257, 256), (64, 1024),
-               (96, 2048), (128, 512), (40, 8192), (77, 1536), (50, 3072), (33, 6144)]
+               (96, 2048), (128, 512), (40, 8192), (77, 1536), (50, 3072), (33, 6144),
+               # 8192-wide rows (an o projection): 1, 2 and 7 rows per lane group
+               (5120, 8192), (8193, 8192), (25601, 8192)]
 
 
 @pytest.fixture(scope="module")
