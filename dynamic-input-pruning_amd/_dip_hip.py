@@ -70,6 +70,9 @@ _SIGS = {
     "dip_qk_norm_rope_cache": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                 ctypes.c_float, _p], _i32),
     "dip_decode_attention_workspace_size": ([_i64, _i64, _i64], _sz),
+    "dip_decode_attention_fused_max_len": ([], _i64),
+    "dip_decode_attention_fused": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                    ctypes.c_float, ctypes.c_float, _p], _i32),
     "dip_decode_attention": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _sz,
                               _p], _i32),
     "dip_set_tuning": ([_i32, _i32], _i32),
@@ -549,6 +552,40 @@ def decode_attention(q, k_cache, v_cache, pos, out, scale: float, ws=None):
     _check(lib.dip_decode_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out),
                                     nh, nkv, hd, max_len, float(scale), _ptr(ws), ws.numel(),
                                     _stream(dev)), "dip_decode_attention")
+    return out
+
+
+def decode_attention_fused_max_len() -> int:
+    return lib.dip_decode_attention_fused_max_len()
+
+
+def decode_attention_fused(qkv, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, out,
+                           n_heads: int, n_kv_heads: int, eps: float, scale: float):
+    """qk_norm_rope_cache followed by decode_attention in one launch (caches
+    of at most decode_attention_fused_max_len() rows)."""
+    dev = _dev(qkv, k_cache, v_cache, out)
+    hd = q_norm_w.numel()
+    if k_cache.dim() != 3 or k_cache.shape != v_cache.shape or k_cache.shape[0] != n_kv_heads \
+            or k_cache.shape[2] != hd:
+        raise RuntimeError("k_cache / v_cache must be [n_kv_heads, max_len, head_dim]")
+    max_len = k_cache.shape[1]
+    _bf16_vec(qkv, (n_heads + 2 * n_kv_heads) * hd, "qkv")
+    _bf16_vec(q_norm_w, hd, "q_norm_w")
+    _bf16_vec(k_norm_w, hd, "k_norm_w")
+    _bf16_vec(cos, max_len * hd, "cos")
+    _bf16_vec(sin, max_len * hd, "sin")
+    _bf16_vec(out, n_heads * hd, "out")
+    _bf16_vec(k_cache, n_kv_heads * max_len * hd, "k_cache")
+    _bf16_vec(v_cache, n_kv_heads * max_len * hd, "v_cache")
+    for t in (q_norm_w, k_norm_w, cos, sin):
+        if t.device != dev:
+            raise RuntimeError("all tensors must be on one device")
+    _pos_tensor(pos, dev)
+    _check(lib.dip_decode_attention_fused(_ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos),
+                                          _ptr(sin), _ptr(pos), _ptr(k_cache), _ptr(v_cache),
+                                          _ptr(out), n_heads, n_kv_heads, hd, max_len,
+                                          float(eps), float(scale), _stream(dev)),
+           "dip_decode_attention_fused")
     return out
 
 

@@ -283,6 +283,214 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(
   reinterpret_cast<uint32_t*>(out)[(size_t)qh * 64 + l] = o0 | (o1 << 16);
 }
 
+// Norm + rotary + cache write + attention in one launch, for caches of at
+// most kFusedMaxLen rows: workgroup = one kv head and its G query heads.
+//   1. waves take the G q heads and the k and v head of the group: RMSNorm
+//      and rotary exactly as qk_rope_cache_kernel; q into LDS (fp32), this
+//      token's k and v into LDS and into cache row pos;
+//   2. wave w takes the 32-row chunks w, w + 4, ... up to pos (row pos from
+//      LDS, not read back), each as in attn_partial_kernel, merged into a
+//      running (max, sum, value sum) per query head;
+//   3. the 4 waves' partials are merged through LDS in a fixed order.
+constexpr int kFusedMaxLen = 512;
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_fused_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_w,
+    const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_p,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint16_t* __restrict__ out,
+    int nh, int nkv, int max_len, float eps, float scale) {
+  __shared__ __align__(16) float qs[G][kHeadDim];
+  __shared__ __align__(16) uint32_t kv_new[2][64];
+  __shared__ uint32_t heads[G + 2][64];  // this group's raw q | k | v
+  __shared__ uint32_t tabs[4][64];       // q_w, k_w, cos row, sin row
+  __shared__ float ps[4][G][kAttnChunk];
+  __shared__ float wm[4][G], wl[4][G];
+  __shared__ float wacc[4][G][kHeadDim];
+  const int kvh = blockIdx.x, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int64_t pos = *pos_p;
+  const bool pos_ok = pos >= 0 && pos < max_len;
+  const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
+  const int half = l & 1;
+
+  // 0. every load that does not depend on this token's k and v, issued at
+  //    once: the group's heads and tables into LDS, the wave's first cache
+  //    chunk into registers
+  for (int i = threadIdx.x; i < (G + 2) * 64; i += 256) {
+    const int hi = i >> 6;
+    const int head = hi < G ? kvh * G + hi : (hi == G ? nh + kvh : nh + nkv + kvh);
+    heads[hi][i & 63] = reinterpret_cast<const uint32_t*>(qkv)[(size_t)head * 64 + (i & 63)];
+  }
+  {
+    const size_t trow = (size_t)(pos_ok ? pos : 0) * 64 + l;
+    const uint32_t* src = wave == 0 ? reinterpret_cast<const uint32_t*>(q_w) + l
+                        : wave == 1 ? reinterpret_cast<const uint32_t*>(k_w) + l
+                        : wave == 2 ? reinterpret_cast<const uint32_t*>(cos_t) + trow
+                                    : reinterpret_cast<const uint32_t*>(sin_t) + trow;
+    tabs[wave][l] = *src;
+  }
+  int start = wave * kAttnChunk;
+  uint4 kr[8];
+  uint32_t vv[kAttnChunk];
+  auto load_chunk = [&](int st) {
+    const int np = (int)((last - st + 1) < kAttnChunk ? (last - st + 1) : kAttnChunk);
+    if ((l >> 1) < np) {
+      const uint4* src = reinterpret_cast<const uint4*>(
+          k_cache + ((size_t)kvh * max_len + st + (l >> 1)) * kHeadDim + half * (kHeadDim / 2));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kr[i] = src[i];
+    }
+    const uint32_t* vcol =
+        reinterpret_cast<const uint32_t*>(v_cache + ((size_t)kvh * max_len + st) * kHeadDim) + l;
+#pragma unroll
+    for (int j = 0; j < kAttnChunk; ++j) vv[j] = j < np ? vcol[(size_t)j * 64] : 0u;
+  };
+  if ((int64_t)start <= last) load_chunk(start);
+  __syncthreads();
+
+  // 1. RMSNorm + rotary of the q heads and the k head; v and k to the cache
+  for (int hi = wave; hi < G + 2; hi += 4) {
+    const uint32_t pair = heads[hi][l];
+    if (hi == G + 1) {
+      kv_new[1][l] = pair;
+      if (pos_ok)
+        reinterpret_cast<uint32_t*>(v_cache)[((size_t)kvh * max_len + pos) * 64 + l] = pair;
+      continue;
+    }
+    const uint32_t wp = tabs[hi < G ? 0 : 1][l];
+    const float x0 = bf16_to_f32(pair & 0xFFFFu), x1 = bf16_to_f32(pair >> 16);
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float r = rsqrtf(ss * (1.0f / (float)kHeadDim) + eps);
+    const uint32_t y0 = f32_to_bf16(bf16_to_f32(wp & 0xFFFFu) * round_bf16(x0 * r));
+    const uint32_t y1 = f32_to_bf16(bf16_to_f32(wp >> 16) * round_bf16(x1 * r));
+    float r0 = bf16_to_f32(__shfl_xor(y0, 32, 64));
+    float r1 = bf16_to_f32(__shfl_xor(y1, 32, 64));
+    if (l < 32) {
+      r0 = -r0;
+      r1 = -r1;
+    }
+    const uint32_t cs = tabs[2][l], sn = tabs[3][l];
+    const uint32_t o0 = f32_to_bf16(round_bf16(bf16_to_f32(y0) * bf16_to_f32(cs & 0xFFFFu)) +
+                                    round_bf16(r0 * bf16_to_f32(sn & 0xFFFFu)));
+    const uint32_t o1 = f32_to_bf16(round_bf16(bf16_to_f32(y1) * bf16_to_f32(cs >> 16)) +
+                                    round_bf16(r1 * bf16_to_f32(sn >> 16)));
+    if (hi < G) {
+      qs[hi][2 * l] = bf16_to_f32(o0);
+      qs[hi][2 * l + 1] = bf16_to_f32(o1);
+    } else {
+      kv_new[0][l] = o0 | (o1 << 16);
+      if (pos_ok)
+        reinterpret_cast<uint32_t*>(k_cache)[((size_t)kvh * max_len + pos) * 64 + l] =
+            o0 | (o1 << 16);
+    }
+  }
+  __syncthreads();
+
+  // 2. this wave's chunks, merged into running per-head partials; row pos
+  //    comes from kv_new (the preloaded copy of it is the cache's old row)
+  float m[G], lsum[G], a0[G], a1[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    lsum[g] = a0[g] = a1[g] = 0.f;
+  }
+  for (; (int64_t)start <= last; start += 4 * kAttnChunk) {
+    const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
+    const bool live = (l >> 1) < npos;
+    if (live && (int64_t)(start + (l >> 1)) == pos) {
+      const uint4* src = reinterpret_cast<const uint4*>(&kv_new[0][0]) + half * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kr[i] = src[i];
+    }
+    if ((int64_t)start <= pos && pos < (int64_t)start + npos) vv[pos - start] = kv_new[1][l];
+
+    float s[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[g] = 0.f;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float k0 = bf16_to_f32(w4[e] & 0xFFFFu), k1 = bf16_to_f32(w4[e] >> 16);
+          const int d = half * (kHeadDim / 2) + i * 8 + 2 * e;
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            s[g] = fmaf(qs[g][d], k0, s[g]);
+            s[g] = fmaf(qs[g][d + 1], k1, s[g]);
+          }
+        }
+      }
+    }
+    float mc[G], lc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float full = s[g] + dpp_mov<0xB1>(s[g]);
+      const float sc = live ? full * scale : -INFINITY;
+      mc[g] = wave_max(sc);
+      const float e = live ? expf(sc - mc[g]) : 0.f;
+      if (half == 0) ps[wave][g][l >> 1] = e;
+      lc[g] = wave_sum(half == 0 ? e : 0.f);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    float c0[G], c1[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) c0[g] = c1[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kAttnChunk; ++j) {
+      if (j < npos) {
+        const float v0 = bf16_to_f32(vv[j] & 0xFFFFu), v1 = bf16_to_f32(vv[j] >> 16);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          c0[g] = fmaf(ps[wave][g][j], v0, c0[g]);
+          c1[g] = fmaf(ps[wave][g][j], v1, c1[g]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mn = fmaxf(m[g], mc[g]);
+      const float fo = expf(m[g] - mn), fn = expf(mc[g] - mn);
+      lsum[g] = lsum[g] * fo + lc[g] * fn;
+      a0[g] = a0[g] * fo + c0[g] * fn;
+      a1[g] = a1[g] * fo + c1[g] * fn;
+      m[g] = mn;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if ((int64_t)(start + 4 * kAttnChunk) <= last) load_chunk(start + 4 * kAttnChunk);
+  }
+
+  // 3. merge the waves in a fixed order
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (l == 0) {
+      wm[wave][g] = m[g];
+      wl[wave][g] = lsum[g];
+    }
+    wacc[wave][g][2 * l] = a0[g];
+    wacc[wave][g][2 * l + 1] = a1[g];
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += 4) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, wm[w][g]);
+    float den = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = wl[w][g] > 0.f ? expf(wm[w][g] - mx) : 0.f;
+      den = fmaf(f, wl[w][g], den);
+      o0 = fmaf(f, wacc[w][g][2 * l], o0);
+      o1 = fmaf(f, wacc[w][g][2 * l + 1], o1);
+    }
+    reinterpret_cast<uint32_t*>(out)[((size_t)kvh * G + g) * 64 + l] =
+        f32_to_bf16(o0 / den) | (f32_to_bf16(o1 / den) << 16);
+  }
+}
+
 template <int G>
 void launch_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const int64_t* pos,
                       uint16_t* out, int nkv, int max_len, int nchunks, float scale, float* part,
@@ -331,6 +539,44 @@ extern "C" int dip_qk_norm_rope_cache(const uint16_t* qkv, const uint16_t* q_nor
   hipLaunchKernelGGL(qk_rope_cache_kernel, dim3((unsigned)(n_heads + 2 * n_kv_heads)), dim3(64), 0,
                      (hipStream_t)stream, qkv, q_norm_w, k_norm_w, cos_table, sin_table, pos,
                      q_out, k_cache, v_cache, (int)n_heads, (int)n_kv_heads, (int)max_len, eps);
+  return hip_status(hipGetLastError());
+}
+
+extern "C" int64_t dip_decode_attention_fused_max_len(void) { return kFusedMaxLen; }
+
+extern "C" int dip_decode_attention_fused(const uint16_t* qkv, const uint16_t* q_norm_w,
+                                          const uint16_t* k_norm_w, const uint16_t* cos_table,
+                                          const uint16_t* sin_table, const int64_t* pos,
+                                          uint16_t* k_cache, uint16_t* v_cache, uint16_t* out,
+                                          int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                          int64_t max_len, float eps, float scale, void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_table || !sin_table || !pos || !k_cache ||
+      !v_cache || !out)
+    return DIP_ERR_NULL;
+  if (head_dim != kHeadDim) return DIP_ERR_UNSUPPORTED;
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads > 4096 ||
+      max_len <= 0 || max_len > kFusedMaxLen)
+    return DIP_ERR_SHAPE;
+  if (!(eps >= 0.f)) return DIP_ERR_ARG;
+  if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
+      !aligned16(cos_table) || !aligned16(sin_table) || !aligned16(q_norm_w) ||
+      !aligned16(k_norm_w))
+    return DIP_ERR_ALIGN;
+  const int nh = (int)n_heads, nkv = (int)n_kv_heads, ml = (int)max_len;
+  hipStream_t s = (hipStream_t)stream;
+#define DIP_FUSED(GG)                                                                            \
+  hipLaunchKernelGGL(attn_fused_kernel<GG>, dim3(nkv), dim3(256), 0, s, qkv, q_norm_w, k_norm_w, \
+                     cos_table, sin_table, pos, k_cache, v_cache, out, nh, nkv, ml, eps, scale)
+  switch (nh / nkv) {
+    case 1: DIP_FUSED(1); break;
+    case 2: DIP_FUSED(2); break;
+    case 4: DIP_FUSED(4); break;
+    case 5: DIP_FUSED(5); break;
+    case 8: DIP_FUSED(8); break;
+    case 16: DIP_FUSED(16); break;
+    default: return DIP_ERR_UNSUPPORTED;
+  }
+#undef DIP_FUSED
   return hip_status(hipGetLastError());
 }
 

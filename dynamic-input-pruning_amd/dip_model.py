@@ -216,9 +216,10 @@ class DIPDecoder:
                  modules that read nothing back to the host per token; a
                  module says it does with `graph_capturable = False`).
       fused:     run the layer's non-MLP steps with this library's decode
-                 kernels (one fused q|k|v GEMV, q/k norm + rotary + cache
-                 write, split-position attention, residual add fused into
-                 each RMSNorm: 11 launches per layer) instead of the HF
+                 kernels (one fused q|k|v GEMV; q/k norm + rotary + cache
+                 write + attention in one launch for caches of up to 512
+                 rows, else three; residual add fused into each RMSNorm: 9
+                 launches per layer, 11 for long caches) instead of the HF
                  modules' PyTorch ops.  None: whenever the model fits them
                  (GPU, bf16, head_dim 128, int4 attention projections).
     """
@@ -322,6 +323,10 @@ class DIPDecoder:
         self._attn_ws = torch.zeros(K.decode_attention_workspace_bytes(self.nh, self.hd,
                                                                        self.max_len),
                                     dtype=torch.uint8, device=dev)
+        # short caches: norm + rotary + cache write + attention in one launch
+        # (one workgroup per kv head); longer ones split the cache over many
+        # workgroups (three launches)
+        self._attn_one_launch = self.max_len <= K.decode_attention_fused_max_len()
 
     def _body_fused(self) -> torch.Tensor:
         K = self._K
@@ -334,11 +339,18 @@ class DIPDecoder:
             a = L.self_attn
             qw, sc = self._qkv_w[i]
             K.int4_gemv(qw, sc, self._x, out=self._qkv)
-            K.qk_norm_rope_cache(self._qkv, a.q_norm.weight, a.k_norm.weight, self.cos, self.sin,
-                                 self.pos, self._q, self.k_cache[i], self.v_cache[i], self.nh,
-                                 self.nkv, a.q_norm.variance_epsilon)
-            K.decode_attention(self._q, self.k_cache[i], self.v_cache[i], self.pos, self._o,
-                               a.scaling, ws=self._attn_ws)
+            if self._attn_one_launch:
+                K.decode_attention_fused(self._qkv, a.q_norm.weight, a.k_norm.weight, self.cos,
+                                         self.sin, self.pos, self.k_cache[i], self.v_cache[i],
+                                         self._o, self.nh, self.nkv, a.q_norm.variance_epsilon,
+                                         a.scaling)
+            else:
+                K.qk_norm_rope_cache(self._qkv, a.q_norm.weight, a.k_norm.weight, self.cos,
+                                     self.sin, self.pos, self._q, self.k_cache[i],
+                                     self.v_cache[i], self.nh, self.nkv,
+                                     a.q_norm.variance_epsilon)
+                K.decode_attention(self._q, self.k_cache[i], self.v_cache[i], self.pos, self._o,
+                                   a.scaling, ws=self._attn_ws)
             K.int4_gemv(a.o_proj.qweight, a.o_proj.scales, self._o, out=self._a)
             pn = L.post_attention_layernorm
             K.add_rmsnorm(self._h, self._a, pn.weight, self._x, pn.variance_epsilon)

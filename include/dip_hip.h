@@ -345,6 +345,22 @@ int dip_qk_norm_rope_cache(const uint16_t* qkv, const uint16_t* q_norm_w,
  * (else DIP_ERR_UNSUPPORTED).
  */
 size_t dip_decode_attention_workspace_size(int64_t n_heads, int64_t head_dim, int64_t max_len);
+
+/*
+ * dip_decode_attention_fused: dip_qk_norm_rope_cache followed by
+ * dip_decode_attention (q_out not kept) in one launch of one workgroup per
+ * kv head, for caches of at most dip_decode_attention_fused_max_len() rows
+ * (512; else DIP_ERR_SHAPE).  The token's own cache row is taken from the
+ * workgroup's copy, not read back.  Same cache rows bit for bit; the
+ * attention sums the same fp32 terms merged in another order.  No workspace.
+ */
+int64_t dip_decode_attention_fused_max_len(void);
+int dip_decode_attention_fused(const uint16_t* qkv, const uint16_t* q_norm_w,
+                               const uint16_t* k_norm_w, const uint16_t* cos_table,
+                               const uint16_t* sin_table, const int64_t* pos, uint16_t* k_cache,
+                               uint16_t* v_cache, uint16_t* out, int64_t n_heads,
+                               int64_t n_kv_heads, int64_t head_dim, int64_t max_len, float eps,
+                               float scale, void* stream);
 int dip_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                          const int64_t* pos, uint16_t* out, int64_t n_heads, int64_t n_kv_heads,
                          int64_t head_dim, int64_t max_len, float scale, void* workspace,

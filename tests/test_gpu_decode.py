@@ -147,6 +147,43 @@ def test_decode_attention(K, nh, nkv):
         assert not ((ulps > 2) & (err > 1e-5 * float(ref.abs().max()))).any()
 
 
+@pytest.mark.parametrize("nh,nkv", [(4, 4), (4, 2), (32, 8), (40, 8), (64, 8), (64, 4)])
+def test_decode_attention_fused_matches_split(K, nh, nkv):
+    """The one-launch norm + rotary + cache write + attention against the
+    two-step path on the same inputs: the cache rows bit for bit (and no
+    other row touched), the output within the attention bars of the fp64
+    reference taken on the split path's q."""
+    hd, max_len, eps = 128, 300, 1e-6
+    scale = 1 / math.sqrt(hd)
+    g = torch.Generator(device="cuda").manual_seed(7 * nh + nkv)
+    qn = (1 + 0.1 * torch.randn(hd, device="cuda", generator=g)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(hd, device="cuda", generator=g)).to(torch.bfloat16)
+    cos, sin = _tables(max_len)
+    base_k = torch.randn(nkv, max_len, hd, device="cuda", generator=g).to(torch.bfloat16)
+    base_v = torch.randn(nkv, max_len, hd, device="cuda", generator=g).to(torch.bfloat16)
+    for pos in (0, 31, 32, 100, 200, max_len - 1):
+        print(f"decode_attention_fused nh={nh} nkv={nkv} pos={pos}", flush=True)
+        qkv = (torch.randn((nh + 2 * nkv) * hd, device="cuda", generator=g) * 2).to(torch.bfloat16)
+        p = torch.tensor([pos], device="cuda")
+        kc1, vc1 = base_k.clone(), base_v.clone()
+        q = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
+        K.qk_norm_rope_cache(qkv, qn, kn, cos, sin, p, q, kc1, vc1, nh, nkv, eps)
+        split = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
+        K.decode_attention(q, kc1, vc1, p, split, scale)
+        kc2, vc2 = base_k.clone(), base_v.clone()
+        fused = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
+        K.decode_attention_fused(qkv, qn, kn, cos, sin, p, kc2, vc2, fused, nh, nkv, eps, scale)
+        assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+        assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+        ref = _attn_ref(q.view(nh, hd), kc1, vc1, pos, scale)
+        got = fused.view(nh, hd).double().cpu()
+        assert float((got - ref).abs().max() / ref.abs().max()) < 1e-2
+        ulps = ulp_diff(_bits(fused), _bits(ref.float().to(torch.bfloat16))).reshape(nh, hd)
+        err = (got - ref).abs().numpy()
+        assert not ((ulps > 2) & (err > 1e-5 * float(ref.abs().max()))).any()
+        assert ulp_diff(_bits(fused), _bits(split)).max() <= 2
+
+
 def test_decode_attention_rejects_bad_arguments(K):
     q = torch.zeros(3 * 128, dtype=torch.bfloat16, device="cuda")
     kc = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device="cuda")

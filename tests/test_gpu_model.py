@@ -113,6 +113,25 @@ def test_fused_decode_matches_module_path(ckpt, streaming, keep, bound):
     assert_confident_argmax(got, ref, bound)
 
 
+def test_long_cache_decode_matches_short(ckpt, streaming):
+    """A cache longer than the one-launch attention handles (the split path:
+    norm + rotary + cache write, per-chunk partials, merge) against the
+    one-launch path, teacher-forced on the same tokens."""
+    from dip_model import DIPDecoder
+    import _dip_hip as K
+    model, _, prompt = streaming
+    print(f"long vs short cache decode {ckpt[0]}", flush=True)
+    short = DIPDecoder(model, 32)
+    long_ = DIPDecoder(model, K.decode_attention_fused_max_len() + 88)
+    assert short._attn_one_launch and not long_._attn_one_launch
+    seq, got = long_.generate(prompt, NEW, return_logits=True)
+    ref = teacher_forced_logits(short, seq, PLEN)
+    err = max_rel(got, ref)
+    print(f"  max_rel {err:.3e}", flush=True)
+    assert err < 8e-2
+    assert_confident_argmax(got, ref, 8e-2)
+
+
 def test_module_decode_equals_hf_incremental_forward(ckpt, streaming):
     """DIPDecoder's module path (fused=False) is transformers' own
     incremental forward, one token at a time with its DynamicCache, through
