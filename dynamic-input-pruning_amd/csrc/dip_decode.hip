@@ -285,14 +285,25 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(
 
 // Norm + rotary + cache write + attention in one launch, for caches of at
 // most kFusedMaxLen rows: workgroup = one kv head and its G query heads.
-//   1. waves take the G q heads and the k and v head of the group: RMSNorm
-//      and rotary exactly as qk_rope_cache_kernel; q into LDS (fp32), this
+//   0. every load that does not need this token's k and v is issued first:
+//      the group's q | k | v heads, the norm weights and the cos / sin rows
+//      into LDS, each wave's first 32-row chunk of the cache into registers;
+//   1. RMSNorm + rotary as qk_rope_cache_kernel; q into LDS as bf16, this
 //      token's k and v into LDS and into cache row pos;
-//   2. wave w takes the 32-row chunks w, w + 4, ... up to pos (row pos from
-//      LDS, not read back), each as in attn_partial_kernel, merged into a
-//      running (max, sum, value sum) per query head;
+//   2. wave w takes the chunks w, w + 4, ...: the scores on bf16 MFMA
+//      (v_mfma_f32_16x16x32_bf16, A = 16 cache rows, B = the q heads, exact
+//      products, fp32 sums; row pos from LDS, not read back), softmax in
+//      fp32, the value sum in fp32 on the VALU, merged into a running (max,
+//      sum, value sum) per query head;
 //   3. the 4 waves' partials are merged through LDS in a fixed order.
-constexpr int kFusedMaxLen = 512;
+constexpr int kFusedMaxLen = 128;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+DIP_DEV bf16x8_t as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
+}
 
 template <int G>
 __global__ __launch_bounds__(256) void attn_fused_kernel(
@@ -301,27 +312,28 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     const uint16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_p,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint16_t* __restrict__ out,
     int nh, int nkv, int max_len, float eps, float scale) {
-  __shared__ __align__(16) float qs[G][kHeadDim];
+  static_assert(G <= 16, "one MFMA column per query head");
+  __shared__ __align__(16) uint32_t qb[16][64 + 4];   // q as bf16 pairs; heads >= G are 0
   __shared__ __align__(16) uint32_t kv_new[2][64];
   __shared__ uint32_t heads[G + 2][64];  // this group's raw q | k | v
   __shared__ uint32_t tabs[4][64];       // q_w, k_w, cos row, sin row
   __shared__ float ps[4][G][kAttnChunk];
+  __shared__ float cm[4][G], cl[4][G];
   __shared__ float wm[4][G], wl[4][G];
   __shared__ float wacc[4][G][kHeadDim];
   const int kvh = blockIdx.x, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int l16 = l & 15, kb = l >> 4;
   const int64_t pos = *pos_p;
   const bool pos_ok = pos >= 0 && pos < max_len;
   const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
-  const int half = l & 1;
 
-  // 0. every load that does not depend on this token's k and v, issued at
-  //    once: the group's heads and tables into LDS, the wave's first cache
-  //    chunk into registers
+  // 0. loads
   for (int i = threadIdx.x; i < (G + 2) * 64; i += 256) {
     const int hi = i >> 6;
     const int head = hi < G ? kvh * G + hi : (hi == G ? nh + kvh : nh + nkv + kvh);
     heads[hi][i & 63] = reinterpret_cast<const uint32_t*>(qkv)[(size_t)head * 64 + (i & 63)];
   }
+  for (int i = threadIdx.x + G * 64; i < 16 * 64; i += 256) qb[i >> 6][i & 63] = 0u;
   {
     const size_t trow = (size_t)(pos_ok ? pos : 0) * 64 + l;
     const uint32_t* src = wave == 0 ? reinterpret_cast<const uint32_t*>(q_w) + l
@@ -331,16 +343,23 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     tabs[wave][l] = *src;
   }
   int start = wave * kAttnChunk;
-  uint4 kr[8];
-  uint32_t vv[kAttnChunk];
+  uint4 ka[2][4];       // A operand: cache rows start + 16t + l16, dims 32 kb .. 32 kb + 31
+  uint32_t vv[kAttnChunk];  // values: rows start + j, dims 2l, 2l + 1
   auto load_chunk = [&](int st) {
-    const int np = (int)((last - st + 1) < kAttnChunk ? (last - st + 1) : kAttnChunk);
-    if ((l >> 1) < np) {
-      const uint4* src = reinterpret_cast<const uint4*>(
-          k_cache + ((size_t)kvh * max_len + st + (l >> 1)) * kHeadDim + half * (kHeadDim / 2));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kr[i] = src[i];
+    for (int t = 0; t < 2; ++t) {
+      const int row = st + 16 * t + l16;
+      if ((int64_t)row <= last) {
+        const uint4* src = reinterpret_cast<const uint4*>(
+            k_cache + ((size_t)kvh * max_len + row) * kHeadDim + 32 * kb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ka[t][j] = src[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ka[t][j] = make_uint4(0, 0, 0, 0);
+      }
     }
+    const int np = (int)((last - st + 1) < kAttnChunk ? (last - st + 1) : kAttnChunk);
     const uint32_t* vcol =
         reinterpret_cast<const uint32_t*>(v_cache + ((size_t)kvh * max_len + st) * kHeadDim) + l;
 #pragma unroll
@@ -376,8 +395,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     const uint32_t o1 = f32_to_bf16(round_bf16(bf16_to_f32(y1) * bf16_to_f32(cs >> 16)) +
                                     round_bf16(r1 * bf16_to_f32(sn >> 16)));
     if (hi < G) {
-      qs[hi][2 * l] = bf16_to_f32(o0);
-      qs[hi][2 * l + 1] = bf16_to_f32(o1);
+      qb[hi][l] = o0 | (o1 << 16);
     } else {
       kv_new[0][l] = o0 | (o1 << 16);
       if (pos_ok)
@@ -387,8 +405,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   }
   __syncthreads();
 
-  // 2. this wave's chunks, merged into running per-head partials; row pos
-  //    comes from kv_new (the preloaded copy of it is the cache's old row)
+  // 2. B operand (q head l16, dims 32 kb .. 32 kb + 31) once; then the chunks
+  uint4 bq[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const uint4*>(&qb[l16][16 * kb + 4 * j]);
   float m[G], lsum[G], a0[G], a1[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -397,45 +417,55 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   }
   for (; (int64_t)start <= last; start += 4 * kAttnChunk) {
     const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
-    const bool live = (l >> 1) < npos;
-    if (live && (int64_t)(start + (l >> 1)) == pos) {
-      const uint4* src = reinterpret_cast<const uint4*>(&kv_new[0][0]) + half * 8;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kr[i] = src[i];
+    for (int t = 0; t < 2; ++t) {
+      if ((int64_t)(start + 16 * t + l16) == pos) {  // this token's row from LDS
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          ka[t][j] = *reinterpret_cast<const uint4*>(&kv_new[0][16 * kb + 4 * j]);
+      }
     }
     if ((int64_t)start <= pos && pos < (int64_t)start + npos) vv[pos - start] = kv_new[1][l];
 
-    float s[G];
+    // scores: lane (head l16, rows 4 kb + r of tile t)
+    float sc[2][4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) s[g] = 0.f;
-    if (live) {
+    for (int t = 0; t < 2; ++t) {
+      floatx4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+      for (int j = 0; j < 4; ++j)
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][j]), as_bf16x8(bq[j]), d, 0,
+                                                    0, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float k0 = bf16_to_f32(w4[e] & 0xFFFFu), k1 = bf16_to_f32(w4[e] >> 16);
-          const int d = half * (kHeadDim / 2) + i * 8 + 2 * e;
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            s[g] = fmaf(qs[g][d], k0, s[g]);
-            s[g] = fmaf(qs[g][d + 1], k1, s[g]);
-          }
-        }
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = 16 * t + 4 * kb + r < npos;
+        sc[t][r] = ok ? d[r] * scale : -INFINITY;
       }
     }
-    float mc[G], lc[G];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float full = s[g] + dpp_mov<0xB1>(s[g]);
-      const float sc = live ? full * scale : -INFINITY;
-      mc[g] = wave_max(sc);
-      const float e = live ? expf(sc - mc[g]) : 0.f;
-      if (half == 0) ps[wave][g][l >> 1] = e;
-      lc[g] = wave_sum(half == 0 ? e : 0.f);
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[t][r]);
+    mx = row_pair_max32(row_pair_max16(mx));  // over the lanes of head l16
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = sc[t][r] == -INFINITY ? 0.f : expf(sc[t][r] - mx);
+        sum += e;
+        if (l16 < G) ps[wave][l16][16 * t + 4 * kb + r] = e;
+      }
+    sum = row_pair_sum32(row_pair_sum16(sum));
+    if (kb == 0 && l16 < G) {
+      cm[wave][l16] = mx;
+      cl[wave][l16] = sum;
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+
+    // values: lane l takes dimensions 2l, 2l + 1
     float c0[G], c1[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) c0[g] = c1[g] = 0.f;
@@ -452,9 +482,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float mn = fmaxf(m[g], mc[g]);
-      const float fo = expf(m[g] - mn), fn = expf(mc[g] - mn);
-      lsum[g] = lsum[g] * fo + lc[g] * fn;
+      const float mc = cm[wave][g], lc = cl[wave][g];
+      const float mn = fmaxf(m[g], mc);
+      const float fo = expf(m[g] - mn), fn = expf(mc - mn);
+      lsum[g] = lsum[g] * fo + lc * fn;
       a0[g] = a0[g] * fo + c0[g] * fn;
       a1[g] = a1[g] * fo + c1[g] * fn;
       m[g] = mn;

@@ -217,7 +217,7 @@ class DIPDecoder:
                  module says it does with `graph_capturable = False`).
       fused:     run the layer's non-MLP steps with this library's decode
                  kernels (one fused q|k|v GEMV; q/k norm + rotary + cache
-                 write + attention in one launch for caches of up to 512
+                 write + attention in one launch for caches of up to 128
                  rows, else three; residual add fused into each RMSNorm: 9
                  launches per layer, 11 for long caches) instead of the HF
                  modules' PyTorch ops.  None: whenever the model fits them
