@@ -34,6 +34,13 @@ DIP_DEV float wave_max(float v) { return group_max<64>(v); }
 
 DIP_DEV float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+DIP_DEV bf16x8_t as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
+}
+
 // h = bf16(h + add) when add is given; out = RMSNorm(h) * w.  One workgroup;
 // thread t owns the 16-byte vectors t, t + 256, ... (8 values each), all
 // loaded before anything is stored.
@@ -150,11 +157,10 @@ __global__ __launch_bounds__(64) void qk_rope_cache_kernel(
     reinterpret_cast<uint32_t*>(k_cache)[((size_t)(head - nh) * max_len + pos) * 64 + l] = o;
 }
 
-// Attention, pass 1: workgroup (chunk c, kv head) takes cache positions
-// [32c, 32c + 32) up to pos and the G query heads that share the kv head.
-// Scores: lanes 2j and 2j + 1 take position j, each one half of the head
-// dimensions, and add their halves.  Value sum: lane l takes dimensions 2l
-// and 2l + 1 over the chunk's positions, all value loads issued first.
+// Attention, pass 1: workgroup (one wave) = (32-row chunk c, kv head): the
+// scores of the G query heads over the chunk's rows up to pos on bf16 MFMA
+// (A = 16 cache rows, B = the q heads; exact products, fp32 sums), softmax
+// in fp32, the value sum in fp32 on the VALU (lane l: dimensions 2l, 2l + 1).
 // Writes per query head the chunk's max score m, sum of exp(s - m) and the
 // unnormalised value sum.
 template <int G>
@@ -162,71 +168,74 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, const int64_t* __restrict__ pos_p,
     float* __restrict__ part, int max_len, int nchunks, float scale) {
-  __shared__ __align__(16) float qs[G][kHeadDim];
+  static_assert(G <= 16, "one MFMA column per query head");
+  __shared__ __align__(16) uint32_t qb[16][64 + 4];  // q as bf16 pairs; heads >= G are 0
   __shared__ float ps[G][kAttnChunk];
+  __shared__ float cm[G], cl[G];
   const int c = blockIdx.x, kvh = blockIdx.y, l = threadIdx.x;
+  const int l16 = l & 15, kb = l >> 4;
   const int64_t pos = *pos_p;
   const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
   const int start = c * kAttnChunk;
   if ((int64_t)start > last) return;  // no position of this chunk is attended
   const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
 
-  const int half = l & 1;
-  const int p = start + (l >> 1);
-  const bool live = (l >> 1) < npos;
-  uint4 kr[8];
-  if (live) {
-    const uint4* src = reinterpret_cast<const uint4*>(
-        k_cache + ((size_t)kvh * max_len + p) * kHeadDim + half * (kHeadDim / 2));
+  uint4 ka[2][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = src[i];
+  for (int t = 0; t < 2; ++t) {
+    const int row = start + 16 * t + l16;
+    if ((int64_t)row <= last) {
+      const uint4* src = reinterpret_cast<const uint4*>(
+          k_cache + ((size_t)kvh * max_len + row) * kHeadDim + 32 * kb);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ka[t][j] = src[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ka[t][j] = make_uint4(0, 0, 0, 0);
+    }
   }
   const uint32_t* vcol =
       reinterpret_cast<const uint32_t*>(v_cache + ((size_t)kvh * max_len + start) * kHeadDim) + l;
   uint32_t vv[kAttnChunk];
 #pragma unroll
   for (int j = 0; j < kAttnChunk; ++j) vv[j] = j < npos ? vcol[(size_t)j * 64] : 0u;
-  const uint4* qsrc = reinterpret_cast<const uint4*>(q + (size_t)kvh * G * kHeadDim);
-  float* qflat = &qs[0][0];
-  for (int i = l; i < G * kHeadDim / 8; i += 64) {
-    const uint4 v = qsrc[i];
-    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qflat[i * 8 + 2 * e] = bf16_to_f32(w4[e] & 0xFFFFu);
-      qflat[i * 8 + 2 * e + 1] = bf16_to_f32(w4[e] >> 16);
-    }
-  }
+  const uint32_t* qsrc = reinterpret_cast<const uint32_t*>(q + (size_t)kvh * G * kHeadDim);
+  for (int i = l; i < 16 * 64; i += 64) qb[i >> 6][i & 63] = (i >> 6) < G ? qsrc[i] : 0u;
   __syncthreads();
 
-  float s[G];
+  uint4 bq[4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) s[g] = 0.f;
-  if (live) {
+  for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const uint4*>(&qb[l16][16 * kb + 4 * j]);
+  float sc[2][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+  for (int t = 0; t < 2; ++t) {
+    floatx4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float k0 = bf16_to_f32(w4[e] & 0xFFFFu), k1 = bf16_to_f32(w4[e] >> 16);
-        const int d = half * (kHeadDim / 2) + i * 8 + 2 * e;
+    for (int j = 0; j < 4; ++j)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][j]), as_bf16x8(bq[j]), d, 0, 0,
+                                                  0);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          s[g] = fmaf(qs[g][d], k0, s[g]);
-          s[g] = fmaf(qs[g][d + 1], k1, s[g]);
-        }
-      }
-    }
+    for (int r = 0; r < 4; ++r) sc[t][r] = 16 * t + 4 * kb + r < npos ? d[r] * scale : -INFINITY;
   }
-  float m[G], lsum[G];
+  float mx = -INFINITY;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float full = s[g] + dpp_mov<0xB1>(s[g]);  // the other half of the head
-    const float sc = live ? full * scale : -INFINITY;
-    m[g] = wave_max(sc);
-    const float e = live ? expf(sc - m[g]) : 0.f;
-    if (half == 0) ps[g][l >> 1] = e;
-    lsum[g] = wave_sum(half == 0 ? e : 0.f);
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[t][r]);
+  mx = row_pair_max32(row_pair_max16(mx));
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = sc[t][r] == -INFINITY ? 0.f : expf(sc[t][r] - mx);
+      sum += e;
+      if (l16 < G) ps[l16][16 * t + 4 * kb + r] = e;
+    }
+  sum = row_pair_sum32(row_pair_sum16(sum));
+  if (kb == 0 && l16 < G) {
+    cm[l16] = mx;
+    cl[l16] = sum;
   }
   __syncthreads();
 
@@ -249,38 +258,62 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   for (int g = 0; g < G; ++g) {
     float* o = out + g * kPartFloats;
     if (l == 0) {
-      o[0] = m[g];
-      o[1] = lsum[g];
+      o[0] = cm[g];
+      o[1] = cl[g];
     }
     o[2 + 2 * l] = a0[g];
     o[3 + 2 * l] = a1[g];
   }
 }
 
-// Attention, pass 2: one wave per query head merges the chunks 0 .. pos/32
-// (rescaling each by exp(m_c - max m)) and writes bf16(sum / l).
-__global__ __launch_bounds__(64) void attn_combine_kernel(
+// Attention, pass 2: one workgroup per query head merges the chunks
+// 0 .. pos/32: wave w takes chunks w, w + 4, ... with a one-pass running
+// rescale (max, sum, value sum), then the 4 waves merge through LDS in a
+// fixed order and write bf16(sum / l).
+__global__ __launch_bounds__(256) void attn_combine_kernel(
     const float* __restrict__ part, const int64_t* __restrict__ pos_p, uint16_t* __restrict__ out,
     int G, int max_len, int nchunks) {
-  const int qh = blockIdx.x, l = threadIdx.x;
+  __shared__ float wm[4], wl[4];
+  __shared__ float wa[4][kHeadDim];
+  const int qh = blockIdx.x, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int kvh = qh / G, g = qh % G;
   const int64_t pos = *pos_p;
   const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
   const int nc = last < 0 ? 0 : (int)(last / kAttnChunk) + 1;
   const float* base = part + (size_t)kvh * nchunks * G * kPartFloats + (size_t)g * kPartFloats;
   const size_t stride = (size_t)G * kPartFloats;
-  float mx = -INFINITY;
-  for (int c = 0; c < nc; ++c) mx = fmaxf(mx, base[c * stride]);
-  float den = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int c = 0; c < nc; ++c) {
+  float mx = -INFINITY, den = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int c = wave; c < nc; c += 4) {
     const float* pc = base + c * stride;
-    const float f = expf(pc[0] - mx);
-    den = fmaf(f, pc[1], den);
-    a0 = fmaf(f, pc[2 + 2 * l], a0);
-    a1 = fmaf(f, pc[3 + 2 * l], a1);
+    const float mc = pc[0], lc = pc[1], v0 = pc[2 + 2 * l], v1 = pc[3 + 2 * l];
+    const float mn = fmaxf(mx, mc);
+    const float fo = expf(mx - mn), fn = expf(mc - mn);
+    den = den * fo + lc * fn;
+    a0 = a0 * fo + v0 * fn;
+    a1 = a1 * fo + v1 * fn;
+    mx = mn;
   }
-  const uint32_t o0 = f32_to_bf16(a0 / den), o1 = f32_to_bf16(a1 / den);
-  reinterpret_cast<uint32_t*>(out)[(size_t)qh * 64 + l] = o0 | (o1 << 16);
+  if (l == 0) {
+    wm[wave] = mx;
+    wl[wave] = den;
+  }
+  wa[wave][2 * l] = a0;
+  wa[wave][2 * l + 1] = a1;
+  __syncthreads();
+  if (wave != 0) return;
+  float m = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) m = fmaxf(m, wm[w]);
+  float d = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = wl[w] > 0.f ? expf(wm[w] - m) : 0.f;
+    d = fmaf(f, wl[w], d);
+    o0 = fmaf(f, wa[w][2 * l], o0);
+    o1 = fmaf(f, wa[w][2 * l + 1], o1);
+  }
+  reinterpret_cast<uint32_t*>(out)[(size_t)qh * 64 + l] =
+      f32_to_bf16(o0 / d) | (f32_to_bf16(o1 / d) << 16);
 }
 
 // Norm + rotary + cache write + attention in one launch, for caches of at
@@ -297,13 +330,6 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(
 //      sum, value sum) per query head;
 //   3. the 4 waves' partials are merged through LDS in a fixed order.
 constexpr int kFusedMaxLen = 128;
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-DIP_DEV bf16x8_t as_bf16x8(const uint4& v) {
-  return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
-}
 
 template <int G>
 __global__ __launch_bounds__(256) void attn_fused_kernel(
@@ -528,7 +554,7 @@ void launch_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                       hipStream_t stream) {
   hipLaunchKernelGGL((attn_partial_kernel<G>), dim3(nchunks, nkv), dim3(64), 0, stream, q, kc, vc,
                      pos, part, max_len, nchunks, scale);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv * G), dim3(64), 0, stream, part, pos, out, G,
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(nkv * G), dim3(256), 0, stream, part, pos, out, G,
                      max_len, nchunks);
 }
 
