@@ -66,6 +66,8 @@ _SIGS = {
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
     "dip_int4_gemm": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dip_int4_gemv_rmsnorm": ([_p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _i64, _i64, _p],
+                              _i32),
     "dip_add_rmsnorm": ([_p, _p, _p, _p, _i64, ctypes.c_float, _p], _i32),
     "dip_qk_norm_rope_cache": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                 ctypes.c_float, _p], _i32),
@@ -174,6 +176,33 @@ def int4_gemv(qweight, scales, x, act: int = 0, out=None):
                            "values on the weights' device")
     _check(lib.dip_int4_gemv(_ptr(qweight), _ptr(scales), _ptr(x), _ptr(out), rows, cols,
                              int(act), _stream(dev)), "dip_int4_gemv")
+    return out
+
+
+# Input widths the GEMV's RMSNorm prologue is built for (the staged-x widths).
+NORM_GEMV_COLS = frozenset((2560, 4096, 5120))
+
+
+def int4_gemv_rmsnorm(qweight, scales, h, add, norm_w, eps: float, h_out=None, out=None):
+    """out = GEMV of bf16(norm_w * bf16(v * rsqrt(mean(v^2) + eps))) with
+    v = bf16(h + add); v also goes to h_out when given (h_out must be a
+    different buffer from h and add)."""
+    qweight, scales, rows, cols = _weights(qweight, scales, "int4_gemv_rmsnorm")
+    dev = _dev(qweight, scales, h, norm_w)
+    _bf16_vec(h, cols, "h")
+    _bf16_vec(norm_w, cols, "norm_w")
+    for name, t in (("add", add), ("h_out", h_out)):
+        if t is not None:
+            _bf16_vec(t, cols, name)
+            if t.device != dev:
+                raise RuntimeError(f"{name} must be on the weights' device")
+    if out is None:
+        out = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    else:
+        _bf16_vec(out, rows, "out")
+    _check(lib.dip_int4_gemv_rmsnorm(_ptr(qweight), _ptr(scales), _ptr(h), _ptr(add),
+                                     _ptr(norm_w), float(eps), _ptr(h_out), _ptr(out), rows,
+                                     cols, _stream(dev)), "dip_int4_gemv_rmsnorm")
     return out
 
 

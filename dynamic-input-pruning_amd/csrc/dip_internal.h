@@ -42,6 +42,12 @@ struct RowdotArgs {
   int rows_b;  // rows of matrix B (kDual)
   int ngrp;    // row groups (set by the launcher)
   uint32_t* rotate;  // if set: workgroup 0 copies rotate[1] to rotate[0] (speculation state)
+  // RMSNorm prologue (dip_int4_gemv_rmsnorm): x = bf16(w * bf16(v * rsqrt(mean(v^2)
+  // + eps))) with v = bf16(x + norm_add); workgroup 0 writes v to norm_h_out
+  const uint16_t* norm_w;
+  const uint16_t* norm_add;
+  uint16_t* norm_h_out;
+  float norm_eps;
 };
 
 struct DownArgs {
@@ -107,6 +113,9 @@ struct SpecArgs {
 
 // Launchers (return hipSuccess or a DIP_ERR_* code).
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
+// Contiguous rows with the RMSNorm prologue (staged-x widths only).
+bool rowdot_norm_supported(int64_t in_features);
+int launch_rowdot_norm(const RowdotArgs& a, hipStream_t stream);
 int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,

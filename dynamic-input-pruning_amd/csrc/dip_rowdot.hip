@@ -28,8 +28,9 @@ namespace dip {
 
 constexpr int kRowdotMaxThreads = 256;
 
-template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
+template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
 __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a) {
+  static_assert(!NORM || XS, "the RMSNorm prologue needs the staged x");
   constexpr int D = ROWS < 2 ? ROWS : 2;  // rows of loads in flight per group
   static_assert(ROWS <= LPR, "rows per group");
   extern __shared__ __align__(16) uint32_t xlds[];
@@ -45,8 +46,18 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
 
   // 1. x loads first (XS: one chunk per thread, index clamped)
   uint4 xs[XS ? 4 : CH * 4];
+  [[maybe_unused]] uint4 xa[NORM ? 4 : 1], xw[NORM ? 4 : 1];
   if constexpr (XS) {
     load_x_chunk(a.x, nchunks, xs);
+    if constexpr (NORM) {
+      load_x_chunk(a.norm_w, nchunks, xw);
+      if (a.norm_add) {
+        load_x_chunk(a.norm_add, nchunks, xa);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xa[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
   } else {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -71,6 +82,9 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   uint32_t xp[CH][4][4];
   float bias[CH];
   if constexpr (XS) {
+    if constexpr (NORM)
+      norm_x_chunk(xs, xa, xw, nchunks, a.norm_eps, a.norm_h_out,
+                   reinterpret_cast<float*>(xlds + x_pairs_lds_bytes(a.in_features) / 4));
     stage_x_pairs<LPR>(xs, xlds, nchunks);
     x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
   } else {
@@ -143,15 +157,15 @@ RowdotPlan plan_rowdot(int nrows, int lpr, bool balanced) {
   return RowdotPlan{rows, groups, (nrows + rows * groups - 1) / (rows * groups)};
 }
 
-template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS>
+template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
 void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   a.ngrp = p.blocks * p.groups;
-  const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) : 0;
-  hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, ROWS>), dim3(p.blocks),
+  const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) + (NORM ? 16 : 0) : 0;
+  hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, ROWS, NORM>), dim3(p.blocks),
                      dim3(p.groups * LPR), lds, stream, a);
 }
 
-template <int LPR, int CH, int SRC, int EPI>
+template <int LPR, int CH, int SRC, int EPI, bool NORM = false>
 int launch_one(const RowdotArgs& a, hipStream_t stream) {
   // the widths of Qwen3-4B/8B/14B/32B stage x through LDS; every ROWS the
   // plan can pick is instantiated
@@ -160,24 +174,25 @@ int launch_one(const RowdotArgs& a, hipStream_t stream) {
     const RowdotPlan p = plan_rowdot(a.nrows, LPR, SRC == kContig);
     if constexpr (SRC == kContig) {  // balanced plan: any rows per group up to 8
       switch (p.rows) {
-        case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
-        case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
-        case 3: launch_variant<LPR, CH, SRC, EPI, true, 3>(a, p, stream); break;
-        case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
-        case 5: launch_variant<LPR, CH, SRC, EPI, true, 5>(a, p, stream); break;
-        case 6: launch_variant<LPR, CH, SRC, EPI, true, 6>(a, p, stream); break;
-        case 7: launch_variant<LPR, CH, SRC, EPI, true, 7>(a, p, stream); break;
-        default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
+        case 1: launch_variant<LPR, CH, SRC, EPI, true, 1, NORM>(a, p, stream); break;
+        case 2: launch_variant<LPR, CH, SRC, EPI, true, 2, NORM>(a, p, stream); break;
+        case 3: launch_variant<LPR, CH, SRC, EPI, true, 3, NORM>(a, p, stream); break;
+        case 4: launch_variant<LPR, CH, SRC, EPI, true, 4, NORM>(a, p, stream); break;
+        case 5: launch_variant<LPR, CH, SRC, EPI, true, 5, NORM>(a, p, stream); break;
+        case 6: launch_variant<LPR, CH, SRC, EPI, true, 6, NORM>(a, p, stream); break;
+        case 7: launch_variant<LPR, CH, SRC, EPI, true, 7, NORM>(a, p, stream); break;
+        default: launch_variant<LPR, CH, SRC, EPI, true, 8, NORM>(a, p, stream); break;
       }
     } else {  // power-of-two plan: 1, 2, 4 or 8
       switch (p.rows) {
-        case 1: launch_variant<LPR, CH, SRC, EPI, true, 1>(a, p, stream); break;
-        case 2: launch_variant<LPR, CH, SRC, EPI, true, 2>(a, p, stream); break;
-        case 4: launch_variant<LPR, CH, SRC, EPI, true, 4>(a, p, stream); break;
-        default: launch_variant<LPR, CH, SRC, EPI, true, 8>(a, p, stream); break;
+        case 1: launch_variant<LPR, CH, SRC, EPI, true, 1, NORM>(a, p, stream); break;
+        case 2: launch_variant<LPR, CH, SRC, EPI, true, 2, NORM>(a, p, stream); break;
+        case 4: launch_variant<LPR, CH, SRC, EPI, true, 4, NORM>(a, p, stream); break;
+        default: launch_variant<LPR, CH, SRC, EPI, true, 8, NORM>(a, p, stream); break;
       }
     }
   } else {
+    static_assert(!NORM, "the RMSNorm prologue is built for the staged widths only");
     const int rows = LPR >= 4 ? 4 : LPR;
     const int groups = 256 / LPR;
     const RowdotPlan p{rows, groups, (a.nrows + rows * groups - 1) / (rows * groups)};
@@ -208,6 +223,20 @@ int dispatch_layout(const RowdotArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+bool rowdot_norm_supported(int64_t in_features) {
+  const int64_t chunks = in_features / kChunkCols;
+  return in_features % kChunkCols == 0 && (chunks == 160 || chunks == 128 || chunks == 80);
+}
+
+int launch_rowdot_norm(const RowdotArgs& a, hipStream_t stream) {
+  if (a.nrows == 0) return DIP_OK;
+  const int chunks = a.in_features / kChunkCols;
+  if (chunks == 160) return launch_one<32, 5, kContig, kRaw, true>(a, stream);
+  if (chunks == 128) return launch_one<32, 4, kContig, kRaw, true>(a, stream);
+  if (chunks == 80) return launch_one<16, 5, kContig, kRaw, true>(a, stream);
+  return DIP_ERR_UNSUPPORTED;
+}
 
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream) {
   if (a.nrows == 0) return DIP_OK;
@@ -271,6 +300,28 @@ extern "C" int dip_int4_gemv(const int8_t* qweight, const uint16_t* scales, cons
   if (act != DIP_ACT_NONE && act != DIP_ACT_SILU) return DIP_ERR_ARG;
   RowdotArgs a = base_args(qweight, scales, x, out, out_features, in_features);
   return launch_rowdot(kContig, act == DIP_ACT_SILU ? kSilu : kRaw, a, (hipStream_t)stream);
+}
+
+extern "C" int dip_int4_gemv_rmsnorm(const int8_t* qweight, const uint16_t* scales,
+                                     const uint16_t* h, const uint16_t* add,
+                                     const uint16_t* norm_w, float eps, uint16_t* h_out,
+                                     uint16_t* out, int64_t out_features, int64_t in_features,
+                                     void* stream) {
+  int st = check_matrix(qweight, scales, out_features, in_features);
+  if (st) return st;
+  if (!h || !norm_w || !out) return DIP_ERR_NULL;
+  if (!rowdot_norm_supported(in_features)) return DIP_ERR_UNSUPPORTED;
+  if (!(eps >= 0.f)) return DIP_ERR_ARG;
+  if (!aligned16(h) || !aligned16(norm_w) || (add && !aligned16(add)) ||
+      (h_out && !aligned16(h_out)))
+    return DIP_ERR_ALIGN;
+  if (h_out && (h_out == h || h_out == add)) return DIP_ERR_ARG;  // read while written
+  RowdotArgs a = base_args(qweight, scales, h, out, out_features, in_features);
+  a.norm_w = norm_w;
+  a.norm_add = add;
+  a.norm_h_out = h_out;
+  a.norm_eps = eps;
+  return launch_rowdot_norm(a, (hipStream_t)stream);
 }
 
 extern "C" int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc,

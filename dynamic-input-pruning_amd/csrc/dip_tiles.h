@@ -127,6 +127,58 @@ DIP_DEV void stage_x_pairs(const uint4 xs[4], uint32_t* xlds, int nchunks) {
   __syncthreads();
 }
 
+// RMSNorm prologue of the staged x: thread t < nchunks holds chunk t of h
+// (xs), of the residual addend (xa, zeros when there is none) and of the
+// norm weight (xw).  v = bf16(h + add); the block sums v^2 (red: 4 floats of
+// LDS, one block barrier); xs becomes bf16(w * bf16(v * rsqrt(mean + eps))),
+// the rounding of transformers' Qwen3RMSNorm.  Workgroup 0 writes v to
+// h_out (when given).
+DIP_DEV void norm_x_chunk(uint4 xs[4], const uint4 xa[4], const uint4 xw[4], int nchunks,
+                          float eps, uint16_t* h_out, float* red) {
+  const bool mine = (int)threadIdx.x < nchunks;
+  uint32_t vw[16];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t hw[4] = {xs[i].x, xs[i].y, xs[i].z, xs[i].w};
+    const uint32_t aw[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = f32_to_bf16(bf16_to_f32(hw[e] & 0xFFFFu) + bf16_to_f32(aw[e] & 0xFFFFu));
+      const uint32_t hi = f32_to_bf16(bf16_to_f32(hw[e] >> 16) + bf16_to_f32(aw[e] >> 16));
+      vw[4 * i + e] = lo | (hi << 16);
+      const float a = bf16_to_f32(lo), b = bf16_to_f32(hi);
+      ss += a * a + b * b;
+    }
+  }
+  ss = group_sum<64>(mine ? ss : 0.f);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
+  const float r = rsqrtf(tot * (1.0f / (float)(nchunks * kChunkCols)) + eps);
+  if (blockIdx.x == 0 && mine && h_out) {
+    uint4* dst = reinterpret_cast<uint4*>(h_out) + threadIdx.x * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(vw[4 * i], vw[4 * i + 1], vw[4 * i + 2], vw[4 * i + 3]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t ww[4] = {xw[i].x, xw[i].y, xw[i].z, xw[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t v = vw[4 * i + e];
+      const uint32_t lo = f32_to_bf16(bf16_to_f32(ww[e] & 0xFFFFu) *
+                                      bf16_to_f32(f32_to_bf16(bf16_to_f32(v & 0xFFFFu) * r)));
+      const uint32_t hi = f32_to_bf16(bf16_to_f32(ww[e] >> 16) *
+                                      bf16_to_f32(f32_to_bf16(bf16_to_f32(v >> 16) * r)));
+      o[e] = lo | (hi << 16);
+    }
+    xs[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // Lane l's CH chunks of staged pairs and biases, into VGPRs.
 template <int LPR, int CH>
 DIP_DEV void x_pairs_to_regs(const uint32_t* xlds, int nchunks, int l, uint32_t xp[CH][4][4],

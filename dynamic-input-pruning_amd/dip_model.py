@@ -218,9 +218,10 @@ class DIPDecoder:
       fused:     run the layer's non-MLP steps with this library's decode
                  kernels (one fused q|k|v GEMV; q/k norm + rotary + cache
                  write + attention in one launch for caches of up to 128
-                 rows, else three; residual add fused into each RMSNorm: 9
-                 launches per layer, 11 for long caches) instead of the HF
-                 modules' PyTorch ops.  None: whenever the model fits them
+                 rows, else three; residual adds fused into the RMSNorms
+                 and the input RMSNorm into the q|k|v GEMV: 8 launches per
+                 layer, 10 for long caches) instead of the HF modules'
+                 PyTorch ops.  None: whenever the model fits them
                  (GPU, bf16, head_dim 128, int4 attention projections).
     """
 
@@ -314,7 +315,10 @@ class DIPDecoder:
                          if isinstance(L.mlp, StreamingDIPMlp) else
                          (lambda x, m=L.mlp, H=self.hidden: m(x.view(1, 1, H)).reshape(-1))
                          for L in self.layers]
-        self._h = torch.empty(self.hidden, dtype=bf, device=dev)
+        # two residual buffers: the q|k|v GEMV with the input RMSNorm folded in
+        # reads one and writes the updated residual to the other
+        self._hres = [torch.empty(self.hidden, dtype=bf, device=dev) for _ in range(2)]
+        self._norm_gemv = self.hidden in K.NORM_GEMV_COLS
         self._x = torch.empty(self.hidden, dtype=bf, device=dev)
         self._a = torch.empty(self.hidden, dtype=bf, device=dev)
         self._qkv = torch.empty((self.nh + 2 * self.nkv) * self.hd, dtype=bf, device=dev)
@@ -332,13 +336,22 @@ class DIPDecoder:
         K = self._K
         inner = self.model.model
         H = self.hidden
-        torch.index_select(inner.embed_tokens.weight, 0, self.tok, out=self._h.view(1, H))
-        n0 = self.layers[0].input_layernorm
-        K.add_rmsnorm(self._h, None, n0.weight, self._x, n0.variance_epsilon)
+        h, other = self._hres
+        torch.index_select(inner.embed_tokens.weight, 0, self.tok, out=h.view(1, H))
+        y = None
         for i, L in enumerate(self.layers):
             a = L.self_attn
             qw, sc = self._qkv_w[i]
-            K.int4_gemv(qw, sc, self._x, out=self._qkv)
+            n_in = L.input_layernorm
+            if self._norm_gemv:
+                # residual add + input RMSNorm inside the q|k|v GEMV
+                K.int4_gemv_rmsnorm(qw, sc, h, y, n_in.weight, n_in.variance_epsilon,
+                                    h_out=other if y is not None else None, out=self._qkv)
+                if y is not None:
+                    h, other = other, h
+            else:
+                K.add_rmsnorm(h, y, n_in.weight, self._x, n_in.variance_epsilon)
+                K.int4_gemv(qw, sc, self._x, out=self._qkv)
             if self._attn_one_launch:
                 K.decode_attention_fused(self._qkv, a.q_norm.weight, a.k_norm.weight, self.cos,
                                          self.sin, self.pos, self.k_cache[i], self.v_cache[i],
@@ -353,10 +366,9 @@ class DIPDecoder:
                                    a.scaling, ws=self._attn_ws)
             K.int4_gemv(a.o_proj.qweight, a.o_proj.scales, self._o, out=self._a)
             pn = L.post_attention_layernorm
-            K.add_rmsnorm(self._h, self._a, pn.weight, self._x, pn.variance_epsilon)
+            K.add_rmsnorm(h, self._a, pn.weight, self._x, pn.variance_epsilon)
             y = self._mlp_fns[i](self._x)
-            nn_ = self.layers[i + 1].input_layernorm if i + 1 < len(self.layers) else inner.norm
-            K.add_rmsnorm(self._h, y, nn_.weight, self._x, nn_.variance_epsilon)
+        K.add_rmsnorm(h, y, inner.norm.weight, self._x, inner.norm.variance_epsilon)
         return self._x.view(1, 1, H)
 
     # -- one decode step (device-side token and position) ---------------------

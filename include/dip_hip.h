@@ -285,6 +285,21 @@ int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t
                          int64_t row_bytes, int64_t src_rows, int threads);
 
 /*
+ * dip_int4_gemv with the input RMSNorm of a decoder layer folded in:
+ * v = bf16(h + add) (add may be NULL), x = bf16(norm_w * bf16(v * rsqrt(
+ * mean(v^2) + eps))) (transformers' Qwen3RMSNorm, fp32 mean), out = the
+ * GEMV of x; v is also written to h_out when h_out is non-NULL (it must not
+ * be h or add: every workgroup reads them).  Each workgroup normalises x
+ * itself, so the launch replaces an RMSNorm launch before the GEMV.
+ * in_features 5120, 4096 or 2560 (else DIP_ERR_UNSUPPORTED).  No
+ * counterpart kernel in the reference (its decode runs the norm and the
+ * projection as separate PyTorch ops).
+ */
+int dip_int4_gemv_rmsnorm(const int8_t* qweight, const uint16_t* scales, const uint16_t* h,
+                          const uint16_t* add, const uint16_t* norm_w, float eps, uint16_t* h_out,
+                          uint16_t* out, int64_t out_features, int64_t in_features, void* stream);
+
+/*
  * out[m, n] = bf16( sum_c (q*s)[n, c] * x[m, c] ) for m < M tokens: the int4
  * projection of a prompt (more than one token) on bf16 MFMA, weights read
  * once as packed nibbles.  x bf16 [M, in_features] row-major, out bf16

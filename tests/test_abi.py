@@ -94,6 +94,10 @@ def test_argument_rejection_before_launch():
     assert L.dip_get_tuning(99) == -6
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
     assert L.dip_ca_assemble(None, p, p, p, p, p, p, 10, 5, None) == -1
+    # GEMV with the RMSNorm prologue: unsupported width, aliasing, NULL h
+    assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, None, p, 8, 1024, None) == -4
+    assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, p, p, 8, 5120, None) == -6
+    assert L.dip_int4_gemv_rmsnorm(p, p, None, None, p, 1e-6, None, p, 8, 5120, None) == -1
     # prompt GEMM: NULL weights, width not a multiple of 128, no tokens (no
     # buffers needed), misaligned x
     assert L.dip_int4_gemm(None, p, p, p, 4, 64, 128, None) == -1

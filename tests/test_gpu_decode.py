@@ -184,6 +184,38 @@ def test_decode_attention_fused_matches_split(K, nh, nkv):
         assert ulp_diff(_bits(fused), _bits(split)).max() <= 2
 
 
+@pytest.mark.parametrize("rows,cols", [(10240, 5120), (6144, 4096), (5120, 2560), (77, 5120)])
+def test_int4_gemv_rmsnorm(K, rows, cols):
+    """The GEMV with the input RMSNorm folded in: the residual it writes is
+    bf16(h + add) bit for bit; its output is the GEMV of the normalised x,
+    within the GEMV bars of the oracle on the x torch's Qwen3RMSNorm math
+    gives (the sums of squares run in another order, so x may differ by a
+    bf16 ulp in a few places)."""
+    import dip_oracle as O
+    from gpu_util import dev, dev_bf16, gemv_abs_terms, host_bf16, random_int4, rel_err
+    print(f"int4_gemv_rmsnorm rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows + cols)
+    qw, sc = random_int4(rng, rows, cols)
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    h = (torch.randn(cols, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    add = torch.randn(cols, device="cuda", generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(cols, device="cuda", generator=g)).to(torch.bfloat16)
+    h_out = torch.full_like(h, 7.0)
+    out = K.int4_gemv_rmsnorm(dev(qw), dev_bf16(sc), h, add, w, 1e-6, h_out=h_out)
+    assert torch.equal(h_out.view(torch.int16), (h + add).view(torch.int16))
+    x = _bits(_hf_rmsnorm(h + add, w, 1e-6))
+    ref = O.gemv_f64(qw, sc, x)
+    got = host_bf16(out)
+    assert rel_err(got, ref) < 1e-2
+    assert float(np.max(np.abs(O.bf16_to_f32(got) - ref)) / np.max(np.abs(ref))) < 1e-2
+    # no residual addend and no residual written
+    out2 = K.int4_gemv_rmsnorm(dev(qw), dev_bf16(sc), h, None, w, 1e-6)
+    ref2 = O.gemv_f64(qw, sc, _bits(_hf_rmsnorm(h, w, 1e-6)))
+    assert rel_err(host_bf16(out2), ref2) < 1e-2
+    with pytest.raises(RuntimeError):   # the residual written over its own input
+        K.int4_gemv_rmsnorm(dev(qw), dev_bf16(sc), h, add, w, 1e-6, h_out=h)
+
+
 def test_decode_attention_rejects_bad_arguments(K):
     q = torch.zeros(3 * 128, dtype=torch.bfloat16, device="cuda")
     kc = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device="cuda")
