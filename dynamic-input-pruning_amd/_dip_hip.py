@@ -58,6 +58,8 @@ _SIGS = {
     "dip_mlp_decode": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz,
                         _p, _p], _i32),
     "dip_mlp_state_size": ([], _sz),
+    "dip_mlp_decode_rmsnorm": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p,
+                                _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p, _p], _i32),
     "dip_gate_silu_topk_spec": ([_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p,
                                  _p], _i32),
     "dip_int4_gather_down_by_channel": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p],
@@ -616,6 +618,50 @@ def decode_attention_fused(qkv, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_ca
                                           float(eps), float(scale), _stream(dev)),
            "dip_decode_attention_fused")
     return out
+
+
+def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res, add, norm_w,
+                       eps: float, k, *, res_out=None, x_out=None, y=None, g=None, idx=None,
+                       h=None, ws=None, state=None):
+    """mlp_decode on x = RMSNorm(res + add) * norm_w, the norm folded into the
+    gate launch; the updated residual goes to res_out (if given) and x to
+    x_out.  Returns (y, g, idx, h, x_out)."""
+    gate_qw, gate_sc, inter, hidden = _weights(gate_qw, gate_sc, "gate")
+    dev = _dev(gate_qw, res, norm_w)
+    _bf16_vec(res, hidden, "res")
+    _bf16_vec(norm_w, hidden, "norm_w")
+    for name, t in (("add", add), ("res_out", res_out), ("x_out", x_out)):
+        if t is not None:
+            _bf16_vec(t, hidden, name)
+            if t.device != dev:
+                raise RuntimeError(f"{name} must be on the weights' device")
+    k = int(k)
+    if not 0 <= k <= inter:
+        raise RuntimeError(f"k={k} outside [0, {inter}]")
+    if x_out is None:
+        x_out = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
+    if y is None:
+        y = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
+    if g is None:
+        g = torch.empty(inter, dtype=torch.bfloat16, device=dev)
+    if idx is None:
+        idx = torch.empty(k, dtype=torch.int32, device=dev)
+    if h is None:
+        h = torch.empty(k, dtype=torch.bfloat16, device=dev)
+    nbytes = lib.dip_mlp_workspace_size(hidden, inter, k)
+    if ws is None:
+        ws = workspace(dev, nbytes, "mlp")
+    elif ws.numel() < nbytes:
+        raise RuntimeError("workspace too small")
+    if state is not None and (state.device != dev or state.dtype != torch.int32
+                              or state.numel() * 4 < lib.dip_mlp_state_size()):
+        raise RuntimeError("state must be this device's mlp_state() tensor")
+    _check(lib.dip_mlp_decode_rmsnorm(
+        _ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc), _ptr(down_t_qw), _ptr(down_t_sc),
+        _ptr(res), _ptr(add), _ptr(norm_w), float(eps), _ptr(res_out), _ptr(x_out), _ptr(y),
+        _ptr(g), _ptr(idx), _ptr(h), hidden, inter, k, _ptr(ws), ws.numel(),
+        None if state is None else _ptr(state), _stream(dev)), "dip_mlp_decode_rmsnorm")
+    return y, g, idx, h, x_out
 
 
 TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "gate_mfma": 3}

@@ -47,6 +47,7 @@ struct RowdotArgs {
   const uint16_t* norm_w;
   const uint16_t* norm_add;
   uint16_t* norm_h_out;
+  uint16_t* norm_x_out;  // workgroup 0 also writes the normalised x here (if set)
   float norm_eps;
 };
 
@@ -115,7 +116,13 @@ struct SpecArgs {
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
 // Contiguous rows with the RMSNorm prologue (staged-x widths only).
 bool rowdot_norm_supported(int64_t in_features);
-int launch_rowdot_norm(const RowdotArgs& a, hipStream_t stream);
+int launch_rowdot_norm(int epi, const RowdotArgs& a, hipStream_t stream);
+// The top-k + speculative up launch that follows the gate in a decode step
+// (dip_gate_silu_topk_spec without its gate launch).
+int launch_spec_after_gate(const uint16_t* g, int64_t inter, int64_t hidden, int64_t k,
+                           int32_t* idx, uint16_t* h_full, const int8_t* up_qw,
+                           const uint16_t* up_sc, const uint16_t* x, void* workspace,
+                           void* state, hipStream_t stream);
 int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,

@@ -266,6 +266,76 @@ extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t 
   return kMlpTopkBytes + hfull + align256(down_workspace_bytes(k, hidden));
 }
 
+extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gate_sc,
+                                      const int8_t* up_qw, const uint16_t* up_sc,
+                                      const int8_t* down_t_qw, const uint16_t* down_t_sc,
+                                      const uint16_t* h, const uint16_t* add,
+                                      const uint16_t* norm_w, float eps, uint16_t* h_res_out,
+                                      uint16_t* x_out, uint16_t* y, uint16_t* g_out,
+                                      int32_t* idx_out, uint16_t* h_out, int64_t hidden,
+                                      int64_t inter, int64_t k, void* workspace, size_t ws_bytes,
+                                      void* layer_state, void* stream) {
+  if (!gate_qw || !gate_sc || !up_qw || !up_sc || !h || !norm_w || !x_out || !g_out || !y)
+    return DIP_ERR_NULL;
+  if (k < 0 || k > inter || inter <= 0 || inter > INT32_MAX) return DIP_ERR_SHAPE;
+  if (k > 0 && (!idx_out || !h_out)) return DIP_ERR_NULL;
+  if (!rowdot_norm_supported(hidden)) return DIP_ERR_UNSUPPORTED;
+  if (!(eps >= 0.f)) return DIP_ERR_ARG;
+  if (!aligned16(gate_qw) || !aligned16(up_qw) || !aligned16(h) || !aligned16(norm_w) ||
+      !aligned16(x_out) || !aligned16(g_out) || (add && !aligned16(add)) ||
+      (h_res_out && !aligned16(h_res_out)))
+    return DIP_ERR_ALIGN;
+  // every workgroup of the gate reads h and add while workgroup 0 writes
+  // the residual and x
+  if (x_out == h || x_out == add || (h_res_out && (h_res_out == h || h_res_out == add)))
+    return DIP_ERR_ARG;
+  if (!workspace || ws_bytes < dip_mlp_workspace_size(hidden, inter, k)) return DIP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return DIP_ERR_ALIGN;
+  char* ws = static_cast<char*>(workspace);
+  const size_t hfull_bytes = align256((size_t)inter * sizeof(uint16_t));
+  char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
+  const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
+  hipStream_t s = (hipStream_t)stream;
+  RowdotArgs a{};
+  a.qw_a = gate_qw;
+  a.sc_a = gate_sc;
+  a.qw_safe = gate_qw;
+  a.sc_safe = gate_sc;
+  a.x = h;
+  a.out = g_out;
+  a.nrows = (int)inter;
+  a.in_features = (int)hidden;
+  a.rows_a = (int)inter;
+  a.norm_w = norm_w;
+  a.norm_add = add;
+  a.norm_h_out = h_res_out;
+  a.norm_x_out = x_out;
+  a.norm_eps = eps;
+  const bool spec = layer_state && k > 0 && topk_spec_supported(hidden) && inter <= kTopkMaxN;
+  if (spec) {
+    if (reinterpret_cast<uintptr_t>(layer_state) & 3u) return DIP_ERR_ALIGN;
+    a.rotate = static_cast<uint32_t*>(layer_state);
+    int st = launch_rowdot_norm(kSilu, a, s);
+    if (st) return st;
+    uint16_t* h_full = reinterpret_cast<uint16_t*>(ws + kMlpTopkBytes);
+    st = launch_spec_after_gate(g_out, inter, hidden, k, idx_out, h_full, up_qw, up_sc, x_out, ws,
+                                layer_state, s);
+    if (st) return st;
+    return dip_int4_gather_down_by_channel(down_t_qw, down_t_sc, h_full, idx_out, y, h_out,
+                                           inter, hidden, k, down_ws, down_bytes, stream);
+  }
+  int st = launch_rowdot_norm(kSilu, a, s);
+  if (st) return st;
+  st = dip_topk_select(g_out, idx_out, inter, k, ws, kMlpTopkBytes, stream);
+  if (st) return st;
+  if (k > 0) {
+    st = dip_up_gather_h(up_qw, up_sc, x_out, idx_out, g_out, h_out, inter, hidden, k, stream);
+    if (st) return st;
+  }
+  return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k,
+                              down_ws, down_bytes, stream);
+}
+
 extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
                               const int8_t* up_qw, const uint16_t* up_sc,
                               const int8_t* down_t_qw, const uint16_t* down_t_sc,

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   float bias[CH];
   if constexpr (XS) {
     if constexpr (NORM)
-      norm_x_chunk(xs, xa, xw, nchunks, a.norm_eps, a.norm_h_out,
+      norm_x_chunk(xs, xa, xw, nchunks, a.norm_eps, a.norm_h_out, a.norm_x_out,
                    reinterpret_cast<float*>(xlds + x_pairs_lds_bytes(a.in_features) / 4));
     stage_x_pairs<LPR>(xs, xlds, nchunks);
     x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
@@ -229,13 +229,34 @@ bool rowdot_norm_supported(int64_t in_features) {
   return in_features % kChunkCols == 0 && (chunks == 160 || chunks == 128 || chunks == 80);
 }
 
-int launch_rowdot_norm(const RowdotArgs& a, hipStream_t stream) {
-  if (a.nrows == 0) return DIP_OK;
+template <int EPI>
+int launch_norm_epi(const RowdotArgs& a, hipStream_t stream) {
   const int chunks = a.in_features / kChunkCols;
-  if (chunks == 160) return launch_one<32, 5, kContig, kRaw, true>(a, stream);
-  if (chunks == 128) return launch_one<32, 4, kContig, kRaw, true>(a, stream);
-  if (chunks == 80) return launch_one<16, 5, kContig, kRaw, true>(a, stream);
+  if (chunks == 160) return launch_one<32, 5, kContig, EPI, true>(a, stream);
+  if (chunks == 128) return launch_one<32, 4, kContig, EPI, true>(a, stream);
+  if (chunks == 80) return launch_one<16, 5, kContig, EPI, true>(a, stream);
   return DIP_ERR_UNSUPPORTED;
+}
+
+int launch_rowdot_norm(int epi, const RowdotArgs& a, hipStream_t stream) {
+  if (a.nrows == 0) return DIP_OK;
+  if (epi == kRaw) return launch_norm_epi<kRaw>(a, stream);
+  if (epi == kSilu) return launch_norm_epi<kSilu>(a, stream);
+  return DIP_ERR_ARG;
+}
+
+int launch_spec_after_gate(const uint16_t* g, int64_t inter, int64_t hidden, int64_t k,
+                           int32_t* idx, uint16_t* h_full, const int8_t* up_qw,
+                           const uint16_t* up_sc, const uint16_t* x, void* workspace,
+                           void* state, hipStream_t stream) {
+  SpecArgs sp{};
+  sp.up_qw = up_qw;
+  sp.up_sc = up_sc;
+  sp.x = x;
+  sp.h_full = h_full;
+  sp.state = static_cast<uint32_t*>(state);
+  sp.hidden = (int)hidden;
+  return launch_topk_spec(g, inter, k, idx, workspace, sp, stream);
 }
 
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream) {
@@ -321,7 +342,7 @@ extern "C" int dip_int4_gemv_rmsnorm(const int8_t* qweight, const uint16_t* scal
   a.norm_add = add;
   a.norm_h_out = h_out;
   a.norm_eps = eps;
-  return launch_rowdot_norm(a, (hipStream_t)stream);
+  return launch_rowdot_norm(kRaw, a, (hipStream_t)stream);
 }
 
 extern "C" int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc,
@@ -365,14 +386,8 @@ extern "C" int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* ga
   a.rotate = static_cast<uint32_t*>(state);
   st = launch_rowdot(kContig, kSilu, a, (hipStream_t)stream);
   if (st) return st;
-  SpecArgs sp{};
-  sp.up_qw = up_qw;
-  sp.up_sc = up_sc;
-  sp.x = x;
-  sp.h_full = h_full;
-  sp.state = static_cast<uint32_t*>(state);
-  sp.hidden = (int)hidden;
-  return launch_topk_spec(g, inter, k, idx, workspace, sp, (hipStream_t)stream);
+  return launch_spec_after_gate(g, inter, hidden, k, idx, h_full, up_qw, up_sc, x, workspace,
+                                state, (hipStream_t)stream);
 }
 
 extern "C" int dip_int4_gather_gemv(const int8_t* qweight, const uint16_t* scales,

@@ -132,9 +132,9 @@ DIP_DEV void stage_x_pairs(const uint4 xs[4], uint32_t* xlds, int nchunks) {
 // norm weight (xw).  v = bf16(h + add); the block sums v^2 (red: 4 floats of
 // LDS, one block barrier); xs becomes bf16(w * bf16(v * rsqrt(mean + eps))),
 // the rounding of transformers' Qwen3RMSNorm.  Workgroup 0 writes v to
-// h_out (when given).
+// h_out and the normalised x to x_out (when given).
 DIP_DEV void norm_x_chunk(uint4 xs[4], const uint4 xa[4], const uint4 xw[4], int nchunks,
-                          float eps, uint16_t* h_out, float* red) {
+                          float eps, uint16_t* h_out, uint16_t* x_out, float* red) {
   const bool mine = (int)threadIdx.x < nchunks;
   uint32_t vw[16];
   float ss = 0.f;
@@ -176,6 +176,11 @@ DIP_DEV void norm_x_chunk(uint4 xs[4], const uint4 xa[4], const uint4 xw[4], int
       o[e] = lo | (hi << 16);
     }
     xs[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (blockIdx.x == 0 && mine && x_out) {
+    uint4* dst = reinterpret_cast<uint4*>(x_out) + threadIdx.x * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = xs[i];
   }
 }
 

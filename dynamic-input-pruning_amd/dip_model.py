@@ -219,8 +219,9 @@ class DIPDecoder:
                  kernels (one fused q|k|v GEMV; q/k norm + rotary + cache
                  write + attention in one launch for caches of up to 128
                  rows, else three; residual adds fused into the RMSNorms
-                 and the input RMSNorm into the q|k|v GEMV: 8 launches per
-                 layer, 10 for long caches) instead of the HF modules'
+                 the input RMSNorm into the q|k|v GEMV and the
+                 post-attention one into the DIP MLP's gate: 7 launches per
+                 layer, 9 for long caches) instead of the HF modules'
                  PyTorch ops.  None: whenever the model fits them
                  (GPU, bf16, head_dim 128, int4 attention projections).
     """
@@ -319,6 +320,8 @@ class DIPDecoder:
         # reads one and writes the updated residual to the other
         self._hres = [torch.empty(self.hidden, dtype=bf, device=dev) for _ in range(2)]
         self._norm_gemv = self.hidden in K.NORM_GEMV_COLS
+        self._mlp_norm = [self._norm_gemv and isinstance(L.mlp, StreamingDIPMlp)
+                          for L in self.layers]
         self._x = torch.empty(self.hidden, dtype=bf, device=dev)
         self._a = torch.empty(self.hidden, dtype=bf, device=dev)
         self._qkv = torch.empty((self.nh + 2 * self.nkv) * self.hd, dtype=bf, device=dev)
@@ -366,8 +369,14 @@ class DIPDecoder:
                                    a.scaling, ws=self._attn_ws)
             K.int4_gemv(a.o_proj.qweight, a.o_proj.scales, self._o, out=self._a)
             pn = L.post_attention_layernorm
-            K.add_rmsnorm(h, self._a, pn.weight, self._x, pn.variance_epsilon)
-            y = self._mlp_fns[i](self._x)
+            if self._mlp_norm[i]:
+                # residual add + post-attention RMSNorm inside the MLP's gate
+                y = L.mlp.decode_rmsnorm(h, self._a, pn.weight, pn.variance_epsilon, other,
+                                         self._x)
+                h, other = other, h
+            else:
+                K.add_rmsnorm(h, self._a, pn.weight, self._x, pn.variance_epsilon)
+                y = self._mlp_fns[i](self._x)
         K.add_rmsnorm(h, y, inner.norm.weight, self._x, inner.norm.variance_epsilon)
         return self._x.view(1, 1, H)
 

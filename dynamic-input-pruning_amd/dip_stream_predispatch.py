@@ -168,6 +168,23 @@ class StreamingDIPMlp(nn.Module):
                                   state=self._spec_state)
         return y
 
+    def decode_rmsnorm(self, res, add, norm_w, eps, res_out, x_out):
+        """One decode token with the preceding RMSNorm folded in (the whole-
+        model decode loop): x_out = RMSNorm(res + add) * norm_w, res_out =
+        res + add, returns this module's y for x_out (the same values as
+        forward on x_out)."""
+        b = self.buf
+        if self.keep_ratio >= 0.999 or self.out_features not in K.NORM_GEMV_COLS:
+            res_out.copy_(res)
+            K.add_rmsnorm(res_out, add, norm_w, x_out, eps)
+            return self._decode_one(x_out)
+        ws = b.workspace(self.out_features, self.inter, self.k)
+        y, _, _, _, _ = K.mlp_decode_rmsnorm(
+            self.gate_qw, self.gate_sc, self.up_qw, self.up_sc, self.down_t_qw, self.down_t_sc,
+            res, add, norm_w, eps, self.k, res_out=res_out, x_out=x_out, g=b.g(self.inter),
+            idx=b.idx, h=b.h, ws=ws, state=self._spec_state)
+        return y
+
     def forward(self, x):
         if x.dim() != 3 or x.shape[1] != 1:
             return self._dense(x)

@@ -276,6 +276,25 @@ int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t*
                    void* workspace, size_t ws_bytes, void* layer_state, void* stream);
 
 /*
+ * dip_mlp_decode with the post-attention RMSNorm of a decoder layer folded
+ * into its gate launch: v = bf16(h + add) (add may be NULL), x = bf16(norm_w
+ * * bf16(v * rsqrt(mean(v^2) + eps))); the gate's workgroup 0 writes v to
+ * h_res_out (if non-NULL) and x to x_out, which the up rows then read.
+ * y, g_out, idx_out and h_out are dip_mlp_decode's on that x, bit for bit.
+ * x_out and h_res_out must differ from h and add.  hidden 5120, 4096 or
+ * 2560 (else DIP_ERR_UNSUPPORTED).  No counterpart kernel in the reference
+ * (its decode runs the norm as separate PyTorch ops before
+ * StreamingDIPMlp.forward).
+ */
+int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
+                           const uint16_t* up_sc, const int8_t* down_t_qw,
+                           const uint16_t* down_t_sc, const uint16_t* h, const uint16_t* add,
+                           const uint16_t* norm_w, float eps, uint16_t* h_res_out,
+                           uint16_t* x_out, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
+                           uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
+                           void* workspace, size_t ws_bytes, void* layer_state, void* stream);
+
+/*
  * Host-side row gather for the cache-aware miss path: copies rows
  * src + ids[i] * row_bytes -> dst + i * row_bytes for i < n using up to
  * `threads` host threads (the pinned index_select of dip_ca.py:148-153).

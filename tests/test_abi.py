@@ -94,6 +94,11 @@ def test_argument_rejection_before_launch():
     assert L.dip_get_tuning(99) == -6
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
     assert L.dip_ca_assemble(None, p, p, p, p, p, p, 10, 5, None) == -1
+    # MLP step with the RMSNorm in its gate: unsupported width, aliasing
+    assert L.dip_mlp_decode_rmsnorm(p, p, p, p, p, p, p, None, p, 1e-6, None, p, p, p, p, p,
+                                    1024, 3072, 100, p, 1 << 20, None, None) == -4
+    assert L.dip_mlp_decode_rmsnorm(p, p, p, p, p, p, p, None, p, 1e-6, None, p, p, p, p, p,
+                                    5120, 3072, 100, p, 1 << 20, None, None) == -6
     # GEMV with the RMSNorm prologue: unsupported width, aliasing, NULL h
     assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, None, p, 8, 1024, None) == -4
     assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, p, p, 8, 5120, None) == -6

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import dip_oracle as O
-from gpu_util import host_bf16
+from gpu_util import host_bf16, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -173,3 +173,41 @@ def test_spec_stack_graph_replays(K):
         torch.cuda.synchronize()
         for a, b in zip(spec.y, plain.y):
             assert torch.equal(_bits(a), _bits(b)), rep
+
+
+def test_mlp_decode_rmsnorm_equals_mlp_decode_on_its_x(K):
+    """The decode step with the post-attention RMSNorm folded into the gate:
+    the residual it writes is bf16(res + add), its x is within one bf16 ulp
+    of the separate RMSNorm kernel's, and y, g, idx and h equal
+    mlp_decode's on that x, bit for bit, over several tokens (speculative
+    and stage-by-stage)."""
+    from quantize import quantize_tensor_int4_groupwise
+    for H, I in [(5120, 25600), (2560, 9728)]:
+        print(f"mlp_decode_rmsnorm H={H} I={I}", flush=True)
+        gen = torch.Generator(device="cuda").manual_seed(H)
+        W = []
+        for _ in range(3):
+            W += list(quantize_tensor_int4_groupwise(
+                torch.randn(I, H, device="cuda", generator=gen) * 0.02))
+        k = O.keep_count(I, 0.6)
+        w = (1 + 0.1 * torch.randn(H, device="cuda", generator=gen)).to(torch.bfloat16)
+        for state in (K.mlp_state("cuda"), None):
+            for t in range(3):
+                res = (torch.randn(H, device="cuda", generator=gen) * 3).to(torch.bfloat16)
+                add = torch.randn(H, device="cuda", generator=gen).to(torch.bfloat16)
+                res_out = torch.empty_like(res)
+                x_out = torch.empty_like(res)
+                a = [v.clone() for v in K.mlp_decode_rmsnorm(*W, res, add, w, 1e-6, k,
+                                                             res_out=res_out, x_out=x_out,
+                                                             state=state)]
+                assert torch.equal(res_out.view(torch.int16), (res + add).view(torch.int16))
+                x_sep = torch.empty_like(res)
+                K.add_rmsnorm((res + add).clone(), None, w, x_sep, 1e-6)
+                d = ulp_diff(x_out.view(torch.int16).cpu().numpy().view(np.uint16),
+                             x_sep.view(torch.int16).cpu().numpy().view(np.uint16))
+                assert d.max() <= 1
+                b = [v.clone() for v in K.mlp_decode(*W, x_out, k)]
+                for u, v in zip(a[:4], b):
+                    uu = u.view(torch.int16) if u.dtype == torch.bfloat16 else u
+                    vv = v.view(torch.int16) if v.dtype == torch.bfloat16 else v
+                    assert torch.equal(uu, vv), (H, t, state is None)
