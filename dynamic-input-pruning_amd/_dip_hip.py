@@ -68,6 +68,8 @@ _SIGS = {
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
     "dip_int4_gemm": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
+    "dip_int4_gemm_t_workspace_size": ([_i64, _i64, _i64], _sz),
+    "dip_int4_gemm_t": ([_p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p], _i32),
     "dip_int4_gemv_rmsnorm": ([_p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _i64, _i64, _p],
                               _i32),
     "dip_add_rmsnorm": ([_p, _p, _p, _p, _i64, ctypes.c_float, _p], _i32),
@@ -226,6 +228,30 @@ def int4_gemm(qweight, scales, x, out=None):
     _check(lib.dip_int4_gemm(_ptr(qweight), _ptr(scales), _ptr(x2), _ptr(out), m, rows, cols,
                              _stream(dev)), "dip_int4_gemm")
     return out.view(*x.shape[:-1], rows)
+
+
+def int4_gemm_t(qweight_t, scales_t, x, out=None):
+    """out [M, N] = bf16(x [M, K] @ bf16(q*s)) for W stored as K rows of N
+    (the transposed down matrix), on bf16 MFMA."""
+    qweight_t, scales_t, k_rows, n = _weights(qweight_t, scales_t, "int4_gemm_t")
+    dev = _dev(qweight_t, scales_t, x)
+    if x.dtype != torch.bfloat16 or x.shape[-1] != k_rows:
+        raise RuntimeError(f"x must be bf16 [..., {k_rows}]")
+    x2 = x.reshape(-1, k_rows)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous().clone() if x2.data_ptr() % 16 else x2.contiguous()
+    m = x2.shape[0]
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    elif (out.dtype != torch.bfloat16 or out.numel() != m * n or not out.is_contiguous()
+          or out.device != dev):
+        raise RuntimeError(f"out must be a contiguous bf16 tensor of {m} x {n} values")
+    nbytes = lib.dip_int4_gemm_t_workspace_size(m, n, k_rows)
+    ws = workspace(dev, nbytes, "gemm_t") if nbytes else None
+    _check(lib.dip_int4_gemm_t(_ptr(qweight_t), _ptr(scales_t), _ptr(x2), _ptr(out), m, n, k_rows,
+                               _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
+           "dip_int4_gemm_t")
+    return out.view(*x.shape[:-1], n)
 
 
 def topk_select(s: torch.Tensor, k: int, out=None):

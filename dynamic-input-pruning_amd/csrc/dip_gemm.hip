@@ -25,6 +25,8 @@
 // columns 32 kb .. 32 kb + 31 and slice j uses its 8 columns 8j .. 8j + 7),
 // so a lane's nibbles are one contiguous 16-byte load.  The offset term
 // 136 * sum(x) comes from the same MFMA with a constant operand.
+#include <algorithm>
+
 #include "dip_common.h"
 #include "dip_internal.h"
 
@@ -198,6 +200,179 @@ void launch_gemm(const int8_t* qw, const uint16_t* sc, const uint16_t* x, uint16
                        0, s, qw, sc, x, out, M, N, K);
 }
 
+// ---------------------------------------------------------------------------
+// Transposed layout: out[M, N] = bf16( x[M, K] . W[K, N] ) with W stored as
+// rows of K (qweight int8 [K, N/2], scales bf16 [K, N/128]): the transposed
+// down matrix down_t of the dense route's h @ down_t
+// (dip_stream_predispatch.py:213-215).  The scale varies along k here, so
+// each weight becomes the reference's bf16(q * s) (qlinear.dequantize's
+// rounding, exact to it) on its way into LDS:
+//   * a workgroup owns 64 output columns x 16 * TM tokens and a K range
+//     (the K ranges of a split are added by int4_gemm_t_reduce_kernel, in
+//     a fixed order);
+//   * per 128-row step the 256 threads read 128 rows x 32 bytes of nibbles
+//     (thread t: row t / 2, 32 columns) and their scales, and write the
+//     dequantised values transposed into LDS [column][k] (double-buffered,
+//     one barrier per step); nibbles and scales run kGemmTPrefetch steps
+//     ahead in registers;
+//   * wave w reads A = 16 columns x 8 consecutive k (one 16-byte LDS read
+//     per slice) and B = x[token][k .. k + 7] straight from L2, and
+//     accumulates on v_mfma_f32_16x16x32_bf16.
+constexpr int kGemmTStep = 128;     // K rows per step
+constexpr int kGemmTStride = 128 + 8;  // LDS row of one column: 128 k + 16 B of padding
+constexpr int kGemmTPrefetch = 4;
+
+template <int TM>
+__global__ __launch_bounds__(kGemmThreads) void int4_gemm_t_kernel(
+    const int8_t* __restrict__ qw, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ out, float* __restrict__ part, int M, int N, int K, int kchunk) {
+  __shared__ __align__(16) uint16_t wt[2][64][kGemmTStride];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kb = lane >> 4, l16 = lane & 15;
+  const int n0 = blockIdx.x * 64;
+  const int tok0 = blockIdx.y * TM * 16;
+  const int k0 = blockIdx.z * kchunk;
+  const int k1 = min(K, k0 + kchunk);
+  const int nsteps = (k1 - k0 + kGemmTStep - 1) / kGemmTStep;
+  const int ngroups_n = N >> 7;
+
+  // staging role: row r of the step, columns n0 + 32 c .. + 31
+  const int sr = threadIdx.x >> 1, scol = 32 * (threadIdx.x & 1);
+  const bool col_ok = n0 + scol < N;
+  auto load_w = [&](int step, uint4& wv, uint32_t& s) {
+    const int row = k0 + step * kGemmTStep + sr;
+    if (row < k1 && col_ok) {
+      wv = *reinterpret_cast<const uint4*>(qw + (size_t)row * (N >> 1) + ((n0 + scol) >> 1));
+      s = sc[(size_t)row * ngroups_n + ((n0 + scol) >> 7)];
+    } else {
+      wv = make_uint4(0, 0, 0, 0);
+      s = 0u;
+    }
+  };
+  auto stage = [&](int buf, const uint4& wv, uint32_t s) {
+    const float sf = bf16_to_f32(s);
+    const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int q = (int)((w4[i] >> (4 * b)) & 0xFu);
+        const float v = (float)(q - ((q & 8) << 1)) * sf;
+        wt[buf][scol + 8 * i + b][sr] = (uint16_t)f32_to_bf16(v);
+      }
+    }
+  };
+  // B operand: token l16 of each tile, k .. k + 7 at column quarter kb
+  const uint16_t* xrow[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) xrow[t] = x + (size_t)min(tok0 + t * 16 + l16, M - 1) * K;
+
+  // x operands of one step: slice j, token tile t (zeros past the K range)
+  auto load_x = [&](int step, uint4 (&dst)[kGemmTStep / 32][TM]) {
+#pragma unroll
+    for (int j = 0; j < kGemmTStep / 32; ++j) {
+      const int kk = k0 + step * kGemmTStep + 32 * j + 8 * kb;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        dst[j][t] = (step < nsteps && kk < k1) ? *reinterpret_cast<const uint4*>(xrow[t] + kk)
+                                               : make_uint4(0, 0, 0, 0);
+    }
+  };
+  // x one step ahead in registers for up to 32 tokens; the 64-token tiling
+  // loads it in place (the extra registers would cost it occupancy)
+  constexpr bool kXAhead = TM <= 2;
+  [[maybe_unused]] uint4 xc[kGemmTStep / 32][TM];
+  if constexpr (kXAhead) load_x(0, xc);
+
+  uint4 wq[kGemmTPrefetch];
+  uint32_t sq[kGemmTPrefetch];
+#pragma unroll
+  for (int p = 0; p < kGemmTPrefetch; ++p) {
+    if (p < nsteps) load_w(p, wq[p], sq[p]);
+  }
+  floatx4 acc[TM];
+#pragma unroll
+  for (int t = 0; t < TM; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if (nsteps > 0) stage(0, wq[0], sq[0]);
+  if (kGemmTPrefetch < nsteps) load_w(kGemmTPrefetch, wq[0], sq[0]);
+  __syncthreads();
+
+  for (int i0 = 0; i0 < nsteps; i0 += kGemmTPrefetch) {
+#pragma unroll
+    for (int p = 0; p < kGemmTPrefetch; ++p) {
+      const int i = i0 + p;
+      if (i < nsteps) {
+        const int buf = i & 1;
+        // stage step i + 1 into the other buffer while this one is read
+        if (i + 1 < nsteps) {
+          const int pn = (p + 1) % kGemmTPrefetch;
+          stage(buf ^ 1, wq[pn], sq[pn]);
+          if (i + 1 + kGemmTPrefetch < nsteps) load_w(i + 1 + kGemmTPrefetch, wq[pn], sq[pn]);
+        }
+        if constexpr (kXAhead) {
+          // the next step's x operands, in flight while this step multiplies
+          uint4 xn[kGemmTStep / 32][TM];
+          load_x(i + 1, xn);
+#pragma unroll
+          for (int j = 0; j < kGemmTStep / 32; ++j) {
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(
+                &wt[buf][16 * wave + l16][32 * j + 8 * kb]);
+#pragma unroll
+            for (int t = 0; t < TM; ++t)
+              acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(xc[j][t]), acc[t], 0,
+                                                               0, 0);
+          }
+#pragma unroll
+          for (int j = 0; j < kGemmTStep / 32; ++j)
+#pragma unroll
+            for (int t = 0; t < TM; ++t) xc[j][t] = xn[j][t];
+        } else {
+          const int kbase = k0 + i * kGemmTStep;
+#pragma unroll
+          for (int j = 0; j < kGemmTStep / 32; ++j) {
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(
+                &wt[buf][16 * wave + l16][32 * j + 8 * kb]);
+            const int kk = kbase + 32 * j + 8 * kb;
+#pragma unroll
+            for (int t = 0; t < TM; ++t) {
+              uint4 bv = make_uint4(0, 0, 0, 0);
+              if (kk < k1) bv = *reinterpret_cast<const uint4*>(xrow[t] + kk);
+              acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bv), acc[t], 0, 0, 0);
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const int tok = tok0 + t * 16 + l16;
+    if (tok >= M) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = n0 + 16 * wave + 4 * kb + r;
+      if (col >= N) continue;
+      if (part)
+        part[((size_t)blockIdx.z * M + tok) * N + col] = acc[t][r];
+      else
+        out[(size_t)tok * N + col] = (uint16_t)f32_to_bf16(acc[t][r]);
+    }
+  }
+}
+
+// Sum of the K split's fp32 partials in split order, rounded to bf16.
+__global__ __launch_bounds__(256) void int4_gemm_t_reduce_kernel(const float* __restrict__ part,
+                                                                 uint16_t* __restrict__ out,
+                                                                 size_t mn, int splits) {
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < mn; e += (size_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (int z = 0; z < splits; ++z) v += part[(size_t)z * mn + e];
+    out[e] = (uint16_t)f32_to_bf16(v);
+  }
+}
+
 }  // namespace
 }  // namespace dip
 
@@ -222,5 +397,67 @@ extern "C" int dip_int4_gemm(const int8_t* qweight, const uint16_t* scales, cons
     launch_gemm<2, 8>(qweight, scales, x, out, M, N, K, s);
   else
     launch_gemm<4, 4>(qweight, scales, x, out, M, N, K, s);
+  return hip_status(hipGetLastError());
+}
+
+namespace {
+// K split of dip_int4_gemm_t: about two workgroups per CU over the
+// (64-column, 16*TM-token) tiles, at most 16 ranges, whole 128-row steps.
+int gemm_t_splits(int64_t m, int64_t n, int64_t k) {
+  const int64_t tm = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  const int64_t tiles = ((n + 63) / 64) * ((m + 16 * tm - 1) / (16 * tm));
+  const int64_t want = (2LL * device_cus() + tiles - 1) / tiles;
+  const int64_t max_split = (k + kGemmTStep - 1) / kGemmTStep;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(want, 16), max_split));
+}
+}  // namespace
+
+extern "C" size_t dip_int4_gemm_t_workspace_size(int64_t m, int64_t out_features,
+                                                 int64_t in_features) {
+  if (m <= 0 || out_features <= 0 || in_features <= 0) return 0;
+  const int splits = gemm_t_splits(m, out_features, in_features);
+  return splits > 1 ? (size_t)splits * (size_t)m * (size_t)out_features * sizeof(float) : 0;
+}
+
+extern "C" int dip_int4_gemm_t(const int8_t* qweight_t, const uint16_t* scales_t,
+                               const uint16_t* x, uint16_t* out, int64_t m, int64_t out_features,
+                               int64_t in_features, void* workspace, size_t ws_bytes,
+                               void* stream) {
+  if (!qweight_t || !scales_t) return DIP_ERR_NULL;
+  if (m < 0 || out_features <= 0 || in_features <= 0 || out_features % kGroupSize != 0 ||
+      in_features % 8 != 0 || out_features > (1 << 20) || in_features > INT32_MAX / 2 ||
+      m > 64 * 65535 || m * out_features > ((int64_t)1 << 40))
+    return DIP_ERR_SHAPE;
+  if (m == 0) return DIP_OK;
+  if (!x || !out) return DIP_ERR_NULL;
+  if (!aligned16(qweight_t) || !aligned16(x)) return DIP_ERR_ALIGN;
+  const int M = (int)m, N = (int)out_features, K = (int)in_features;
+  const int TM = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const int gy = (M + 16 * TM - 1) / (16 * TM);
+  const int gx = (N + 63) / 64;
+  int splits = gemm_t_splits(m, out_features, in_features);
+  const size_t need = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+  if (need > 0 && (!workspace || ws_bytes < need)) return DIP_ERR_WORKSPACE;
+  if (splits > 1 && !aligned16(workspace)) return DIP_ERR_ALIGN;
+  const int kchunk = ((K + splits - 1) / splits + kGemmTStep - 1) / kGemmTStep * kGemmTStep;
+  splits = (K + kchunk - 1) / kchunk;
+  float* part = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(gx, gy, splits);
+  if (TM == 1)
+    hipLaunchKernelGGL(int4_gemm_t_kernel<1>, grid, dim3(kGemmThreads), 0, s, qweight_t, scales_t,
+                       x, out, part, M, N, K, kchunk);
+  else if (TM == 2)
+    hipLaunchKernelGGL(int4_gemm_t_kernel<2>, grid, dim3(kGemmThreads), 0, s, qweight_t, scales_t,
+                       x, out, part, M, N, K, kchunk);
+  else
+    hipLaunchKernelGGL(int4_gemm_t_kernel<4>, grid, dim3(kGemmThreads), 0, s, qweight_t, scales_t,
+                       x, out, part, M, N, K, kchunk);
+  if (splits > 1) {
+    const size_t mn = (size_t)M * N;
+    const unsigned blocks = (unsigned)std::min<size_t>((mn + 255) / 256, 2048);
+    hipLaunchKernelGGL(int4_gemm_t_reduce_kernel, dim3(blocks), dim3(256), 0, s, part, out, mn,
+                       splits);
+  }
   return hip_status(hipGetLastError());
 }

@@ -27,7 +27,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 import _dip_hip as K
-from qlinear import GROUP_SIZE, dequantize, int4_linear
+from qlinear import GROUP_SIZE, dequantize, int4_linear, int4_linear_t
 from dip_stream_predispatch import _transpose_down_to_int4, _use_gather, _use_down  # noqa: F401
 
 _use_ca_fused = True
@@ -179,9 +179,7 @@ class CADIPMlp(nn.Module):
         g = F.silu(self._gate(x))
         u = int4_linear(x, self.up_qw.to(self.device), self.up_sc.to(self.device))
         h = g * u
-        dn_t = dequantize(self.down_t_qw.to(self.device),
-                          self.down_t_sc.to(self.device)).to(x.dtype)
-        return h @ dn_t
+        return int4_linear_t(h, self.down_t_qw.to(self.device), self.down_t_sc.to(self.device))
 
 
 def calibrate_cache_from_counts(cas, counts):

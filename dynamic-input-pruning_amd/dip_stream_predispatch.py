@@ -28,7 +28,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 import _dip_hip as K
-from qlinear import GROUP_SIZE, dequantize, int4_linear, _unpack_int4
+from qlinear import GROUP_SIZE, dequantize, int4_linear, int4_linear_t, _unpack_int4
 from quantize import pack_int4
 
 # The reference decides these from which kernel .so files it found; here the
@@ -199,8 +199,7 @@ class StreamingDIPMlp(nn.Module):
         g = F.silu(self._gate(x))
         u = int4_linear(x, self.up_qw, self.up_sc)
         h = g * u
-        dn_t = dequantize(self.down_t_qw, self.down_t_sc).to(x.dtype)
-        return h @ dn_t
+        return int4_linear_t(h, self.down_t_qw, self.down_t_sc)
 
     # Introspection used by tests: the intermediates of the last decode call.
     def last_selection(self):

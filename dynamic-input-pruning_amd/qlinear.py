@@ -54,6 +54,18 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor) ->
     return F.linear(x, dequantize(qweight, scales).to(x.dtype))
 
 
+def int4_linear_t(x: torch.Tensor, qweight_t: torch.Tensor, scales_t: torch.Tensor) -> torch.Tensor:
+    """x @ bf16(q*s) for a matrix stored as rows of the input dimension (the
+    transposed down matrix) on the device, in x's dtype: the int4 MFMA GEMM
+    for up to GEMM_MAX_TOKENS rows of x, else x @ dequantize (the reference's
+    route, dip_stream_predispatch.py:213-215)."""
+    import _dip_hip as K
+    rows = x.numel() // x.shape[-1]
+    if rows <= GEMM_MAX_TOKENS:
+        return K.int4_gemm_t(qweight_t, scales_t, x.to(torch.bfloat16)).to(x.dtype)
+    return x @ dequantize(qweight_t, scales_t).to(x.dtype)
+
+
 def _unpack_int4(qweight: torch.Tensor) -> torch.Tensor:
     """int8 [R, C/2] -> int8 [R, C] in [-8, 7] (qlinear.py:28-50)."""
     q = qweight.view(torch.uint8) if qweight.dtype == torch.int8 else qweight.to(torch.uint8)

@@ -333,6 +333,23 @@ int dip_int4_gemm(const int8_t* qweight, const uint16_t* scales, const uint16_t*
                   void* stream);
 
 /*
+ * out[m, n] = bf16( sum_c x[m, c] * bf16(q*s)[c, n] ) for W stored as rows
+ * of in_features (qweight_t int8 [in_features, out_features/2], scales_t
+ * bf16 [in_features, out_features/128]): the dense route's h @ down_t for a
+ * prompt (dip_stream_predispatch.py:213-215) on bf16 MFMA, without the bf16
+ * copy of down_t.  Each weight enters as the reference's bf16(q*s); fp32
+ * sums; one bf16 rounding.  K is split over workgroups when the output has
+ * few column tiles; the workspace (dip_int4_gemm_t_workspace_size bytes,
+ * 0 when no split is needed) holds their fp32 partials, added in a fixed
+ * order by a second launch.  out_features a multiple of 128, in_features a
+ * multiple of 8; qweight_t and x 16-byte aligned.
+ */
+size_t dip_int4_gemm_t_workspace_size(int64_t m, int64_t out_features, int64_t in_features);
+int dip_int4_gemm_t(const int8_t* qweight_t, const uint16_t* scales_t, const uint16_t* x,
+                    uint16_t* out, int64_t m, int64_t out_features, int64_t in_features,
+                    void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * One-token decode steps of a Qwen3 decoder layer around the DIP MLP, for
  * the whole-model decode loop.  The reference has no kernels of its own
  * here: its decode runs these steps through transformers' Qwen3 modules

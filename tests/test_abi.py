@@ -103,6 +103,11 @@ def test_argument_rejection_before_launch():
     assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, None, p, 8, 1024, None) == -4
     assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, p, p, 8, 5120, None) == -6
     assert L.dip_int4_gemv_rmsnorm(p, p, None, None, p, 1e-6, None, p, 8, 5120, None) == -1
+    # transposed prompt GEMM: NULL, output width, zero tokens, workspace
+    assert L.dip_int4_gemm_t(None, p, p, p, 4, 128, 64, p, 16, None) == -1
+    assert L.dip_int4_gemm_t(p, p, p, p, 4, 100, 64, p, 16, None) == -2
+    assert L.dip_int4_gemm_t(p, p, None, None, 0, 128, 64, None, 0, None) == 0
+    assert L.dip_int4_gemm_t_workspace_size(0, 5120, 25600) == 0
     # prompt GEMM: NULL weights, width not a multiple of 128, no tokens (no
     # buffers needed), misaligned x
     assert L.dip_int4_gemm(None, p, p, p, 4, 64, 128, None) == -1

@@ -62,3 +62,44 @@ def test_int4_gemm_zero_tokens_and_errors(K):
     assert out.shape == (0, 64)
     with pytest.raises(RuntimeError):
         K.int4_gemm(qw, sc, torch.zeros(3, 64, dtype=torch.bfloat16, device="cuda"))
+
+
+def _dequant_f64(qw, sc):
+    """bf16(q*s) of the reference's dequantize, as float64."""
+    return O.bf16_to_f32(O.dequantize(qw, sc)).astype(np.float64)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 512, 128), (2, 3072, 2560), (7, 25600, 5120),
+                                   (32, 25600, 5120), (33, 1000, 256), (64, 12288, 4096)])
+def test_int4_gemm_t_matches_oracle(K, m, k, n):
+    """The transposed layout (W = down_t [K, N/2], scales along N): each
+    weight enters as the reference's bf16(q*s); fp32 sums within the
+    fp32-accumulation bound of an fp64 product of the same bf16 weights."""
+    print(f"int4_gemm_t m={m} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(m * 7 + k)
+    qw, sc = random_int4(rng, k, n)
+    xs = np.stack([random_bf16(rng, k) for _ in range(m)])
+    out = K.int4_gemm_t(dev(qw), dev_bf16(sc), dev_bf16(xs))
+    assert out.shape == (m, n)
+    got = O.bf16_to_f32(host_bf16(out)).astype(np.float64)
+    w = _dequant_f64(qw, sc)
+    xf = O.bf16_to_f32(xs).astype(np.float64)
+    ref = xf @ w
+    terms = np.abs(xf) @ np.abs(w)
+    bound = 2.0 ** -8 * np.abs(ref) + 2.0 ** -17 * terms
+    assert (np.abs(got - ref) <= bound).all()
+    assert float(np.abs(got - ref).max() / np.abs(ref).max()) < 1e-2
+
+
+@pytest.mark.parametrize("m", [5, 32, 64])
+def test_int4_gemm_t_matches_dense_route(K, m):
+    """The reference's prompt route for down: h @ dequantize(down_t)."""
+    from qlinear import dequantize
+    from quantize import quantize_tensor_int4_groupwise
+    g = torch.Generator(device="cuda").manual_seed(m)
+    qw, sc = quantize_tensor_int4_groupwise(torch.randn(25600, 5120, device="cuda", generator=g)
+                                            * 0.02)
+    h = torch.randn(m, 25600, device="cuda", generator=g).to(torch.bfloat16)
+    got = K.int4_gemm_t(qw, sc, h).float()
+    ref = (h @ dequantize(qw, sc)).float()
+    assert float((got - ref).abs().max() / ref.abs().max()) < 1e-2
