@@ -67,6 +67,8 @@ _SIGS = {
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
+    "dip_host_gather_rows_multi": ([_p, _p, _p, _i64, _p, _i64, _i64, _i32], _i32),
+    "dip_host_stream_rows": ([_p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _p, _p], _i32),
     "dip_int4_gemm": ([_p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dip_int4_gemm_t_workspace_size": ([_i64, _i64, _i64], _sz),
     "dip_int4_gemm_t": ([_p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p], _i32),
@@ -724,3 +726,79 @@ def host_gather_rows(src: torch.Tensor, ids: torch.Tensor, dst: torch.Tensor,
         raise RuntimeError("dst too small or row size mismatch")
     _check(lib.dip_host_gather_rows(_ptr(src), _ptr(ids), _ptr(dst), n, row_bytes, src.shape[0],
                                     int(threads)), "dip_host_gather_rows")
+
+
+def _host_pieces(srcs, dsts, n):
+    """Row sizes of matching host matrices (same row count in srcs, at least
+    n rows in dsts)."""
+    if len(srcs) != len(dsts) or not srcs:
+        raise RuntimeError("need matching, non-empty src/dst lists")
+    rows = srcs[0].shape[0]
+    rbs = []
+    for s, d in zip(srcs, dsts):
+        if s.device.type != "cpu" or d.device.type != "cpu":
+            raise RuntimeError("host row gathers work on host tensors")
+        if not (s.is_contiguous() and d.is_contiguous()):
+            raise RuntimeError("host row gathers need contiguous src/dst")
+        if s.shape[0] != rows:
+            raise RuntimeError("every source needs the same row count")
+        rb = s[0].numel() * s.element_size() if rows else 0
+        if d.shape[0] < n or (n and d[0].numel() * d.element_size() != rb):
+            raise RuntimeError("dst too small or row size mismatch")
+        rbs.append(rb)
+    return rows, rbs
+
+
+def _ptr_array(ts):
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
+def host_gather_rows_multi(srcs, ids: torch.Tensor, dsts, threads: int = 8) -> None:
+    """dsts[p][i] = srcs[p][ids[i]] for every matrix p (same row count) in
+    one pass of the native host thread pool: the index_selects of one miss
+    set (dip_ca.py:148-153)."""
+    if ids.device.type != "cpu":
+        raise RuntimeError("host_gather_rows_multi works on host tensors")
+    ids = ids.to(torch.int32).contiguous()
+    n = ids.numel()
+    rows, rbs = _host_pieces(srcs, dsts, n)
+    src_arr, dst_arr = _ptr_array(srcs), _ptr_array(dsts)
+    rb_arr = (ctypes.c_int64 * len(rbs))(*rbs)
+    _check(lib.dip_host_gather_rows_multi(ctypes.addressof(src_arr), ctypes.addressof(dst_arr),
+                                          ctypes.addressof(rb_arr), len(rbs), _ptr(ids), n, rows,
+                                          int(threads)), "dip_host_gather_rows_multi")
+
+
+def host_stream_rows(srcs, ids: torch.Tensor, pinned, dsts, chunk_rows: int = 2048,
+                     threads: int = 8, stream=None, timing: bool = False):
+    """Gather rows srcs[p][ids] into the pinned host staging pinned[p] and
+    copy them to the device tensors dsts[p] (rows 0 .. n-1) on `stream`
+    (default: the current stream of dsts' device), chunk by chunk so that a
+    chunk's copy overlaps the next chunk's gather: the miss stream of
+    dip_ca.py:146-156.  Returns once the copies are queued; with timing,
+    waits for them and returns their summed copy time in ms (else None)."""
+    if ids.device.type != "cpu":
+        raise RuntimeError("host_stream_rows takes host ids")
+    ids = ids.to(torch.int32).contiguous()
+    n = ids.numel()
+    rows, rbs = _host_pieces(srcs, pinned, n)
+    if len(dsts) != len(srcs):
+        raise RuntimeError("need one device destination per source")
+    dev = dsts[0].device
+    for d, rb in zip(dsts, rbs):
+        if d.device != dev or d.device.type != "cuda" or not d.is_contiguous():
+            raise RuntimeError("destinations must be contiguous tensors on one GPU")
+        if d.shape[0] < n or (n and d[0].numel() * d.element_size() != rb):
+            raise RuntimeError("device destination too small or row size mismatch")
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    src_arr, pin_arr, dst_arr = _ptr_array(srcs), _ptr_array(pinned), _ptr_array(dsts)
+    rb_arr = (ctypes.c_int64 * len(rbs))(*rbs)
+    ms = ctypes.c_float(0.0)
+    _check(lib.dip_host_stream_rows(ctypes.addressof(src_arr), ctypes.addressof(pin_arr),
+                                    ctypes.addressof(dst_arr), ctypes.addressof(rb_arr), len(rbs),
+                                    _ptr(ids), n, rows, int(chunk_rows), int(threads),
+                                    ctypes.c_void_p(stream.cuda_stream),
+                                    ctypes.byref(ms) if timing else None),
+           "dip_host_stream_rows")
+    return float(ms.value) if timing else None

@@ -2,7 +2,12 @@
 // host-side miss gather, the one-call resident MLP decode step and the
 // library's status helpers.
 #include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
 #include <cstring>
+#include <functional>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -220,35 +225,221 @@ extern "C" int dip_dequant_rows(const int8_t* qweight, const uint16_t* scales,
   return hip_status(hipGetLastError());
 }
 
-extern "C" int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t n,
-                                    int64_t row_bytes, int64_t src_rows, int threads) {
-  if (n < 0 || row_bytes < 0 || src_rows < 0) return DIP_ERR_SHAPE;
-  if (n == 0 || row_bytes == 0) return DIP_OK;
-  if (!src || !ids || !dst) return DIP_ERR_NULL;
+// ---------------------------------------------------------------------------
+// Host-side miss gather (the pinned index_select of dip_ca.py:148-153) on a
+// persistent pool of host threads.  The cache-aware module gathers once per
+// layer and token, and creating threads (or waking them through the kernel)
+// per call costs about as much as a chunk's copy, so the pool is created on
+// first use, lives until the process ends (its workers are detached and its
+// state is never destroyed, so exit does not wait for them), and a worker
+// spins for a while on the job counter before it sleeps.  Jobs from
+// different caller threads run one after another.
+// ---------------------------------------------------------------------------
+namespace {
+
+class HostPool {
+ public:
+  static HostPool& get() {
+    static HostPool* pool = new HostPool();  // never destroyed: workers may still wait on it
+    return *pool;
+  }
+
+  // Run fn(t) for every t in [0, n) on the caller and up to n - 1 workers;
+  // returns when all n calls have returned.
+  void run(int n, const std::function<void(int)>& fn) {
+    std::lock_guard<std::mutex> one_job(run_mu_);
+    std::unique_lock<std::mutex> lk(mu_);
+    while ((int)nworkers_ < n - 1 && nworkers_ < kMaxWorkers) {
+      // a new worker takes part from the job about to be published on
+      const uint64_t g = gen_.load(std::memory_order_relaxed);
+      std::thread([this, g] { worker(g); }).detach();
+      ++nworkers_;
+    }
+    fn_ = &fn;
+    njobs_ = n;
+    next_ = 0;
+    finished_ = 0;
+    gen_.fetch_add(1, std::memory_order_release);
+    cv_.notify_all();
+    claim(lk);
+    done_cv_.wait(lk, [&] { return finished_ == njobs_; });
+    fn_ = nullptr;
+  }
+
+ private:
+  static constexpr unsigned kMaxWorkers = 63;
+  static constexpr auto kSpin = std::chrono::microseconds(2000);
+
+  // Take job indices until none is left (mu_ held on entry and exit; the
+  // job's fields only change under mu_, so an index always belongs to the
+  // fn_ read with it).
+  void claim(std::unique_lock<std::mutex>& lk) {
+    while (next_ < njobs_) {
+      const int t = next_++;
+      const std::function<void(int)>* f = fn_;
+      lk.unlock();
+      (*f)(t);
+      lk.lock();
+      if (++finished_ == njobs_) done_cv_.notify_all();
+    }
+  }
+
+  void worker(uint64_t seen) {
+    for (;;) {
+      // spin (yielding) for the next job, then sleep on the condition
+      const auto t0 = std::chrono::steady_clock::now();
+      while (gen_.load(std::memory_order_acquire) == seen &&
+             std::chrono::steady_clock::now() - t0 < kSpin)
+        std::this_thread::yield();
+      std::unique_lock<std::mutex> lk(mu_);
+      cv_.wait(lk, [&] { return gen_.load(std::memory_order_relaxed) != seen; });
+      seen = gen_.load(std::memory_order_relaxed);
+      claim(lk);
+    }
+  }
+
+  std::mutex run_mu_, mu_;
+  std::condition_variable cv_, done_cv_;
+  std::atomic<uint64_t> gen_{0};
+  const std::function<void(int)>* fn_ = nullptr;
+  int njobs_ = 0, next_ = 0, finished_ = 0;
+  unsigned nworkers_ = 0;
+};
+
+int check_pieces(int npieces, const void* const* src, void* const* dst, const int64_t* row_bytes,
+                 const int32_t* ids, int64_t n, int64_t src_rows) {
+  if (n < 0 || src_rows < 0 || npieces < 0 || npieces > 64) return DIP_ERR_SHAPE;
+  if (n == 0 || npieces == 0) return DIP_OK;
+  if (!ids || !src || !dst || !row_bytes) return DIP_ERR_NULL;
+  for (int p = 0; p < npieces; ++p) {
+    if (row_bytes[p] < 0) return DIP_ERR_SHAPE;
+    if (row_bytes[p] > 0 && (!src[p] || !dst[p])) return DIP_ERR_NULL;
+  }
   for (int64_t i = 0; i < n; ++i)
     if (ids[i] < 0 || ids[i] >= src_rows) return DIP_ERR_SHAPE;
-  const char* s = static_cast<const char*>(src);
-  char* d = static_cast<char*>(dst);
-  auto work = [&](int64_t b, int64_t e) {
-    for (int64_t i = b; i < e; ++i)
-      std::memcpy(d + i * row_bytes, s + (int64_t)ids[i] * row_bytes, (size_t)row_bytes);
-  };
-  int nt = std::max(1, threads);
-  if ((int64_t)nt > n) nt = (int)n;
-  if (nt == 1) {
-    work(0, n);
-    return DIP_OK;
-  }
-  std::vector<std::thread> pool;
-  pool.reserve(nt - 1);
-  const int64_t per = (n + nt - 1) / nt;
-  for (int t = 1; t < nt; ++t) {
-    const int64_t b = t * per, e = std::min(n, b + per);
-    if (b < e) pool.emplace_back(work, b, e);
-  }
-  work(0, std::min(n, per));
-  for (auto& th : pool) th.join();
   return DIP_OK;
+}
+
+// dst_p[i] = src_p[ids[i]] for every piece p and i in [b, e).
+void copy_rows(int npieces, const void* const* src, void* const* dst, const int64_t* row_bytes,
+               const int32_t* ids, int64_t b, int64_t e) {
+  for (int p = 0; p < npieces; ++p) {
+    const int64_t rb = row_bytes[p];
+    const char* s = static_cast<const char*>(src[p]);
+    char* d = static_cast<char*>(dst[p]);
+    for (int64_t i = b; i < e; ++i) std::memcpy(d + i * rb, s + (int64_t)ids[i] * rb, (size_t)rb);
+  }
+}
+
+int pool_threads(int threads, int64_t n) {
+  int nt = std::max(1, std::min(threads, 64));
+  return (int)std::min<int64_t>(nt, n);
+}
+
+int gather_rows(int npieces, const void* const* src, void* const* dst, const int64_t* row_bytes,
+                const int32_t* ids, int64_t n, int64_t src_rows, int threads) {
+  const int st = check_pieces(npieces, src, dst, row_bytes, ids, n, src_rows);
+  if (st || n == 0 || npieces == 0) return st;
+  const int nt = pool_threads(threads, n);
+  const int64_t per = (n + nt - 1) / nt;
+  auto work = [&](int t) {
+    copy_rows(npieces, src, dst, row_bytes, ids, std::min(n, t * per), std::min(n, (t + 1) * per));
+  };
+  if (nt == 1)
+    work(0);
+  else
+    HostPool::get().run(nt, work);
+  return DIP_OK;
+}
+
+}  // namespace
+
+extern "C" int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t n,
+                                    int64_t row_bytes, int64_t src_rows, int threads) {
+  return gather_rows(1, &src, &dst, &row_bytes, ids, n, src_rows, threads);
+}
+
+extern "C" int dip_host_gather_rows_multi(const void* const* src, void* const* dst,
+                                          const int64_t* row_bytes, int64_t npieces,
+                                          const int32_t* ids, int64_t n, int64_t src_rows,
+                                          int threads) {
+  if (npieces < 0 || npieces > 64) return DIP_ERR_SHAPE;
+  return gather_rows((int)npieces, src, dst, row_bytes, ids, n, src_rows, threads);
+}
+
+extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
+                                    void* const* dst, const int64_t* row_bytes, int64_t npieces,
+                                    const int32_t* ids, int64_t n, int64_t src_rows,
+                                    int64_t chunk_rows, int threads, void* stream,
+                                    float* copy_ms) {
+  if (copy_ms) *copy_ms = 0.f;
+  if (chunk_rows <= 0) return DIP_ERR_ARG;
+  int st = check_pieces((int)npieces, src, pinned, row_bytes, ids, n, src_rows);
+  if (st) return st;
+  st = check_pieces((int)npieces, pinned, dst, row_bytes, ids, n, src_rows);
+  if (st || n == 0 || npieces == 0) return st;
+  const int np = (int)npieces;
+  const int64_t nchunks = (n + chunk_rows - 1) / chunk_rows;
+  const int nt = pool_threads(threads, chunk_rows);
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<hipEvent_t> ev;
+  if (copy_ms) {
+    ev.assign(2 * nchunks, nullptr);
+    for (auto& e : ev)
+      if (hipEventCreate(&e) != hipSuccess) {
+        for (auto& e2 : ev)
+          if (e2) (void)hipEventDestroy(e2);
+        return hip_status(hipGetLastError());
+      }
+  }
+  // left[c]: thread slices of chunk c not yet gathered; the thread that
+  // takes it to zero queues the chunk's copies (one at a time, so a chunk's
+  // events bracket only its own copies)
+  std::vector<std::atomic<int>> left(nchunks);
+  for (auto& l : left) l.store(nt, std::memory_order_relaxed);
+  std::atomic<int> err{0};
+  std::mutex issue_mu;
+  auto work = [&](int t) {
+    for (int64_t c = 0; c < nchunks; ++c) {
+      const int64_t c0 = c * chunk_rows, c1 = std::min(n, c0 + chunk_rows);
+      const int64_t per = (c1 - c0 + nt - 1) / nt;
+      copy_rows(np, src, pinned, row_bytes, ids, std::min(c1, c0 + t * per),
+                std::min(c1, c0 + (t + 1) * per));
+      if (left[c].fetch_sub(1, std::memory_order_acq_rel) != 1) continue;
+      std::lock_guard<std::mutex> g(issue_mu);
+      hipError_t e = hipSuccess;
+      if (copy_ms) e = hipEventRecord(ev[2 * c], s);
+      for (int p = 0; p < np && e == hipSuccess; ++p) {
+        const int64_t rb = row_bytes[p];
+        if (rb == 0) continue;
+        e = hipMemcpyAsync(static_cast<char*>(dst[p]) + c0 * rb,
+                           static_cast<const char*>(pinned[p]) + c0 * rb,
+                           (size_t)((c1 - c0) * rb), hipMemcpyHostToDevice, s);
+      }
+      if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[2 * c + 1], s);
+      if (e != hipSuccess) err.store((int)e);
+    }
+  };
+  if (nt == 1)
+    work(0);
+  else
+    HostPool::get().run(nt, work);
+  st = err.load();
+  if (copy_ms) {
+    float total = 0.f;
+    if (!st) {
+      for (int64_t c = 0; c < nchunks && !st; ++c) {
+        float ms = 0.f;
+        hipError_t e = hipEventSynchronize(ev[2 * c + 1]);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[2 * c], ev[2 * c + 1]);
+        if (e != hipSuccess) st = (int)e;
+        total += ms;
+      }
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    *copy_ms = total;
+  }
+  return st;
 }
 
 // ---------------------------------------------------------------------------

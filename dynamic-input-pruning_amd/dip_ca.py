@@ -21,6 +21,7 @@ ascending channel id (dip_ca.py:107-113).
 from __future__ import annotations
 
 import os
+import time
 
 import torch
 import torch.nn as nn
@@ -61,10 +62,23 @@ class CABuffers:
         self.copy_stream = torch.cuda.Stream(device=dev)
         self.h = torch.empty(k, dtype=torch.bfloat16, device=dev)
         self._g = {}
-        self.host_threads = int(os.environ.get("DIP_HOST_THREADS", "8"))
+        # the per-token read-back: n_hit, n_miss and the miss ids
+        self.host_counts = torch.empty(2, dtype=torch.int32).pin_memory()
+        self.host_miss = torch.empty(k, dtype=torch.int32).pin_memory()
+        # host threads of the native miss gather (default: this process's
+        # cores, at most 8; more measured no faster against PCIe)
+        self.host_threads = int(os.environ.get(
+            "DIP_HOST_THREADS", str(max(1, min(8, len(os.sched_getaffinity(0)))))))
+        # miss rows per gather / copy chunk: each chunk's H2D copy runs while
+        # the host gathers the next one
+        self.stream_chunk = int(os.environ.get("DIP_STREAM_CHUNK", "2048"))
         # statistics of the last forward (hit rate, bytes streamed)
         self.last_n_hit = 0
         self.last_n_miss = 0
+        # when a list: one (bytes, seconds of the gather-and-queue call, ms
+        # of copy-stream time of its H2D copies) per streamed miss set; the
+        # call then also waits for its copies
+        self.transfers = None
 
     def g(self, inter: int) -> torch.Tensor:
         t = self._g.get(inter)
@@ -133,35 +147,43 @@ class CADIPMlp(nn.Module):
         return int4_linear(x, self.gate_qw, self.gate_sc)
 
     def _stream_misses(self, miss_ids_cpu: torch.Tensor, n_miss: int):
-        """Pinned row gather of the misses (native threads) + async H2D on the
-        copy stream (dip_ca.py:146-156)."""
+        """Pinned row gather of the misses + async H2D on the copy stream
+        (dip_ca.py:146-156) as one native call: host threads gather the up
+        and down_t rows of buf.stream_chunk misses at a time, and each
+        chunk's copies are queued as soon as it is gathered, so they run
+        while the next chunk is gathered."""
         b = self.buf
-        t = b.host_threads
-        K.host_gather_rows(self.up_qw, miss_ids_cpu, b.pin_up_qw, t)
-        K.host_gather_rows(self.up_sc, miss_ids_cpu, b.pin_up_sc, t)
-        K.host_gather_rows(self.down_t_qw, miss_ids_cpu, b.pin_dn_qw, t)
-        K.host_gather_rows(self.down_t_sc, miss_ids_cpu, b.pin_dn_sc, t)
-        main = torch.cuda.current_stream(self.device)
-        b.copy_stream.wait_stream(main)
-        with torch.cuda.stream(b.copy_stream):
-            b.gpu_up_qw[:n_miss].copy_(b.pin_up_qw[:n_miss], non_blocking=True)
-            b.gpu_up_sc[:n_miss].copy_(b.pin_up_sc[:n_miss], non_blocking=True)
-            b.gpu_dn_qw[:n_miss].copy_(b.pin_dn_qw[:n_miss], non_blocking=True)
-            b.gpu_dn_sc[:n_miss].copy_(b.pin_dn_sc[:n_miss], non_blocking=True)
+        pins = (b.pin_up_qw, b.pin_up_sc, b.pin_dn_qw, b.pin_dn_sc)
+        # the staging rows are free once the previous layer's reads are done
+        b.copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+        timing = b.transfers is not None
+        t0 = time.perf_counter()
+        ms = K.host_stream_rows((self.up_qw, self.up_sc, self.down_t_qw, self.down_t_sc),
+                                miss_ids_cpu, pins,
+                                (b.gpu_up_qw, b.gpu_up_sc, b.gpu_dn_qw, b.gpu_dn_sc),
+                                chunk_rows=b.stream_chunk, threads=b.host_threads,
+                                stream=b.copy_stream, timing=timing)
+        if timing:
+            nbytes = n_miss * sum(p.stride(0) * p.element_size() for p in pins)
+            b.transfers.append((nbytes, time.perf_counter() - t0, ms))
 
     def _decode_one(self, xv: torch.Tensor) -> torch.Tensor:
         b = self.buf
         g, idx = K.gate_silu_topk(self.gate_qw, self.gate_sc, xv, self.k, g=b.g(self.inter))
         combined, src, row, miss, counts = K.ca_assemble(self.id2slot, idx)
-        n_hit, n_miss = (int(v) for v in counts.cpu())   # host sync, as the reference
+        # one read-back of the counts and the miss ids (the host sync the
+        # reference also has, dip_ca.py:139-146)
+        b.host_counts.copy_(counts, non_blocking=True)
+        b.host_miss.copy_(miss, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        n_hit, n_miss = (int(v) for v in b.host_counts)
         b.last_n_hit, b.last_n_miss = n_hit, n_miss
         h = b.h[: self.k]
-        if n_hit:
+        if n_hit:  # runs on the GPU while the host gathers the misses
             K.ca_fused_gemv(self._res_up_qw, self._res_up_sc, b.gpu_up_qw, b.gpu_up_sc, xv,
                             src[:n_hit], row[:n_hit], g=g, gid=combined[:n_hit], out=h[:n_hit])
         if n_miss:
-            miss_cpu = miss[:n_miss].cpu()
-            self._stream_misses(miss_cpu, n_miss)
+            self._stream_misses(b.host_miss[:n_miss], n_miss)
             torch.cuda.current_stream(self.device).wait_stream(b.copy_stream)
             K.ca_fused_gemv(self._res_up_qw, self._res_up_sc, b.gpu_up_qw, b.gpu_up_sc, xv,
                             src[n_hit:], row[n_hit:], g=g, gid=combined[n_hit:], out=h[n_hit:])
@@ -180,6 +202,25 @@ class CADIPMlp(nn.Module):
         u = int4_linear(x, self.up_qw.to(self.device), self.up_sc.to(self.device))
         h = g * u
         return int4_linear_t(h, self.down_t_qw.to(self.device), self.down_t_sc.to(self.device))
+
+
+def zipf_counts(inter: int, k: int, tokens: int = 128, s: float = 1.1, seed: int = 0):
+    """Synthetic stand-in for the selection counts calibrate_cache gathers
+    over generate (dip_ca.py:272-309): channel popularity follows Zipf(s)
+    over a seeded random ranking of the channels, and each of `tokens`
+    synthetic tokens selects k distinct channels, drawn without replacement
+    with probability proportional to popularity (Gumbel top-k: the k largest
+    log(w) + Gumbel noise are a draw of k items without replacement
+    proportional to w).  Returns int64 counts [inter] on the host."""
+    if not 0 < k <= inter:
+        raise ValueError(f"need 0 < k <= inter, got k={k} inter={inter}")
+    gen = torch.Generator().manual_seed(seed)
+    rank = torch.randperm(inter, generator=gen)  # rank[c] = popularity rank of channel c
+    logw = -s * torch.log1p(rank.double())       # log(1 / (rank + 1)^s)
+    u = torch.rand(tokens, inter, generator=gen, dtype=torch.float64).clamp_(1e-300, 1.0)
+    keys = logw.unsqueeze(0) - torch.log(-torch.log(u))
+    sel = keys.topk(k, dim=1).indices
+    return torch.bincount(sel.reshape(-1), minlength=inter).to(torch.long)
 
 
 def calibrate_cache_from_counts(cas, counts):

@@ -304,6 +304,35 @@ int dip_host_gather_rows(const void* src, const int32_t* ids, void* dst, int64_t
                          int64_t row_bytes, int64_t src_rows, int threads);
 
 /*
+ * dip_host_gather_rows over several matrices that share the row ids (the
+ * four index_selects of one miss set, dip_ca.py:148-153) in one pass:
+ * dst[p] + i * row_bytes[p] <- src[p] + ids[i] * row_bytes[p] for every
+ * piece p < npieces (at most 64) and i < n.  The threads come from a
+ * persistent pool created on first use.  Host pointers; returns DIP_OK or
+ * a DIP_ERR_* code.
+ */
+int dip_host_gather_rows_multi(const void* const* src, void* const* dst,
+                               const int64_t* row_bytes, int64_t npieces, const int32_t* ids,
+                               int64_t n, int64_t src_rows, int threads);
+
+/*
+ * The cache-aware miss stream (dip_ca.py:146-156: pinned index_select, then
+ * non_blocking H2D copies on a side stream) as one pipelined call: the ids
+ * are taken in chunks of chunk_rows; for each chunk the host threads gather
+ * the rows of every piece into pinned[p] (host, pinned, at least n rows),
+ * and the thread that completes the chunk queues its copies
+ * pinned[p] -> dst[p] (device, at least n rows) on `stream`, so a chunk's
+ * copy runs while the next chunk is gathered.  Returns once every copy is
+ * queued (not finished).  When copy_ms is non-NULL, each chunk's copies are
+ * bracketed by events, the call waits for them and writes the summed copy
+ * time in milliseconds.  Returns DIP_OK, a DIP_ERR_* code or a hipError_t.
+ */
+int dip_host_stream_rows(const void* const* src, void* const* pinned, void* const* dst,
+                         const int64_t* row_bytes, int64_t npieces, const int32_t* ids,
+                         int64_t n, int64_t src_rows, int64_t chunk_rows, int threads,
+                         void* stream, float* copy_ms);
+
+/*
  * dip_int4_gemv with the input RMSNorm of a decoder layer folded in:
  * v = bf16(h + add) (add may be NULL), x = bf16(norm_w * bf16(v * rsqrt(
  * mean(v^2) + eps))) (transformers' Qwen3RMSNorm, fp32 mean), out = the

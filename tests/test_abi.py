@@ -175,6 +175,48 @@ def test_host_gather_rows():
         K.host_gather_rows(src, bad, torch.zeros(2, 2560, dtype=torch.int8))
 
 
+def test_host_gather_rows_multi_and_pool_reuse():
+    """Several matrices in one pass, thread counts above and below the row
+    count, and many back-to-back jobs on the persistent pool."""
+    rng = np.random.default_rng(1)
+    srcs = [torch.from_numpy(rng.integers(-128, 128, size=(400, 2560), dtype=np.int8)),
+            torch.from_numpy(rng.standard_normal((400, 40)).astype(np.float32)).to(torch.bfloat16),
+            torch.from_numpy(rng.integers(-128, 128, size=(400, 96), dtype=np.int8))]
+    for rep in range(50):
+        n = int(rng.integers(1, 300))
+        ids = torch.from_numpy(rng.integers(0, 400, size=n).astype(np.int32))
+        dsts = [torch.zeros(n + 2, *s.shape[1:], dtype=s.dtype) for s in srcs]
+        K.host_gather_rows_multi(srcs, ids, dsts, threads=(1, 3, 8, 16)[rep % 4])
+        for s, d in zip(srcs, dsts):
+            assert torch.equal(d[:n], s[ids.long()])
+            assert torch.all(d[n:] == 0)
+    with pytest.raises(RuntimeError):
+        K.host_gather_rows_multi(srcs, torch.tensor([0, 400], dtype=torch.int32),
+                                 [torch.zeros(2, *s.shape[1:], dtype=s.dtype) for s in srcs])
+    with pytest.raises(RuntimeError):  # row counts differ
+        K.host_gather_rows_multi([srcs[0], srcs[1][:10]], torch.tensor([0], dtype=torch.int32),
+                                 [torch.zeros(1, 2560, dtype=torch.int8),
+                                  torch.zeros(1, 40, dtype=torch.bfloat16)])
+
+
+def test_host_stream_rows_rejects_before_any_copy():
+    L = K.lib
+    p = ctypes.c_void_p(16)
+    arr = (ctypes.c_void_p * 1)(16)
+    rb = (ctypes.c_int64 * 1)(64)
+    ids_bad = (ctypes.c_int32 * 2)(0, 10)
+    a = ctypes.addressof
+    # chunk_rows <= 0, then an id past src_rows: both before any HIP call
+    assert L.dip_host_stream_rows(a(arr), a(arr), a(arr), a(rb), 1, a(ids_bad), 2, 10, 0, 4, None,
+                                  None) == -6
+    assert L.dip_host_stream_rows(a(arr), a(arr), a(arr), a(rb), 1, a(ids_bad), 2, 10, 64, 4, None,
+                                  None) == -2
+    # nothing to stream: OK without touching the device
+    assert L.dip_host_stream_rows(a(arr), a(arr), a(arr), a(rb), 1, a(ids_bad), 0, 10, 64, 4, None,
+                                  None) == 0
+    assert L.dip_host_stream_rows(None, None, None, None, 1, p, 2, 10, 64, 4, None, None) == -1
+
+
 def test_python_layer_rejects_host_tensors():
     qw = torch.zeros(8, 64, dtype=torch.int8)
     sc = torch.zeros(8, 1, dtype=torch.bfloat16)
