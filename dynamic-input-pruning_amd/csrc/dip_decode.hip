@@ -317,12 +317,18 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
 }
 
 // Norm + rotary + cache write + attention in one launch, for caches of at
-// most kFusedMaxLen rows: workgroup = one kv head and its G query heads.
+// most kFusedMaxLen rows: workgroup = HPW consecutive query heads of one kv
+// head (group = nh / nkv query heads share it).  Every workgroup of a group
+// normalises and rotates the group's k itself; only the group's first
+// workgroup writes k and v to cache row pos (the others take this token's
+// row from their own LDS copy, never from the cache).  One query head per
+// workgroup spreads a layer over nh workgroups instead of nkv, which takes
+// the per-head norm, rotary, softmax and value sums off one serial chain.
 //   0. every load that does not need this token's k and v is issued first:
-//      the group's q | k | v heads, the norm weights and the cos / sin rows
-//      into LDS, each wave's first 32-row chunk of the cache into registers;
+//      the q heads, k and v, the norm weights and the cos / sin rows into
+//      LDS, each wave's first 32-row chunk of the cache into registers;
 //   1. RMSNorm + rotary as qk_rope_cache_kernel; q into LDS as bf16, this
-//      token's k and v into LDS and into cache row pos;
+//      token's k and v into LDS (and into cache row pos);
 //   2. wave w takes the chunks w, w + 4, ...: the scores on bf16 MFMA
 //      (v_mfma_f32_16x16x32_bf16, A = 16 cache rows, B = the q heads, exact
 //      products, fp32 sums; row pos from LDS, not read back), softmax in
@@ -331,35 +337,38 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
 //   3. the 4 waves' partials are merged through LDS in a fixed order.
 constexpr int kFusedMaxLen = 128;
 
-template <int G>
+template <int HPW>
 __global__ __launch_bounds__(256) void attn_fused_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_w,
     const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ cos_t,
     const uint16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_p,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint16_t* __restrict__ out,
     int nh, int nkv, int max_len, float eps, float scale) {
-  static_assert(G <= 16, "one MFMA column per query head");
-  __shared__ __align__(16) uint32_t qb[16][64 + 4];   // q as bf16 pairs; heads >= G are 0
+  static_assert(HPW <= 16, "one MFMA column per query head");
+  const int group = nh / nkv;           // query heads per kv head
+  const int h0 = blockIdx.x * HPW;      // this workgroup's first query head
+  const bool writer = h0 % group == 0;  // the group's first workgroup writes the cache
+  __shared__ __align__(16) uint32_t qb[16][64 + 4];   // q as bf16 pairs; heads >= HPW are 0
   __shared__ __align__(16) uint32_t kv_new[2][64];
-  __shared__ uint32_t heads[G + 2][64];  // this group's raw q | k | v
-  __shared__ uint32_t tabs[4][64];       // q_w, k_w, cos row, sin row
-  __shared__ float ps[4][G][kAttnChunk];
-  __shared__ float cm[4][G], cl[4][G];
-  __shared__ float wm[4][G], wl[4][G];
-  __shared__ float wacc[4][G][kHeadDim];
-  const int kvh = blockIdx.x, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __shared__ uint32_t heads[HPW + 2][64];  // raw q heads | k | v
+  __shared__ uint32_t tabs[4][64];         // q_w, k_w, cos row, sin row
+  __shared__ float ps[4][HPW][kAttnChunk];
+  __shared__ float cm[4][HPW], cl[4][HPW];
+  __shared__ float wm[4][HPW], wl[4][HPW];
+  __shared__ float wacc[4][HPW][kHeadDim];
+  const int kvh = h0 / group, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int l16 = l & 15, kb = l >> 4;
   const int64_t pos = *pos_p;
   const bool pos_ok = pos >= 0 && pos < max_len;
   const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
 
   // 0. loads
-  for (int i = threadIdx.x; i < (G + 2) * 64; i += 256) {
+  for (int i = threadIdx.x; i < (HPW + 2) * 64; i += 256) {
     const int hi = i >> 6;
-    const int head = hi < G ? kvh * G + hi : (hi == G ? nh + kvh : nh + nkv + kvh);
+    const int head = hi < HPW ? h0 + hi : (hi == HPW ? nh + kvh : nh + nkv + kvh);
     heads[hi][i & 63] = reinterpret_cast<const uint32_t*>(qkv)[(size_t)head * 64 + (i & 63)];
   }
-  for (int i = threadIdx.x + G * 64; i < 16 * 64; i += 256) qb[i >> 6][i & 63] = 0u;
+  for (int i = threadIdx.x + HPW * 64; i < 16 * 64; i += 256) qb[i >> 6][i & 63] = 0u;
   {
     const size_t trow = (size_t)(pos_ok ? pos : 0) * 64 + l;
     const uint32_t* src = wave == 0 ? reinterpret_cast<const uint32_t*>(q_w) + l
@@ -395,15 +404,15 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   __syncthreads();
 
   // 1. RMSNorm + rotary of the q heads and the k head; v and k to the cache
-  for (int hi = wave; hi < G + 2; hi += 4) {
+  for (int hi = wave; hi < HPW + 2; hi += 4) {
     const uint32_t pair = heads[hi][l];
-    if (hi == G + 1) {
+    if (hi == HPW + 1) {
       kv_new[1][l] = pair;
-      if (pos_ok)
+      if (pos_ok && writer)
         reinterpret_cast<uint32_t*>(v_cache)[((size_t)kvh * max_len + pos) * 64 + l] = pair;
       continue;
     }
-    const uint32_t wp = tabs[hi < G ? 0 : 1][l];
+    const uint32_t wp = tabs[hi < HPW ? 0 : 1][l];
     const float x0 = bf16_to_f32(pair & 0xFFFFu), x1 = bf16_to_f32(pair >> 16);
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float r = rsqrtf(ss * (1.0f / (float)kHeadDim) + eps);
@@ -420,11 +429,11 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
                                     round_bf16(r0 * bf16_to_f32(sn & 0xFFFFu)));
     const uint32_t o1 = f32_to_bf16(round_bf16(bf16_to_f32(y1) * bf16_to_f32(cs >> 16)) +
                                     round_bf16(r1 * bf16_to_f32(sn >> 16)));
-    if (hi < G) {
+    if (hi < HPW) {
       qb[hi][l] = o0 | (o1 << 16);
     } else {
       kv_new[0][l] = o0 | (o1 << 16);
-      if (pos_ok)
+      if (pos_ok && writer)
         reinterpret_cast<uint32_t*>(k_cache)[((size_t)kvh * max_len + pos) * 64 + l] =
             o0 | (o1 << 16);
     }
@@ -435,9 +444,9 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   uint4 bq[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const uint4*>(&qb[l16][16 * kb + 4 * j]);
-  float m[G], lsum[G], a0[G], a1[G];
+  float m[HPW], lsum[HPW], a0[HPW], a1[HPW];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < HPW; ++g) {
     m[g] = -INFINITY;
     lsum[g] = a0[g] = a1[g] = 0.f;
   }
@@ -481,10 +490,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
       for (int r = 0; r < 4; ++r) {
         const float e = sc[t][r] == -INFINITY ? 0.f : expf(sc[t][r] - mx);
         sum += e;
-        if (l16 < G) ps[wave][l16][16 * t + 4 * kb + r] = e;
+        if (l16 < HPW) ps[wave][l16][16 * t + 4 * kb + r] = e;
       }
     sum = row_pair_sum32(row_pair_sum16(sum));
-    if (kb == 0 && l16 < G) {
+    if (kb == 0 && l16 < HPW) {
       cm[wave][l16] = mx;
       cl[wave][l16] = sum;
     }
@@ -492,22 +501,22 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 
     // values: lane l takes dimensions 2l, 2l + 1
-    float c0[G], c1[G];
+    float c0[HPW], c1[HPW];
 #pragma unroll
-    for (int g = 0; g < G; ++g) c0[g] = c1[g] = 0.f;
+    for (int g = 0; g < HPW; ++g) c0[g] = c1[g] = 0.f;
 #pragma unroll
     for (int j = 0; j < kAttnChunk; ++j) {
       if (j < npos) {
         const float v0 = bf16_to_f32(vv[j] & 0xFFFFu), v1 = bf16_to_f32(vv[j] >> 16);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < HPW; ++g) {
           c0[g] = fmaf(ps[wave][g][j], v0, c0[g]);
           c1[g] = fmaf(ps[wave][g][j], v1, c1[g]);
         }
       }
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < HPW; ++g) {
       const float mc = cm[wave][g], lc = cl[wave][g];
       const float mn = fmaxf(m[g], mc);
       const float fo = expf(m[g] - mn), fn = expf(mc - mn);
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
 
   // 3. merge the waves in a fixed order
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < HPW; ++g) {
     if (l == 0) {
       wm[wave][g] = m[g];
       wl[wave][g] = lsum[g];
@@ -531,7 +540,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     wacc[wave][g][2 * l + 1] = a1[g];
   }
   __syncthreads();
-  for (int g = wave; g < G; g += 4) {
+  for (int g = wave; g < HPW; g += 4) {
     float mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 4; ++w) mx = fmaxf(mx, wm[w][g]);
@@ -543,7 +552,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
       o0 = fmaf(f, wacc[w][g][2 * l], o0);
       o1 = fmaf(f, wacc[w][g][2 * l + 1], o1);
     }
-    reinterpret_cast<uint32_t*>(out)[((size_t)kvh * G + g) * 64 + l] =
+    reinterpret_cast<uint32_t*>(out)[((size_t)h0 + g) * 64 + l] =
         f32_to_bf16(o0 / den) | (f32_to_bf16(o1 / den) << 16);
   }
 }
@@ -621,19 +630,9 @@ extern "C" int dip_decode_attention_fused(const uint16_t* qkv, const uint16_t* q
     return DIP_ERR_ALIGN;
   const int nh = (int)n_heads, nkv = (int)n_kv_heads, ml = (int)max_len;
   hipStream_t s = (hipStream_t)stream;
-#define DIP_FUSED(GG)                                                                            \
-  hipLaunchKernelGGL(attn_fused_kernel<GG>, dim3(nkv), dim3(256), 0, s, qkv, q_norm_w, k_norm_w, \
-                     cos_table, sin_table, pos, k_cache, v_cache, out, nh, nkv, ml, eps, scale)
-  switch (nh / nkv) {
-    case 1: DIP_FUSED(1); break;
-    case 2: DIP_FUSED(2); break;
-    case 4: DIP_FUSED(4); break;
-    case 5: DIP_FUSED(5); break;
-    case 8: DIP_FUSED(8); break;
-    case 16: DIP_FUSED(16); break;
-    default: return DIP_ERR_UNSUPPORTED;
-  }
-#undef DIP_FUSED
+  // one query head per workgroup
+  hipLaunchKernelGGL(attn_fused_kernel<1>, dim3(nh), dim3(256), 0, s, qkv, q_norm_w, k_norm_w,
+                     cos_table, sin_table, pos, k_cache, v_cache, out, nh, nkv, ml, eps, scale);
   return hip_status(hipGetLastError());
 }
 

@@ -167,9 +167,11 @@ void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
 
 template <int LPR, int CH, int SRC, int EPI, bool NORM = false>
 int launch_one(const RowdotArgs& a, hipStream_t stream) {
-  // the widths of Qwen3-4B/8B/14B/32B stage x through LDS; every ROWS the
-  // plan can pick is instantiated
-  constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5);
+  // the widths of Qwen3-4B/8B/14B/32B (hidden and, at 8192, the 32B o
+  // projection's input) stage x through LDS; every ROWS the plan can pick
+  // is instantiated
+  constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5) ||
+                       (LPR == 64 && CH == 4);
   if constexpr (hot) {
     const RowdotPlan p = plan_rowdot(a.nrows, LPR, SRC == kContig);
     if constexpr (SRC == kContig) {  // balanced plan: any rows per group up to 8
@@ -212,7 +214,7 @@ int dispatch_layout(const RowdotArgs& a, hipStream_t stream) {
   DIP_TRY(32, 2)   // 2048
   DIP_TRY(32, 3)   // 3072
   DIP_TRY(32, 6)   // 6144
-  DIP_TRY(32, 8)   // 8192
+  DIP_TRY(64, 4)   // 8192 (Qwen3-32B o_proj: 64 heads x 128)
   DIP_TRY(32, 1)   // 1024
   DIP_TRY(16, 3)   // 1536
   DIP_TRY(16, 1)   // 512

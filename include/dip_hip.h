@@ -429,11 +429,13 @@ size_t dip_decode_attention_workspace_size(int64_t n_heads, int64_t head_dim, in
 /*
  * dip_decode_attention_fused: dip_qk_norm_rope_cache followed by
  * dip_decode_attention (q_out not kept) in one launch of one workgroup per
- * kv head, for caches of at most dip_decode_attention_fused_max_len() rows
- * (128; else DIP_ERR_SHAPE).  The token's own cache row is taken from the
- * workgroup's copy, not read back.  Same cache rows bit for bit; the scores
- * are summed on bf16 MFMA (exact products, fp32 sums) and the chunks merged
- * in another order.  No workspace.
+ * query head, for caches of at most dip_decode_attention_fused_max_len()
+ * rows (128; else DIP_ERR_SHAPE) and any n_heads that n_kv_heads divides.
+ * The first workgroup of each kv head's group writes the cache row; every
+ * workgroup takes the token's own row from its copy, not read back.  Same
+ * cache rows bit for bit; the scores are summed on bf16 MFMA (exact
+ * products, fp32 sums) and the chunks merged in another order.  No
+ * workspace.
  */
 int64_t dip_decode_attention_fused_max_len(void);
 int dip_decode_attention_fused(const uint16_t* qkv, const uint16_t* q_norm_w,

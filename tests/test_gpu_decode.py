@@ -147,12 +147,13 @@ def test_decode_attention(K, nh, nkv):
         assert not ((ulps > 2) & (err > 1e-5 * float(ref.abs().max()))).any()
 
 
-@pytest.mark.parametrize("nh,nkv", [(4, 4), (4, 2), (32, 8), (40, 8), (64, 8), (64, 4)])
+@pytest.mark.parametrize("nh,nkv", [(4, 4), (4, 2), (24, 8), (32, 8), (40, 8), (64, 8), (64, 4)])
 def test_decode_attention_fused_matches_split(K, nh, nkv):
     """The one-launch norm + rotary + cache write + attention against the
     two-step path on the same inputs: the cache rows bit for bit (and no
     other row touched), the output within the attention bars of the fp64
-    reference taken on the split path's q."""
+    reference taken on the two-step path's q, and within 2 ulps of the split
+    attention where that is built for the grouping."""
     hd, max_len, eps = 128, K.decode_attention_fused_max_len(), 1e-6
     scale = 1 / math.sqrt(hd)
     g = torch.Generator(device="cuda").manual_seed(7 * nh + nkv)
@@ -168,8 +169,12 @@ def test_decode_attention_fused_matches_split(K, nh, nkv):
         kc1, vc1 = base_k.clone(), base_v.clone()
         q = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
         K.qk_norm_rope_cache(qkv, qn, kn, cos, sin, p, q, kc1, vc1, nh, nkv, eps)
-        split = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
-        K.decode_attention(q, kc1, vc1, p, split, scale)
+        # the split path is built for groups of 1, 2, 4, 5, 8 and 16 query
+        # heads; the fused one for any grouping
+        split = None
+        if nh // nkv in (1, 2, 4, 5, 8, 16):
+            split = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
+            K.decode_attention(q, kc1, vc1, p, split, scale)
         kc2, vc2 = base_k.clone(), base_v.clone()
         fused = torch.empty(nh * hd, dtype=torch.bfloat16, device="cuda")
         K.decode_attention_fused(qkv, qn, kn, cos, sin, p, kc2, vc2, fused, nh, nkv, eps, scale)
@@ -181,7 +186,8 @@ def test_decode_attention_fused_matches_split(K, nh, nkv):
         ulps = ulp_diff(_bits(fused), _bits(ref.float().to(torch.bfloat16))).reshape(nh, hd)
         err = (got - ref).abs().numpy()
         assert not ((ulps > 2) & (err > 1e-5 * float(ref.abs().max()))).any()
-        assert ulp_diff(_bits(fused), _bits(split)).max() <= 2
+        if split is not None:
+            assert ulp_diff(_bits(fused), _bits(split)).max() <= 2
 
 
 @pytest.mark.parametrize("rows,cols", [(10240, 5120), (6144, 4096), (5120, 2560), (77, 5120)])
