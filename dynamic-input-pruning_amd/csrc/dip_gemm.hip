@@ -14,13 +14,18 @@
 // So the weights enter exactly as q * s in fp32 (the reference rounds q * s
 // to bf16 first); the output is rounded to bf16 once.
 //
-// Tiling: a workgroup is 4 waves on 16 * RT weight rows and 16 * TM tokens;
-// the 4 / RT waves of one 16-row tile split the K groups between them (wave
-// ks takes groups ks, ks + KS, ...) and add their partial sums through LDS
-// at the end, in a fixed order.  Nothing else is shared: each lane loads
-// its own 16 bytes of nibbles and 64 bytes of x per group (x is small and
-// stays in L2), weights and scales PW groups ahead and x two groups ahead,
-// so no barrier sits in the main loop.  Inside a 32-column MFMA slice the k
+// Tiling: a wave owns RW tiles of 16 weight rows and 16 * TM tokens, so each
+// x operand it loads feeds RW row tiles (x comes from L2, and with one row
+// tile per wave its re-reads, not the weights, bounded the kernel: the
+// 32-token 25600 x 5120 product took 91 us with RW = 1, 46 us with RW = 4);
+// the 136 * sum(x) term is computed once per x operand.  A workgroup is 4
+// waves on RT such row super-tiles; the 4 / RT waves of one super-tile
+// split the K groups between them (wave ks takes groups ks, ks + KS, ...)
+// and add their partial sums through LDS at the end, in a fixed order.
+// Nothing else is shared: each lane loads its own 16 bytes of nibbles per
+// row tile and 64 bytes of x per group, weights and scales PW groups ahead
+// and x two groups ahead, so no barrier sits in the main loop.  RW is 4 for
+// at least 8192 rows, else 2 (fewer, larger tiles leave CUs idle there).  Inside a 32-column MFMA slice the k
 // order is permuted identically for both operands (lane quarter kb holds
 // columns 32 kb .. 32 kb + 31 and slice j uses its 8 columns 8j .. 8j + 7),
 // so a lane's nibbles are one contiguous 16-byte load.  The offset term
@@ -55,45 +60,54 @@ DIP_DEV bf16x8_t as_bf16x8(const uint4& v) {
   return __builtin_bit_cast(bf16x8_t, u32x4_t{v.x, v.y, v.z, v.w});
 }
 
-template <int TM, int RT, int PW>
+template <int TM, int RT, int PW, int RW>
 __global__ __launch_bounds__(kGemmThreads) void int4_gemm_kernel(
     const int8_t* __restrict__ qw, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ x,
     uint16_t* __restrict__ out, int M, int N, int K) {
   static_assert(PW % 2 == 0, "x ring of 2 inside the weight ring");
-  constexpr int KS = 4 / RT;  // waves per 16-row tile (K split)
-  __shared__ float red[KS > 1 ? 4 : 1][TM][4][64];
+  constexpr int KS = 4 / RT;  // waves per row super-tile (K split)
+  __shared__ float red[KS > 1 ? 4 : 1][RW][TM][4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rt = wave / KS, ks = wave % KS;
-  const int row0 = blockIdx.x * (16 * RT) + rt * 16;
+  // this wave's RW 16-row tiles: rows row0 + 16 u + ...
+  const int row0 = (blockIdx.x * RT + rt) * (16 * RW);
   const int tok0 = blockIdx.y * TM * 16;
   const int ngroups = K >> 7;
   const int ng = ngroups > ks ? (ngroups - ks + KS - 1) / KS : 0;  // this wave's groups
   const int kb = lane >> 4, l16 = lane & 15;
 
-  // A operand: weight row l16, columns 32 kb .. 32 kb + 31 of each group
-  const uint4* wp =
-      reinterpret_cast<const uint4*>(qw + (size_t)min(row0 + l16, N - 1) * (K >> 1)) + kb;
+  // A operand: weight row l16 of tile u, columns 32 kb .. 32 kb + 31 of each group
+  const uint4* wp[RW];
+  // D: token l16, rows 4 kb + r of tile u; their scales
+  const uint16_t* sp[RW][4];
+#pragma unroll
+  for (int u = 0; u < RW; ++u) {
+    wp[u] = reinterpret_cast<const uint4*>(qw + (size_t)min(row0 + 16 * u + l16, N - 1) *
+                                                     (K >> 1)) + kb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sp[u][r] = sc + (size_t)min(row0 + 16 * u + 4 * kb + r, N - 1) * ngroups;
+  }
   // B operand: token l16 of each 16-token tile, the same columns
   const uint4* xp[TM];
 #pragma unroll
   for (int t = 0; t < TM; ++t)
     xp[t] = reinterpret_cast<const uint4*>(x + (size_t)min(tok0 + t * 16 + l16, M - 1) * K) +
             4 * kb;
-  // D: token l16, rows 4 kb + r; their scales
-  const uint16_t* sp[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) sp[r] = sc + (size_t)min(row0 + 4 * kb + r, N - 1) * ngroups;
 
-  uint4 wq[PW];
-  uint32_t sq[PW][4];
+  uint4 wq[PW][RW];
+  uint32_t sq[PW][RW][4];
   uint4 xq[2][TM][4];
 #pragma unroll
   for (int p = 0; p < PW; ++p) {
     if (p < ng) {
       const int g = ks + p * KS;
-      wq[p] = wp[4 * g];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sq[p][r] = sp[r][g];
+      for (int u = 0; u < RW; ++u) {
+        wq[p][u] = wp[u][4 * g];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sq[p][u][r] = sp[u][r][g];
+      }
     }
   }
 #pragma unroll
@@ -109,41 +123,54 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_kernel(
 
   const bf16x8_t c136 = __builtin_bit_cast(
       bf16x8_t, u32x4_t{kOffsetPair, kOffsetPair, kOffsetPair, kOffsetPair});
-  floatx4 acc[TM];
+  floatx4 acc[RW][TM];
 #pragma unroll
-  for (int t = 0; t < TM; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < RW; ++u)
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[u][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   for (int i0 = 0; i0 < ng; i0 += PW) {
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
       const int i = i0 + p;
       if (i < ng) {
-        const bf16x8_t a0 = offset_bf16x8(wq[p].x), a1 = offset_bf16x8(wq[p].y);
-        const bf16x8_t a2 = offset_bf16x8(wq[p].z), a3 = offset_bf16x8(wq[p].w);
-        float s4[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s4[r] = bf16_to_f32(sq[p][r]);
+        // 136 * (sum of the group's x) per token: shared by the RW row tiles
+        floatx4 d1[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-          const bf16x8_t b0 = as_bf16x8(xq[p & 1][t][0]), b1 = as_bf16x8(xq[p & 1][t][1]);
-          const bf16x8_t b2 = as_bf16x8(xq[p & 1][t][2]), b3 = as_bf16x8(xq[p & 1][t][3]);
-          floatx4 d = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, d, 0, 0, 0);
-          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b0, d1, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
-          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b1, d1, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2, d, 0, 0, 0);
-          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b2, d1, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b3, d, 0, 0, 0);
-          d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, b3, d1, 0, 0, 0);
+          d1[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(s4[r], d[r] - d1[r], acc[t][r]);
+          for (int v = 0; v < 4; ++v)
+            d1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(c136, as_bf16x8(xq[p & 1][t][v]),
+                                                            d1[t], 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < RW; ++u) {
+          const bf16x8_t a0 = offset_bf16x8(wq[p][u].x), a1 = offset_bf16x8(wq[p][u].y);
+          const bf16x8_t a2 = offset_bf16x8(wq[p][u].z), a3 = offset_bf16x8(wq[p][u].w);
+          float s4[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s4[r] = bf16_to_f32(sq[p][u][r]);
+#pragma unroll
+          for (int t = 0; t < TM; ++t) {
+            floatx4 d = {0.f, 0.f, 0.f, 0.f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, as_bf16x8(xq[p & 1][t][0]), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, as_bf16x8(xq[p & 1][t][1]), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, as_bf16x8(xq[p & 1][t][2]), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, as_bf16x8(xq[p & 1][t][3]), d, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[u][t][r] = fmaf(s4[r], d[r] - d1[t][r], acc[u][t][r]);
+          }
         }
         if (i + PW < ng) {
           const int g = ks + (i + PW) * KS;
-          wq[p] = wp[4 * g];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sq[p][r] = sp[r][g];
+          for (int u = 0; u < RW; ++u) {
+            wq[p][u] = wp[u][4 * g];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sq[p][u][r] = sp[u][r][g];
+          }
         }
         if (i + 2 < ng) {
           const int g = ks + (i + 2) * KS;
@@ -158,46 +185,67 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_kernel(
 
   if constexpr (KS > 1) {
 #pragma unroll
-    for (int t = 0; t < TM; ++t)
+    for (int u = 0; u < RW; ++u)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][u][t][r][lane] = acc[u][t][r];
     __syncthreads();
     if (ks != 0) return;
 #pragma unroll
     for (int w = 1; w < KS; ++w)
 #pragma unroll
-      for (int t = 0; t < TM; ++t)
+      for (int u = 0; u < RW; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] += red[wave + w][t][r][lane];
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[u][t][r] += red[wave + w][u][t][r][lane];
   }
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
     const int tok = tok0 + t * 16 + l16;
     if (tok >= M) continue;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + 4 * kb + r;
-      if (row < N) out[(size_t)tok * N + row] = (uint16_t)f32_to_bf16(acc[t][r]);
-    }
+    for (int u = 0; u < RW; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 16 * u + 4 * kb + r;
+        if (row < N) out[(size_t)tok * N + row] = (uint16_t)f32_to_bf16(acc[u][t][r]);
+      }
   }
 }
 
-template <int TM, int PW>
+template <int TM, int PW, int RW>
 void launch_gemm(const int8_t* qw, const uint16_t* sc, const uint16_t* x, uint16_t* out, int M,
                  int N, int K, hipStream_t s) {
-  // 16 * RT rows per workgroup: as many rows as keep at least two
-  // workgroups per CU, the rest of the 4 waves splitting K
+  // 16 * RW rows per wave; 16 * RW * RT rows per workgroup: as many rows as
+  // keep at least two workgroups per CU, the rest of the 4 waves splitting K
   const int cus = device_cus();
   const unsigned gy = (unsigned)((M + 16 * TM - 1) / (16 * TM));
-  if ((long long)N >= 64LL * 2 * cus)
-    hipLaunchKernelGGL((int4_gemm_kernel<TM, 4, PW>), dim3((N + 63) / 64, gy), dim3(kGemmThreads),
-                       0, s, qw, sc, x, out, M, N, K);
-  else if ((long long)N >= 32LL * 2 * cus)
-    hipLaunchKernelGGL((int4_gemm_kernel<TM, 2, PW>), dim3((N + 31) / 32, gy), dim3(kGemmThreads),
-                       0, s, qw, sc, x, out, M, N, K);
+  const long long tile = 16LL * RW;
+  if ((long long)N >= tile * 4 * 2 * cus)
+    hipLaunchKernelGGL((int4_gemm_kernel<TM, 4, PW, RW>), dim3((N + tile * 4 - 1) / (tile * 4), gy),
+                       dim3(kGemmThreads), 0, s, qw, sc, x, out, M, N, K);
+  else if ((long long)N >= tile * 2 * 2 * cus)
+    hipLaunchKernelGGL((int4_gemm_kernel<TM, 2, PW, RW>), dim3((N + tile * 2 - 1) / (tile * 2), gy),
+                       dim3(kGemmThreads), 0, s, qw, sc, x, out, M, N, K);
   else
-    hipLaunchKernelGGL((int4_gemm_kernel<TM, 1, PW>), dim3((N + 15) / 16, gy), dim3(kGemmThreads),
-                       0, s, qw, sc, x, out, M, N, K);
+    hipLaunchKernelGGL((int4_gemm_kernel<TM, 1, PW, RW>), dim3((N + tile - 1) / tile, gy),
+                       dim3(kGemmThreads), 0, s, qw, sc, x, out, M, N, K);
+}
+
+// The token tiling for M tokens, RW row tiles per wave; the weight prefetch
+// depth shrinks as RW grows so the wave stays within 256 VGPRs.
+template <int RW>
+void launch_tokens(const int8_t* qw, const uint16_t* sc, const uint16_t* x, uint16_t* out, int M,
+                   int N, int K, hipStream_t s) {
+  constexpr int kPW8 = 8 / RW >= 2 ? 8 / RW : 2, kPW4 = 4 / RW >= 2 ? 4 / RW : 2;
+  if (M <= 16)
+    launch_gemm<1, kPW8, RW>(qw, sc, x, out, M, N, K, s);
+  else if (M <= 32)
+    launch_gemm<2, kPW8, RW>(qw, sc, x, out, M, N, K, s);
+  else
+    launch_gemm<4, kPW4, RW>(qw, sc, x, out, M, N, K, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -391,12 +439,10 @@ extern "C" int dip_int4_gemm(const int8_t* qweight, const uint16_t* scales, cons
   if (!aligned16(qweight) || !aligned16(x)) return DIP_ERR_ALIGN;
   const int M = (int)m, N = (int)out_features, K = (int)in_features;
   hipStream_t s = (hipStream_t)stream;
-  if (M <= 16)
-    launch_gemm<1, 8>(qweight, scales, x, out, M, N, K, s);
-  else if (M <= 32)
-    launch_gemm<2, 8>(qweight, scales, x, out, M, N, K, s);
+  if (N >= 8192)
+    launch_tokens<4>(qweight, scales, x, out, M, N, K, s);
   else
-    launch_gemm<4, 4>(qweight, scales, x, out, M, N, K, s);
+    launch_tokens<2>(qweight, scales, x, out, M, N, K, s);
   return hip_status(hipGetLastError());
 }
 
