@@ -1,0 +1,51 @@
+"""The HIP path on the committed regression fixtures (tests/golden/*.npz):
+top-k indices and quantized bytes bit-exact, the decode step's indices
+bit-exact and y within max|err|/max|ref| <= 1e-2 of the fixture's fp64 y."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import dev, dev_bf16, host_bf16, rel_err
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def K():
+    import _dip_hip
+    return _dip_hip
+
+
+def _load(name):
+    return np.load(GOLDEN / name, allow_pickle=False)
+
+
+def test_topk_on_fixtures(K):
+    z = _load("topk_cases.npz")
+    for name, k in zip(z["names"], z["ks"]):
+        print(f"golden top-k case {name} k={int(k)}", flush=True)
+        idx = K.topk_select(dev_bf16(z[f"g_{name}"]), int(k)).cpu().numpy()
+        assert np.array_equal(idx, z[f"idx_{name}"]), name
+
+
+def test_quantizer_on_fixture(K):
+    z = _load("quant_cases.npz")
+    qw, sc = K.quantize_int4(torch.from_numpy(z["w"]).cuda())
+    assert np.array_equal(qw.cpu().numpy(), z["qweight"])
+    assert np.array_equal(host_bf16(sc), z["scales"])
+    assert np.array_equal(host_bf16(K.dequant_rows(qw, sc, mode=1)), z["dequant"])
+
+
+def test_decode_step_on_fixture(K):
+    z = _load("mlp_small.npz")
+    k = int(z["k"])
+    y, g, idx, h = K.mlp_decode(dev(z["gate_qw"]), dev_bf16(z["gate_sc"]), dev(z["up_qw"]),
+                                dev_bf16(z["up_sc"]), dev(z["down_t_qw"]), dev_bf16(z["down_t_sc"]),
+                                dev_bf16(z["x"]), k)
+    idx = idx.cpu().numpy()
+    if np.array_equal(host_bf16(g), z["g"]):
+        assert np.array_equal(idx, z["idx"])
+    assert rel_err(host_bf16(y), z["y_f64"]) < 1e-2
