@@ -317,7 +317,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
 }
 
 // Norm + rotary + cache write + attention in one launch, for caches of at
-// most kFusedMaxLen rows: workgroup = HPW consecutive query heads of one kv
+// most kFusedMaxLen rows (4 waves up to 128 rows, 16 beyond, which walk the
+// 32-row chunks 16 at a time): workgroup = HPW consecutive query heads of one kv
 // head (group = nh / nkv query heads share it).  Every workgroup of a group
 // normalises and rotates the group's k itself; only the group's first
 // workgroup writes k and v to cache row pos (the others take this token's
@@ -329,22 +330,28 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
 //      LDS, each wave's first 32-row chunk of the cache into registers;
 //   1. RMSNorm + rotary as qk_rope_cache_kernel; q into LDS as bf16, this
 //      token's k and v into LDS (and into cache row pos);
-//   2. wave w takes the chunks w, w + 4, ...: the scores on bf16 MFMA
+//   2. wave w of NW takes the chunks w, w + NW, ...: the scores on bf16 MFMA
 //      (v_mfma_f32_16x16x32_bf16, A = 16 cache rows, B = the q heads, exact
 //      products, fp32 sums; row pos from LDS, not read back), softmax in
 //      fp32, the value sum in fp32 on the VALU, merged into a running (max,
 //      sum, value sum) per query head;
-//   3. the 4 waves' partials are merged through LDS in a fixed order.
-constexpr int kFusedMaxLen = 128;
+//   3. the NW waves' partials are merged through LDS in a fixed order.
+// One launch wins over the split path up to about 900 cache rows (64 query /
+// 8 kv heads: 11.9 against 15.6 us at 512 rows, 18.3 against 17.3 at 1024);
+// beyond, each query head's workgroup re-reading its kv head's rows costs
+// more than the split path's extra launches.
+constexpr int kFusedMaxLen = 1024;
 
-template <int HPW>
-__global__ __launch_bounds__(256) void attn_fused_kernel(
+template <int HPW, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_fused_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_w,
     const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ cos_t,
     const uint16_t* __restrict__ sin_t, const int64_t* __restrict__ pos_p,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, uint16_t* __restrict__ out,
     int nh, int nkv, int max_len, float eps, float scale) {
   static_assert(HPW <= 16, "one MFMA column per query head");
+  static_assert(NW >= 4 && NW <= 16, "waves");
+  constexpr int kThreads = NW * 64;
   const int group = nh / nkv;           // query heads per kv head
   const int h0 = blockIdx.x * HPW;      // this workgroup's first query head
   const bool writer = h0 % group == 0;  // the group's first workgroup writes the cache
@@ -352,10 +359,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   __shared__ __align__(16) uint32_t kv_new[2][64];
   __shared__ uint32_t heads[HPW + 2][64];  // raw q heads | k | v
   __shared__ uint32_t tabs[4][64];         // q_w, k_w, cos row, sin row
-  __shared__ float ps[4][HPW][kAttnChunk];
-  __shared__ float cm[4][HPW], cl[4][HPW];
-  __shared__ float wm[4][HPW], wl[4][HPW];
-  __shared__ float wacc[4][HPW][kHeadDim];
+  __shared__ float ps[NW][HPW][kAttnChunk];
+  __shared__ float cm[NW][HPW], cl[NW][HPW];
+  __shared__ float wm[NW][HPW], wl[NW][HPW];
+  __shared__ float wacc[NW][HPW][kHeadDim];
   const int kvh = h0 / group, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int l16 = l & 15, kb = l >> 4;
   const int64_t pos = *pos_p;
@@ -363,13 +370,13 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   const int64_t last = pos < (int64_t)max_len ? pos : (int64_t)max_len - 1;
 
   // 0. loads
-  for (int i = threadIdx.x; i < (HPW + 2) * 64; i += 256) {
+  for (int i = threadIdx.x; i < (HPW + 2) * 64; i += kThreads) {
     const int hi = i >> 6;
     const int head = hi < HPW ? h0 + hi : (hi == HPW ? nh + kvh : nh + nkv + kvh);
     heads[hi][i & 63] = reinterpret_cast<const uint32_t*>(qkv)[(size_t)head * 64 + (i & 63)];
   }
-  for (int i = threadIdx.x + HPW * 64; i < 16 * 64; i += 256) qb[i >> 6][i & 63] = 0u;
-  {
+  for (int i = threadIdx.x + HPW * 64; i < 16 * 64; i += kThreads) qb[i >> 6][i & 63] = 0u;
+  if (wave < 4) {
     const size_t trow = (size_t)(pos_ok ? pos : 0) * 64 + l;
     const uint32_t* src = wave == 0 ? reinterpret_cast<const uint32_t*>(q_w) + l
                         : wave == 1 ? reinterpret_cast<const uint32_t*>(k_w) + l
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
   __syncthreads();
 
   // 1. RMSNorm + rotary of the q heads and the k head; v and k to the cache
-  for (int hi = wave; hi < HPW + 2; hi += 4) {
+  for (int hi = wave; hi < HPW + 2; hi += NW) {
     const uint32_t pair = heads[hi][l];
     if (hi == HPW + 1) {
       kv_new[1][l] = pair;
@@ -450,7 +457,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     m[g] = -INFINITY;
     lsum[g] = a0[g] = a1[g] = 0.f;
   }
-  for (; (int64_t)start <= last; start += 4 * kAttnChunk) {
+  for (; (int64_t)start <= last; start += NW * kAttnChunk) {
     const int npos = (int)((last - start + 1) < kAttnChunk ? (last - start + 1) : kAttnChunk);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -526,7 +533,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
       m[g] = mn;
     }
     __builtin_amdgcn_wave_barrier();
-    if ((int64_t)(start + 4 * kAttnChunk) <= last) load_chunk(start + 4 * kAttnChunk);
+    if ((int64_t)(start + NW * kAttnChunk) <= last) load_chunk(start + NW * kAttnChunk);
   }
 
   // 3. merge the waves in a fixed order
@@ -540,13 +547,13 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(
     wacc[wave][g][2 * l + 1] = a1[g];
   }
   __syncthreads();
-  for (int g = wave; g < HPW; g += 4) {
+  for (int g = wave; g < HPW; g += NW) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, wm[w][g]);
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, wm[w][g]);
     float den = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float f = wl[w][g] > 0.f ? expf(wm[w][g] - mx) : 0.f;
       den = fmaf(f, wl[w][g], den);
       o0 = fmaf(f, wacc[w][g][2 * l], o0);
@@ -630,9 +637,16 @@ extern "C" int dip_decode_attention_fused(const uint16_t* qkv, const uint16_t* q
     return DIP_ERR_ALIGN;
   const int nh = (int)n_heads, nkv = (int)n_kv_heads, ml = (int)max_len;
   hipStream_t s = (hipStream_t)stream;
-  // one query head per workgroup
-  hipLaunchKernelGGL(attn_fused_kernel<1>, dim3(nh), dim3(256), 0, s, qkv, q_norm_w, k_norm_w,
-                     cos_table, sin_table, pos, k_cache, v_cache, out, nh, nkv, ml, eps, scale);
+  // one query head per workgroup; 16 waves (chunks 16 at a time) for caches
+  // of more than 128 rows
+  if (ml <= 128)
+    hipLaunchKernelGGL((attn_fused_kernel<1, 4>), dim3(nh), dim3(256), 0, s, qkv, q_norm_w,
+                       k_norm_w, cos_table, sin_table, pos, k_cache, v_cache, out, nh, nkv, ml,
+                       eps, scale);
+  else
+    hipLaunchKernelGGL((attn_fused_kernel<1, 16>), dim3(nh), dim3(1024), 0, s, qkv, q_norm_w,
+                       k_norm_w, cos_table, sin_table, pos, k_cache, v_cache, out, nh, nkv, ml,
+                       eps, scale);
   return hip_status(hipGetLastError());
 }
 

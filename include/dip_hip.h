@@ -430,7 +430,7 @@ size_t dip_decode_attention_workspace_size(int64_t n_heads, int64_t head_dim, in
  * dip_decode_attention_fused: dip_qk_norm_rope_cache followed by
  * dip_decode_attention (q_out not kept) in one launch of one workgroup per
  * query head, for caches of at most dip_decode_attention_fused_max_len()
- * rows (128; else DIP_ERR_SHAPE) and any n_heads that n_kv_heads divides.
+ * rows (1024; else DIP_ERR_SHAPE) and any n_heads that n_kv_heads divides.
  * The first workgroup of each kv head's group writes the cache row; every
  * workgroup takes the token's own row from its copy, not read back.  Same
  * cache rows bit for bit; the scores are summed on bf16 MFMA (exact

@@ -133,8 +133,8 @@ def test_argument_rejection_before_launch():
     assert L.dip_decode_attention(p, p, p, p, p, 6, 2, 128, 16, 1.0, p, big, None) == -4
     assert L.dip_decode_attention(p, p, p, p, p, 8, 2, 128, 16, 1.0, p, 16, None) == -5
     assert L.dip_decode_attention(p, p, p, p, p, 8, 2, 96, 16, 1.0, p, big, None) == -4
-    assert L.dip_decode_attention_fused_max_len() == 128
-    assert L.dip_decode_attention_fused(p, p, p, p, p, p, p, p, p, 8, 2, 128, 129, 1e-6, 1.0,
+    assert L.dip_decode_attention_fused_max_len() == 1024
+    assert L.dip_decode_attention_fused(p, p, p, p, p, p, p, p, p, 8, 2, 128, 1025, 1e-6, 1.0,
                                         None) == -2
     assert L.dip_decode_attention_fused(p, p, p, p, p, p, p, p, p, 7, 2, 128, 64, 1e-6, 1.0,
                                         None) == -2

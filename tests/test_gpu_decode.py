@@ -147,14 +147,16 @@ def test_decode_attention(K, nh, nkv):
         assert not ((ulps > 2) & (err > 1e-5 * float(ref.abs().max()))).any()
 
 
+@pytest.mark.parametrize("cap", [128, 1024])
 @pytest.mark.parametrize("nh,nkv", [(4, 4), (4, 2), (24, 8), (32, 8), (40, 8), (64, 8), (64, 4)])
-def test_decode_attention_fused_matches_split(K, nh, nkv):
+def test_decode_attention_fused_matches_split(K, nh, nkv, cap):
     """The one-launch norm + rotary + cache write + attention against the
     two-step path on the same inputs: the cache rows bit for bit (and no
     other row touched), the output within the attention bars of the fp64
     reference taken on the two-step path's q, and within 2 ulps of the split
     attention where that is built for the grouping."""
-    hd, max_len, eps = 128, K.decode_attention_fused_max_len(), 1e-6
+    # cap 128: the 4-wave launch; 1024 (the limit): 16 waves
+    hd, max_len, eps = 128, min(cap, K.decode_attention_fused_max_len()), 1e-6
     scale = 1 / math.sqrt(hd)
     g = torch.Generator(device="cuda").manual_seed(7 * nh + nkv)
     qn = (1 + 0.1 * torch.randn(hd, device="cuda", generator=g)).to(torch.bfloat16)
@@ -162,8 +164,8 @@ def test_decode_attention_fused_matches_split(K, nh, nkv):
     cos, sin = _tables(max_len)
     base_k = torch.randn(nkv, max_len, hd, device="cuda", generator=g).to(torch.bfloat16)
     base_v = torch.randn(nkv, max_len, hd, device="cuda", generator=g).to(torch.bfloat16)
-    for pos in (0, 15, 16, 31, 32, 100, max_len - 1):
-        print(f"decode_attention_fused nh={nh} nkv={nkv} pos={pos}", flush=True)
+    for pos in sorted({0, 15, 16, 31, 32, 100, max_len // 2 + 3, max_len - 1}):
+        print(f"decode_attention_fused nh={nh} nkv={nkv} max_len={max_len} pos={pos}", flush=True)
         qkv = (torch.randn((nh + 2 * nkv) * hd, device="cuda", generator=g) * 2).to(torch.bfloat16)
         p = torch.tensor([pos], device="cuda")
         kc1, vc1 = base_k.clone(), base_v.clone()

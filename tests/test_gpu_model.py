@@ -113,17 +113,20 @@ def test_fused_decode_matches_module_path(ckpt, streaming, keep, bound):
     assert_confident_argmax(got, ref, bound)
 
 
-def test_long_cache_decode_matches_short(ckpt, streaming):
-    """A cache longer than the one-launch attention handles (the split path:
-    norm + rotary + cache write, per-chunk partials, merge) against the
-    one-launch path, teacher-forced on the same tokens."""
+@pytest.mark.parametrize("long_kind", ["split", "one-launch-16-waves"])
+def test_long_cache_decode_matches_short(ckpt, streaming, long_kind):
+    """A longer cache against a 32-row one (the 4-wave one-launch
+    attention), teacher-forced on the same tokens: beyond the one-launch
+    limit (the split path: norm + rotary + cache write, per-chunk partials,
+    merge), and at 300 rows (the 16-wave one-launch attention)."""
     from dip_model import DIPDecoder
     import _dip_hip as K
     model, _, prompt = streaming
-    print(f"long vs short cache decode {ckpt[0]}", flush=True)
+    print(f"long ({long_kind}) vs short cache decode {ckpt[0]}", flush=True)
     short = DIPDecoder(model, 32)
-    long_ = DIPDecoder(model, K.decode_attention_fused_max_len() + 88)
-    assert short._attn_one_launch and not long_._attn_one_launch
+    split = long_kind == "split"
+    long_ = DIPDecoder(model, K.decode_attention_fused_max_len() + 88 if split else 300)
+    assert short._attn_one_launch and long_._attn_one_launch != split
     seq, got = long_.generate(prompt, NEW, return_logits=True)
     ref = teacher_forced_logits(short, seq, PLEN)
     err = max_rel(got, ref)
