@@ -7,8 +7,10 @@
 //   * row block rb: 256 consecutive selected positions j.
 // A block of 256 threads holds 256/LPR "slots" of LPR lanes; slot s walks the
 // LPR rows j = 256*rb + s + i*(256/LPR), i < LPR.  Lane l of a slot fetches
-// the id and h of the slot's l-th row; each row's id and h are shuffled to
-// the slot when it comes up.  The row loop is straight-line code (LPR is a
+// the id, h and the scales of the slot's column groups (one or two) of the
+// slot's l-th row, and turns them into the row's coefficients 16*h*s; each
+// row's id and coefficient are shuffled to the slot when it comes up, so
+// every lane issues one memory instruction per row (its 16-byte chunk).  The row loop is straight-line code (LPR is a
 // compile-time constant; positions past k are clamped and contribute 0), so
 // every load is unconditional and all of a slot's rows are in flight at once.
 // Each lane keeps 32 fp32 accumulators (its outputs).
@@ -41,6 +43,7 @@ constexpr int kRedSplit = 4;             // interleaved row-block splits per out
 
 template <int LPR, int SRC>
 __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
+  static_assert(LPR % kChunksPerGroup == 0 && LPR / kChunksPerGroup <= 2, "groups per slot");
   constexpr int kSlots = kThreads / LPR;
   constexpr int kCols = LPR * kDownAcc;  // outputs per column block
   __shared__ float red[down_red_floats<LPR>()];
@@ -70,15 +73,23 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   const uint32_t h_l = a.h[hix];
   if (a.h_out && cb == 0 && jl < a.k) a.h_out[jl] = (uint16_t)h_l;
 
+  // lane l: the scales of row l for the slot's NG column groups
+  constexpr int NG = LPR / kChunksPerGroup;
+  const int g0 = cb * LPR / kChunksPerGroup;
+  uint32_t s_l[NG];
+  load_down_scales<SRC, NG>(a, rid_l, g0, ngroups, s_l);
+
   DownRow ring[LPR];
 #pragma unroll
   for (int d = 0; d < LPR; ++d)
-    load_down_row<SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ngroups, ring[d]);
+    load_down_row<SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ring[d]);
 
+  float f_l[NG];
+  down_coef<NG>(rid_l, h_l, s_l, f_l);
   float acc[kDownAcc];
 #pragma unroll
   for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
-  down_accumulate<LPR>(ring, rid_l, h_l, gbase, acc);
+  down_accumulate<LPR, NG>(ring, f_l, cc0 / kChunksPerGroup - g0, gbase, acc);
   down_block_partial<LPR, false>(acc, red, a.partial + (size_t)rb * a.out_features +
                                                (size_t)cb * kCols, slot, l);
 }

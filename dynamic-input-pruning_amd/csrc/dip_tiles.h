@@ -274,54 +274,77 @@ DIP_DEV uint32_t down_row(const DownArgs& a, int j) {
 }
 
 struct DownRow {
-  uint4 w;     // the lane's 16-byte chunk of the row
-  uint32_t s;  // bf16 scale of the chunk's group
+  uint4 w;  // the lane's 16-byte chunk of the row
 };
 
-// Unconditional loads of a lane's chunk cc0 and its scale for one row (bad
-// and padding ids read row 0 of the safe matrix).
+// Unconditional load of a lane's chunk cc0 of one row (bad and padding ids
+// read row 0 of the safe matrix).
 template <int SRC>
 DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, int cc0, size_t row_bytes,
-                           int ngroups, DownRow& R) {
+                           DownRow& R) {
   const bool bad = rid >= kPadRow;
   const bool isb = SRC == kDual && !bad && (rid & kSrcB);
   const int8_t* qw = bad ? a.qw_safe : (isb ? a.qw_b : a.qw_a);
-  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
   const uint32_t r = bad ? 0u : (rid & ~kSrcB);
   R.w = ldg_nt(reinterpret_cast<const uint4*>(qw + (size_t)r * row_bytes) + cc0);
-  R.s = sc[(size_t)r * ngroups + cc0 / kChunksPerGroup];
 }
 
-// acc[m] += (q/16)[row, 32*cc0 + m] * 16*h*s over the slot's LPR rows.
+// The NG bf16 scales of groups g0 .. g0 + NG - 1 of row rid (a slot's LPR
+// chunks span NG = LPR / 4 groups).  Issued by the lane that owns the row,
+// once per tile, instead of one scale load per row by every lane.
+template <int SRC, int NG>
+DIP_DEV void load_down_scales(const DownArgs& a, uint32_t rid, int g0, int ngroups,
+                              uint32_t s[NG]) {
+  const bool bad = rid >= kPadRow;
+  const bool isb = SRC == kDual && !bad && (rid & kSrcB);
+  const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
+  const uint32_t r = bad ? 0u : (rid & ~kSrcB);
+#pragma unroll
+  for (int i = 0; i < NG; ++i) s[i] = sc[(size_t)r * ngroups + g0 + i];
+}
+
+// The row's coefficients 16*h*s per group (padding row: 0, bad id: NaN),
+// computed as (h*s)*16 in fp32 (exact: two 8-bit significands).  Integer
+// selects on the bits keep this branch-free.
+template <int NG>
+DIP_DEV void down_coef(uint32_t rid, uint32_t h, const uint32_t s[NG], float f[NG]) {
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    uint32_t fb = __float_as_uint(bf16_to_f32(h) * bf16_to_f32(s[i]) * 16.0f);
+    fb = rid == kPadRow ? 0u : fb;
+    fb = rid == kBadRow ? 0x7FC00000u : fb;
+    f[i] = __uint_as_float(fb);
+  }
+}
+
+// acc[m] += (q/16)[row, 32*cc0 + m] * 16*h*s over the slot's LPR rows; row
+// i's coefficient comes from lane gbase + i (f[hi] for this lane's group).
 // v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for the low
 // nibble of any byte (high nibbles after one shift): one convert and one FMA
-// per weight.  A padding row contributes 0, a bad id NaN.
-template <int LPR>
-DIP_DEV void down_accumulate(const DownRow ring[LPR], uint32_t rid_l, uint32_t h_l, int gbase,
+// per weight.
+template <int LPR, int NG>
+DIP_DEV void down_accumulate(const DownRow ring[LPR], const float f[NG], int hi, int gbase,
                              float acc[kDownAcc]) {
 #pragma unroll
   for (int i = 0; i < LPR; ++i) {
     const DownRow& R = ring[i];
-    const uint32_t rid = __shfl(rid_l, gbase + i, 64);
-    const uint32_t hb = __shfl(h_l, gbase + i, 64);
-    // integer selects on the bits keep this branch-free (a branch here sinks
-    // the scale load into it and costs a full vmcnt(0) wait)
-    uint32_t fb = __float_as_uint(bf16_to_f32(hb) * bf16_to_f32(R.s) * 16.0f);
-    fb = rid == kPadRow ? 0u : fb;
-    fb = rid == kBadRow ? 0x7FC00000u : fb;
-    const float f16 = __uint_as_float(fb);
+    float f16 = __shfl(f[0], gbase + i, 64);
+    if constexpr (NG == 2) {
+      const float f1 = __shfl(f[1], gbase + i, 64);
+      f16 = hi ? f1 : f16;
+    }
     const uint32_t wv[4] = {R.w.x, R.w.y, R.w.z, R.w.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint32_t hi = wv[q] >> 4;
+      const uint32_t hq = wv[q] >> 4;
       acc[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, acc[8 * q + 0]);
-      acc[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hi), f16, acc[8 * q + 1]);
+      acc[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hq), f16, acc[8 * q + 1]);
       acc[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, acc[8 * q + 2]);
-      acc[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hi), f16, acc[8 * q + 3]);
+      acc[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hq), f16, acc[8 * q + 3]);
       acc[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, acc[8 * q + 4]);
-      acc[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hi), f16, acc[8 * q + 5]);
+      acc[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hq), f16, acc[8 * q + 5]);
       acc[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, acc[8 * q + 6]);
-      acc[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hi), f16, acc[8 * q + 7]);
+      acc[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hq), f16, acc[8 * q + 7]);
     }
     // Keep each row's conversions next to their FMAs: left free, the
     // scheduler hoists every row's conversions ahead of the FMAs and needs
