@@ -190,13 +190,16 @@ class DIPStack:
             graphs[name] = g
         return graphs
 
-    def stage_times_ms(self, reps: int = 3):
+    def stage_times_ms(self, reps: int = 3, samples: int = 5):
         """Average duration of one launch of each kernel stage: each stage's
-        graph (one launch per layer, back to back) is replayed between two
-        HIP events on the replaying stream; time / (layers * reps).  The
-        top-k stage (with speculation: the top-k / speculative-up launch)
-        reads the g its gate launch wrote, so its time is that of gate +
-        top-k minus that of the gate alone."""
+        graph (one launch per layer, back to back) is replayed `reps` times
+        between two HIP events on the replaying stream, time / (layers *
+        reps); of `samples` such averages the median is kept, so one
+        disturbed sample does not move the figure.  The top-k stage (with
+        speculation: the top-k / speculative-up launch) reads the g its gate
+        launch wrote, so its time is that of gate + top-k minus that of the
+        gate alone."""
+        import statistics
         self.run_token()
         torch.cuda.synchronize(self.device)
         graphs = self.stage_graphs()
@@ -204,14 +207,17 @@ class DIPStack:
         out = {}
         for name, g in graphs.items():
             g.replay()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(reps):
-                g.replay()
-            e1.record(stream)
-            torch.cuda.synchronize(self.device)
-            out[name] = e0.elapsed_time(e1) / (reps * self.layers)
+            means = []
+            for _ in range(samples):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(stream)
+                torch.cuda.synchronize(self.device)
+                means.append(e0.elapsed_time(e1) / (reps * self.layers))
+            out[name] = statistics.median(means)
         topk = max(out.pop("gate_topk") - out["gate_silu"], 0.0)
         res = {"gate_silu": out["gate_silu"]}
         if self.spec:
