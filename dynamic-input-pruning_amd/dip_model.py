@@ -211,22 +211,26 @@ class DIPDecoder:
       model:     a Qwen3ForCausalLM-shaped model (model.model.layers[i] with
                  self_attn.{q,k,v,o}_proj, q_norm, k_norm, input_layernorm,
                  post_attention_layernorm and mlp); any MLP module works.
-      max_len:   cache length (prompt + generated tokens).
+      max_len:   cache length (prompt + generated tokens).  Up to 1024 rows
+                 the attention runs in one launch per layer, beyond it on
+                 the three-launch split path, so the default covers the
+                 reference's benchmark (a short prompt + 64 tokens) on the
+                 fast path; pass more for longer sequences.
       use_graph: capture the decode step in a HIP graph (needs a GPU and MLP
                  modules that read nothing back to the host per token; a
                  module says it does with `graph_capturable = False`).
       fused:     run the layer's non-MLP steps with this library's decode
-                 kernels (one fused q|k|v GEMV; q/k norm + rotary + cache
-                 write + attention in one launch for caches of up to 128
-                 rows, else three; residual adds fused into the RMSNorms
-                 the input RMSNorm into the q|k|v GEMV and the
-                 post-attention one into the DIP MLP's gate: 7 launches per
-                 layer, 9 for long caches) instead of the HF modules'
-                 PyTorch ops.  None: whenever the model fits them
-                 (GPU, bf16, head_dim 128, int4 attention projections).
+                 kernels instead of the HF modules' PyTorch ops: one fused
+                 q|k|v GEMV with the residual add and the input RMSNorm
+                 folded in; q/k norm + rotary + cache write + attention in
+                 one launch for caches of up to 1024 rows, else three; the
+                 o projection; the post-attention residual add and RMSNorm
+                 folded into the DIP MLP's gate (7 launches per layer, 9 for
+                 long caches).  None: whenever the model fits them (GPU,
+                 bf16, head_dim 128, int4 attention projections).
     """
 
-    def __init__(self, model: nn.Module, max_len: int = 2048, use_graph: bool = True,
+    def __init__(self, model: nn.Module, max_len: int = 1024, use_graph: bool = True,
                  fused=None):
         inner = model.model
         cfg = model.config
