@@ -199,6 +199,39 @@ def test_host_gather_rows_multi_and_pool_reuse():
                                   torch.zeros(1, 40, dtype=torch.bfloat16)])
 
 
+def test_host_gather_pool_under_concurrent_callers():
+    """Several host threads calling the gather at once (ctypes releases the
+    GIL): the persistent pool runs their jobs one after another and every
+    caller gets exactly its own rows."""
+    import threading
+    rng = np.random.default_rng(2)
+    src = torch.from_numpy(rng.integers(-128, 128, size=(500, 640), dtype=np.int8))
+    sc = torch.from_numpy(rng.standard_normal((500, 5)).astype(np.float32)).to(torch.bfloat16)
+    errors = []
+
+    def worker(seed):
+        r = np.random.default_rng(seed)
+        try:
+            for _ in range(40):
+                n = int(r.integers(1, 400))
+                ids = torch.from_numpy(r.integers(0, 500, size=n).astype(np.int32))
+                d0 = torch.empty(n, 640, dtype=torch.int8)
+                d1 = torch.empty(n, 5, dtype=torch.bfloat16)
+                K.host_gather_rows_multi([src, sc], ids, [d0, d1], threads=int(r.integers(1, 9)))
+                if not (torch.equal(d0, src[ids.long()]) and torch.equal(d1, sc[ids.long()])):
+                    errors.append(seed)
+                    return
+        except Exception as e:  # surfaced below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(6)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
 def test_host_stream_rows_rejects_before_any_copy():
     L = K.lib
     p = ctypes.c_void_p(16)
