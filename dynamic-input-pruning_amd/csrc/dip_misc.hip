@@ -233,7 +233,8 @@ extern "C" int dip_dequant_rows(const int8_t* qweight, const uint16_t* scales,
 // first use, lives until the process ends (its workers are detached and its
 // state is never destroyed, so exit does not wait for them), and a worker
 // spins for a while on the job counter before it sleeps.  Jobs from
-// different caller threads run one after another.
+// different caller threads run one after another.  The workers only copy
+// host memory; every HIP call stays on the calling thread.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -265,6 +266,37 @@ class HostPool {
     done_cv_.wait(lk, [&] { return finished_ == njobs_; });
     fn_ = nullptr;
   }
+
+  // The same with the caller taking no job: start() publishes n jobs to n
+  // workers and returns, so the caller can work on their results as they
+  // complete; finish() waits for all of them.  Every start() must be
+  // followed by finish() on the same thread, and *fn must live until
+  // finish() returns (a pointer, so that no temporary std::function can be
+  // bound to it).
+  void start(int n, const std::function<void(int)>* fn) {
+    run_mu_.lock();
+    std::unique_lock<std::mutex> lk(mu_);
+    while ((int)nworkers_ < n && nworkers_ < kMaxWorkers) {
+      const uint64_t g = gen_.load(std::memory_order_relaxed);
+      std::thread([this, g] { worker(g); }).detach();
+      ++nworkers_;
+    }
+    fn_ = fn;
+    njobs_ = n;
+    next_ = 0;
+    finished_ = 0;
+    gen_.fetch_add(1, std::memory_order_release);
+    cv_.notify_all();
+  }
+  void finish() {
+    {
+      std::unique_lock<std::mutex> lk(mu_);
+      done_cv_.wait(lk, [&] { return finished_ == njobs_; });
+      fn_ = nullptr;
+    }
+    run_mu_.unlock();
+  }
+  static constexpr int max_async_jobs() { return (int)kMaxWorkers; }
 
  private:
   static constexpr unsigned kMaxWorkers = 63;
@@ -380,7 +412,7 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
   if (st || n == 0 || npieces == 0) return st;
   const int np = (int)npieces;
   const int64_t nchunks = (n + chunk_rows - 1) / chunk_rows;
-  const int nt = pool_threads(threads, chunk_rows);
+  const int nt = std::min(pool_threads(threads, chunk_rows), HostPool::max_async_jobs());
   hipStream_t s = (hipStream_t)stream;
   std::vector<hipEvent_t> ev;
   if (copy_ms) {
@@ -392,51 +424,52 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
         return hip_status(hipGetLastError());
       }
   }
-  // left[c]: thread slices of chunk c not yet gathered; the thread that
-  // takes it to zero queues the chunk's copies (one at a time, so a chunk's
-  // events bracket only its own copies)
+  // The pool's threads only gather (left[c]: their slices of chunk c not yet
+  // gathered); this thread queues each chunk's copies as soon as it is
+  // complete, so every HIP call stays on the caller's thread.
   std::vector<std::atomic<int>> left(nchunks);
   for (auto& l : left) l.store(nt, std::memory_order_relaxed);
-  std::atomic<int> err{0};
-  std::mutex issue_mu;
-  auto work = [&](int t) {
+  // a named std::function: the workers call it until pool.finish() returns
+  const std::function<void(int)> work = [&](int t) {
     for (int64_t c = 0; c < nchunks; ++c) {
       const int64_t c0 = c * chunk_rows, c1 = std::min(n, c0 + chunk_rows);
       const int64_t per = (c1 - c0 + nt - 1) / nt;
       copy_rows(np, src, pinned, row_bytes, ids, std::min(c1, c0 + t * per),
                 std::min(c1, c0 + (t + 1) * per));
-      if (left[c].fetch_sub(1, std::memory_order_acq_rel) != 1) continue;
-      std::lock_guard<std::mutex> g(issue_mu);
-      hipError_t e = hipSuccess;
-      if (copy_ms) e = hipEventRecord(ev[2 * c], s);
-      for (int p = 0; p < np && e == hipSuccess; ++p) {
-        const int64_t rb = row_bytes[p];
-        if (rb == 0) continue;
-        e = hipMemcpyAsync(static_cast<char*>(dst[p]) + c0 * rb,
-                           static_cast<const char*>(pinned[p]) + c0 * rb,
-                           (size_t)((c1 - c0) * rb), hipMemcpyHostToDevice, s);
-      }
-      if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[2 * c + 1], s);
-      if (e != hipSuccess) err.store((int)e);
+      left[c].fetch_sub(1, std::memory_order_release);
     }
   };
-  if (nt == 1)
-    work(0);
-  else
-    HostPool::get().run(nt, work);
-  st = err.load();
+  hipError_t e = hipSuccess;
+  HostPool& pool = HostPool::get();
+  pool.start(nt, &work);
+  for (int64_t c = 0; c < nchunks; ++c) {
+    while (left[c].load(std::memory_order_acquire) != 0) std::this_thread::yield();
+    if (e != hipSuccess) continue;  // let the gather finish; report the first error
+    const int64_t c0 = c * chunk_rows, c1 = std::min(n, c0 + chunk_rows);
+    if (copy_ms) e = hipEventRecord(ev[2 * c], s);
+    for (int p = 0; p < np && e == hipSuccess; ++p) {
+      const int64_t rb = row_bytes[p];
+      if (rb == 0) continue;
+      e = hipMemcpyAsync(static_cast<char*>(dst[p]) + c0 * rb,
+                         static_cast<const char*>(pinned[p]) + c0 * rb,
+                         (size_t)((c1 - c0) * rb), hipMemcpyHostToDevice, s);
+    }
+    if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[2 * c + 1], s);
+  }
+  pool.finish();
+  st = e == hipSuccess ? DIP_OK : (int)e;
   if (copy_ms) {
     float total = 0.f;
     if (!st) {
       for (int64_t c = 0; c < nchunks && !st; ++c) {
         float ms = 0.f;
-        hipError_t e = hipEventSynchronize(ev[2 * c + 1]);
-        if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[2 * c], ev[2 * c + 1]);
-        if (e != hipSuccess) st = (int)e;
+        hipError_t e2 = hipEventSynchronize(ev[2 * c + 1]);
+        if (e2 == hipSuccess) e2 = hipEventElapsedTime(&ms, ev[2 * c], ev[2 * c + 1]);
+        if (e2 != hipSuccess) st = (int)e2;
         total += ms;
       }
     }
-    for (auto& e : ev) (void)hipEventDestroy(e);
+    for (auto& ev1 : ev) (void)hipEventDestroy(ev1);
     *copy_ms = total;
   }
   return st;

@@ -318,11 +318,12 @@ int dip_host_gather_rows_multi(const void* const* src, void* const* dst,
 /*
  * The cache-aware miss stream (dip_ca.py:146-156: pinned index_select, then
  * non_blocking H2D copies on a side stream) as one pipelined call: the ids
- * are taken in chunks of chunk_rows; for each chunk the host threads gather
- * the rows of every piece into pinned[p] (host, pinned, at least n rows),
- * and the thread that completes the chunk queues its copies
- * pinned[p] -> dst[p] (device, at least n rows) on `stream`, so a chunk's
- * copy runs while the next chunk is gathered.  Returns once every copy is
+ * are taken in chunks of chunk_rows; for each chunk the library's host
+ * threads gather the rows of every piece into pinned[p] (host, pinned, at
+ * least n rows), and the calling thread queues the chunk's copies
+ * pinned[p] -> dst[p] (device, at least n rows) on `stream` as soon as it is
+ * gathered, so a chunk's copy runs while the next chunk is gathered.  Only
+ * the calling thread makes HIP calls.  Returns once every copy is
  * queued (not finished).  When copy_ms is non-NULL, each chunk's copies are
  * bracketed by events, the call waits for them and writes the summed copy
  * time in milliseconds.  Returns DIP_OK, a DIP_ERR_* code or a hipError_t.

@@ -232,6 +232,33 @@ def test_host_gather_pool_under_concurrent_callers():
     assert not errors, errors
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="copies into host stand-ins: CPU only")
+def test_host_stream_rows_gathers_on_the_pool_without_a_device():
+    """The miss stream's gather runs on the pool's threads while the calling
+    thread waits for each chunk and queues its copies; with no device every
+    copy fails, so the call returns HIP's status after the whole gather
+    (staging rows exact, destinations never written).  Repeated calls with
+    chunk sizes that do and do not divide n reuse the pool."""
+    rng = np.random.default_rng(3)
+    rows, n = 3000, 1700
+    srcs = [torch.from_numpy(rng.integers(-128, 128, size=(rows, 2560), dtype=np.int8)),
+            torch.from_numpy(rng.standard_normal((rows, 40)).astype(np.float32)).to(torch.bfloat16)]
+    a = ctypes.addressof
+    arr = lambda ts: (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])  # noqa: E731
+    rb = (ctypes.c_int64 * 2)(2560, 80)
+    for chunk in (500, 1700, 333, 4096):
+        ids = torch.from_numpy(rng.integers(0, rows, size=n).astype(np.int32))
+        pins = [torch.zeros(n, *s.shape[1:], dtype=s.dtype) for s in srcs]
+        dsts = [torch.zeros(n, *s.shape[1:], dtype=s.dtype) for s in srcs]
+        a_s, a_p, a_d = arr(srcs), arr(pins), arr(dsts)
+        st = K.lib.dip_host_stream_rows(a(a_s), a(a_p), a(a_d), a(rb), 2, ids.data_ptr(), n, rows,
+                                        chunk, 8, None, None)
+        assert st > 0, st  # a hipError_t from the first copy
+        for p, s in zip(pins, srcs):
+            assert torch.equal(p, s[ids.long()]), chunk
+        assert all(not d.any() for d in dsts)
+
+
 def test_host_stream_rows_rejects_before_any_copy():
     L = K.lib
     p = ctypes.c_void_p(16)
