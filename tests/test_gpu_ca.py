@@ -104,3 +104,35 @@ def test_ca_module_chunk_size_does_not_change_y(layer):
         buf.stream_chunk = chunk
         ys.append(m(x))
     assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2])
+
+
+@pytest.mark.parametrize("case", ["all_hits", "all_misses"])
+def test_ca_module_all_hits_and_all_misses(layer, case):
+    """The split's extremes: every selected channel resident (no rows
+    streamed) and none resident (every row streamed, no hit GEMV)."""
+    from dip_ca import CABuffers, CADIPMlp
+    L = layer
+    d = torch.device("cuda:0")
+    k = O.keep_count(I, KEEP)
+    x = O.make_x(H, seed=5)
+    g = O.silu_bf16(O.gemv_bf16(L["gate_qw"], L["gate_sc"], x))
+    idx = O.topk_select(g, k)
+    frac = 1.0 if case == "all_hits" else FRAC
+    buf = CABuffers(k, H // 2, H // 128, H, H // 128, d)
+    m = CADIPMlp(dev(L["gate_qw"]), dev_bf16(L["gate_sc"]), dev(L["up_qw"]),
+                 dev_bf16(L["up_sc"]), dev(L["down_t_qw"]), dev_bf16(L["down_t_sc"]), buf,
+                 KEEP, frac, d, down_transposed=True)
+    if case == "all_hits":
+        hot = torch.arange(I)
+    else:  # the first cache_n channels the token does not select
+        unselected = np.setdiff1d(np.arange(I), idx)
+        hot = torch.from_numpy(unselected[: m.cache_n].astype(np.int64))
+    m.set_cache(hot)
+    print(f"CA {case}: cache_n={m.cache_n}", flush=True)
+    y = m(dev_bf16(x).reshape(1, 1, -1))
+    idx_dev = O.topk_select(host_bf16(buf.g(I)), k)
+    id2slot = m.id2slot.cpu().numpy()
+    ref = O.ca_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"], L["down_t_qw"],
+                       L["down_t_sc"], id2slot, x, k, idx=idx_dev)
+    assert buf.last_n_hit == ref["n_hit"] == (k if case == "all_hits" else 0)
+    assert rel_err(host_bf16(y.reshape(-1)), ref["y_f64"]) < 1e-2
