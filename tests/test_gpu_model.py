@@ -239,6 +239,13 @@ def test_cache_aware_model_calibrates_and_decodes(ckpt, streaming):
     print(f"  max_rel {err:.3e}  hits {cas[0].buf.last_n_hit} misses {cas[0].buf.last_n_miss}",
           flush=True)
     assert err < 2e-2
+    # determinism, as the reference checks it (tests/test_ca_determinism.py:
+    # 16-50: two generations, identical output): two greedy generates of the
+    # cache-aware model give the same tokens and bit-identical logits
+    dec = DIPDecoder(ca_model, 32, use_graph=False)
+    s1, l1 = dec.generate(prompt, NEW, return_logits=True)
+    s2, l2 = dec.generate(prompt, NEW, return_logits=True)
+    assert torch.equal(s1, s2) and torch.equal(l1, l2)
 
 
 @pytest.mark.parametrize("cols", [256, 512, 1024, 2048, 2560, 4096, 5120, 8192])
