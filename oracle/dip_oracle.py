@@ -16,9 +16,11 @@ calls exactly that op on the CPU, and ``silu_bf16_np`` restates it in numpy
 so the two can pin each other.
 
 Every function cites the reference file:line it follows.  Parity pinning:
-every function is checked in tests/test_oracle.py against known-answer
-vectors, closed forms, invariants or brute force (see the test docstrings);
-none is left unpinned.
+every public function is checked in tests/test_oracle.py against
+known-answer vectors, closed forms, invariants, brute force or an
+independent second route (the PyTorch restatement of qlinear.py against the
+numpy one, the C top-k against the numpy top-k); the test docstrings say
+which.  No function is left parity unpinned.
 """
 from __future__ import annotations
 
@@ -279,11 +281,41 @@ def dip_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x_bits, k,
 
 
 def dense_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x_bits):
-    """StreamingDIPMlp._dense for one token (dip_stream_predispatch.py:206-215):
-    g = silu(gate(x)), u = bf16(x @ up^T), h = bf16(g*u), y = bf16(h @ down_t)."""
+    """The DIP computation over every channel in channel order: dip_forward
+    with k = I and idx = 0..I-1, i.e. the kernels' exact fp32 q*s weights for
+    up and down.  This is NOT the reference's keep >= 0.999 route, which
+    multiplies by bf16-rounded weights (dense_literal_forward)."""
     inter = np.asarray(up_qw).shape[0]
     return dip_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x_bits,
                        inter, idx=np.arange(inter, dtype=np.int32))
+
+
+def dense_literal_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x_bits):
+    """StreamingDIPMlp._dense for one decode token, literally
+    (dip_stream_predispatch.py:177-179 route keep >= 0.999 here; :206-215):
+
+      g    = silu(_gate(x))            _gate takes the int4 GEMV kernel for a
+                                       decode token (:166-171): exact q*s
+      up_w = dequantize(up)            bf16(q*s) (qlinear.py:53-64)
+      u    = bf16(F.linear(x, up_w))   fp32 sum of x * bf16(q*s)
+      h    = bf16(g * u)
+      dn_t = dequantize(down_t)        bf16(q*s)
+      y    = bf16(h @ dn_t)            fp32 sum of h * bf16(q*s)
+
+    Sums are taken in float64 (the library GEMMs' fp32 summation order is
+    not part of the contract).  Returns the dict of dip_forward (idx = all
+    channels)."""
+    inter = np.asarray(up_qw).shape[0]
+    pre = gemv_bf16(gate_qw, gate_sc, x_bits)
+    g = silu_bf16(pre)
+    xf = bf16_to_f32(x_bits).astype(np.float64)
+    up_w = bf16_to_f32(dequantize(up_qw, up_sc)).astype(np.float64)
+    u = f32_to_bf16((up_w @ xf).astype(np.float32))
+    h = h_bf16(g, u)
+    dn_w = bf16_to_f32(dequantize(down_t_qw, down_t_sc)).astype(np.float64)
+    y64 = bf16_to_f32(h).astype(np.float64) @ dn_w
+    return dict(pre=pre, g=g, idx=np.arange(inter, dtype=np.int32), u=u, h=h, y_f64=y64,
+                y=f32_to_bf16(y64.astype(np.float32)))
 
 
 def ca_split(idx: np.ndarray, id2slot: np.ndarray):
@@ -392,8 +424,16 @@ def torch_dequantize(qweight, scales):
     return (qf * s).reshape(out_f, in_f).to(torch.bfloat16)
 
 
-def torch_cpu_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k):
-    """One DIP decode step on host torch tensors (bf16 x [H]); returns y bf16."""
+def torch_cpu_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k,
+                      return_all=False):
+    """One DIP decode step on host torch tensors (bf16 x [H]); returns y bf16
+    [1, H], or with return_all the dict (g, idx, u, h, y) of torch tensors.
+
+    The gate runs through dequantize + F.linear as QuantLinear.forward does
+    (qlinear.py:86-88), so its weights are bf16(q*s) where the reference's
+    decode gate kernel uses the exact q*s (int4_gemv.cu:71-72); g may
+    therefore differ from the kernel route's by a rounding, and the top-k is
+    taken on this route's own g."""
     import torch
     import torch.nn.functional as F
     xb = x.reshape(1, -1)
@@ -405,4 +445,7 @@ def torch_cpu_forward(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k
     h = (g[idx] * u).to(torch.bfloat16)
     dn = torch_dequantize(torch.index_select(down_t_qw, 0, idx),
                           torch.index_select(down_t_sc, 0, idx))
-    return h.reshape(1, -1) @ dn
+    y = h.reshape(1, -1) @ dn
+    if return_all:
+        return dict(g=g, idx=idx, u=u, h=h, y=y.reshape(-1))
+    return y

@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import dev, dev_bf16, host_bf16, rel_err
+import dip_oracle as O
+from gpu_util import dev, dev_bf16, host_bf16, rel_err, ulp_diff
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -46,6 +47,12 @@ def test_decode_step_on_fixture(K):
                                 dev_bf16(z["up_sc"]), dev(z["down_t_qw"]), dev_bf16(z["down_t_sc"]),
                                 dev_bf16(z["x"]), k)
     idx = idx.cpu().numpy()
-    if np.array_equal(host_bf16(g), z["g"]):
+    g_h = host_bf16(g)
+    # g may move by an ulp with the fp32 summation order; the top-k is then
+    # checked on the device's own g, so the index check never disappears
+    assert ulp_diff(g_h, z["g"]).max() <= 2
+    if np.array_equal(g_h, z["g"]):
         assert np.array_equal(idx, z["idx"])
+    else:
+        assert np.array_equal(idx, O.topk_select(g_h, k))
     assert rel_err(host_bf16(y), z["y_f64"]) < 1e-2

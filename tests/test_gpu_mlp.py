@@ -95,6 +95,15 @@ def test_module_streaming_dip(K, config0_layer):
         assert y.shape == (1, 1, 5120) and y.dtype == torch.bfloat16
         y_h = host_bf16(y.reshape(-1))
         if keep >= 0.999:
+            # the reference routes keep >= 0.999 to _dense, whose up and down
+            # weights are bf16(q*s) (dip_stream_predispatch.py:177-179,
+            # 206-215): the bar is against that literal route; the all-channel
+            # DIP route on exact q*s is checked as well
+            lit = O.dense_literal_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"],
+                                          L["down_t_qw"], L["down_t_sc"], x)
+            err_lit = rel_err(y_h, lit["y_f64"])
+            print(f"keep 1.0 vs the _dense literal: rel err {err_lit:.2e}", flush=True)
+            assert err_lit < 1e-2
             ref = O.dense_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"],
                                   L["down_t_qw"], L["down_t_sc"], x)
         else:

@@ -406,3 +406,173 @@ def test_dip_forward_tiny_against_loops():
     np.testing.assert_allclose(out["y_f64"], y, rtol=1e-9, atol=1e-12)
     pre = O.f32_to_bf16((wg @ xf).astype(np.float32))
     assert np.array_equal(out["pre"], pre)
+
+
+# ---------------------------------------------------------------------------
+# The PyTorch restatement (cpu_baseline of bench.py) against the numpy one
+# ---------------------------------------------------------------------------
+
+
+def _t(a):
+    """numpy int8 / uint16-bf16 bits -> torch CPU tensor (int8 / bfloat16)."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    return torch.from_numpy(a)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_torch_unpack_and_dequantize_bit_identical():
+    """torch_unpack_int4 / torch_dequantize (qlinear.py:28-64 in torch ops)
+    equal the numpy unpack_int4 / dequantize on all 256 bytes, under random
+    scales and the tie scale 0x3F81 (q = 3 gives 3.0234375, a bf16 tie that
+    rounds to even), and on the known-answer bytes."""
+    b = np.tile(np.arange(256, dtype=np.uint8), 3).reshape(6, 128).view(np.int8)
+    assert np.array_equal(O.torch_unpack_int4(_t(b)).numpy(), O.unpack_int4(b))
+    rng = np.random.default_rng(7)
+    sc = O.f32_to_bf16(rng.random((6, 2), dtype=np.float32) * 0.05 + 1e-4)
+    sc[0, :] = 0x3F81
+    sc[1, 0] = 0x0000
+    got = _bits(O.torch_dequantize(_t(b), _t(sc)))
+    assert np.array_equal(got, O.dequantize(b, sc))
+    kb = np.array([[0x8F, 0x7F, 0x08] + [0] * 61], dtype=np.uint8).view(np.int8)
+    assert O.torch_unpack_int4(_t(kb)).numpy()[0, :6].tolist() == [-1, -8, -1, 7, -8, 0]
+    tie = O.pack_int4(np.array([[3] * 128], dtype=np.int8))
+    t_out = O.bf16_to_f32(_bits(O.torch_dequantize(_t(tie), _t(np.array([[0x3F81]], np.uint16)))))
+    assert np.all(t_out == np.float32(3.03125))
+
+
+def test_torch_cpu_forward_matches_the_numpy_route():
+    """torch_cpu_forward (the timed cpu_baseline) computes the reference's
+    forward: its idx is topk_select of its own g, its g is bf16(silu(bf16 of
+    the bf16(q*s) GEMV)) within one bf16 ulp of a float64 evaluation, and its
+    y is within 1e-2 of dip_forward's on that idx."""
+    H, I = 256, 768
+    k = O.keep_count(I, 0.6)
+    L = O.make_layer(H, I, seed=11)
+    x = O.make_x(H, seed=12)
+    out = O.torch_cpu_forward(_t(L["gate_qw"]), _t(L["gate_sc"]), _t(L["up_qw"]), _t(L["up_sc"]),
+                              _t(L["down_t_qw"]), _t(L["down_t_sc"]), _t(x), k, return_all=True)
+    g = _bits(out["g"])
+    idx = out["idx"].numpy()
+    assert np.array_equal(idx, O.topk_select(g, k))
+    wg = O.bf16_to_f32(O.dequantize(L["gate_qw"], L["gate_sc"])).astype(np.float64)
+    pre = O.f32_to_bf16((wg @ O.bf16_to_f32(x).astype(np.float64)).astype(np.float32))
+    g_ref = O.silu_bf16(pre)
+    d = np.abs(g.astype(np.int32) - g_ref.astype(np.int32))
+    assert d.max() <= 1 and np.count_nonzero(d) <= I // 50
+    ref = O.dip_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"], L["down_t_qw"],
+                        L["down_t_sc"], x, k, idx=idx)
+    y = O.bf16_to_f32(_bits(out["y"])).astype(np.float64)
+    assert np.abs(y - ref["y_f64"]).max() / np.abs(ref["y_f64"]).max() < 1e-2
+    # a planted slip (h without g) is caught by the same bar
+    slip = O.down_f64(L["down_t_qw"], L["down_t_sc"], ref["u"], rows=idx)
+    assert np.abs(y - slip).max() / np.abs(ref["y_f64"]).max() > 1e-2
+
+
+# ---------------------------------------------------------------------------
+# ca_forward and the two dense routes
+# ---------------------------------------------------------------------------
+
+
+def test_ca_forward_equals_dip_forward_per_channel():
+    """ca_forward (dip_ca.py:127-188) reorders the selection into [hits,
+    misses] but computes the same h per channel and the same y: h of every
+    channel equals dip_forward's for that channel, the split covers idx
+    exactly once, and y_f64 agrees to float64 rounding (a different sum
+    order)."""
+    H, I = 256, 512
+    k = O.keep_count(I, 0.6)
+    L = O.make_layer(H, I, seed=5)
+    x = O.make_x(H, seed=6)
+    rng = np.random.default_rng(8)
+    hot = np.sort(rng.choice(I, size=150, replace=False))
+    id2slot = np.full(I, -1, dtype=np.int64)
+    id2slot[hot] = np.arange(hot.size)
+    ca = O.ca_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"], L["down_t_qw"],
+                      L["down_t_sc"], id2slot, x, k)
+    dip = O.dip_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"], L["down_t_qw"],
+                        L["down_t_sc"], x, k, idx=ca["idx"])
+    assert sorted(ca["combined"].tolist()) == sorted(ca["idx"].tolist())
+    assert 0 < ca["n_hit"] < k
+    h_by_ch = dict(zip(dip["idx"].tolist(), dip["h"].tolist()))
+    assert [h_by_ch[c] for c in ca["combined"].tolist()] == ca["h"].tolist()
+    np.testing.assert_allclose(ca["y_f64"], dip["y_f64"], rtol=1e-12, atol=1e-15)
+    assert np.array_equal(ca["g"], dip["g"])
+
+
+def test_dense_literal_uses_bf16_weights():
+    """dense_literal_forward (_dense, dip_stream_predispatch.py:206-215)
+    multiplies by bf16(q*s): with the tie scale 0x3F81 and q = 3 on one
+    weight of up and of down_t, a one-hot x and one channel, u and y take the
+    rounded weight 3.03125 where the kernels' route takes 3.0234375."""
+    H, I = 128, 1
+    one_q = np.zeros((I, H), dtype=np.int8)
+    one_q[0, 0] = 3
+    w3 = O.pack_int4(one_q)
+    sc = np.array([[0x3F81]], dtype=np.uint16)
+    g_q = np.zeros((I, H), dtype=np.int8)
+    g_q[0, 0] = 4                      # pre = 4 * 1.0 * x0
+    gate_sc = np.array([[0x3F80]], dtype=np.uint16)
+    x = np.zeros(H, dtype=np.uint16)
+    x[0] = 0x3F80                      # x0 = 1
+    lit = O.dense_literal_forward(O.pack_int4(g_q), gate_sc, w3, sc, w3, sc, x)
+    dense = O.dense_forward(O.pack_int4(g_q), gate_sc, w3, sc, w3, sc, x)
+    assert O.bf16_to_f32(lit["u"])[0] == np.float32(3.03125)
+    assert O.bf16_to_f32(dense["u"])[0] == np.float32(3.03125)  # bf16(3.0234375) is the tie too
+    h = O.bf16_to_f32(lit["h"])[0]
+    assert lit["y_f64"][0] == float(h) * 3.03125
+    assert dense["y_f64"][0] == float(O.bf16_to_f32(dense["h"])[0]) * 3.0234375
+    assert np.all(lit["y_f64"][1:] == 0)
+
+
+def test_dense_literal_equals_dense_on_exact_grids():
+    """With power-of-two scales every q*s is a bf16 value, so bf16(q*s) =
+    q*s and the literal route equals the all-channel DIP route bit for bit;
+    with ordinary scales they differ (the rounding is real) but agree to
+    well within 1e-2."""
+    H, I = 256, 384
+    rng = np.random.default_rng(9)
+    mats = []
+    for _ in range(3):
+        q = rng.integers(-8, 8, size=(I, H)).astype(np.int8)
+        e = rng.integers(-9, -5, size=(I, H // 128))
+        sc = O.f32_to_bf16(np.ldexp(np.float32(1.0), e).astype(np.float32))
+        mats.append((O.pack_int4(q), sc))
+    x = O.make_x(H, seed=10)
+    (gq, gs), (uq, us), (dq, ds) = mats
+    lit = O.dense_literal_forward(gq, gs, uq, us, dq, ds, x)
+    den = O.dense_forward(gq, gs, uq, us, dq, ds, x)
+    assert np.array_equal(lit["u"], den["u"]) and np.array_equal(lit["h"], den["h"])
+    assert np.array_equal(lit["y_f64"], den["y_f64"])
+    L = O.make_layer(H, I, seed=13)
+    lit = O.dense_literal_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"],
+                                  L["down_t_qw"], L["down_t_sc"], x)
+    den = O.dense_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"],
+                          L["down_t_qw"], L["down_t_sc"], x)
+    assert not np.array_equal(lit["y_f64"], den["y_f64"])
+    assert np.abs(lit["y_f64"] - den["y_f64"]).max() / np.abs(lit["y_f64"]).max() < 1e-2
+
+
+def test_dense_literal_matches_torch_dense_route():
+    """The reference's own ops for _dense on the CPU (dequantize + F.linear
+    in bf16, g * u, h @ dequantize(down_t)) agree with dense_literal_forward:
+    u within one bf16 ulp, y within 1e-2."""
+    import torch.nn.functional as F
+    H, I = 256, 512
+    L = O.make_layer(H, I, seed=14)
+    x = O.make_x(H, seed=15)
+    lit = O.dense_literal_forward(L["gate_qw"], L["gate_sc"], L["up_qw"], L["up_sc"],
+                                  L["down_t_qw"], L["down_t_sc"], x)
+    xb = _t(x).reshape(1, -1)
+    g = _t(lit["g"]).reshape(1, -1)
+    u = F.linear(xb, O.torch_dequantize(_t(L["up_qw"]), _t(L["up_sc"])))
+    h = g * u
+    y = h @ O.torch_dequantize(_t(L["down_t_qw"]), _t(L["down_t_sc"]))
+    du = np.abs(_bits(u).reshape(-1).astype(np.int32) - lit["u"].astype(np.int32))
+    assert du.max() <= 1
+    yt = O.bf16_to_f32(_bits(y).reshape(-1)).astype(np.float64)
+    assert np.abs(yt - lit["y_f64"]).max() / np.abs(lit["y_f64"]).max() < 1e-2
