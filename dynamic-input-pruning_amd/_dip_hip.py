@@ -49,8 +49,8 @@ _SIGS = {
     "dip_up_gather_h": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p], _i32),
     "dip_gather_down_workspace_size": ([_i64, _i64], _sz),
     "dip_int4_gather_down": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p], _i32),
-    "dip_ca_fused_gemv": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p],
-                          _i32),
+    "dip_ca_fused_gemv": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64,
+                           _p], _i32),
     "dip_ca_down": ([_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p], _i32),
     "dip_ca_assemble": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_dequant_rows": ([_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p], _i32),
@@ -383,9 +383,10 @@ def ca_fused_gemv(res_qw, res_sc, str_qw, str_sc, x, src, row, g=None, gid=None,
         gid = _indices(gid, "gid")
     if out is None:
         out = torch.empty(k, dtype=torch.bfloat16, device=dev)
+    g_len = g.numel() if g is not None else 0
     _check(lib.dip_ca_fused_gemv(_ptr(res_qw), _ptr(res_sc), _ptr(str_qw), _ptr(str_sc),
-                                 _ptr(x), _ptr(src), _ptr(row), _ptr(g), _ptr(gid), _ptr(out),
-                                 res_rows, str_rows, cols, k, _stream(dev)),
+                                 _ptr(x), _ptr(src), _ptr(row), _ptr(g), _ptr(gid), g_len,
+                                 _ptr(out), res_rows, str_rows, cols, k, _stream(dev)),
            "dip_ca_fused_gemv")
     return out
 

@@ -33,6 +33,7 @@ struct RowdotArgs {
   const int32_t* sel2;
   const int32_t* gid;
   const uint16_t* g;
+  int g_len;   // kH with kDual: channel ids gid[j] outside [0, g_len) yield NaN
   uint16_t* out;
   const int8_t* qw_safe;   // a matrix with at least one row: read in place of bad rows
   const uint16_t* sc_safe;

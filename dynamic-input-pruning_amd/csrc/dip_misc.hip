@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "dip_common.h"
+#include "dip_host_pool.h"
 #include "dip_internal.h"
 
 namespace dip {
@@ -226,117 +227,10 @@ extern "C" int dip_dequant_rows(const int8_t* qweight, const uint16_t* scales,
 }
 
 // ---------------------------------------------------------------------------
-// Host-side miss gather (the pinned index_select of dip_ca.py:148-153) on a
-// persistent pool of host threads.  The cache-aware module gathers once per
-// layer and token, and creating threads (or waking them through the kernel)
-// per call costs about as much as a chunk's copy, so the pool is created on
-// first use, lives until the process ends (its workers are detached and its
-// state is never destroyed, so exit does not wait for them), and a worker
-// spins for a while on the job counter before it sleeps.  Jobs from
-// different caller threads run one after another.  The workers only copy
-// host memory; every HIP call stays on the calling thread.
+// Host-side miss gather (the pinned index_select of dip_ca.py:148-153) on the
+// persistent host thread pool of dip_host_pool.h.
 // ---------------------------------------------------------------------------
 namespace {
-
-class HostPool {
- public:
-  static HostPool& get() {
-    static HostPool* pool = new HostPool();  // never destroyed: workers may still wait on it
-    return *pool;
-  }
-
-  // Run fn(t) for every t in [0, n) on the caller and up to n - 1 workers;
-  // returns when all n calls have returned.
-  void run(int n, const std::function<void(int)>& fn) {
-    std::lock_guard<std::mutex> one_job(run_mu_);
-    std::unique_lock<std::mutex> lk(mu_);
-    while ((int)nworkers_ < n - 1 && nworkers_ < kMaxWorkers) {
-      // a new worker takes part from the job about to be published on
-      const uint64_t g = gen_.load(std::memory_order_relaxed);
-      std::thread([this, g] { worker(g); }).detach();
-      ++nworkers_;
-    }
-    fn_ = &fn;
-    njobs_ = n;
-    next_ = 0;
-    finished_ = 0;
-    gen_.fetch_add(1, std::memory_order_release);
-    cv_.notify_all();
-    claim(lk);
-    done_cv_.wait(lk, [&] { return finished_ == njobs_; });
-    fn_ = nullptr;
-  }
-
-  // The same with the caller taking no job: start() publishes n jobs to n
-  // workers and returns, so the caller can work on their results as they
-  // complete; finish() waits for all of them.  Every start() must be
-  // followed by finish() on the same thread, and *fn must live until
-  // finish() returns (a pointer, so that no temporary std::function can be
-  // bound to it).
-  void start(int n, const std::function<void(int)>* fn) {
-    run_mu_.lock();
-    std::unique_lock<std::mutex> lk(mu_);
-    while ((int)nworkers_ < n && nworkers_ < kMaxWorkers) {
-      const uint64_t g = gen_.load(std::memory_order_relaxed);
-      std::thread([this, g] { worker(g); }).detach();
-      ++nworkers_;
-    }
-    fn_ = fn;
-    njobs_ = n;
-    next_ = 0;
-    finished_ = 0;
-    gen_.fetch_add(1, std::memory_order_release);
-    cv_.notify_all();
-  }
-  void finish() {
-    {
-      std::unique_lock<std::mutex> lk(mu_);
-      done_cv_.wait(lk, [&] { return finished_ == njobs_; });
-      fn_ = nullptr;
-    }
-    run_mu_.unlock();
-  }
-  static constexpr int max_async_jobs() { return (int)kMaxWorkers; }
-
- private:
-  static constexpr unsigned kMaxWorkers = 63;
-  static constexpr auto kSpin = std::chrono::microseconds(2000);
-
-  // Take job indices until none is left (mu_ held on entry and exit; the
-  // job's fields only change under mu_, so an index always belongs to the
-  // fn_ read with it).
-  void claim(std::unique_lock<std::mutex>& lk) {
-    while (next_ < njobs_) {
-      const int t = next_++;
-      const std::function<void(int)>* f = fn_;
-      lk.unlock();
-      (*f)(t);
-      lk.lock();
-      if (++finished_ == njobs_) done_cv_.notify_all();
-    }
-  }
-
-  void worker(uint64_t seen) {
-    for (;;) {
-      // spin (yielding) for the next job, then sleep on the condition
-      const auto t0 = std::chrono::steady_clock::now();
-      while (gen_.load(std::memory_order_acquire) == seen &&
-             std::chrono::steady_clock::now() - t0 < kSpin)
-        std::this_thread::yield();
-      std::unique_lock<std::mutex> lk(mu_);
-      cv_.wait(lk, [&] { return gen_.load(std::memory_order_relaxed) != seen; });
-      seen = gen_.load(std::memory_order_relaxed);
-      claim(lk);
-    }
-  }
-
-  std::mutex run_mu_, mu_;
-  std::condition_variable cv_, done_cv_;
-  std::atomic<uint64_t> gen_{0};
-  const std::function<void(int)>* fn_ = nullptr;
-  int njobs_ = 0, next_ = 0, finished_ = 0;
-  unsigned nworkers_ = 0;
-};
 
 int check_pieces(int npieces, const void* const* src, void* const* dst, const int64_t* row_bytes,
                  const int32_t* ids, int64_t n, int64_t src_rows) {

@@ -115,8 +115,12 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
         const float f = bf16_to_f32(v);
         v = f32_to_bf16(f / (1.0f + expf(-f)));
       } else if (EPI == kH) {
+        // a gathered row id is already range-checked against g (rows = channels)
         const int ch = (SRC == kGather) ? (int)rid_lane : a.gid[(int)jl];
-        v = f32_to_bf16(bf16_to_f32(a.g[ch]) * bf16_to_f32(v));
+        if (SRC != kGather && (unsigned)ch >= (unsigned)a.g_len)
+          v = 0x7FC0u;
+        else
+          v = f32_to_bf16(bf16_to_f32(a.g[ch]) * bf16_to_f32(v));
       }
     }
     a.out[(int)jl] = (uint16_t)v;
@@ -429,9 +433,9 @@ extern "C" int dip_up_gather_h(const int8_t* qweight, const uint16_t* scales, co
 extern "C" int dip_ca_fused_gemv(const int8_t* res_qw, const uint16_t* res_sc,
                                  const int8_t* str_qw, const uint16_t* str_sc, const uint16_t* x,
                                  const int32_t* src, const int32_t* row, const uint16_t* g,
-                                 const int32_t* gid, uint16_t* out, int64_t res_rows,
-                                 int64_t str_rows, int64_t in_features, int64_t k,
-                                 void* stream) {
+                                 const int32_t* gid, int64_t g_len, uint16_t* out,
+                                 int64_t res_rows, int64_t str_rows, int64_t in_features,
+                                 int64_t k, void* stream) {
   int st = check_matrix(res_qw, res_sc, res_rows, in_features);
   if (st) return st;
   st = check_matrix(str_qw, str_sc, str_rows, in_features);
@@ -440,6 +444,7 @@ extern "C" int dip_ca_fused_gemv(const int8_t* res_qw, const uint16_t* res_sc,
   if (k == 0) return DIP_OK;
   if (!x || !out || !src || !row) return DIP_ERR_NULL;
   if (g && !gid) return DIP_ERR_NULL;
+  if (g && (g_len <= 0 || g_len > INT32_MAX)) return DIP_ERR_SHAPE;
   if (!aligned16(x)) return DIP_ERR_ALIGN;
   if (res_rows == 0 && str_rows == 0) return DIP_ERR_SHAPE;
   RowdotArgs a = base_args(res_qw, res_sc, x, out, k, in_features);
@@ -453,6 +458,7 @@ extern "C" int dip_ca_fused_gemv(const int8_t* res_qw, const uint16_t* res_sc,
   a.sel2 = row;
   a.g = g;
   a.gid = gid;
+  a.g_len = g ? (int)g_len : 0;
   a.rows_a = (int)res_rows;
   a.rows_b = (int)str_rows;
   return launch_rowdot(kDual, g ? kH : kRaw, a, (hipStream_t)stream);

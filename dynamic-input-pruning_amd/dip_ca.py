@@ -154,8 +154,10 @@ class CADIPMlp(nn.Module):
         while the next chunk is gathered."""
         b = self.buf
         pins = (b.pin_up_qw, b.pin_up_sc, b.pin_dn_qw, b.pin_dn_sc)
-        # the staging rows are free once the previous layer's reads are done
-        b.copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+        # No wait on the compute stream: _decode_one synchronised it on the
+        # host before the read-back, so the previous layer's reads of the
+        # staging rows are done, and the hits' GEMV queued since reads only
+        # resident rows.  The copies therefore overlap that GEMV.
         timing = b.transfers is not None
         t0 = time.perf_counter()
         ms = K.host_stream_rows((self.up_qw, self.up_sc, self.down_t_qw, self.down_t_sc),

@@ -159,12 +159,14 @@ int dip_get_tuning(int knob);
  * (src[j] == 0, row res[row[j]]) or the streamed staging buffer
  * (src[j] != 0, row str[row[j]]).  Replaces ca_fused_ops::ca_fused_gemv
  * (kernels/ca_fused/ca_fused_gemv.cu:87-112).  If g != NULL the output is
- * h[j] = bf16(g[gid[j]] * bf16(dot)) instead (dip_ca.py:185-186).
+ * h[j] = bf16(g[gid[j]] * bf16(dot)) instead (dip_ca.py:185-186); g holds
+ * g_len values, and a channel id gid[j] outside [0, g_len) makes h[j] NaN
+ * (0x7FC0) like an out-of-range row id, instead of a read past g.
  */
 int dip_ca_fused_gemv(const int8_t* res_qw, const uint16_t* res_sc, const int8_t* str_qw,
                       const uint16_t* str_sc, const uint16_t* x, const int32_t* src,
                       const int32_t* row, const uint16_t* g, const int32_t* gid,
-                      uint16_t* out, int64_t res_rows, int64_t str_rows,
+                      int64_t g_len, uint16_t* out, int64_t res_rows, int64_t str_rows,
                       int64_t in_features, int64_t k, void* stream);
 
 /*

@@ -326,3 +326,12 @@ def test_bad_row_ids_poison_instead_of_faulting(K):
     out = host_bf16(K.int4_gather_gemv(dev(qw), dev_bf16(sc), dev_bf16(x), dev(idx)))
     assert out[1] == 0x7FC0 and out[3] == 0x7FC0
     assert out[0] != 0x7FC0 and out[2] != 0x7FC0
+    # cache-aware fused h: channel ids outside g poison h instead of reading past g
+    g = random_bf16(rng, 40)
+    src = np.zeros(4, np.int32)
+    row = np.array([1, 2, 3, 4], np.int32)
+    gid = np.array([0, 40, 39, -5], np.int32)   # 40 and -5 are outside g
+    h = host_bf16(K.ca_fused_gemv(dev(qw), dev_bf16(sc), dev(qw), dev_bf16(sc), dev_bf16(x),
+                                  dev(src), dev(row), g=dev_bf16(g), gid=dev(gid)))
+    assert h[1] == 0x7FC0 and h[3] == 0x7FC0
+    assert h[0] != 0x7FC0 and h[2] != 0x7FC0
