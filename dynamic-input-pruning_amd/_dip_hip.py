@@ -58,6 +58,8 @@ _SIGS = {
     "dip_mlp_decode": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz,
                         _p, _p], _i32),
     "dip_mlp_state_size": ([], _sz),
+    "dip_mlp_decode_noalloc": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p,
+                                _p], _i32),
     "dip_mlp_decode_rmsnorm": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p,
                                 _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p, _p], _i32),
     "dip_gate_silu_topk_spec": ([_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p,
@@ -521,6 +523,41 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
                               _ptr(idx), _ptr(h), hidden, inter, k, _ptr(ws), ws.numel(),
                               None if state is None else _ptr(state), _stream(dev)),
            "dip_mlp_decode")
+    return y, g, idx, h
+
+
+def mlp_decode_noalloc(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y, g,
+                       idx, h, state=None):
+    """mlp_decode with the workspace in the library's per-GPU scratch array
+    (dip_mlp_decode_noalloc): the caller passes every output, nothing is
+    allocated.  Calls that overlap on one GPU race on the scratch array."""
+    gate_qw, gate_sc, inter, hidden = _weights(gate_qw, gate_sc, "gate")
+    up_qw, up_sc, inter2, hidden2 = _weights(up_qw, up_sc, "up")
+    down_t_qw, down_t_sc, inter3, hidden3 = _weights(down_t_qw, down_t_sc, "down_t")
+    if not (inter == inter2 == inter3 and hidden == hidden2 == hidden3):
+        raise RuntimeError("gate/up/down_t shapes disagree")
+    dev = _dev(gate_qw, up_qw, down_t_qw, x)
+    k = int(k)
+    if not 0 <= k <= inter:
+        raise RuntimeError(f"k={k} outside [0, {inter}]")
+    x = x.reshape(-1)
+    for t, dt, name, shape in ((x, torch.bfloat16, "x", (hidden,)), (y, torch.bfloat16, "y", (hidden,)),
+                               (g, torch.bfloat16, "g", (inter,)), (idx, torch.int32, "idx", (k,)),
+                               (h, torch.bfloat16, "h", (k,))):
+        # used in place: a copy would allocate (and outputs would land in it)
+        if (not isinstance(t, torch.Tensor) or t.dtype != dt or tuple(t.shape) != shape
+                or t.device != dev or not t.is_contiguous() or t.data_ptr() % 16):
+            raise RuntimeError(f"{name} must be a contiguous 16-byte aligned {dt} tensor of "
+                               f"shape {shape} on {dev}")
+    if state is not None:
+        if (state.device != dev or state.dtype != torch.int32 or not state.is_contiguous()
+                or state.numel() * 4 < lib.dip_mlp_state_size()):
+            raise RuntimeError("state must be this device's mlp_state() tensor")
+    _check(lib.dip_mlp_decode_noalloc(_ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc),
+                                      _ptr(down_t_qw), _ptr(down_t_sc), _ptr(x), _ptr(y), _ptr(g),
+                                      _ptr(idx), _ptr(h), hidden, inter, k,
+                                      None if state is None else _ptr(state), _stream(dev)),
+           "dip_mlp_decode_noalloc")
     return y, g, idx, h
 
 

@@ -141,6 +141,7 @@ extern "C" const char* dip_status_string(int status) {
     case DIP_ERR_UNSUPPORTED: return "no kernel instantiation for this shape";
     case DIP_ERR_WORKSPACE: return "workspace missing or too small";
     case DIP_ERR_ARG: return "invalid argument";
+    case DIP_ERR_SCRATCH: return "the shape needs more workspace than the no-alloc scratch holds";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -39,7 +39,8 @@ enum {
   DIP_ERR_ALIGN = -3,       /* a pointer is not 16-byte aligned */
   DIP_ERR_UNSUPPORTED = -4, /* the shape has no kernel instantiation */
   DIP_ERR_WORKSPACE = -5,   /* workspace missing or smaller than required */
-  DIP_ERR_ARG = -6          /* any other invalid argument */
+  DIP_ERR_ARG = -6,         /* any other invalid argument */
+  DIP_ERR_SCRATCH = -7      /* the shape needs more than the no-alloc scratch holds */
 };
 
 enum { DIP_ACT_NONE = 0, DIP_ACT_SILU = 1 };
@@ -276,6 +277,27 @@ int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t*
                    const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
                    uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
                    void* workspace, size_t ws_bytes, void* layer_state, void* stream);
+
+/*
+ * dip_mlp_decode for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments and outputs as
+ * dip_mlp_decode without the workspace: the step's workspace is a
+ * DIP_NOALLOC_SCRATCH_BYTES device array the library holds on every GPU it
+ * runs on until the process ends (its address is looked up at the first
+ * call on a device, with that device current).  A shape whose
+ * dip_mlp_workspace_size exceeds it returns DIP_ERR_SCRATCH.  The call
+ * allocates nothing.  All calls on one GPU share its array, so calls that
+ * overlap on one GPU (other streams or threads) race; calls in stream order
+ * do not (nothing in the array is read before the same call writes it).
+ */
+#define DIP_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int dip_mlp_decode_noalloc(const int8_t* gate_qw, const uint16_t* gate_sc,
+                           const int8_t* up_qw, const uint16_t* up_sc,
+                           const int8_t* down_t_qw, const uint16_t* down_t_sc,
+                           const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
+                           uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
+                           void* layer_state, void* stream);
 
 /*
  * dip_mlp_decode with the post-attention RMSNorm of a decoder layer folded
