@@ -730,7 +730,7 @@ def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res
     return y, g, idx, h, x_out
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "gate_mfma": 3}
+TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "step": 3}
 
 
 def set_tuning(name: str, value: int) -> None:

@@ -188,6 +188,28 @@ DIP_DEV float group_max(float v) {
   return v;
 }
 
+// DPP move with zero fill: lanes whose source is outside the row (or whose
+// row is masked off) read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+DIP_DEV uint32_t dpp_zero(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, true);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: Hillis-Steele within
+// rows of 16 (row_shr 1, 2, 4, 8), then row_bcast:15 / row_bcast:31 carry
+// the row totals into the later rows.
+DIP_DEV uint32_t wave_prefix(uint32_t v) {
+  v += dpp_zero<0x111>(v);        // row_shr:1
+  v += dpp_zero<0x112>(v);        // row_shr:2
+  v += dpp_zero<0x114>(v);        // row_shr:4
+  v += dpp_zero<0x118>(v);        // row_shr:8
+  v += dpp_zero<0x142, 0xA>(v);   // row_bcast:15 -> rows 1, 3
+  v += dpp_zero<0x143, 0xC>(v);   // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+DIP_DEV uint32_t lane63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
+
 // 128-bit streaming load (weights are read once per call: non-temporal).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 DIP_DEV uint4 ldg_nt(const uint4* p) {

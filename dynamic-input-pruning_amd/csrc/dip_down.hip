@@ -168,6 +168,12 @@ void launch_down(int src, const DownArgs& a, int blocks, hipStream_t stream) {
 
 }  // namespace
 
+int launch_down_reduce(const float* partial, int row_blocks, int out_features, uint16_t* y,
+                       hipStream_t stream) {
+  launch_reduce(partial, row_blocks, out_features, y, stream);
+  return hip_status(hipGetLastError());
+}
+
 size_t down_workspace_bytes(int64_t k, int64_t out_features) {
   // one fp32 partial row of out_features per block of 256 selected positions
   if (out_features <= 0) return 256;

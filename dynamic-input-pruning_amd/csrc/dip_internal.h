@@ -50,7 +50,28 @@ struct RowdotArgs {
   uint16_t* norm_h_out;
   uint16_t* norm_x_out;  // workgroup 0 also writes the normalised x here (if set)
   float norm_eps;
+  // decode gate (kContig + kSilu) of the fused step, with spec = the layer
+  // state ([1] speculation key, [2] key band lo | hi << 16): each workgroup b
+  // writes
+  //   * its rows whose magnitude key is at or above spec[1] (NaN never) to
+  //     cand_list[b * kCandCap ...] (channel | g bits << 16, in lane order),
+  //     their number to cand_count[b] and its largest flushed key
+  //     (0xFFFFFFFF if none is valid) to cand_max[b];
+  //   * its rows whose key lies in the band [lo, hi) to band_list[b *
+  //     kBandSlot ...] (the first kBandSlot of them, same format), their
+  //     number to band_count[b] and the number of rows whose key is at or
+  //     above hi to above_count[b] (both 0 when the band is empty).
+  uint32_t* cand_list;
+  uint32_t* cand_count;
+  uint32_t* cand_max;
+  const uint32_t* spec;
+  uint32_t* band_list;
+  uint32_t* band_count;
+  uint32_t* above_count;
 };
+constexpr int kCandCap = 128;     // >= rows per gate workgroup (256/LPR groups x at most 8 rows)
+constexpr int kMaxCandWgs = 1024; // gate workgroups with candidate lists (the fused step ranks them)
+constexpr int kBandSlot = 16;     // band entries kept per gate workgroup
 
 struct DownArgs {
   const int8_t* qw_a;
@@ -89,12 +110,18 @@ struct TopkMeta {
   uint64_t stamp[6];   // wall_clock64() at the select kernel's phase boundaries (diagnostics)
   uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
   // wall_clock64() in two speculation workgroups (the first and the middle
-  // one): start, list built, x staged, done (diagnostics)
+  // one): start, list built, x staged, done; the fused step kernel puts
+  // workgroup 0's cut sub-phases in spec_stamp[0] (diagnostics)
   uint64_t spec_stamp[2][4];
+  // the fused step: the next call's speculation key and key band (workgroup 0
+  // of the step writes them, the finish copies them to the layer state)
+  uint32_t next_key;
+  uint32_t next_band;
 };
 
 // The top-k workspace holds the last call's TopkMeta.
 constexpr size_t kTopkWorkspace = 512;
+static_assert(sizeof(TopkMeta) <= kTopkWorkspace, "TopkMeta fits the top-k workspace");
 
 // Top-k + speculative up (one launch): workgroups [0, ntopk) run the select,
 // the rest compute h_full[c] = bf16(g[c] * bf16(up[c] . x)) for every channel
@@ -112,6 +139,67 @@ struct SpecArgs {
   int chan_per_wg;    // set by the launcher
   int ntopk;          // set by the launcher
 };
+
+// The decode step after the gate in one launch (dip_step.hip): the top-k
+// cut, up rows, h and per-workgroup down partials; then the finish launch
+// (dip_topk.hip): y from the partials, idx and h_out.
+constexpr int kStepMaxWorkgroups = 256;
+// Layer state of the fused step: [0] and [1] the speculation key (the
+// four-launch path reads [0] as the key in use and [1] as the next), [2] the
+// key band lo | hi << 16 the gate lists (0: none), [3] unused.  The finish
+// launch writes all of them.
+constexpr int kStepStateWords = 4;
+struct StepArgs {
+  const uint16_t* g;
+  int n;
+  int k;
+  const uint16_t* x;
+  int hidden;
+  const int8_t* up_qw;
+  const uint16_t* up_sc;
+  const int8_t* dn_qw;
+  const uint16_t* dn_sc;
+  uint16_t* h_full;          // [n] h by channel
+  float* partial;            // [grid][hidden]
+  const uint32_t* state;     // kStepStateWords (read only: the finish writes it)
+  TopkMeta* meta;
+  const uint32_t* cand_list; // the gate's lists (RowdotArgs::cand_*, band_*)
+  const uint32_t* cand_count;
+  const uint32_t* cand_max;
+  const uint32_t* band_list;
+  const uint32_t* band_count;
+  const uint32_t* above_count;
+  int gate_wgs;              // gate workgroups (entries of cand_count)
+  int margin;                // set by the launcher
+  int stamps;                // set by the launcher
+};
+struct FinishArgs {
+  const float* partial;
+  int rows;                  // partial rows (the step's grid)
+  int hidden;
+  uint16_t* y;
+  const uint16_t* g;
+  int n;
+  int k;
+  const TopkMeta* meta;
+  const uint16_t* h_full;
+  int32_t* idx;
+  uint16_t* h_out;
+  uint32_t* state;           // if set: gets the next call's key and band from meta
+  int ny;                    // set by the launcher
+};
+int step_grid();
+int step_max_gate_wgs();
+bool step_supported(int64_t hidden, int64_t inter);
+size_t step_partial_bytes(int64_t hidden);
+int launch_step(const StepArgs& a, hipStream_t stream);
+int launch_finish(const FinishArgs& a, hipStream_t stream);
+// The grid (workgroups) launch_rowdot / launch_rowdot_norm use for a
+// contiguous GEMV of nrows rows of in_features columns.
+int rowdot_contig_blocks(int64_t nrows, int64_t in_features);
+// y[o] = bf16(sum over rows rb < row_blocks of partial[rb][o]) in a fixed order.
+int launch_down_reduce(const float* partial, int row_blocks, int out_features, uint16_t* y,
+                       hipStream_t stream);
 
 // Launchers (return hipSuccess or a DIP_ERR_* code).
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream);
@@ -134,9 +222,6 @@ int64_t down_max_k();  // largest k the down path accepts
 // The top-k select kernel: idx from s (TopkMeta into the workspace).
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
                        hipStream_t stream);
-// The contiguous GEMV on int8 MFMA (DIP_ERR_UNSUPPORTED for shapes it does
-// not cover: the caller then runs the row-dot kernel).
-int launch_mfma_gemv(int epi, const RowdotArgs& a, hipStream_t stream);
 // The top-k + speculative-up launch (hidden widths of topk_spec_supported).
 bool topk_spec_supported(int64_t hidden);
 int launch_topk_spec(const uint16_t* g, int64_t n, int64_t k, int32_t* idx, void* ws,

@@ -42,6 +42,14 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   const int nchunks = a.in_features / kChunkCols;
   const int grp = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
   const int ngrp = a.ngrp;
+  // the fused step's speculation key and key band (the layer state; the
+  // finish launch of the step rewrites it, never this launch)
+  [[maybe_unused]] uint32_t cand_key = 0, band = 0;
+  if constexpr (SRC == kContig && EPI == kSilu)
+    if (a.cand_count) {
+      cand_key = a.spec[1];
+      band = a.spec[2];
+    }
   if (a.rotate && blockIdx.x == 0 && threadIdx.x == 0) a.rotate[0] = a.rotate[1];
 
   // 1. x loads first (XS: one chunk per thread, index clamped)
@@ -105,8 +113,8 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   }
 
   // 6. epilogue: lane l finishes row l
+  uint32_t v = 0;
   if (valid_l) {
-    uint32_t v;
     if (rid_lane == kBadRow) {
       v = 0x7FC0u;
     } else {
@@ -124,6 +132,52 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
       }
     }
     a.out[(int)jl] = (uint16_t)v;
+  }
+  if constexpr (SRC == kContig && EPI == kSilu) {
+    if (a.cand_count) {  // uniform: the decode gate of the fused step
+      // per wave: candidate / band / above counts and the largest key; then
+      // each list gets its entries in lane order, waves in order
+      __shared__ uint32_t wcnt[kRowdotMaxThreads / 64][3];
+      __shared__ float wmx[kRowdotMaxThreads / 64];
+      const int wave = threadIdx.x >> 6;
+      const uint32_t kk = v & 0x7FFFu;
+      const bool ok = valid_l && kk <= 0x7F80u;
+      const uint32_t blo = band & 0xFFFFu, bhi = band >> 16;
+      const bool cand = ok && kk >= cand_key;
+      const bool inb = ok && kk >= blo && kk < bhi;
+      const bool abv = ok && bhi != 0u && kk >= bhi;
+      const uint64_t m = __ballot(cand), mb = __ballot(inb), ma = __ballot(abv);
+      float mk = ok ? bf16_to_f32(kk < 0x80u ? 0u : kk) : -1.f;
+      mk = group_max<64>(mk);
+      if (lane == 0) {
+        wcnt[wave][0] = (uint32_t)__popcll(m);
+        wcnt[wave][1] = (uint32_t)__popcll(mb);
+        wcnt[wave][2] = (uint32_t)__popcll(ma);
+        wmx[wave] = mk;
+      }
+      __syncthreads();
+      uint32_t base = 0, total = 0, bbase = 0, btotal = 0, atotal = 0;
+      float bm = -1.f;
+      for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+        base += w < wave ? wcnt[w][0] : 0u;
+        bbase += w < wave ? wcnt[w][1] : 0u;
+        total += wcnt[w][0];
+        btotal += wcnt[w][1];
+        atotal += wcnt[w][2];
+        bm = fmaxf(bm, wmx[w]);
+      }
+      const uint64_t below = (1ull << lane) - 1ull;
+      const uint32_t entry = (uint32_t)jl | (v << 16);
+      if (cand) a.cand_list[(size_t)blockIdx.x * kCandCap + base + (uint32_t)__popcll(m & below)] = entry;
+      const uint32_t bpos = bbase + (uint32_t)__popcll(mb & below);
+      if (inb && bpos < (uint32_t)kBandSlot) a.band_list[(size_t)blockIdx.x * kBandSlot + bpos] = entry;
+      if (threadIdx.x == 0) {
+        a.cand_count[blockIdx.x] = total;
+        a.cand_max[blockIdx.x] = bm < 0.f ? 0xFFFFFFFFu : (__float_as_uint(bm) >> 16);
+        a.band_count[blockIdx.x] = btotal;
+        a.above_count[blockIdx.x] = atotal;
+      }
+    }
   }
 }
 
@@ -230,6 +284,12 @@ int dispatch_layout(const RowdotArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+int rowdot_contig_blocks(int64_t nrows, int64_t in_features) {
+  const int64_t chunks = in_features / kChunkCols;
+  const int lpr = (chunks == 80 || chunks == 48 || chunks == 16) ? 16 : (chunks == 256 ? 64 : 32);
+  return plan_rowdot((int)nrows, lpr, true).blocks;
+}
+
 bool rowdot_norm_supported(int64_t in_features) {
   const int64_t chunks = in_features / kChunkCols;
   return in_features % kChunkCols == 0 && (chunks == 160 || chunks == 128 || chunks == 80);
@@ -267,10 +327,6 @@ int launch_spec_after_gate(const uint16_t* g, int64_t inter, int64_t hidden, int
 
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream) {
   if (a.nrows == 0) return DIP_OK;
-  if (src == kContig && tuning(DIP_TUNE_GATE_MFMA)) {
-    const int st = launch_mfma_gemv(epi, a, stream);
-    if (st != DIP_ERR_UNSUPPORTED) return st;
-  }
 #define DIP_CASE(S, E) \
   if (src == (S) && epi == (E)) return dispatch_layout<S, E>(a, stream);
   DIP_CASE(kContig, kRaw)
@@ -369,7 +425,7 @@ extern "C" int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc
   return launch_topk_select(g, inter, k, idx, workspace, (hipStream_t)stream);
 }
 
-extern "C" size_t dip_mlp_state_size(void) { return 2 * sizeof(uint32_t); }
+extern "C" size_t dip_mlp_state_size(void) { return kStepStateWords * sizeof(uint32_t); }
 
 extern "C" int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
                                        const int8_t* up_qw, const uint16_t* up_sc,

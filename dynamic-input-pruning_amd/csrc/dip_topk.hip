@@ -47,28 +47,6 @@ constexpr uint32_t kMinNormalKey = 0x0080u;
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// DPP move with zero fill: lanes whose source is outside the row (or whose
-// row is masked off) read 0.
-template <int CTRL, int ROW_MASK = 0xF>
-DIP_DEV uint32_t dpp_zero(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xF, true);
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave: Hillis-Steele within
-// rows of 16 (row_shr 1, 2, 4, 8), then row_bcast:15 / row_bcast:31 carry
-// the row totals into the later rows.
-DIP_DEV uint32_t wave_prefix(uint32_t v) {
-  v += dpp_zero<0x111>(v);        // row_shr:1
-  v += dpp_zero<0x112>(v);        // row_shr:2
-  v += dpp_zero<0x114>(v);        // row_shr:4
-  v += dpp_zero<0x118>(v);        // row_shr:8
-  v += dpp_zero<0x142, 0xA>(v);   // row_bcast:15 -> rows 1, 3
-  v += dpp_zero<0x143, 0xC>(v);   // row_bcast:31 -> rows 2, 3
-  return v;
-}
-
-DIP_DEV uint32_t lane63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
-
 // Per 16-bit half: 1 if d < span1 (unsigned), else 0.  Saturating packed
 // subtract then min with 1, as two VOP3P instructions (written as asm so the
 // compiler keeps them packed instead of splitting into per-half compares).
@@ -616,6 +594,165 @@ __global__ __launch_bounds__(kThreads) void topk_spec_kernel(
                        (int)gridDim.x - sp.ntopk);
 }
 
+
+// ---------------------------------------------------------------------------
+// Finish of the fused decode step (after dip_step.hip's launch), one launch of
+// two kinds of workgroups:
+//   * workgroups [0, ny): y[o] = bf16(sum of the step workgroups' partial
+//     rows), the rows in a fixed order (four interleaved ascending splits,
+//     added in order);
+//   * workgroups [ny, ny + ceil(n/2048)): idx and h_out for one slice of
+//     2048 channels.  The step recorded the bisection's lo / hi (so the tier
+//     cuts) and the tier totals; each workgroup counts the tiers of the
+//     channels before its slice (packed 16-bit counting), places its slice's
+//     selected channels at their positions — tier A in ascending id, then
+//     tier B in ascending id up to k (topk_select.cu:64-132) — and copies
+//     each one's h from h_full.  The first one also fills the unfilled slots
+//     with channel 0 (topk_select.cu:160).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kFinThreads = 256;
+constexpr int kFinOut = 32;                   // outputs per y workgroup
+constexpr int kFinSplit = kFinThreads / kFinOut;
+constexpr int kFinBatch = 32;                 // partial rows in flight per thread
+constexpr int kFinSlice = 2048;               // channels per idx workgroup
+constexpr int kFinCountBatch = 16;            // 8-channel chunks in flight per thread
+}  // namespace
+
+__global__ __launch_bounds__(kFinThreads) void finish_kernel(FinishArgs a) {
+  __shared__ float part[kFinSplit][kFinOut];
+  __shared__ uint32_t wtot[kFinThreads / 64][3];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if ((int)blockIdx.x < a.ny) {
+    // split p sums rows p, p + kFinSplit, ... (all loads of a batch issued
+    // before the adds), then the splits in order
+    const int oo = tid % kFinOut, p = tid / kFinOut;
+    const int o = min((int)blockIdx.x * kFinOut + oo, a.hidden - 1);
+    float s = 0.f;
+    for (int r0 = p; r0 < a.rows; r0 += kFinBatch * kFinSplit) {
+      float v[kFinBatch];
+#pragma unroll
+      for (int u = 0; u < kFinBatch; ++u) {
+        const int rb = min(r0 + u * kFinSplit, a.rows - 1);
+        v[u] = a.partial[(size_t)rb * a.hidden + o];
+      }
+#pragma unroll
+      for (int u = 0; u < kFinBatch; ++u) s = r0 + u * kFinSplit < a.rows ? s + v[u] : s;
+    }
+    part[p][oo] = s;
+    __syncthreads();
+    if (p == 0 && (int)blockIdx.x * kFinOut + oo < a.hidden) {
+      float t = part[0][oo];
+#pragma unroll
+      for (int qq = 1; qq < kFinSplit; ++qq) t += part[qq][oo];
+      a.y[blockIdx.x * kFinOut + oo] = (uint16_t)f32_to_bf16(t);
+    }
+    return;
+  }
+  const int n = a.n;
+  const uint32_t uk = (uint32_t)a.k;
+  const int slice0 = ((int)blockIdx.x - a.ny) * kFinSlice;
+  const uint32_t cut_a = max((__float_as_uint(a.meta->hi) >> 16) + 1u, kMinNormalKey);
+  const uint32_t cut_b = max((__float_as_uint(a.meta->lo) >> 16) + 1u, kMinNormalKey);
+  const Cuts c = make_cuts(cut_a, cut_b);
+  const uint32_t tot_a = (uint32_t)a.meta->count_a, tot_b = (uint32_t)a.meta->count_b;
+  // tier counts of the channels before the slice (whole 8-channel chunks:
+  // slice0 <= n is a multiple of 8), a batch of chunks in flight at a time
+  uint32_t pa = 0, pb = 0;
+  for (int base0 = tid * 8; base0 < slice0; base0 += kFinThreads * 8 * kFinCountBatch) {
+    uint32_t w[kFinCountBatch][4];
+    // unconditional loads (chunk 0 stands in past the slice), masked after
+    // all of them are issued
+#pragma unroll
+    for (int u = 0; u < kFinCountBatch; ++u) {
+      const int base = base0 + u * kFinThreads * 8;
+      const uint4 v = *reinterpret_cast<const uint4*>(a.g + (base < slice0 ? base : 0));
+      w[u][0] = v.x;
+      w[u][1] = v.y;
+      w[u][2] = v.z;
+      w[u][3] = v.w;
+    }
+#pragma unroll
+    for (int u = 0; u < kFinCountBatch; ++u) {
+      if (base0 + u * kFinThreads * 8 >= slice0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[u][e] = 0xFFFFFFFFu;  // NaN: in no tier
+      }
+      const uint32_t t = tier_counts8(w[u], c.cut_a2, c.span_a2, c.cut_b2, c.span_b2);
+      pa += t & 0xFFFFu;
+      pb += t >> 16;
+    }
+  }
+  // my 8 channels of the slice, in order
+  const int my = slice0 + tid * 8;
+  uint32_t w[4];
+  load_chunk8(a.g, n, my, w);
+  if (my < n && my + 8 > n) load_tail8(a.g, n, my, w);
+  // their h, in one load (h_full spans whole 256-byte blocks past n)
+  const uint4 hq = *reinterpret_cast<const uint4*>(a.h_full + (my < n ? my : 0));
+  const uint32_t hw[4] = {hq.x, hq.y, hq.z, hq.w};
+  uint32_t ta = 0, tb = 0, flags = 0;  // flags: 2 bits per value (1 = A, 2 = B)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t kk = (w[e >> 1] >> (16 * (e & 1))) & 0x7FFFu;
+    const bool ia = kk - c.cut_a < c.span_a;
+    const bool ib = kk - c.cut_b < c.span_b;
+    ta += ia ? 1u : 0u;
+    tb += ib ? 1u : 0u;
+    flags |= (ia ? 1u : (ib ? 2u : 0u)) << (2 * e);
+  }
+  const uint32_t own = ta | (tb << 16);
+  const uint32_t incl = wave_prefix(own);
+  const uint32_t sa = lane63(wave_prefix(pa)), sb = lane63(wave_prefix(pb));
+  if (lane == 63) wtot[wave][0] = incl;
+  if (lane == 0) {
+    wtot[wave][1] = sa;
+    wtot[wave][2] = sb;
+  }
+  __syncthreads();
+  uint32_t before = 0, pre_a = 0, pre_b = 0;
+#pragma unroll
+  for (int wv = 0; wv < kFinThreads / 64; ++wv) {
+    before += wv < wave ? wtot[wv][0] : 0u;
+    pre_a += wtot[wv][1];
+    pre_b += wtot[wv][2];
+  }
+  const uint32_t ex = before + incl - own;
+  uint32_t pos_a = pre_a + (ex & 0xFFFFu), pos_b = tot_a + pre_b + (ex >> 16);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t f = (flags >> (2 * e)) & 3u;
+    const uint32_t pos = f == 1u ? pos_a : pos_b;
+    if (f != 0u && pos < uk) {
+      a.idx[pos] = my + e;
+      a.h_out[pos] = (uint16_t)(hw[e >> 1] >> (16 * (e & 1)));
+    }
+    pos_a += f == 1u ? 1u : 0u;
+    pos_b += f == 2u ? 1u : 0u;
+  }
+  if (slice0 == 0) {  // unfilled slots: channel 0
+    const uint32_t filled = min(uk, tot_a + tot_b);
+    for (uint32_t pp = filled + (uint32_t)tid; pp < uk; pp += kFinThreads) {
+      a.idx[pp] = 0;
+      a.h_out[pp] = a.h_full[0];
+    }
+    if (a.state && tid == 0) {  // the next call's speculation key and band
+      const uint32_t key = a.meta->next_key, band = a.meta->next_band;
+      a.state[0] = key;
+      a.state[1] = key;
+      a.state[2] = band;
+      a.state[3] = 0u;
+    }
+  }
+}
+
+int launch_finish(const FinishArgs& args, hipStream_t stream) {
+  FinishArgs a = args;
+  a.ny = (a.hidden + kFinOut - 1) / kFinOut;
+  const int ni = (a.n + kFinSlice - 1) / kFinSlice;
+  hipLaunchKernelGGL(finish_kernel, dim3(a.ny + ni), dim3(kFinThreads), 0, stream, a);
+  return hip_status(hipGetLastError());
+}
 
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
                        hipStream_t stream) {

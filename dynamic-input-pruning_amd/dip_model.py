@@ -485,6 +485,11 @@ class DIPDecoder:
             raise ValueError(f"{plen} + {max_new_tokens} tokens exceed max_len {self.max_len}")
         toks = torch.empty(max_new_tokens, dtype=torch.long, device=self.device)
         logs = []
+        # every generation starts from fresh speculation keys, so the same
+        # prompt gives the same tokens and logits bit for bit
+        for m in self.model.modules():
+            if hasattr(m, "reset_speculation"):
+                m.reset_speculation()
         last = self.prefill(ids)
         for t in range(max_new_tokens):
             if return_logits:

@@ -88,6 +88,13 @@ class DIPStack:
     def bytes_per_token(self) -> int:
         return self.layers * bytes_per_layer(self.hidden, self.inter, self.k)
 
+    def reset_speculation(self):
+        """Zero every layer's speculation state (the next token speculates on
+        every channel, as the first token of a new stack does)."""
+        for st in self.state:
+            if st is not None:
+                st.zero_()
+
     def run_token(self):
         """All layers on self.x, in stream order (one dip_mlp_decode each)."""
         for lw, y, st in zip(self.w, self.y, self.state):

@@ -139,9 +139,17 @@ class StreamingDIPMlp(nn.Module):
         self.down_t_sc = dn_t_sc.to(self.device).contiguous()
         self.out_features = self.down_t_qw.shape[1] * 2
         self.k = shared.k
-        # which channels the next token's up rows are speculated on (decides
-        # only which workgroups compute which h, never a value)
+        # which channels the next token's up rows are speculated on: it
+        # decides which workgroup handles which channel, so it never changes
+        # g, idx or h, and y only within fp32 rounding (the grouping of the
+        # down sum); reset_speculation() makes the next call repeat a fresh
+        # module's bits
         self._spec_state = K.mlp_state(self.device)
+
+    def reset_speculation(self):
+        """Forget the speculation key (the next call speculates on every
+        channel, as the first call of a new module does)."""
+        self._spec_state.zero_()
 
     def _gate(self, x):
         """gate_proj(x) (dip_stream_predispatch.py:166-174)."""

@@ -139,17 +139,19 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
  *                               on the channels at or above the magnitude of
  *                               rank k + inter * this / 1024 (0..1024) (8)
- *   DIP_TUNE_GATE_MFMA          1: contiguous GEMVs (the gate) of widths
- *                               5120 and 4096 with at least 2 * CUs * 16 *
- *                               DIP_TUNE_ROWDOT_WGS_PER_CU rows run on int8
- *                               MFMA; 0: on the row-dot kernel (0)
+ *   DIP_TUNE_STEP               1: a decode step with speculation state runs
+ *                               its top-k, up rows, h and down partials in
+ *                               one launch after the gate, then a finish
+ *                               launch (three launches); 0: top-k +
+ *                               speculative up, then down + reduce (four
+ *                               launches) (0: the faster on MI355X today)
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
   DIP_TUNE_TOPK_STAMPS = 1,
   DIP_TUNE_SPEC_MARGIN = 2,
-  DIP_TUNE_GATE_MFMA = 3,
+  DIP_TUNE_STEP = 3,
   DIP_TUNE_COUNT = 4
 };
 int dip_set_tuning(int knob, int value);

@@ -60,7 +60,8 @@ def test_checkpoint_to_resident_stack(tmp_path):
         assert np.array_equal(idx_h, O.topk_select(g_h, stack.k)), i
         tail = O.dip_forward(gq, gs, uq, us, dtq, dts, x, stack.k, idx=idx_h)
         assert rel_err(host_bf16(y), tail["y_f64"]) < 1e-2, i
-        assert torch.equal(y.view(torch.int16), stack.y[i].view(torch.int16)), i
+        # the stack's speculative step: the same sum in another fp32 grouping
+        assert rel_err(host_bf16(stack.y[i]), tail["y_f64"]) < 1e-2, i
 
     names, mods, _ = C.load_streaming_mlps(tmp_path, 0.6, "cuda")
     xin = dev_bf16(x).reshape(1, 1, H)

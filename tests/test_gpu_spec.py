@@ -1,11 +1,17 @@
 """GPU parity of the decode step with speculative up rows.
 
-dip_mlp_decode with a layer state runs the gate, then one launch holding the
-top-k select and the up rows of the channels the state names, then the down
-gather of h by channel.  Whatever the state holds, y, g, idx and h must be
-bit-identical to the stage-by-stage step (no state), which the other GPU
-tests pin against the oracle; the state itself must hold the magnitude key of
-rank k + margin of the last call's g.
+dip_mlp_decode with a layer state runs the gate (which also lists, per
+workgroup, its candidate channels and the channels inside the state's key
+band), one launch holding the top-k cut, the up rows, h and each workgroup's
+down partial, then the finish (y, idx, h, the next state).  Whatever the
+state holds, g, idx and h must be bit-identical to the stage-by-stage step
+(no state), which the other GPU tests pin against the oracle.  y is the same
+sum of the same exact products in another fp32 order (which workgroup sums
+which channel depends on the state), so it must agree to within a few fp32
+roundings: one bf16 ulp, except where the sum cancels to near zero; a missing
+or doubled channel moves y by about 1/sqrt(k) of its size.  For a given state
+the step is deterministic.  The state itself must then hold the magnitude key
+of rank k + margin of the call's g and a key band that contains its cut.
 """
 import numpy as np
 import pytest
@@ -19,10 +25,16 @@ pytestmark = pytest.mark.gpu
 MARGIN_PER_1024 = 8  # DIP_TUNE_SPEC_MARGIN default
 
 
-@pytest.fixture(scope="module")
-def K():
+@pytest.fixture(scope="module", params=[0, 1], ids=["four-launch", "fused"])
+def K(request):
+    """The library with the decode step's speculative path set to the
+    four-launch form (top-k + up, down, reduce) or the fused one (one launch
+    for top-k, up and down partials, then the finish)."""
     import _dip_hip
-    return _dip_hip
+    old = _dip_hip.get_tuning("step")
+    _dip_hip.set_tuning("step", request.param)
+    yield _dip_hip
+    _dip_hip.set_tuning("step", old)
 
 
 def _weights(H, I, seed):
@@ -54,6 +66,56 @@ def _assert_same(a, b, what):
         assert torch.equal(_bits(u), _bits(v)), f"{what}: {name} differs"
 
 
+def _assert_y_close(u, v, what):
+    """Two fp32 sums of the same exact products in different groupings, each
+    rounded to bf16: every output within one bf16 ulp, except where the sum
+    cancels to near zero (|y| below 1e-3 of max|y|), where the two may differ
+    by fp32 rounding of the large terms (at most 1e-4 of max|y|).  A missing
+    or doubled channel moves y by about 1/sqrt(k) of max|y| (> 1e-2)."""
+    yu, yv = host_bf16(u), host_bf16(v)
+    a = O.bf16_to_f32(yu).astype(np.float64)
+    b = O.bf16_to_f32(yv).astype(np.float64)
+    top = max(np.abs(b).max(), 1e-30)
+    small = np.abs(b) < 1e-3 * top
+    d = ulp_diff(yu, yv)
+    assert (d[~small] <= 1).all(), f"{what}: y differs by {d[~small].max()} ulps"
+    assert (np.abs(a - b)[small] <= 1e-4 * top).all(), f"{what}: near-zero y"
+    assert np.abs(a - b).max() <= 4e-3 * top, f"{what}: y rel err"
+
+
+def _assert_step(a, b, what):
+    """g, idx, h bit-identical; y close (another fp32 summation order)."""
+    for name, u, v in zip(("g", "idx", "h"), a[1:], b[1:]):
+        assert torch.equal(_bits(u), _bits(v)), f"{what}: {name} differs"
+    _assert_y_close(a[0], b[0], what)
+
+
+def _state(key, band=(0, 0)):
+    """A decode state: the speculation key (twice) and the key band [lo, hi)
+    the gate lists ((0, 0): none, the whole-g path)."""
+    lo, hi = band
+    return torch.tensor([key, key, lo | (hi << 16), 0], dtype=torch.int32, device="cuda")
+
+
+def _assert_next_state(K, state, g, k, margin, what, first=False):
+    """The state a call leaves: its rank k + margin key as the next key; the
+    four-launch path keeps the key it used in [0] (0 after the first call),
+    the fused one the next key in both and a band that holds the cut (the
+    key of rank k + 1)."""
+    st = state.cpu().numpy().view(np.uint32)
+    key = _rank_key(g, k + margin)
+    assert st[1] == key, what
+    if not K.get_tuning("step"):
+        if first:
+            assert st[0] == 0, what  # a zeroed state speculates on every channel
+        return
+    assert st[0] == key, what
+    lo, hi = int(st[2]) & 0xFFFF, int(st[2]) >> 16
+    cut = _rank_key(g, k + 1)
+    if cut >= 0x80:
+        assert 0x80 <= lo <= cut < hi <= 0x7F81 and hi - lo <= 256, (what, lo, cut, hi)
+
+
 def _rank_key(g, r):
     """Magnitude key (|bf16 bits|) of rank r (1 = largest) among the values
     that are not NaN; 0 when there are fewer than r."""
@@ -70,13 +132,12 @@ def test_spec_matches_stagewise(K, H, I, keep):
     margin = I * MARGIN_PER_1024 // 1024
     for t in range(4):
         x = _x(H, 100 + t)
+        st0 = state.clone()
         got = _step(K, W, x, k, state)
         ref = _step(K, W, x, k)
-        _assert_same(got, ref, f"H={H} token {t}")
-        st = state.cpu().numpy().view(np.uint32)
-        assert st[1] == _rank_key(ref[1], k + margin), t
-        if t == 0:
-            assert st[0] == 0  # a zeroed state speculates on every channel
+        _assert_step(got, ref, f"H={H} token {t}")
+        _assert_same(_step(K, W, x, k, st0), got, f"H={H} token {t}: same state, same bits")
+        _assert_next_state(K, state, ref[1], k, margin, t, first=t == 0)
 
 
 def test_spec_any_state_value(K):
@@ -91,10 +152,17 @@ def test_spec_any_state_value(K):
     g = ref[1]
     keys = [0, 0xFFFF, _rank_key(g, k), _rank_key(g, k // 2), _rank_key(g, k + 2000), 0x7F80,
             0x7FFF, 1]
-    for key in keys:
-        state = torch.tensor([key, key], dtype=torch.int32, device="cuda")
-        got = _step(K, W, x, k, state)
-        _assert_same(got, ref, f"key {key:#x}")
+    cut = _rank_key(g, k + 1)
+    lo, hi = _rank_key(g, k + 300), _rank_key(g, k - 100) + 1
+    # key bands: none (the whole-g path), around the cut, off by a few keys
+    # (a tier outside: the whole-g path), far off, one key wide, wider than
+    # the band path takes, reaching below normal keys, empty
+    bands = [(0, 0), (lo, hi), (lo + 3, hi), (lo, cut), (cut + 1, cut + 40), (cut, cut + 1),
+             (cut - 255, cut + 1), (cut - 256, cut + 1), (0x40, cut + 5), (cut, cut)]
+    for band in bands:
+        for key in keys:
+            got = _step(K, W, x, k, _state(key, band))
+            _assert_step(got, ref, f"key {key:#x} band {band}")
 
 
 def test_spec_unfilled_slots_use_channel_0(K):
@@ -112,13 +180,12 @@ def test_spec_unfilled_slots_use_channel_0(K):
     ref = _step(K, W0, x, k)
     assert (ref[2][200:] == 0).all()  # unfilled slots hold channel 0
     for key in (0, 1, 0xFFFF, _rank_key(ref[1], 100)):
-        state = torch.tensor([key, key], dtype=torch.int32, device="cuda")
-        _assert_same(_step(K, W0, x, k, state), ref, f"key {key:#x}")
+        for band in ((0, 0), (_rank_key(ref[1], 190), _rank_key(ref[1], 100) + 1)):
+            _assert_step(_step(K, W0, x, k, _state(key, band)), ref, f"key {key:#x}")
     gs[0] = W[1][0]         # channel 0 nonzero again
     ref = _step(K, W0, x, k)
     for key in (0, 0xFFFF):
-        state = torch.tensor([key, key], dtype=torch.int32, device="cuda")
-        _assert_same(_step(K, W0, x, k, state), ref, f"key {key:#x}, channel 0 live")
+        _assert_step(_step(K, W0, x, k, _state(key)), ref, f"key {key:#x}, channel 0 live")
 
 
 def test_spec_margin_knob(K):
@@ -132,9 +199,8 @@ def test_spec_margin_knob(K):
             for t in range(3):
                 x = _x(H, 30 + t)
                 ref = _step(K, W, x, k)
-                _assert_same(_step(K, W, x, k, state), ref, f"margin {m} token {t}")
-                st = state.cpu().numpy().view(np.uint32)
-                assert st[1] == _rank_key(ref[1], k + I * m // 1024)
+                _assert_step(_step(K, W, x, k, state), ref, f"margin {m} token {t}")
+                _assert_next_state(K, state, ref[1], k, I * m // 1024, f"margin {m}")
     finally:
         K.set_tuning("spec_margin", MARGIN_PER_1024)
 
@@ -172,7 +238,7 @@ def test_spec_stack_graph_replays(K):
         plain.run_token()
         torch.cuda.synchronize()
         for a, b in zip(spec.y, plain.y):
-            assert torch.equal(_bits(a), _bits(b)), rep
+            _assert_y_close(a, b, f"replay {rep}")
 
 
 def test_mlp_decode_rmsnorm_equals_mlp_decode_on_its_x(K):
@@ -207,7 +273,7 @@ def test_mlp_decode_rmsnorm_equals_mlp_decode_on_its_x(K):
                              x_sep.view(torch.int16).cpu().numpy().view(np.uint16))
                 assert d.max() <= 1
                 b = [v.clone() for v in K.mlp_decode(*W, x_out, k)]
-                for u, v in zip(a[:4], b):
-                    uu = u.view(torch.int16) if u.dtype == torch.bfloat16 else u
-                    vv = v.view(torch.int16) if v.dtype == torch.bfloat16 else v
-                    assert torch.equal(uu, vv), (H, t, state is None)
+                if state is None:
+                    _assert_same(a[:4], b, f"H={H} token {t}")
+                else:
+                    _assert_step(a[:4], b, f"H={H} token {t} (state)")
