@@ -368,6 +368,28 @@ def int4_gather_down(down_t, scales, h, indices=None, out=None):
     return out
 
 
+def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out=None):
+    """y[o] = bf16(sum_j h_full[indices[j]] * (q*s)[indices[j], o]) with h
+    indexed by channel (the decode step's form); h_out[j] (if given) gets
+    h_full[indices[j]]."""
+    down_t, scales, rows, out_f = _weights(down_t, scales, "int4_gather_down_by_channel")
+    dev = _dev(down_t, scales, h_full, indices)
+    h_full = _want(h_full.reshape(-1), torch.bfloat16, "h_full", (rows,))
+    indices = _indices(indices)
+    k = indices.numel()
+    if h_out is not None:
+        h_out = _want(h_out, torch.bfloat16, "h_out", (k,))
+    if out is None:
+        out = torch.empty(out_f, dtype=torch.bfloat16, device=dev)
+    nbytes = lib.dip_gather_down_workspace_size(k, out_f)
+    ws = workspace(dev, nbytes, "down")
+    _check(lib.dip_int4_gather_down_by_channel(_ptr(down_t), _ptr(scales), _ptr(h_full),
+                                               _ptr(indices), _ptr(out), _ptr(h_out), rows,
+                                               out_f, k, _ptr(ws), ws.numel(), _stream(dev)),
+           "dip_int4_gather_down_by_channel")
+    return out
+
+
 def ca_fused_gemv(res_qw, res_sc, str_qw, str_sc, x, src, row, g=None, gid=None, out=None):
     res_qw, res_sc, res_rows, cols = _weights(res_qw, res_sc, "ca_fused_gemv.res")
     str_qw, str_sc, str_rows, cols2 = _weights(str_qw, str_sc, "ca_fused_gemv.str")

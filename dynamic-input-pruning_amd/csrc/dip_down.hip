@@ -37,8 +37,8 @@ constexpr int kThreads = kDownThreads;
 constexpr int kRowsPerBlock = kThreads;  // 256/LPR slots x LPR rows each
 constexpr int kXcds = 8;                 // MI355X: 8 XCDs, workgroups dispatched round-robin
 constexpr int kMaxRowBlocks = 512;       // k <= 131072
-constexpr int kRedOut = 64;              // outputs per reduce block
-constexpr int kRedSplit = 4;             // interleaved row-block splits per output
+constexpr int kRedOut = 32;              // outputs per reduce block
+constexpr int kRedSplit = 8;             // interleaved row-block splits per output
 }  // namespace
 
 template <int LPR, int SRC>
@@ -94,10 +94,10 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
                                                (size_t)cb * kCols, slot, l);
 }
 
-// y[o] = bf16(sum over row blocks rb of partial[rb][o]), rb ascending in four
-// interleaved splits (split p sums rb = p, p+4, ...), the splits then added
-// in order 0..3.  A thread issues all its loads at once (NB per split; row
-// blocks past row_blocks read a clamped address and are skipped).
+// y[o] = bf16(sum over row blocks rb of partial[rb][o]), rb ascending in
+// kRedSplit interleaved splits (split p sums rb = p, p+kRedSplit, ...), the
+// splits then added in order.  A thread issues all its loads at once (NB per
+// split; row blocks past row_blocks read a clamped address and are skipped).
 template <int NB>
 __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
     const float* __restrict__ partial, int row_blocks, int out_features, uint16_t* __restrict__ y) {
@@ -148,8 +148,8 @@ void launch_reduce(const float* partial, int row_blocks, int out_features, uint1
   const unsigned blocks = (unsigned)((out_features + kRedOut - 1) / kRedOut);
   const dim3 threads(kRedOut * kRedSplit);
   const int per = (row_blocks + kRedSplit - 1) / kRedSplit;  // row blocks per split
-  if (per <= 4)
-    hipLaunchKernelGGL((down_reduce_kernel<4>), dim3(blocks), threads, 0, stream, partial,
+  if (per <= 8)
+    hipLaunchKernelGGL((down_reduce_kernel<8>), dim3(blocks), threads, 0, stream, partial,
                        row_blocks, out_features, y);
   else
     hipLaunchKernelGGL((down_reduce_kernel<16>), dim3(blocks), threads, 0, stream, partial,

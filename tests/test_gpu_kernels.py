@@ -335,3 +335,20 @@ def test_bad_row_ids_poison_instead_of_faulting(K):
                                   dev(src), dev(row), g=dev_bf16(g), gid=dev(gid)))
     assert h[1] == 0x7FC0 and h[3] == 0x7FC0
     assert h[0] != 0x7FC0 and h[2] != 0x7FC0
+
+
+def test_gather_down_by_channel(K):
+    """dip_int4_gather_down_by_channel: h indexed by channel (the decode
+    step's form), h_out[j] = h_full[idx[j]], y against the fp64 sum."""
+    rng = np.random.default_rng(28)
+    rows, k, out_f = 12288, 7373, 4096
+    qw, sc = random_int4(rng, rows, out_f)
+    idx = np.sort(rng.permutation(rows)[:k]).astype(np.int32)
+    h_full = random_bf16(rng, rows)
+    h_out = torch.empty(k, dtype=torch.bfloat16, device="cuda")
+    y = host_bf16(K.int4_gather_down_by_channel(dev(qw), dev_bf16(sc), dev_bf16(h_full), dev(idx),
+                                                h_out=h_out))
+    assert np.array_equal(host_bf16(h_out), h_full[idx])
+    ref = O.down_f64(qw, sc, h_full[idx], rows=idx)
+    assert rel_err(y, ref) < 1e-2
+    assert_fp32_close(y, ref, down_abs_terms(qw, sc, h_full[idx], rows=idx))
