@@ -289,6 +289,55 @@ def cache_aware(args) -> int:
     return 0
 
 
+def read_ceiling(args) -> int:
+    """The read bandwidth this GPU gives the decode step's two access
+    patterns, measured with the library's probe kernels (no arithmetic):
+    a contiguous read of the gate matrix's bytes (67.584 MB) and of a whole
+    layer's (148.685 MB), the up/down gather (15360 sorted random rows of
+    2560 B out of 25600, keep 0.6), and a device-to-device copy of each
+    size.  Buffers rotate through 8 copies (6 matrices for the gather) so
+    the memory-side cache holds none of them.  One JSON line."""
+    import torch
+    import _dip_hip as K
+
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    reps = max(8, args.steps)
+
+    def timed(fn):
+        fn(0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for r in range(reps):
+            fn(r)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / reps  # us per launch, back to back
+
+    out = {"metric": "HBM read ceiling (probe kernels)", "unit": "TB/s", "reps": reps}
+    for name, nbytes in (("read_67.6MB", 67584000), ("read_148.7MB", 148684800)):
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(8)]
+        us = timed(lambda r: K.read_probe(bufs[r % 8], sink))
+        out[name] = {"us": round(us, 2), "TB/s": round(nbytes / us / 1e6, 3)}
+        dst = torch.empty_like(bufs[0])
+        us = timed(lambda r: dst.copy_(bufs[r % 8]))
+        out["d2d_copy_" + name.split("_")[1]] = {"us": round(us, 2),
+                                                 "TB/s_read_plus_write": round(2 * nbytes / us / 1e6, 3)}
+        del bufs, dst
+        torch.cuda.empty_cache()
+    n, k, rb = 25600, 15360, 2560
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    mats, idxs = [], []
+    for _ in range(6):
+        mats.append(torch.ones(n, rb, dtype=torch.uint8, device=dev))
+        idxs.append(torch.sort(torch.randperm(n, generator=gen)[:k]).values.to(torch.int32).to(dev))
+    us = timed(lambda r: K.gather_probe(mats[r % 6], idxs[r % 6], sink))
+    out["gather_15360x2560B_of_25600"] = {"us": round(us, 2), "TB/s": round(k * rb / us / 1e6, 3)}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -316,6 +365,9 @@ def main(argv=None):
                     help="instead of the resident stack, time cache-aware DIP decode with this "
                          "fraction of channels resident (misses streamed from pinned host "
                          "memory over PCIe); prints its own JSON line")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="instead of the decode step, measure the read bandwidth of the "
+                         "step's access patterns with probe kernels; prints its own JSON line")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed run, copy a buffer of this many MiB device to device "
                          "(the reference transfer for scaling HBM byte counters)")
@@ -326,6 +378,8 @@ def main(argv=None):
               "part of this build (--gpus must be 1)", file=sys.stderr)
         return 2
 
+    if args.ceiling:
+        return read_ceiling(args)
     if args.whole_model:
         return whole_model(args)
     if args.ca is not None:

@@ -67,6 +67,8 @@ _SIGS = {
     "dip_int4_gather_down_by_channel": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p],
                                         _i32),
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
+    "dip_read_probe": ([_p, _sz, _p, _p], _i32),
+    "dip_gather_probe": ([_p, _i64, _i64, _p, _i64, _p, _p], _i32),
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
     "dip_host_gather_rows_multi": ([_p, _p, _p, _i64, _p, _i64, _i64, _i32], _i32),
@@ -388,6 +390,20 @@ def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out
                                                out_f, k, _ptr(ws), ws.numel(), _stream(dev)),
            "dip_int4_gather_down_by_channel")
     return out
+
+
+def read_probe(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    """Measurement: read all of buf (device, 16-byte multiple) once."""
+    _check(lib.dip_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
+                              _stream(buf.device)), "dip_read_probe")
+
+
+def gather_probe(mat: torch.Tensor, idx: torch.Tensor, sink: torch.Tensor) -> None:
+    """Measurement: read the rows idx of the 2-D byte matrix mat."""
+    idx = _indices(idx)
+    _check(lib.dip_gather_probe(_ptr(mat), mat.shape[0], mat.shape[1] * mat.element_size(),
+                                _ptr(idx), idx.numel(), _ptr(sink), _stream(mat.device)),
+           "dip_gather_probe")
 
 
 def ca_fused_gemv(res_qw, res_sc, str_qw, str_sc, x, src, row, g=None, gid=None, out=None):

@@ -51,6 +51,19 @@ const char* dip_status_string(int status);
 /* Library version as an integer (major * 10000 + minor * 100 + patch). */
 int dip_version(void);
 
+/*
+ * Measurement kernels (no counterpart in the reference: they calibrate the
+ * roofline this build is measured against).  dip_read_probe reads `bytes`
+ * (a multiple of 16) of src front to back; dip_gather_probe reads the rows
+ * idx[0..k) (sorted ids below nrows; others read row 0) of a row-major
+ * matrix of row_bytes (a multiple of 512) per row.  Neither computes
+ * anything; `sink` (4 bytes) is written only if the folded words hit a
+ * fixed constant.
+ */
+int dip_read_probe(const void* src, size_t bytes, uint32_t* sink, void* stream);
+int dip_gather_probe(const void* rows, int64_t nrows, int64_t row_bytes, const int32_t* idx,
+                     int64_t k, uint32_t* sink, void* stream);
+
 /* Highest row count the top-k supports (its keys are staged in LDS). */
 int64_t dip_topk_max_n(void);
 

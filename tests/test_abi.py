@@ -85,7 +85,13 @@ def test_argument_rejection_before_launch():
                                      None) == -5
     assert L.dip_int4_gather_down_by_channel(p, p, p, None, p, None, 25600, 5120, 10, p, need,
                                              None) == -1
-    assert L.dip_mlp_state_size() == 16  # key in use, next key, window centre, spare
+    assert L.dip_mlp_state_size() == 16  # speculation key (twice), key band, spare
+    assert L.dip_read_probe(None, 16, p, None) == -1
+    assert L.dip_read_probe(p, 24, p, None) == -2
+    assert L.dip_read_probe(p + 2, 32, p, None) == -3
+    assert L.dip_gather_probe(p, 100, 2560, None, 10, p, None) == -1
+    assert L.dip_gather_probe(p, 100, 2000, p, 10, p, None) == -2
+    assert L.dip_gather_probe(p, 0, 2560, p, 10, p, None) == -2
     assert L.dip_set_tuning(2, 1025) == -6
     assert L.dip_set_tuning(2, -1) == -6
     assert L.dip_set_tuning(1, 7) == -6
