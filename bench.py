@@ -218,16 +218,40 @@ def cache_aware(args) -> int:
         cas.append(CADIPMlp(*w, buf, args.keep, args.ca, dev, down_transposed=True))
         if (layer + 1) % 16 == 0:
             print(f"[bench] {layer + 1}/{L} layers built", file=sys.stderr, flush=True)
-    counts = [zipf_counts(I, k, tokens=128, s=1.1, seed=1000 + layer) for layer in range(L)]
+    gen = torch.Generator(device=dev).manual_seed(1)
+    n_tok = args.warmup + args.steps
+    if args.ca_calib == "stream":
+        # anisotropic synthetic hidden states: a fixed direction mu plus
+        # iid noise of the same norm, so that some channels are selected
+        # far more often than others (as in real decode); the hot set comes
+        # from the selections of 64 calibration tokens of the same
+        # distribution, disjoint from the timed ones
+        import _dip_hip as K
+        mu = torch.randn(H, device=dev, generator=gen)
+
+        def draw(n):
+            return (mu + torch.randn(n, H, device=dev, generator=gen)).to(torch.bfloat16)
+
+        calib = draw(64)
+        counts = []
+        for c in cas:
+            cnt = torch.zeros(I, dtype=torch.long, device=dev)
+            for t in range(calib.shape[0]):
+                _, idx = K.gate_silu_topk(c.gate_qw, c.gate_sc, calib[t], c.k)
+                cnt.index_add_(0, idx.long(), torch.ones_like(idx, dtype=torch.long))
+            counts.append(cnt.cpu())
+        xs = draw(n_tok)
+        calib_desc = "selections of 64 calibration tokens (fixed direction + noise)"
+    else:
+        counts = [zipf_counts(I, k, tokens=128, s=1.1, seed=1000 + layer) for layer in range(L)]
+        xs = torch.randn(n_tok, H, device=dev, generator=gen).to(torch.bfloat16)
+        calib_desc = "Zipf(1.1) selection counts over 128 synthetic tokens (random x: hits = cache_frac)"
     calibrate_cache_from_counts(cas, counts)
     cache_n = cas[0].cache_n
     row = H // 2 + 2 * (H // 128)
     print(f"[bench] caches set: {cache_n} resident channels per layer "
           f"({2 * cache_n * row / 1e6:.1f} MB)", file=sys.stderr, flush=True)
 
-    gen = torch.Generator(device=dev).manual_seed(1)
-    n_tok = args.warmup + args.steps
-    xs = torch.randn(n_tok, H, device=dev, generator=gen).to(torch.bfloat16)
     hits = []
 
     def token(i):
@@ -272,8 +296,7 @@ def cache_aware(args) -> int:
         "data": "synthetic",
         "config": {
             "workload": f"{args.shape}-shape {L}-layer cache-aware DIP MLP decode, batch 1, "
-                        f"keep {args.keep}, cache_frac {args.ca}, Zipf(1.1) calibration over "
-                        f"128 synthetic tokens",
+                        f"keep {args.keep}, cache_frac {args.ca}, hot set from {calib_desc}",
             "hidden": H, "inter": I, "layers": L, "k": k, "cache_n": cache_n,
             "host_threads": buf.host_threads, "stream_chunk_rows": buf.stream_chunk,
         },
@@ -294,8 +317,8 @@ def read_ceiling(args) -> int:
     patterns, measured with the library's probe kernels (no arithmetic):
     a contiguous read of the gate matrix's bytes (67.584 MB) and of a whole
     layer's (148.685 MB), the up/down gather (15360 sorted random rows of
-    2560 B out of 25600, keep 0.6), and a device-to-device copy of each
-    size.  Buffers rotate through 8 copies (6 matrices for the gather) so
+    2560 B out of 25600, keep 0.6, and the same rows 5120 B wide), and a
+    device-to-device copy of each size.  Buffers rotate through 8 copies (6 matrices for the gather) so
     the memory-side cache holds none of them.  One JSON line."""
     import torch
     import _dip_hip as K
@@ -334,6 +357,13 @@ def read_ceiling(args) -> int:
         idxs.append(torch.sort(torch.randperm(n, generator=gen)[:k]).values.to(torch.int32).to(dev))
     us = timed(lambda r: K.gather_probe(mats[r % 6], idxs[r % 6], sink))
     out["gather_15360x2560B_of_25600"] = {"us": round(us, 2), "TB/s": round(k * rb / us / 1e6, 3)}
+    del mats
+    torch.cuda.empty_cache()
+    # the same rows twice as wide (an up row and a down row side by side)
+    mats = [torch.ones(n, 2 * rb, dtype=torch.uint8, device=dev) for _ in range(6)]
+    us = timed(lambda r: K.gather_probe(mats[r % 6], idxs[r % 6], sink))
+    out["gather_15360x5120B_of_25600"] = {"us": round(us, 2),
+                                          "TB/s": round(2 * k * rb / us / 1e6, 3)}
     print(json.dumps(out), flush=True)
     return 0
 
@@ -365,6 +395,11 @@ def main(argv=None):
                     help="instead of the resident stack, time cache-aware DIP decode with this "
                          "fraction of channels resident (misses streamed from pinned host "
                          "memory over PCIe); prints its own JSON line")
+    ap.add_argument("--ca-calib", choices=("zipf", "stream"), default="zipf",
+                    help="--ca hot set: seeded Zipf counts with iid random x (hits equal "
+                         "cache_frac), or the counted selections of 64 calibration tokens of an "
+                         "anisotropic decode stream (fixed direction + noise) that the timed "
+                         "tokens also follow")
     ap.add_argument("--ceiling", action="store_true",
                     help="instead of the decode step, measure the read bandwidth of the "
                          "step's access patterns with probe kernels; prints its own JSON line")
