@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import dip_oracle as O
-from gpu_util import host_bf16, ulp_diff
+from gpu_util import host_bf16, rel_err, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -277,3 +277,29 @@ def test_mlp_decode_rmsnorm_equals_mlp_decode_on_its_x(K):
                     _assert_same(a[:4], b, f"H={H} token {t}")
                 else:
                     _assert_step(a[:4], b, f"H={H} token {t} (state)")
+
+
+def test_stack_qwen3_32b_shape_two_layers(K):
+    """A 2-layer DIPStack at the Qwen3-32B layer shape (H=5120, I=25600,
+    keep 0.6) with per-layer speculation state and the shared workspace,
+    replayed as one HIP graph: over 3 tokens every layer's y is within 1e-2
+    of the oracle's decode forward on that layer's weights, and the shared
+    idx (the last layer's) is the top-k of the shared g."""
+    from dip_stack import DIPStack
+    H, I = 5120, 25600
+    stack = DIPStack(H, I, 2, 0.6, "cuda", seed=31, spec=True)
+    host = [tuple(lw[n].cpu().numpy() if n.endswith("_qw") else host_bf16(lw[n])
+                  for n in ("gate_qw", "gate_sc", "up_qw", "up_sc", "down_t_qw", "down_t_sc"))
+            for lw in stack.w]
+    stack.capture()
+    for t in range(3):
+        x = O.make_x(H, seed=40 + t)
+        stack.step(torch.from_numpy(x.view(np.int16)).to("cuda").view(torch.bfloat16))
+        torch.cuda.synchronize()
+        g_h = host_bf16(stack.g)
+        assert np.array_equal(stack.idx.cpu().numpy(), O.topk_select(g_h, stack.k)), t
+        for i, w in enumerate(host):
+            ref = O.dip_forward(*w, x, stack.k)
+            err = rel_err(host_bf16(stack.y[i]), ref["y_f64"])
+            print(f"token {t} layer {i}: rel err {err:.2e}", flush=True)
+            assert err < 1e-2, (t, i)
