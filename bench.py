@@ -317,8 +317,8 @@ def read_ceiling(args) -> int:
     patterns, measured with the library's probe kernels (no arithmetic):
     a contiguous read of the gate matrix's bytes (67.584 MB) and of a whole
     layer's (148.685 MB), the up/down gather (15360 sorted random rows of
-    2560 B out of 25600, keep 0.6, and the same rows 5120 B wide), and a
-    device-to-device copy of each size.  Buffers rotate through 8 copies (6 matrices for the gather) so
+    2560 B out of 25600, keep 0.6, each row read whole by one 32-lane
+    group), and a device-to-device copy of each size.  Buffers rotate through 8 copies (6 matrices for the gather) so
     the memory-side cache holds none of them.  One JSON line."""
     import torch
     import _dip_hip as K
@@ -357,13 +357,6 @@ def read_ceiling(args) -> int:
         idxs.append(torch.sort(torch.randperm(n, generator=gen)[:k]).values.to(torch.int32).to(dev))
     us = timed(lambda r: K.gather_probe(mats[r % 6], idxs[r % 6], sink))
     out["gather_15360x2560B_of_25600"] = {"us": round(us, 2), "TB/s": round(k * rb / us / 1e6, 3)}
-    del mats
-    torch.cuda.empty_cache()
-    # the same rows twice as wide (an up row and a down row side by side)
-    mats = [torch.ones(n, 2 * rb, dtype=torch.uint8, device=dev) for _ in range(6)]
-    us = timed(lambda r: K.gather_probe(mats[r % 6], idxs[r % 6], sink))
-    out["gather_15360x5120B_of_25600"] = {"us": round(us, 2),
-                                          "TB/s": round(2 * k * rb / us / 1e6, 3)}
     print(json.dumps(out), flush=True)
     return 0
 

@@ -4,10 +4,10 @@
 //   * contiguous: one buffer read front to back, grid-stride, each thread
 //     kProbeRing 16-byte non-temporal loads in flight (the gate's pattern:
 //     whole rows of one matrix);
-//   * gathered: k rows of row_bytes picked by a sorted index list (the
-//     up/down rows of the selected channels), a 512-thread workgroup per
-//     tile of consecutive positions and 512-byte column segment, 16
-//     streams of 32 lanes, kProbeRing rows in flight per lane.
+//   * gathered: k rows of 2560 bytes picked by a sorted index list (the
+//     up/down rows of the selected channels at H = 5120), each row read
+//     whole by one 32-lane group (five 512-byte load instructions, the up
+//     rows' layout), kProbeRing rows in flight per group.
 // A sink word is written only if the folded value hits a fixed constant
 // (practically never), which keeps every load live.
 #include <algorithm>
@@ -39,36 +39,48 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict
   if (acc == kProbeMagic) sink[0] = acc;
 }
 
-constexpr int kGatherLanes = 32;  // 512-byte column segments
-constexpr int kGatherThreads = 512;
+constexpr int kGatherLanes = 32;  // one row per 32-lane group, 512 bytes per load instruction
+constexpr int kGatherThreads = 256;
+constexpr int kGatherChunks = 5;  // 16-byte chunks per lane: 2560-byte rows
 
+// A 32-lane group reads whole rows: lane l loads chunks l, l + 32, ... of
+// its row (the up rows' layout), kProbeRing rows in flight; group q of the
+// grid takes the rows at positions q, q + groups, ... of the sorted list.
 __global__ __launch_bounds__(kGatherThreads) void gather_probe_kernel(
     const uint4* __restrict__ m, const int32_t* __restrict__ idx, int nrows, int k, int row16,
-    int col_blocks, int pos_per_tile, uint32_t* sink) {
-  const int rb = blockIdx.x / col_blocks, cb = blockIdx.x % col_blocks;
-  constexpr int streams = kGatherThreads / kGatherLanes;
-  const int st = threadIdx.x / kGatherLanes, l = threadIdx.x % kGatherLanes;
-  const int p0 = rb * pos_per_tile, p1 = min(k, p0 + pos_per_tile);
-  const int n = p1 > p0 + st ? (p1 - p0 - st + streams - 1) / streams : 0;
-  const size_t col = (size_t)cb * kGatherLanes + l;
+    uint32_t* sink) {
+  const int groups = gridDim.x * (kGatherThreads / kGatherLanes);
+  const int grp = blockIdx.x * (kGatherThreads / kGatherLanes) + threadIdx.x / kGatherLanes;
+  const int l = threadIdx.x % kGatherLanes;
+  const int n = k > grp ? (k - grp + groups - 1) / groups : 0;
   auto row_at = [&](int i) {  // clamped to my last row (0 when I have none or it is out of range)
-    const int v = idx[p0 + st + streams * min(i, max(n - 1, 0))];
+    const int v = idx[grp + groups * min(i, max(n - 1, 0))];
     return n > 0 && (unsigned)v < (unsigned)nrows ? v : 0;
   };
   uint32_t acc = 0;
-  uint4 ring[kProbeRing];
+  uint4 ring[kProbeRing][kGatherChunks];
+  auto load = [&](int i, int d) {
+    const uint4* r = m + (size_t)row_at(i) * row16 + l;
 #pragma unroll
-  for (int d = 0; d < kProbeRing; ++d) ring[d] = ldg_nt(m + (size_t)row_at(d) * row16 + col);
+    for (int c = 0; c < kGatherChunks; ++c) ring[d][c] = ldg_nt(r + kGatherLanes * c);
+  };
+#pragma unroll
+  for (int d = 0; d < kProbeRing; ++d) load(d, d);
   const int rounds = (n + kProbeRing - 1) / kProbeRing;
   for (int r = 0; r + 1 < rounds; ++r) {
 #pragma unroll
     for (int d = 0; d < kProbeRing; ++d) {
-      acc ^= ring[d].x ^ ring[d].y ^ ring[d].z ^ ring[d].w;
-      ring[d] = ldg_nt(m + (size_t)row_at((r + 1) * kProbeRing + d) * row16 + col);
+#pragma unroll
+      for (int c = 0; c < kGatherChunks; ++c)
+        acc ^= ring[d][c].x ^ ring[d][c].y ^ ring[d][c].z ^ ring[d][c].w;
+      load((r + 1) * kProbeRing + d, d);
     }
   }
 #pragma unroll
-  for (int d = 0; d < kProbeRing; ++d) acc ^= ring[d].x ^ ring[d].y ^ ring[d].z ^ ring[d].w;
+  for (int d = 0; d < kProbeRing; ++d)
+#pragma unroll
+    for (int c = 0; c < kGatherChunks; ++c)
+      acc ^= ring[d][c].x ^ ring[d][c].y ^ ring[d][c].z ^ ring[d][c].w;
   if (acc == kProbeMagic) sink[0] = acc;
 }
 }  // namespace
@@ -90,16 +102,12 @@ extern "C" int dip_gather_probe(const void* rows, int64_t nrows, int64_t row_byt
                                 const int32_t* idx, int64_t k, uint32_t* sink, void* stream) {
   if (!rows || !idx || !sink) return DIP_ERR_NULL;
   if (nrows <= 0 || k <= 0 || k > INT32_MAX || nrows > INT32_MAX ||
-      row_bytes % (16 * kGatherLanes) != 0 || row_bytes <= 0 || row_bytes / 16 > INT32_MAX)
+      row_bytes != 16 * kGatherLanes * kGatherChunks)
     return DIP_ERR_SHAPE;
   if (!aligned16(rows)) return DIP_ERR_ALIGN;
-  const int col_blocks = (int)(row_bytes / (16 * kGatherLanes));
-  // about two tiles per CU
-  const int64_t rb = std::max<int64_t>(1, std::min<int64_t>(k, 2LL * device_cus() / col_blocks));
-  const int pos = (int)((k + rb - 1) / rb);
-  const int tiles = (int)((k + pos - 1) / pos) * col_blocks;
-  hipLaunchKernelGGL(gather_probe_kernel, dim3((unsigned)tiles), dim3(kGatherThreads), 0,
-                     (hipStream_t)stream, static_cast<const uint4*>(rows), idx, (int)nrows, (int)k,
-                     (int)(row_bytes / 16), col_blocks, pos, sink);
+  hipLaunchKernelGGL(gather_probe_kernel, dim3((unsigned)(2 * device_cus())),
+                     dim3(kGatherThreads), 0, (hipStream_t)stream,
+                     static_cast<const uint4*>(rows), idx, (int)nrows, (int)k,
+                     (int)(row_bytes / 16), sink);
   return hip_status(hipGetLastError());
 }

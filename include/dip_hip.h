@@ -56,7 +56,7 @@ int dip_version(void);
  * roofline this build is measured against).  dip_read_probe reads `bytes`
  * (a multiple of 16) of src front to back; dip_gather_probe reads the rows
  * idx[0..k) (sorted ids below nrows; others read row 0) of a row-major
- * matrix of row_bytes (a multiple of 512) per row.  Neither computes
+ * matrix of 2560-byte rows, each row whole by one 32-lane group.  Neither computes
  * anything; `sink` (4 bytes) is written only if the folded words hit a
  * fixed constant.
  */

@@ -90,7 +90,7 @@ def test_argument_rejection_before_launch():
     assert L.dip_read_probe(p, 24, p, None) == -2
     assert L.dip_read_probe(p + 2, 32, p, None) == -3
     assert L.dip_gather_probe(p, 100, 2560, None, 10, p, None) == -1
-    assert L.dip_gather_probe(p, 100, 2000, p, 10, p, None) == -2
+    assert L.dip_gather_probe(p, 100, 5120, p, 10, p, None) == -2
     assert L.dip_gather_probe(p, 0, 2560, p, 10, p, None) == -2
     assert L.dip_set_tuning(2, 1025) == -6
     assert L.dip_set_tuning(2, -1) == -6
