@@ -1,7 +1,8 @@
 """dip_mlp_decode_noalloc (the decode step whose workspace is the library's
 per-GPU scratch array) against dip_mlp_decode with a caller workspace,
 through the C ABI: two calls in a row, the second with a smaller layer, with
-and without the speculation state, plus a shape the scratch cannot hold.
+and without the speculation state (both step forms), plus a shape the
+scratch cannot hold.
 Outputs must be bit-identical (the same kernels on the same inputs)."""
 import numpy as np
 import pytest
@@ -32,8 +33,18 @@ def _outs(H, I, k, fill):
             torch.full((k,), fill, dtype=torch.bfloat16, device=d))
 
 
-@pytest.mark.parametrize("spec", [False, True])
-def test_noalloc_equals_workspace_entry_point(K, spec):
+@pytest.mark.parametrize("spec,step", [(False, 0), (True, 0), (True, 1)],
+                         ids=["stagewise", "four-launch", "fused"])
+def test_noalloc_equals_workspace_entry_point(K, spec, step):
+    old = K.get_tuning("step")
+    K.set_tuning("step", step)
+    try:
+        _noalloc_cases(K, spec)
+    finally:
+        K.set_tuning("step", old)
+
+
+def _noalloc_cases(K, spec):
     cases = [(5120, 25600, 0.6, 0), (1024, 3072, 0.3, 1)]   # second call smaller
     st_ref = K.mlp_state(torch.device("cuda:0")) if spec else None
     st_new = K.mlp_state(torch.device("cuda:0")) if spec else None
