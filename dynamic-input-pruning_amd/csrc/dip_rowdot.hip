@@ -106,10 +106,12 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   for (int i = 0; i < ROWS; ++i) {
     RowRegs<CH>& R = ring[i % D];
     float acc = row_dot_part<CH>(R, xp, bias);
-    acc = group_sum<LPR>(acc);
-    mine = l == i ? acc : mine;
+    // the slot's registers are free once its products are taken: reload it
+    // before the cross-lane reduction, so the next row is in flight sooner
     if (i + D < ROWS)
       load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + i + D, 64), l, row_bytes, ngroups, R);
+    acc = group_sum<LPR>(acc);
+    mine = l == i ? acc : mine;
   }
 
   // 6. epilogue: lane l finishes row l
