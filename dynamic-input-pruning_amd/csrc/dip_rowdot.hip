@@ -42,15 +42,6 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   const int nchunks = a.in_features / kChunkCols;
   const int grp = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
   const int ngrp = a.ngrp;
-  // the fused step's speculation key and key band (the layer state; the
-  // finish launch of the step rewrites it, never this launch)
-  [[maybe_unused]] uint32_t cand_key = 0, band = 0;
-  if constexpr (SRC == kContig && EPI == kSilu)
-    if (a.cand_count) {
-      cand_key = a.spec[1];
-      band = a.spec[2];
-    }
-  if (a.rotate && blockIdx.x == 0 && threadIdx.x == 0) a.rotate[0] = a.rotate[1];
 
   // 1. x loads first (XS: one chunk per thread, index clamped)
   uint4 xs[XS ? 4 : CH * 4];
@@ -75,6 +66,10 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
     }
   }
 
+  // (the x loads stay ahead of the row loads: staging x then waits only for
+  // them, not for the first rows as well)
+  __builtin_amdgcn_sched_barrier(0);
+
   // 2. row ids: lane l resolves row l of the group (clamped, unconditional)
   const long long jl = grp + (long long)l * ngrp;
   const bool valid_l = l < ROWS && jl < a.nrows;
@@ -85,6 +80,24 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
 #pragma unroll
   for (int d = 0; d < D; ++d)
     load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups, ring[d]);
+
+  // 3b. The layer state of a decode step: the fused step's speculation key
+  // and key band (its finish launch rewrites them, never this launch), and
+  // workgroup 0's rotation of the four-launch step's next key into the slot
+  // in use (stored at the end).  Loaded after x and the first rows, so that
+  // waiting for those never waits for these; read at a lane-dependent offset
+  // that is always 0 (in_features < 2^30), since as a uniform value the
+  // compiler would move it to a scalar register right after the load and
+  // wait for it there.
+  const uint32_t zero = threadIdx.x & ((uint32_t)a.in_features >> 30);
+  [[maybe_unused]] uint32_t cand_key = 0, band = 0;
+  if constexpr (SRC == kContig && EPI == kSilu)
+    if (a.cand_count) {
+      cand_key = a.spec[1 + zero];
+      band = a.spec[2 + zero];
+    }
+  const bool rot = a.rotate && blockIdx.x == 0 && threadIdx.x == 0;
+  const uint32_t rot1 = rot ? a.rotate[1 + zero] : 0u;
 
   // 4. x pairs into VGPRs
   uint32_t xp[CH][4][4];
@@ -137,10 +150,10 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   }
   if constexpr (SRC == kContig && EPI == kSilu) {
     if (a.cand_count) {  // uniform: the decode gate of the fused step
-      // per wave: candidate / band / above counts and the largest key; then
-      // each list gets its entries in lane order, waves in order
-      __shared__ uint32_t wcnt[kRowdotMaxThreads / 64][3];
-      __shared__ float wmx[kRowdotMaxThreads / 64];
+      // per wave: candidate / band / above counts and the largest key (one
+      // 16-byte LDS record, all read under one wait); then each list gets
+      // its entries in lane order, waves in order
+      __shared__ uint4 wrec[kRowdotMaxThreads / 64];
       const int wave = threadIdx.x >> 6;
       const uint32_t kk = v & 0x7FFFu;
       const bool ok = valid_l && kk <= 0x7F80u;
@@ -151,22 +164,23 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
       const uint64_t m = __ballot(cand), mb = __ballot(inb), ma = __ballot(abv);
       float mk = ok ? bf16_to_f32(kk < 0x80u ? 0u : kk) : -1.f;
       mk = group_max<64>(mk);
-      if (lane == 0) {
-        wcnt[wave][0] = (uint32_t)__popcll(m);
-        wcnt[wave][1] = (uint32_t)__popcll(mb);
-        wcnt[wave][2] = (uint32_t)__popcll(ma);
-        wmx[wave] = mk;
-      }
+      if (lane == 0)
+        wrec[wave] = make_uint4((uint32_t)__popcll(m), (uint32_t)__popcll(mb),
+                                (uint32_t)__popcll(ma), __float_as_uint(mk));
       __syncthreads();
       uint32_t base = 0, total = 0, bbase = 0, btotal = 0, atotal = 0;
       float bm = -1.f;
-      for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-        base += w < wave ? wcnt[w][0] : 0u;
-        bbase += w < wave ? wcnt[w][1] : 0u;
-        total += wcnt[w][0];
-        btotal += wcnt[w][1];
-        atotal += wcnt[w][2];
-        bm = fmaxf(bm, wmx[w]);
+      const int nwv = (int)(blockDim.x >> 6);
+#pragma unroll
+      for (int w = 0; w < kRowdotMaxThreads / 64; ++w) {
+        const uint4 r = wrec[w];  // records past the block's waves are not used
+        const bool in = w < nwv;
+        base += in && w < wave ? r.x : 0u;
+        bbase += in && w < wave ? r.y : 0u;
+        total += in ? r.x : 0u;
+        btotal += in ? r.y : 0u;
+        atotal += in ? r.z : 0u;
+        bm = in ? fmaxf(bm, __uint_as_float(r.w)) : bm;
       }
       const uint64_t below = (1ull << lane) - 1ull;
       const uint32_t entry = (uint32_t)jl | (v << 16);
@@ -181,6 +195,7 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
       }
     }
   }
+  if (rot) a.rotate[0] = rot1;
 }
 
 // ---------------------------------------------------------------------------
