@@ -170,7 +170,6 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int nchunks = sp.hidden / kChunkCols;
-  const uint32_t sk = sp.state[0];
   const int c0 = u * sp.chan_per_wg;
   const int c1 = min(c0 + sp.chan_per_wg, n);
   const int sw = (u == 0) ? 0 : (u == nspec / 2 ? 1 : -1);
@@ -181,6 +180,10 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
   load_x_chunk(sp.x, nchunks, xs);
   const int c = c0 + tid;
   const uint32_t gb = c < c1 ? (uint32_t)g[c] : 0u;
+  // the speculation key at a lane-dependent offset that is always 0 (hidden
+  // < 2^30): a uniform load would be a scalar load, waited for before the
+  // load of g is even issued; this way both are in flight together
+  const uint32_t sk = sp.state[threadIdx.x & ((uint32_t)sp.hidden >> 30)];
   const bool f = c < c1 && (gb & 0x7FFFu) >= sk;
   const uint64_t m = __ballot(f);
   if (lane == 0) wcnt[wave] = (uint32_t)__popcll(m);
