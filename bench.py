@@ -377,6 +377,9 @@ def main(argv=None):
     ap.add_argument("--no-spec", action="store_true",
                     help="run every layer stage by stage (no speculative up rows during the "
                          "top-k); same outputs, five launches per layer instead of four")
+    ap.add_argument("--no-gm", action="store_true",
+                    help="the down stage reads down_t's [inter, hidden/128] scales instead of "
+                         "their group-major copy")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel eagerly instead of replaying the captured graph "
                          "(for counter collection, which profiles each dispatch)")
@@ -421,7 +424,8 @@ def main(argv=None):
     if args.checkpoint:
         print(f"[bench] loading MLPs of {args.checkpoint} keep={args.keep}", file=sys.stderr,
               flush=True)
-        stack = DIPStack.from_checkpoint(args.checkpoint, args.keep, dev, spec=not args.no_spec)
+        stack = DIPStack.from_checkpoint(args.checkpoint, args.keep, dev, spec=not args.no_spec,
+                                         scales_gm=not args.no_gm)
         shape = dict(hidden=stack.hidden, inter=stack.inter, layers=stack.layers)
     else:
         shape = dict(SHAPES[args.shape])
@@ -430,7 +434,7 @@ def main(argv=None):
         print(f"[bench] building {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
               flush=True)
         stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0,
-                         spec=not args.no_spec)
+                         spec=not args.no_spec, scales_gm=not args.no_gm)
     gen = torch.Generator(device=dev).manual_seed(1)
     n_tok = args.warmup + args.steps
     xs = (torch.randn(n_tok, shape["hidden"], device=dev, generator=gen)).to(torch.bfloat16)
@@ -530,6 +534,7 @@ def main(argv=None):
                         ("N(0,0.02) draws" if not args.checkpoint else "from the checkpoint")),
             "activations": "bf16, fp32 accumulate",
             "speculative_up": not args.no_spec,
+            "down_scales": "row-major" if args.no_gm else "group-major copy",
             "bytes_per_token": stack.bytes_per_token,
         },
         "step_hbm_gbs": round(step_gbs, 1),

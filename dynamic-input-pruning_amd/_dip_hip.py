@@ -55,17 +55,18 @@ _SIGS = {
     "dip_ca_assemble": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_dequant_rows": ([_p, _p, _p, _p, _i64, _i64, _i64, _i32, _p], _i32),
     "dip_mlp_workspace_size": ([_i64, _i64, _i64], _sz),
-    "dip_mlp_decode": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz,
-                        _p, _p], _i32),
+    "dip_mlp_decode": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p,
+                        _sz, _p, _p], _i32),
     "dip_mlp_state_size": ([], _sz),
-    "dip_mlp_decode_noalloc": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p,
-                                _p], _i32),
-    "dip_mlp_decode_rmsnorm": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p,
-                                _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p, _p], _i32),
+    "dip_mlp_decode_noalloc": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
+                                _p, _p], _i32),
+    "dip_mlp_decode_rmsnorm": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, ctypes.c_float, _p, _p,
+                                _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p, _p], _i32),
     "dip_gate_silu_topk_spec": ([_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p,
                                  _p], _i32),
-    "dip_int4_gather_down_by_channel": ([_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p],
-                                        _i32),
+    "dip_int4_gather_down_by_channel": ([_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz,
+                                         _p], _i32),
+    "dip_scales_group_major": ([_p, _p, _i64, _i64, _p], _i32),
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
     "dip_read_probe": ([_p, _sz, _p, _p], _i32),
     "dip_gather_probe": ([_p, _i64, _i64, _p, _i64, _p, _p], _i32),
@@ -370,11 +371,14 @@ def int4_gather_down(down_t, scales, h, indices=None, out=None):
     return out
 
 
-def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out=None):
+def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out=None,
+                                scales_gm=None):
     """y[o] = bf16(sum_j h_full[indices[j]] * (q*s)[indices[j], o]) with h
     indexed by channel (the decode step's form); h_out[j] (if given) gets
-    h_full[indices[j]]."""
+    h_full[indices[j]].  scales_gm: the group-major copy of scales
+    (scales_group_major), read instead of scales when given."""
     down_t, scales, rows, out_f = _weights(down_t, scales, "int4_gather_down_by_channel")
+    scales_gm = _scales_gm(scales_gm, scales)
     dev = _dev(down_t, scales, h_full, indices)
     h_full = _want(h_full.reshape(-1), torch.bfloat16, "h_full", (rows,))
     indices = _indices(indices)
@@ -385,8 +389,9 @@ def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out
         out = torch.empty(out_f, dtype=torch.bfloat16, device=dev)
     nbytes = lib.dip_gather_down_workspace_size(k, out_f)
     ws = workspace(dev, nbytes, "down")
-    _check(lib.dip_int4_gather_down_by_channel(_ptr(down_t), _ptr(scales), _ptr(h_full),
-                                               _ptr(indices), _ptr(out), _ptr(h_out), rows,
+    _check(lib.dip_int4_gather_down_by_channel(_ptr(down_t), _ptr(scales), _ptr(scales_gm),
+                                               _ptr(h_full), _ptr(indices), _ptr(out),
+                                               _ptr(h_out), rows,
                                                out_f, k, _ptr(ws), ws.numel(), _stream(dev)),
            "dip_int4_gather_down_by_channel")
     return out
@@ -511,6 +516,31 @@ def transpose_down_int4(down_qw, down_sc):
     return tq, ts
 
 
+def scales_group_major(scales: torch.Tensor) -> torch.Tensor:
+    """The group-major copy [groups, rows] of a [rows, groups] bf16 scale
+    matrix (dip_scales_group_major): the layout the decode step's down stage
+    reads down_t's scales in when given one."""
+    if scales.dtype != torch.bfloat16 or scales.dim() != 2 or not scales.is_contiguous():
+        raise RuntimeError("scales must be a contiguous 2-D bf16 tensor")
+    rows, groups = scales.shape
+    out = torch.empty(groups, rows, dtype=torch.bfloat16, device=scales.device)
+    _check(lib.dip_scales_group_major(_ptr(scales), _ptr(out), rows, groups,
+                                      _stream(scales.device)), "dip_scales_group_major")
+    return out
+
+
+def _scales_gm(scales_gm, scales):
+    """scales_gm checked against its row-major scales (None passes)."""
+    if scales_gm is None:
+        return None
+    rows, groups = scales.shape
+    if (scales_gm.dtype != torch.bfloat16 or tuple(scales_gm.shape) != (groups, rows)
+            or not scales_gm.is_contiguous() or scales_gm.device != scales.device):
+        raise RuntimeError(f"scales_gm must be a contiguous bf16 [{groups}, {rows}] tensor on "
+                           f"{scales.device} (scales_group_major of the scales)")
+    return scales_gm
+
+
 def mlp_workspace_bytes(hidden: int, inter: int, k: int) -> int:
     return lib.dip_mlp_workspace_size(hidden, inter, k)
 
@@ -522,13 +552,14 @@ def mlp_state(device) -> torch.Tensor:
 
 
 def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=None, g=None,
-               idx=None, h=None, ws=None, state=None):
+               idx=None, h=None, ws=None, state=None, down_t_sc_gm=None):
     """One resident DIP MLP decode step; returns (y, g, idx, h).
 
     state: this layer's mlp_state() tensor, kept across calls.  With it the
     step overlaps the top-k with up rows of the channels the last call ranked
     highest (same outputs, bit for bit); without it the step runs stage by
-    stage."""
+    stage.  down_t_sc_gm: scales_group_major(down_t_sc), which the down
+    stage then reads (same outputs, bit for bit)."""
     gate_qw, gate_sc, inter, hidden = _weights(gate_qw, gate_sc, "gate")
     up_qw, up_sc, inter2, hidden2 = _weights(up_qw, up_sc, "up")
     down_t_qw, down_t_sc, inter3, hidden3 = _weights(down_t_qw, down_t_sc, "down_t")
@@ -556,8 +587,10 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
         if (state.device != dev or state.dtype != torch.int32 or not state.is_contiguous()
                 or state.numel() * 4 < lib.dip_mlp_state_size()):
             raise RuntimeError("state must be this device's mlp_state() tensor")
+    down_t_sc_gm = _scales_gm(down_t_sc_gm, down_t_sc)
     _check(lib.dip_mlp_decode(_ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc),
-                              _ptr(down_t_qw), _ptr(down_t_sc), _ptr(x), _ptr(y), _ptr(g),
+                              _ptr(down_t_qw), _ptr(down_t_sc), _ptr(down_t_sc_gm), _ptr(x),
+                              _ptr(y), _ptr(g),
                               _ptr(idx), _ptr(h), hidden, inter, k, _ptr(ws), ws.numel(),
                               None if state is None else _ptr(state), _stream(dev)),
            "dip_mlp_decode")
@@ -565,7 +598,7 @@ def mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y=
 
 
 def mlp_decode_noalloc(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, k, *, y, g,
-                       idx, h, state=None):
+                       idx, h, state=None, down_t_sc_gm=None):
     """mlp_decode with the workspace in the library's per-GPU scratch array
     (dip_mlp_decode_noalloc): the caller passes every output, nothing is
     allocated.  Calls that overlap on one GPU race on the scratch array."""
@@ -591,8 +624,10 @@ def mlp_decode_noalloc(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, 
         if (state.device != dev or state.dtype != torch.int32 or not state.is_contiguous()
                 or state.numel() * 4 < lib.dip_mlp_state_size()):
             raise RuntimeError("state must be this device's mlp_state() tensor")
+    down_t_sc_gm = _scales_gm(down_t_sc_gm, down_t_sc)
     _check(lib.dip_mlp_decode_noalloc(_ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc),
-                                      _ptr(down_t_qw), _ptr(down_t_sc), _ptr(x), _ptr(y), _ptr(g),
+                                      _ptr(down_t_qw), _ptr(down_t_sc), _ptr(down_t_sc_gm),
+                                      _ptr(x), _ptr(y), _ptr(g),
                                       _ptr(idx), _ptr(h), hidden, inter, k,
                                       None if state is None else _ptr(state), _stream(dev)),
            "dip_mlp_decode_noalloc")
@@ -726,7 +761,7 @@ def decode_attention_fused(qkv, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_ca
 
 def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res, add, norm_w,
                        eps: float, k, *, res_out=None, x_out=None, y=None, g=None, idx=None,
-                       h=None, ws=None, state=None):
+                       h=None, ws=None, state=None, down_t_sc_gm=None):
     """mlp_decode on x = RMSNorm(res + add) * norm_w, the norm folded into the
     gate launch; the updated residual goes to res_out (if given) and x to
     x_out.  Returns (y, g, idx, h, x_out)."""
@@ -760,9 +795,10 @@ def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res
     if state is not None and (state.device != dev or state.dtype != torch.int32
                               or state.numel() * 4 < lib.dip_mlp_state_size()):
         raise RuntimeError("state must be this device's mlp_state() tensor")
+    down_t_sc_gm = _scales_gm(down_t_sc_gm, down_t_sc)
     _check(lib.dip_mlp_decode_rmsnorm(
         _ptr(gate_qw), _ptr(gate_sc), _ptr(up_qw), _ptr(up_sc), _ptr(down_t_qw), _ptr(down_t_sc),
-        _ptr(res), _ptr(add), _ptr(norm_w), float(eps), _ptr(res_out), _ptr(x_out), _ptr(y),
+        _ptr(down_t_sc_gm), _ptr(res), _ptr(add), _ptr(norm_w), float(eps), _ptr(res_out), _ptr(x_out), _ptr(y),
         _ptr(g), _ptr(idx), _ptr(h), hidden, inter, k, _ptr(ws), ws.numel(),
         None if state is None else _ptr(state), _stream(dev)), "dip_mlp_decode_rmsnorm")
     return y, g, idx, h, x_out

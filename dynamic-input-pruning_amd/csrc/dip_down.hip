@@ -20,8 +20,9 @@
 // costs one convert and one FMA: acc += (q/16) * (16*h*s).
 //
 // Reduction, deterministic and without float atomics:
-//   1. the slots of a block are summed through LDS in a fixed order (two
-//      halves of 16 accumulators, to keep the LDS footprint small) and the
+//   1. the slots of a wave are summed in registers (DPP rotations, then
+//      permlane swaps that halve the live accumulators at each step), the
+//      four waves' sums are added in wave order through 4 KB of LDS, and the
 //      block stores its fp32 partial row segment;
 //   2. a reduce kernel sums the row blocks' partials of every output in a
 //      fixed order and rounds to bf16.
@@ -41,12 +42,12 @@ constexpr int kRedOut = 32;              // outputs per reduce block
 constexpr int kRedSplit = 8;             // interleaved row-block splits per output
 }  // namespace
 
-template <int LPR, int SRC>
+template <int LPR, int SRC, int SL>
 __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   static_assert(LPR % kChunksPerGroup == 0 && LPR / kChunksPerGroup <= 2, "groups per slot");
   constexpr int kSlots = kThreads / LPR;
   constexpr int kCols = LPR * kDownAcc;  // outputs per column block
-  __shared__ float red[down_red_floats<LPR>()];
+  __shared__ __align__(16) float red[down_red_floats<LPR>()];
 
   // XCD-aware tile order: workgroups go to the 8 XCDs round-robin, so tile
   // (rb, cb) runs as workgroup b with b % 8 == rb % 8.  All column blocks of
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   constexpr int NG = LPR / kChunksPerGroup;
   const int g0 = cb * LPR / kChunksPerGroup;
   uint32_t s_l[NG];
-  load_down_scales<SRC, NG>(a, rid_l, g0, ngroups, s_l);
+  load_down_scales<SRC, NG, SL>(a, rid_l, g0, ngroups, s_l);
 
   DownRow ring[LPR];
 #pragma unroll
@@ -90,8 +91,7 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
 #pragma unroll
   for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
   down_accumulate<LPR, NG>(ring, f_l, cc0 / kChunksPerGroup - g0, gbase, acc);
-  down_block_partial<LPR, false>(acc, red, a.partial + (size_t)rb * a.out_features +
-                                               (size_t)cb * kCols, slot, l);
+  down_block_partial<LPR>(acc, red, a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols);
 }
 
 // y[o] = bf16(sum over row blocks rb of partial[rb][o]), rb ascending in
@@ -156,14 +156,21 @@ void launch_reduce(const float* partial, int row_blocks, int out_features, uint1
                        row_blocks, out_features, y);
 }
 
-template <int LPR>
+template <int LPR, int SL>
 void launch_down(int src, const DownArgs& a, int blocks, hipStream_t stream) {
-  if (src == kContig)
-    hipLaunchKernelGGL((down_kernel<LPR, kContig>), dim3(blocks), dim3(kThreads), 0, stream, a);
-  else if (src == kGather)
-    hipLaunchKernelGGL((down_kernel<LPR, kGather>), dim3(blocks), dim3(kThreads), 0, stream, a);
-  else
-    hipLaunchKernelGGL((down_kernel<LPR, kDual>), dim3(blocks), dim3(kThreads), 0, stream, a);
+  if constexpr (SL == kScGm) {
+    if (src == kContig)
+      hipLaunchKernelGGL((down_kernel<LPR, kContig, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((down_kernel<LPR, kGather, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
+  } else {
+    if (src == kContig)
+      hipLaunchKernelGGL((down_kernel<LPR, kContig, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
+    else if (src == kGather)
+      hipLaunchKernelGGL((down_kernel<LPR, kGather, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((down_kernel<LPR, kDual, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
+  }
 }
 
 }  // namespace
@@ -187,7 +194,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
              uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream, int h_by_row,
-             uint16_t* h_out) {
+             uint16_t* h_out, const uint16_t* sc_gm) {
   if (!qw_a || !sc_a || !y) return DIP_ERR_NULL;
   if (out_features <= 0 || out_features % kGroupSize != 0 || out_features > (1 << 20))
     return DIP_ERR_SHAPE;
@@ -196,6 +203,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
       rows_b >= INT32_MAX - 1)
     return DIP_ERR_SHAPE;
   if (!aligned16(qw_a) || (qw_b && !aligned16(qw_b))) return DIP_ERR_ALIGN;
+  if (sc_gm && src == kDual) return DIP_ERR_ARG;
   if (k > 0 && !h) return DIP_ERR_NULL;
   if (k == 0) {
     hipLaunchKernelGGL(down_zero_kernel, dim3((unsigned)((out_features + 255) / 256)), dim3(256),
@@ -212,6 +220,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.sc_a = sc_a;
   a.qw_b = qw_b;
   a.sc_b = sc_b;
+  a.sc_gm = sc_gm;
   a.qw_safe = rows_a > 0 ? qw_a : qw_b;
   a.sc_safe = rows_a > 0 ? sc_a : sc_b;
   a.h = h;
@@ -227,8 +236,20 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.col_blocks = (int)(out_features / (kChunkCols * lpr));
   a.row_blocks = (int)((k + kRowsPerBlock - 1) / kRowsPerBlock);
   const int blocks = (a.row_blocks + kXcds - 1) / kXcds * kXcds * a.col_blocks;
-  if (lpr == 8) launch_down<8>(src, a, blocks, stream);
-  else launch_down<4>(src, a, blocks, stream);
+  // the scale pair of a slot is one 32-bit load when every scale matrix is
+  // 4-byte aligned (rows of an even number of groups, pairs at even groups)
+  const bool a4 = lpr == 8 && ((reinterpret_cast<uintptr_t>(sc_a) |
+                                reinterpret_cast<uintptr_t>(sc_b)) & 3u) == 0;
+  if (sc_gm) {
+    if (lpr == 8) launch_down<8, kScGm>(src, a, blocks, stream);
+    else launch_down<4, kScGm>(src, a, blocks, stream);
+  } else if (lpr == 8 && a4) {
+    launch_down<8, kScRow4>(src, a, blocks, stream);
+  } else if (lpr == 8) {
+    launch_down<8, kScRow>(src, a, blocks, stream);
+  } else {
+    launch_down<4, kScRow>(src, a, blocks, stream);
+  }
   int st = hip_status(hipGetLastError());
   if (st) return st;
   launch_reduce(a.partial, a.row_blocks, (int)out_features, y, stream);
@@ -254,13 +275,15 @@ extern "C" int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales
 }
 
 extern "C" int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint16_t* scales,
+                                               const uint16_t* scales_gm,
                                                const uint16_t* h_full, const int32_t* indices,
                                                uint16_t* y, uint16_t* h_out, int64_t rows,
                                                int64_t out_features, int64_t k, void* workspace,
                                                size_t ws_bytes, void* stream) {
   if (k > 0 && !indices) return DIP_ERR_NULL;
   return run_down(kGather, down_t, scales, rows, nullptr, nullptr, 0, h_full, indices, nullptr,
-                  k, out_features, y, workspace, ws_bytes, (hipStream_t)stream, 1, h_out);
+                  k, out_features, y, workspace, ws_bytes, (hipStream_t)stream, 1, h_out,
+                  scales_gm);
 }
 
 extern "C" int dip_ca_down(const int8_t* res_qw, const uint16_t* res_sc, const int8_t* str_qw,

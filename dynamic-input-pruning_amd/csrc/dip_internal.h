@@ -78,6 +78,7 @@ struct DownArgs {
   const uint16_t* sc_a;
   const int8_t* qw_b;
   const uint16_t* sc_b;
+  const uint16_t* sc_gm;   // optional: A's scales group-major [groups][rows_a] (kContig, kGather)
   const uint16_t* h;
   const int32_t* sel;
   const int32_t* sel2;
@@ -216,7 +217,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
              const int8_t* qw_b, const uint16_t* sc_b, int64_t rows_b, const uint16_t* h,
              const int32_t* sel, const int32_t* sel2, int64_t k, int64_t out_features,
              uint16_t* y, void* workspace, size_t ws_bytes, hipStream_t stream,
-             int h_by_row = 0, uint16_t* h_out = nullptr);
+             int h_by_row = 0, uint16_t* h_out = nullptr, const uint16_t* sc_gm = nullptr);
 size_t down_workspace_bytes(int64_t k, int64_t out_features);
 int64_t down_max_k();  // largest k the down path accepts
 // The top-k select kernel: idx from s (TopkMeta into the workspace).

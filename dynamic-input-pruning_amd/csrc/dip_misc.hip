@@ -504,8 +504,8 @@ extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t 
 extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gate_sc,
                                       const int8_t* up_qw, const uint16_t* up_sc,
                                       const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                                      const uint16_t* h, const uint16_t* add,
-                                      const uint16_t* norm_w, float eps, uint16_t* h_res_out,
+                                      const uint16_t* down_t_sc_gm, const uint16_t* h,
+                                      const uint16_t* add, const uint16_t* norm_w, float eps, uint16_t* h_res_out,
                                       uint16_t* x_out, uint16_t* y, uint16_t* g_out,
                                       int32_t* idx_out, uint16_t* h_out, int64_t hidden,
                                       int64_t inter, int64_t k, void* workspace, size_t ws_bytes,
@@ -563,8 +563,9 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
     st = launch_spec_after_gate(g_out, inter, hidden, k, idx_out, h_full, up_qw, up_sc, x_out, ws,
                                 layer_state, s);
     if (st) return st;
-    return dip_int4_gather_down_by_channel(down_t_qw, down_t_sc, h_full, idx_out, y, h_out,
-                                           inter, hidden, k, down_ws, down_bytes, stream);
+    return dip_int4_gather_down_by_channel(down_t_qw, down_t_sc, down_t_sc_gm, h_full, idx_out,
+                                           y, h_out, inter, hidden, k, down_ws, down_bytes,
+                                           stream);
   }
   int st = launch_rowdot_norm(kSilu, a, s);
   if (st) return st;
@@ -574,15 +575,16 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
     st = dip_up_gather_h(up_qw, up_sc, x_out, idx_out, g_out, h_out, inter, hidden, k, stream);
     if (st) return st;
   }
-  return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k,
-                              down_ws, down_bytes, stream);
+  return run_down(kGather, down_t_qw, down_t_sc, inter, nullptr, nullptr, 0, h_out, idx_out,
+                  nullptr, k, hidden, y, down_ws, down_bytes, (hipStream_t)stream, 0, nullptr,
+                  down_t_sc_gm);
 }
 
 extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
                               const int8_t* up_qw, const uint16_t* up_sc,
                               const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                              const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
-                              uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
+                              const uint16_t* down_t_sc_gm, const uint16_t* x, uint16_t* y,
+                              uint16_t* g_out, int32_t* idx_out, uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
                               void* workspace, size_t ws_bytes, void* layer_state,
                               void* stream) {
   if (!g_out || !y || !x) return DIP_ERR_NULL;
@@ -616,8 +618,9 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
     int st = dip_gate_silu_topk_spec(gate_qw, gate_sc, up_qw, up_sc, x, g_out, idx_out, h_full,
                                      inter, hidden, k, ws, kMlpTopkBytes, layer_state, stream);
     if (st) return st;
-    return dip_int4_gather_down_by_channel(down_t_qw, down_t_sc, h_full, idx_out, y, h_out,
-                                           inter, hidden, k, down_ws, down_bytes, stream);
+    return dip_int4_gather_down_by_channel(down_t_qw, down_t_sc, down_t_sc_gm, h_full, idx_out,
+                                           y, h_out, inter, hidden, k, down_ws, down_bytes,
+                                           stream);
   }
   int st = dip_gate_silu_topk(gate_qw, gate_sc, x, g_out, idx_out, inter, hidden, k, ws,
                               kMlpTopkBytes, stream);
@@ -626,6 +629,7 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
     st = dip_up_gather_h(up_qw, up_sc, x, idx_out, g_out, h_out, inter, hidden, k, stream);
     if (st) return st;
   }
-  return dip_int4_gather_down(down_t_qw, down_t_sc, h_out, idx_out, y, inter, hidden, k,
-                              down_ws, down_bytes, stream);
+  return run_down(kGather, down_t_qw, down_t_sc, inter, nullptr, nullptr, 0, h_out, idx_out,
+                  nullptr, k, hidden, y, down_ws, down_bytes, (hipStream_t)stream, 0, nullptr,
+                  down_t_sc_gm);
 }

@@ -53,8 +53,8 @@ int scratch_address(void** out) {
 extern "C" int dip_mlp_decode_noalloc(const int8_t* gate_qw, const uint16_t* gate_sc,
                                       const int8_t* up_qw, const uint16_t* up_sc,
                                       const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                                      const uint16_t* x, uint16_t* y, uint16_t* g_out,
-                                      int32_t* idx_out, uint16_t* h_out, int64_t hidden,
+                                      const uint16_t* down_t_sc_gm, const uint16_t* x,
+                                      uint16_t* y, uint16_t* g_out, int32_t* idx_out, uint16_t* h_out, int64_t hidden,
                                       int64_t inter, int64_t k, void* layer_state,
                                       void* stream) {
   if (hidden < 0 || inter < 0 || k < 0) return DIP_ERR_SHAPE;
@@ -62,6 +62,7 @@ extern "C" int dip_mlp_decode_noalloc(const int8_t* gate_qw, const uint16_t* gat
   void* ws = nullptr;
   const int st = scratch_address(&ws);
   if (st) return st;
-  return dip_mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, y, g_out,
-                        idx_out, h_out, hidden, inter, k, ws, kScratchBytes, layer_state, stream);
+  return dip_mlp_decode(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, down_t_sc_gm, x, y,
+                        g_out, idx_out, h_out, hidden, inter, k, ws, kScratchBytes, layer_state,
+                        stream);
 }

@@ -106,9 +106,38 @@ __global__ __launch_bounds__(256) void transpose_down_kernel(
   }
 }
 
+// sc_gm[g][r] = sc[r][g]: 64 x 64 tiles through LDS, both sides coalesced.
+__global__ __launch_bounds__(256) void scales_group_major_kernel(
+    const uint16_t* __restrict__ sc, uint16_t* __restrict__ gm, int rows, int groups) {
+  __shared__ uint16_t tile[64][65];
+  const int r0 = blockIdx.x * 64, g0 = blockIdx.y * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int r = e / 64, g = e % 64;
+    if (r0 + r < rows && g0 + g < groups) tile[r][g] = sc[(size_t)(r0 + r) * groups + g0 + g];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int g = e / 64, r = e % 64;
+    if (r0 + r < rows && g0 + g < groups) gm[(size_t)(g0 + g) * rows + r0 + r] = tile[r][g];
+  }
+}
+
 }  // namespace dip
 
 using namespace dip;
+
+extern "C" int dip_scales_group_major(const uint16_t* scales, uint16_t* scales_gm, int64_t rows,
+                                      int64_t groups, void* stream) {
+  if (!scales || !scales_gm) return DIP_ERR_NULL;
+  if (rows < 0 || groups <= 0 || rows > INT32_MAX || groups > 65536 ||
+      (rows + 63) / 64 > INT32_MAX)
+    return DIP_ERR_SHAPE;
+  if (rows == 0) return DIP_OK;
+  const dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((groups + 63) / 64));
+  hipLaunchKernelGGL(scales_group_major_kernel, grid, dim3(256), 0, (hipStream_t)stream, scales,
+                     scales_gm, (int)rows, (int)groups);
+  return hip_status(hipGetLastError());
+}
 
 extern "C" int dip_quantize_int4(const void* w, int w_is_bf16, int8_t* qweight, uint16_t* scales,
                                  int64_t rows, int64_t cols, void* stream) {

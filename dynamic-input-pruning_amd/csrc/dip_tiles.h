@@ -292,15 +292,33 @@ DIP_DEV void load_down_row(const DownArgs& a, uint32_t rid, int cc0, size_t row_
 // The NG bf16 scales of groups g0 .. g0 + NG - 1 of row rid (a slot's LPR
 // chunks span NG = LPR / 4 groups).  Issued by the lane that owns the row,
 // once per tile, instead of one scale load per row by every lane.
-template <int SRC, int NG>
+// Scale layouts of the down kernel: kScRow, the reference's [rows][groups]
+// one 16-bit load per group; kScRow4, the same with the NG == 2 pair as one
+// 32-bit load (scale rows 4-byte aligned, g0 even); kScGm, A's scales
+// group-major [groups][rows_a] (sc_gm): the rows of a tile then read
+// neighbouring words of one group row instead of a few bytes of every row's
+// own scale line.
+enum DownScales : int { kScRow = 0, kScRow4 = 1, kScGm = 2 };
+
+template <int SRC, int NG, int SL>
 DIP_DEV void load_down_scales(const DownArgs& a, uint32_t rid, int g0, int ngroups,
                               uint32_t s[NG]) {
   const bool bad = rid >= kPadRow;
   const bool isb = SRC == kDual && !bad && (rid & kSrcB);
   const uint16_t* sc = bad ? a.sc_safe : (isb ? a.sc_b : a.sc_a);
   const uint32_t r = bad ? 0u : (rid & ~kSrcB);
+  if constexpr (SL == kScGm) {
+    static_assert(SRC != kDual, "group-major scales: one matrix");
 #pragma unroll
-  for (int i = 0; i < NG; ++i) s[i] = sc[(size_t)r * ngroups + g0 + i];
+    for (int i = 0; i < NG; ++i) s[i] = a.sc_gm[(size_t)(g0 + i) * a.rows_a + r];
+  } else if constexpr (SL == kScRow4 && NG == 2) {
+    const uint32_t p = *reinterpret_cast<const uint32_t*>(sc + (size_t)r * ngroups + g0);
+    s[0] = p & 0xFFFFu;
+    s[1] = p >> 16;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NG; ++i) s[i] = sc[(size_t)r * ngroups + g0 + i];
+  }
 }
 
 // The row's coefficients 16*h*s per group (padding row: 0, bad id: NaN),
@@ -353,52 +371,76 @@ DIP_DEV void down_accumulate(const DownRow ring[LPR], const float f[NG], int hi,
   }
 }
 
-// LDS floats for the slot reduction of a block.
-template <int LPR>
-constexpr int down_red_floats() {
-  return (kDownThreads / LPR) * LPR * (kDownAcc / 2 + 1);
+// v_permlane{16,32}_swap_b32 on two registers: swaps the odd rows (of 16 /
+// 32 lanes) of a with the even rows of b (inline asm: see row_pair_sum16).
+DIP_DEV void permlane16_swap(float& a, float& b) {
+  uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+DIP_DEV void permlane32_swap(float& a, float& b) {
+  uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
 }
 
-// Sum the block's slots in a fixed order, 16 accumulators at a time, and
-// store the block's LPR*32 partial sums to out[0 .. LPR*32) (coherent: with
-// device-scope stores that write through to memory).  Written out twice
-// rather than as a loop over the halves: as a loop the compiler keeps both
-// halves' sums in flight and needs 170 VGPRs.  Column l*32 + m of the block
-// sits at red[(slot*LPR + l)*kStride + m - half].
-template <int LPR, bool COHERENT>
-DIP_DEV void down_block_partial(const float acc[kDownAcc], float* red, float* out, int slot,
-                                int l) {
-  constexpr int kSlots = kDownThreads / LPR;
-  constexpr int kHalf = kDownAcc / 2;
-  constexpr int kStride = kHalf + 1;  // padded LDS rows: conflict-free both ways
-  float* mine = red + (slot * LPR + l) * kStride;
+// Floats of LDS for the cross-wave step of down_block_partial.
+template <int LPR>
+constexpr int down_red_floats() {
+  return (kDownThreads / 64) * LPR * kDownAcc;
+}
+
+// Sum the block's slots in a fixed order and store the block's LPR*32
+// partial sums to out[0 .. LPR*32).  The slots of a wave (lanes l + LPR*s
+// hold the same 32 columns) are summed in registers:
+//   1. within rows of 16 lanes by DPP rotations (lane l + 8 for LPR = 8;
+//      l + 4, then l + 8 for LPR = 4), every lane of the row receiving the
+//      row's sum;
+//   2. across the row pairs (0,1), (2,3) by v_permlane16_swap of two
+//      accumulators m, m + 16 followed by one add: rows 0 and 2 keep column
+//      m, rows 1 and 3 column m + 16 (16 registers left);
+//   3. across the wave halves by v_permlane32_swap of m, m + 8: lanes 0-31
+//      keep m, lanes 32-63 m + 8 (8 registers left).
+// Register m' of lane i (i % 16 < LPR) then holds column 32*(i % LPR) + m' +
+// 8*(i / 32) + 16*((i / 16) % 2) of the block, summed over the wave's
+// slots; the waves' sums meet in LDS (red: down_red_floats floats) and are
+// added in wave order.
+template <int LPR>
+DIP_DEV void down_block_partial(float acc[kDownAcc], float* red, float* out) {
+  static_assert(LPR == 4 || LPR == 8, "slot width");
+  constexpr int kCols = LPR * kDownAcc;
+  constexpr int kWaves = kDownThreads / 64;
 #pragma unroll
-  for (int m = 0; m < kHalf; ++m) mine[m] = acc[m];
-  __syncthreads();
-  for (int e = threadIdx.x; e < LPR * kHalf; e += kDownThreads) {
-    const int ln = e / kHalf, m = e % kHalf;
-    float s = 0.f;
-#pragma unroll 8
-    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
-    if (COHERENT)
-      __hip_atomic_store(out + ln * kDownAcc + m, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      out[ln * kDownAcc + m] = s;
+  for (int m = 0; m < kDownAcc; ++m) {
+    if constexpr (LPR == 4) acc[m] += dpp_mov<0x124>(acc[m]);  // row_ror:4
+    acc[m] += dpp_mov<0x128>(acc[m]);                          // row_ror:8
   }
-  __syncthreads();  // the first half's reads are done
+  float t[16];
 #pragma unroll
-  for (int m = 0; m < kHalf; ++m) mine[m] = acc[kHalf + m];
+  for (int m = 0; m < 16; ++m) {
+    permlane16_swap(acc[m], acc[m + 16]);
+    t[m] = acc[m] + acc[m + 16];
+  }
+  float u[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    permlane32_swap(t[m], t[m + 8]);
+    u[m] = t[m] + t[m + 8];
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if ((lane & 15) < LPR) {
+    float* dst = red + wave * kCols + 32 * (lane % LPR) + 8 * (lane >> 5) + 16 * ((lane >> 4) & 1);
+    *reinterpret_cast<float4*>(dst) = make_float4(u[0], u[1], u[2], u[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(u[4], u[5], u[6], u[7]);
+  }
   __syncthreads();
-  for (int e = threadIdx.x; e < LPR * kHalf; e += kDownThreads) {
-    const int ln = e / kHalf, m = e % kHalf;
-    float s = 0.f;
-#pragma unroll 8
-    for (int sl = 0; sl < kSlots; ++sl) s += red[(sl * LPR + ln) * kStride + m];
-    if (COHERENT)
-      __hip_atomic_store(out + ln * kDownAcc + kHalf + m, s, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    else
-      out[ln * kDownAcc + kHalf + m] = s;
+  for (int c = threadIdx.x; c < kCols; c += kDownThreads) {
+    float s = red[c];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) s += red[w * kCols + c];
+    out[c] = s;
   }
 }
 

@@ -43,7 +43,8 @@ def bytes_per_layer(hidden: int, inter: int, k: int) -> int:
 
 class DIPStack:
     def __init__(self, hidden: int, inter: int, layers: int, keep_ratio: float = 0.6,
-                 device="cuda:0", seed: int = 0, spec: bool = True, weights=None):
+                 device="cuda:0", seed: int = 0, spec: bool = True, weights=None,
+                 scales_gm: bool = True):
         self.hidden, self.inter, self.layers = hidden, inter, layers
         self.keep_ratio = keep_ratio
         self.k = keep_count(inter, keep_ratio)
@@ -62,6 +63,10 @@ class DIPStack:
                         torch.randn(inter, hidden, device=dev, generator=gen) * 0.02)
                     lw[name + "_qw"], lw[name + "_sc"] = q, s
                 self.w.append(lw)
+        # the group-major copy of down_t's scales the down stage reads
+        # (None: it reads the [inter, hidden/128] scales themselves)
+        for lw in self.w:
+            lw["down_t_sc_gm"] = K.scales_group_major(lw["down_t_sc"]) if scales_gm else None
         self.x = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
         self.y = [torch.empty(hidden, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
         self.g = torch.empty(inter, dtype=torch.bfloat16, device=dev)
@@ -76,13 +81,14 @@ class DIPStack:
 
     @classmethod
     def from_checkpoint(cls, ckpt_dir, keep_ratio: float = 0.6, device="cuda:0",
-                        spec: bool = True):
+                        spec: bool = True, scales_gm: bool = True):
         """Every MLP of an int4 checkpoint in the reference's format
         (dip_checkpoint), resident on `device`, in layer order."""
         from dip_checkpoint import load_mlp_layers
         layers = load_mlp_layers(ckpt_dir, device)
         inter, hidden = layers[0]["up_qw"].shape[0], layers[0]["up_qw"].shape[1] * 2
-        return cls(hidden, inter, len(layers), keep_ratio, device, spec=spec, weights=layers)
+        return cls(hidden, inter, len(layers), keep_ratio, device, spec=spec, weights=layers,
+                   scales_gm=scales_gm)
 
     @property
     def bytes_per_token(self) -> int:
@@ -100,7 +106,8 @@ class DIPStack:
         for lw, y, st in zip(self.w, self.y, self.state):
             K.mlp_decode(lw["gate_qw"], lw["gate_sc"], lw["up_qw"], lw["up_sc"],
                          lw["down_t_qw"], lw["down_t_sc"], self.x, self.k, y=y, g=self.g,
-                         idx=self.idx, h=self.h, ws=self.ws, state=st)
+                         idx=self.idx, h=self.h, ws=self.ws, state=st,
+                         down_t_sc_gm=lw["down_t_sc_gm"])
 
     def capture(self):
         """Capture run_token() as one HIP graph (after an eager warm-up)."""
@@ -167,8 +174,10 @@ class DIPStack:
         def down(st):
             for lw, y in zip(self.w, self.y):
                 if self.spec:
+                    gm = lw["down_t_sc_gm"]
                     K._check(lib.dip_int4_gather_down_by_channel(
-                        lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(), h_full,
+                        lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(),
+                        None if gm is None else gm.data_ptr(), h_full,
                         self.idx.data_ptr(), y.data_ptr(), self.h.data_ptr(), I, H, k,
                         ctypes.c_void_p(down_ws), down_n, st), "down_by_channel")
                 else:

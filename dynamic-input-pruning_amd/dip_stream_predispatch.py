@@ -137,6 +137,10 @@ class StreamingDIPMlp(nn.Module):
                                                        down_sc.to(self.device))
         self.down_t_qw = dn_t_qw.to(self.device).contiguous()
         self.down_t_sc = dn_t_sc.to(self.device).contiguous()
+        # a group-major copy of the same scales (2 bytes per channel and
+        # group): the decode step's down tiles read a column group of many
+        # channels at once, which this layout keeps in a few cache lines
+        self.down_t_sc_gm = K.scales_group_major(self.down_t_sc)
         self.out_features = self.down_t_qw.shape[1] * 2
         self.k = shared.k
         # which channels the next token's up rows are speculated on: it
@@ -173,7 +177,7 @@ class StreamingDIPMlp(nn.Module):
         y, _, _, _ = K.mlp_decode(self.gate_qw, self.gate_sc, self.up_qw, self.up_sc,
                                   self.down_t_qw, self.down_t_sc, xv, self.k,
                                   g=b.g(self.inter), idx=b.idx, h=b.h, ws=ws,
-                                  state=self._spec_state)
+                                  state=self._spec_state, down_t_sc_gm=self.down_t_sc_gm)
         return y
 
     def decode_rmsnorm(self, res, add, norm_w, eps, res_out, x_out):
@@ -190,7 +194,7 @@ class StreamingDIPMlp(nn.Module):
         y, _, _, _, _ = K.mlp_decode_rmsnorm(
             self.gate_qw, self.gate_sc, self.up_qw, self.up_sc, self.down_t_qw, self.down_t_sc,
             res, add, norm_w, eps, self.k, res_out=res_out, x_out=x_out, g=b.g(self.inter),
-            idx=b.idx, h=b.h, ws=ws, state=self._spec_state)
+            idx=b.idx, h=b.h, ws=ws, state=self._spec_state, down_t_sc_gm=self.down_t_sc_gm)
         return y
 
     def forward(self, x):

@@ -237,6 +237,16 @@ int dip_transpose_down_int4(const int8_t* down_qw, const uint16_t* down_sc, int8
                             void* stream);
 
 /*
+ * scales_gm[g][r] = scales[r][g] for a [rows, groups] bf16 scale matrix: the
+ * group-major copy of down_t's scales that the decode step's down stage
+ * reads when given one (dip_mlp_decode's down_t_sc_gm).  A resident layout
+ * of this library with no counterpart in the reference (whose down_t keeps
+ * [inter, hidden/128] scales only); 2 * rows * groups bytes per layer.
+ */
+int dip_scales_group_major(const uint16_t* scales, uint16_t* scales_gm, int64_t rows,
+                           int64_t groups, void* stream);
+
+/*
  * The decode step's first half with speculative up rows: no counterpart in
  * the reference (it replaces gate_kernel.py:29-33 + topk_kernel.py:29-40 +
  * the up half of dip_stream_predispatch.py:196-199 by two launches):
@@ -265,9 +275,14 @@ int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
  * dip_int4_gather_down with h indexed by channel: y = sum_j h_full[idx[j]] *
  * down_t[idx[j]] (the down half of dip_stream_predispatch.py:196-203 after
  * dip_gate_silu_topk_spec); h_out[j] = h_full[idx[j]] when h_out != NULL.
- * Same workspace as dip_int4_gather_down.
+ * Same workspace as dip_int4_gather_down.  scales_gm (optional, may be
+ * NULL): the same scales group-major, [out_features/128][rows]
+ * (dip_scales_group_major); when given the kernel reads the scales there
+ * (same values, same y bit for bit) instead of a few bytes of every
+ * selected row's own scale line.
  */
 int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint16_t* scales,
+                                    const uint16_t* scales_gm,
                                     const uint16_t* h_full, const int32_t* indices,
                                     uint16_t* y, uint16_t* h_out, int64_t rows,
                                     int64_t out_features, int64_t k, void* workspace,
@@ -284,12 +299,15 @@ int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint16_t* scales
  * when set and the width allows, the step runs as dip_gate_silu_topk_spec +
  * dip_int4_gather_down_by_channel (four launches); otherwise as
  * dip_gate_silu_topk + dip_up_gather_h + dip_int4_gather_down (five).  Both
- * give bit-identical outputs.
+ * give bit-identical outputs.  down_t_sc_gm (optional, may be NULL): the
+ * group-major copy of down_t_sc (dip_scales_group_major), which the down
+ * stage then reads instead (same outputs, bit for bit; the opt-in fused
+ * step ignores it).
  */
 size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k);
 int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
                    const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                   const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
+                   const uint16_t* down_t_sc_gm, const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
                    uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
                    void* workspace, size_t ws_bytes, void* layer_state, void* stream);
 
@@ -310,9 +328,9 @@ int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t*
 int dip_mlp_decode_noalloc(const int8_t* gate_qw, const uint16_t* gate_sc,
                            const int8_t* up_qw, const uint16_t* up_sc,
                            const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                           const uint16_t* x, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
-                           uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,
-                           void* layer_state, void* stream);
+                           const uint16_t* down_t_sc_gm, const uint16_t* x, uint16_t* y,
+                           uint16_t* g_out, int32_t* idx_out, uint16_t* h_out, int64_t hidden,
+                           int64_t inter, int64_t k, void* layer_state, void* stream);
 
 /*
  * dip_mlp_decode with the post-attention RMSNorm of a decoder layer folded
@@ -327,7 +345,8 @@ int dip_mlp_decode_noalloc(const int8_t* gate_qw, const uint16_t* gate_sc,
  */
 int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
                            const uint16_t* up_sc, const int8_t* down_t_qw,
-                           const uint16_t* down_t_sc, const uint16_t* h, const uint16_t* add,
+                           const uint16_t* down_t_sc, const uint16_t* down_t_sc_gm,
+                           const uint16_t* h, const uint16_t* add,
                            const uint16_t* norm_w, float eps, uint16_t* h_res_out,
                            uint16_t* x_out, uint16_t* y, uint16_t* g_out, int32_t* idx_out,
                            uint16_t* h_out, int64_t hidden, int64_t inter, int64_t k,

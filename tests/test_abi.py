@@ -65,12 +65,12 @@ def test_argument_rejection_before_launch():
     assert L.dip_int4_gather_down(p, p, p, None, p, 10, 5120, 11, p, need, None) == -2
     # mlp: k > inter, missing outputs
     ws = L.dip_mlp_workspace_size(5120, 25600, 15360)
-    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 30000, p, ws, p,
+    assert L.dip_mlp_decode(p, p, p, p, p, p, None, p, p, p, p, p, 5120, 25600, 30000, p, ws, p,
                             None) == -2
-    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, None, p, p, 5120, 25600, 100, p, ws, p,
+    assert L.dip_mlp_decode(p, p, p, p, p, p, None, p, p, None, p, p, 5120, 25600, 100, p, ws, p,
                             None) == -1
-    assert L.dip_mlp_decode(p, p, p, p, p, p, p, p, p, p, p, 5120, 25600, 15360, p, ws - 1, p,
-                            None) == -5
+    assert L.dip_mlp_decode(p, p, p, p, p, p, None, p, p, p, p, p, 5120, 25600, 15360, p, ws - 1,
+                            p, None) == -5
     # speculative first half: missing state, k = 0, unsupported width, misaligned state
     tw = L.dip_topk_workspace_size(25600)
     assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 100, p, tw, None,
@@ -83,8 +83,12 @@ def test_argument_rejection_before_launch():
                                      None) == -3
     assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 100, p, 8, p,
                                      None) == -5
-    assert L.dip_int4_gather_down_by_channel(p, p, p, None, p, None, 25600, 5120, 10, p, need,
-                                             None) == -1
+    assert L.dip_int4_gather_down_by_channel(p, p, None, p, None, p, None, 25600, 5120, 10, p,
+                                             need, None) == -1
+    # group-major scales: NULL, shapes
+    assert L.dip_scales_group_major(None, p, 10, 40, None) == -1
+    assert L.dip_scales_group_major(p, p, -1, 40, None) == -2
+    assert L.dip_scales_group_major(p, p, 10, 0, None) == -2
     assert L.dip_mlp_state_size() == 16  # speculation key (twice), key band, spare
     assert L.dip_read_probe(None, 16, p, None) == -1
     assert L.dip_read_probe(p, 24, p, None) == -2
@@ -101,10 +105,10 @@ def test_argument_rejection_before_launch():
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
     assert L.dip_ca_assemble(None, p, p, p, p, p, p, 10, 5, None) == -1
     # MLP step with the RMSNorm in its gate: unsupported width, aliasing
-    assert L.dip_mlp_decode_rmsnorm(p, p, p, p, p, p, p, None, p, 1e-6, None, p, p, p, p, p,
-                                    1024, 3072, 100, p, 1 << 20, None, None) == -4
-    assert L.dip_mlp_decode_rmsnorm(p, p, p, p, p, p, p, None, p, 1e-6, None, p, p, p, p, p,
-                                    5120, 3072, 100, p, 1 << 20, None, None) == -6
+    assert L.dip_mlp_decode_rmsnorm(p, p, p, p, p, p, None, p, None, p, 1e-6, None, p, p, p, p,
+                                    p, 1024, 3072, 100, p, 1 << 20, None, None) == -4
+    assert L.dip_mlp_decode_rmsnorm(p, p, p, p, p, p, None, p, None, p, 1e-6, None, p, p, p, p,
+                                    p, 5120, 3072, 100, p, 1 << 20, None, None) == -6
     # GEMV with the RMSNorm prologue: unsupported width, aliasing, NULL h
     assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, None, p, 8, 1024, None) == -4
     assert L.dip_int4_gemv_rmsnorm(p, p, p, None, p, 1e-6, p, p, 8, 5120, None) == -6
