@@ -377,6 +377,9 @@ def main(argv=None):
     ap.add_argument("--no-spec", action="store_true",
                     help="run every layer stage by stage (no speculative up rows during the "
                          "top-k); same outputs, five launches per layer instead of four")
+    ap.add_argument("--step", type=int, choices=(0, 1, 2), default=None,
+                    help="decode step form with speculation state (DIP_TUNE_STEP): 0 four "
+                         "launches, 1 fused, 2 split; default: the library's")
     ap.add_argument("--no-gm", action="store_true",
                     help="the down stage reads down_t's [inter, hidden/128] scales instead of "
                          "their group-major copy")
@@ -421,6 +424,8 @@ def main(argv=None):
     from dip_stack import SHAPES, DIPStack
 
     dev = torch.device("cuda:0")
+    if args.step is not None:
+        K.set_tuning("step", args.step)
     if args.checkpoint:
         print(f"[bench] loading MLPs of {args.checkpoint} keep={args.keep}", file=sys.stderr,
               flush=True)

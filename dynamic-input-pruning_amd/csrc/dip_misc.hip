@@ -185,7 +185,7 @@ extern "C" int dip_set_tuning(int knob, int value) {
       if (value < 0 || value > 1024) return DIP_ERR_ARG;
       break;
     case DIP_TUNE_STEP:
-      if (value != 0 && value != 1) return DIP_ERR_ARG;
+      if (value < 0 || value > 2) return DIP_ERR_ARG;
       break;
     default:
       return DIP_ERR_ARG;
@@ -549,7 +549,7 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
   const bool spec = layer_state && k > 0 && topk_spec_supported(hidden) && inter <= kTopkMaxN;
   if (spec) {
     if (reinterpret_cast<uintptr_t>(layer_state) & 3u) return DIP_ERR_ALIGN;
-    if (tuning(DIP_TUNE_STEP) && step_supported(hidden, inter)) {
+    if (tuning(DIP_TUNE_STEP) == 1 && step_supported(hidden, inter)) {
       const int cst = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x_out,
                                       idx_out, h_out, layer_state, ws, hidden, inter);
       if (cst) return cst;
@@ -580,6 +580,64 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
                   down_t_sc_gm);
 }
 
+namespace {
+// The split decode step (dip_internal.h): the gate launch with the
+// candidates' up rows, the select + candidate-down launch, the reduce.
+int run_split_step(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
+                   const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
+                   const uint16_t* down_t_sc_gm, const uint16_t* x, uint16_t* y,
+                   uint16_t* g_out, int32_t* idx_out, uint16_t* h_out, int64_t hidden,
+                   int64_t inter, int64_t k, void* workspace, void* layer_state,
+                   hipStream_t s) {
+  const int gate_wgs = gate_spec_blocks(inter, hidden);
+  if (gate_wgs < 1) return DIP_ERR_UNSUPPORTED;
+  const MlpWs w = mlp_ws(workspace, hidden, inter, k);
+  const int rt_max = (int)((inter + 255) / 256);
+  const int nfix = (int)((inter + 2047) / 2048);
+  if ((size_t)(rt_max + nfix) * (size_t)hidden * sizeof(float) > w.partial_bytes)
+    return DIP_ERR_WORKSPACE;
+  GateSpecArgs ga{};
+  ga.qw = gate_qw;
+  ga.sc = gate_sc;
+  ga.up_qw = up_qw;
+  ga.up_sc = up_sc;
+  ga.x = x;
+  ga.g = g_out;
+  ga.h_full = w.h_full;
+  ga.state = static_cast<uint32_t*>(layer_state);
+  ga.cand_count = w.cand_count;
+  ga.cand_list = w.cand_list;
+  ga.nrows = (int)inter;
+  ga.in_features = (int)hidden;
+  int st = launch_gate_spec(ga, s);
+  if (st) return st;
+  SelDownArgs sd{};
+  sd.g = g_out;
+  sd.n = (int)inter;
+  sd.k = (int)k;
+  sd.idx = idx_out;
+  sd.h_out = h_out;
+  sd.meta = w.meta;
+  sd.sp.up_qw = up_qw;
+  sd.sp.up_sc = up_sc;
+  sd.sp.x = x;
+  sd.sp.h_full = w.h_full;
+  sd.sp.state = static_cast<uint32_t*>(layer_state);
+  sd.sp.hidden = (int)hidden;
+  sd.dn_qw = down_t_qw;
+  sd.dn_sc = down_t_sc;
+  sd.dn_sc_gm = down_t_sc_gm;
+  sd.cand_count = w.cand_count;
+  sd.cand_list = w.cand_list;
+  sd.gate_wgs = gate_wgs;
+  sd.partial = reinterpret_cast<float*>(w.partial);
+  st = launch_select_down(sd, s);
+  if (st) return st;
+  return launch_split_reduce(reinterpret_cast<const float*>(w.partial), w.meta, rt_max, nfix,
+                             (int)hidden, y, s);
+}
+}  // namespace
+
 extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
                               const int8_t* up_qw, const uint16_t* up_sc,
                               const int8_t* down_t_qw, const uint16_t* down_t_sc,
@@ -595,7 +653,17 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
   const size_t hfull_bytes = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
   char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
   const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
-  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) && step_supported(hidden, inter)) {
+  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) == 2 && split_step_supported(hidden, inter) &&
+      gate_spec_blocks(inter, hidden) > 0) {
+    int st = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, idx_out,
+                             h_out, layer_state, ws, hidden, inter);
+    if (st) return st;
+    if (!aligned16(g_out)) return DIP_ERR_ALIGN;
+    return run_split_step(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, down_t_sc_gm, x,
+                          y, g_out, idx_out, h_out, hidden, inter, k, workspace, layer_state,
+                          (hipStream_t)stream);
+  }
+  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) == 1 && step_supported(hidden, inter)) {
     // gate (+ SiLU, candidate and band lists), the fused step, the finish
     int st = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, idx_out,
                              h_out, layer_state, ws, hidden, inter);

@@ -269,14 +269,23 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
 // Select: R rounds of one 8-value chunk per thread cover n <= 8192 R values;
 // workgroup w places values [2048 w, 2048 (w + 1)).
 // ---------------------------------------------------------------------------
-// The select body, run by workgroups 0 .. nblk-1 of a launch.  SPEC (the
-// decode step with speculative up rows): also records the magnitude key at
-// rank k + margin for the next call and computes h for the selected channels
-// that the speculation workgroups skip (residual_rows).
-template <int R, bool SPEC, int LPR, int CH>
+// The select body, run by workgroups 0 .. nblk-1 of a launch.  MODE
+// kSelSpec (the decode step with speculative up rows): also records the
+// magnitude key at rank k + margin for the next call and computes h for the
+// selected channels that the speculation workgroups skip (residual_rows).
+// MODE kSelSplit (the split step's second launch): the same key, then
+// split_select_tail.
+enum SelMode : int { kSelPlain = 0, kSelSpec = 1, kSelSplit = 2 };
+template <int LPR, int CH>
+DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool s0, bool s1,
+                               uint32_t pos0, uint32_t pos1, uint32_t uk, uint32_t filled,
+                               uint32_t sk, uint32_t* lds);
+
+template <int R, int MODE, int LPR, int CH>
 DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
                        TopkMeta* __restrict__ meta, int stamps, int nblk, const SpecArgs& sp,
-                       uint32_t* hist) {
+                       uint32_t* hist, const SelDownArgs* sd = nullptr) {
+  constexpr bool SPEC = MODE != kSelPlain;
   __shared__ uint32_t wtot[kWaves];
   __shared__ uint32_t wsum_a[kWaves], wsum_b[kWaves], wside[kWaves], wown[kWaves];
   __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b, sh_spec, sh_rcount;
@@ -533,7 +542,7 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
   // unfilled slots (fewer than k values qualify) are 0, as in the reference
   const uint32_t filled = min(uk, tot_a + tot_b);
   int rcount = 0;
-  if constexpr (SPEC) {
+  if constexpr (MODE == kSelSpec) {
     // Residual h: selected channels whose key is below the speculation key
     // (the speculation workgroups compute every channel at or above it), and
     // channel 0 when unfilled slots point at it.  The histogram is no longer
@@ -562,8 +571,13 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
     meta->count_a = (int32_t)tot_a;
     meta->count_b = (int32_t)tot_b;
   }
-  if constexpr (SPEC) {
+  if constexpr (MODE == kSelSpec) {
     if (rcount > 0) residual_rows<LPR, CH>(sp, hist, rcount, hist + kSlice);
+  }
+  if constexpr (MODE == kSelSplit) {
+    __syncthreads();  // every wave is past the histogram reads: its LDS is reused
+    split_select_tail<LPR, CH>(*sd, my, mine, (a0 | q0) && pos0 < uk, (a1 | q1) && pos1 < uk,
+                               pos0, pos1, uk, filled, sk, hist, stamps);
   }
   if (stamp) {
     meta->stamp[5] = wall_clock64();
@@ -579,7 +593,7 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
   // accesses, which are slow when misaligned
   extern __shared__ __align__(16) uint32_t hist[];  // kFineBins bins
   const SpecArgs none{};
-  topk_body<R, false, 32, 5>(s, n, k, idx, meta, stamps, (int)gridDim.x, none, hist);
+  topk_body<R, kSelPlain, 32, 5>(s, n, k, idx, meta, stamps, (int)gridDim.x, none, hist);
 }
 
 // Top-k + speculative up rows in one launch: workgroups [0, sp.ntopk) run
@@ -591,10 +605,343 @@ __global__ __launch_bounds__(kThreads) void topk_spec_kernel(
     TopkMeta* __restrict__ meta, int stamps, SpecArgs sp) {
   extern __shared__ __align__(16) uint32_t lds[];  // 128-bit LDS accesses: keep aligned
   if ((int)blockIdx.x < sp.ntopk)
-    topk_body<R, true, LPR, CH>(s, n, k, idx, meta, stamps, sp.ntopk, sp, lds);
+    topk_body<R, kSelSpec, LPR, CH>(s, n, k, idx, meta, stamps, sp.ntopk, sp, lds);
   else
     spec_rows<LPR, CH>(s, n, sp, (int)blockIdx.x - sp.ntopk, lds, meta, stamps,
                        (int)gridDim.x - sp.ntopk);
+}
+
+
+// ---------------------------------------------------------------------------
+// The split decode step's second launch (dip_internal.h): select workgroups
+// [0, ntopk) and down workgroups after them.  No workgroup waits for another.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kSubThreads = 128;                  // a down sub-tile: two waves
+constexpr int kSubTiles = kThreads / kSubThreads; // per down workgroup
+constexpr int kTilePos = 256;                     // list positions per down tile
+constexpr int kSubSlots = kSubThreads / 8;        // 8-lane slots of a sub-tile
+constexpr int kSlotRows = kTilePos / kSubSlots;   // rows per slot (two per lane)
+constexpr uint32_t kNoEntry = 0xFFFFFFFFu;
+
+// Wave-ordered exclusive prefix of per-thread counts c (< 2^16 in total):
+// returns my offset and sets *total; scratch: kWaves words of LDS.  Ends with
+// a block barrier.
+DIP_DEV uint32_t block_offset(uint32_t c, uint32_t* scratch, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t incl = wave_prefix(c);
+  if (lane == 63) scratch[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t v = scratch[w];
+    before += w < wave ? v : 0u;
+    tot += v;
+  }
+  *total = tot;
+  __syncthreads();  // scratch may be reused
+  return before + incl - c;
+}
+
+// acc[m] += (q/16)[row ch, columns 8t .. 8t+7] * f for the dword t of the row.
+DIP_DEV void fix_accumulate(uint32_t w, float f, float acc[8]) {
+  const uint32_t hq = w >> 4;
+  acc[0] = fmaf(cvt_nibble_div16<0>(w), f, acc[0]);
+  acc[1] = fmaf(cvt_nibble_div16<0>(hq), f, acc[1]);
+  acc[2] = fmaf(cvt_nibble_div16<1>(w), f, acc[2]);
+  acc[3] = fmaf(cvt_nibble_div16<1>(hq), f, acc[3]);
+  acc[4] = fmaf(cvt_nibble_div16<2>(w), f, acc[4]);
+  acc[5] = fmaf(cvt_nibble_div16<2>(hq), f, acc[5]);
+  acc[6] = fmaf(cvt_nibble_div16<3>(w), f, acc[6]);
+  acc[7] = fmaf(cvt_nibble_div16<3>(hq), f, acc[7]);
+}
+
+// scale of (row ch, group g) of the down matrix, group-major copy if given
+DIP_DEV uint32_t down_scale(const SelDownArgs& a, uint32_t ch, int g) {
+  return a.dn_sc_gm ? a.dn_sc_gm[(size_t)g * a.n + ch]
+                    : a.dn_sc[(size_t)ch * (a.sp.hidden >> 7) + g];
+}
+}  // namespace
+
+// After the placement of a select workgroup's slice (values my, my + 1; s0
+// / s1: selected at pos0 / pos1): candidates are the values whose raw key
+// lies in [sk, 0x7F80) (the gate launch computed their h).
+//   * residual channels: selected non-candidates, and channel 0 when it
+//     fills unfilled slots without being a candidate: h from their up rows
+//     (h_full, and h_out for the selected ones);
+//   * h_out of the selected candidates from h_full; the unfilled slots
+//     (workgroup 0) get channel 0's h;
+//   * one fix-up partial row: + the selected residual rows, - the rows of
+//     candidates that were not selected, + channel 0 once per unfilled slot
+//     (workgroup 0), each as h * (q/16) * 16 s with the products of the down
+//     tiles; entries in a fixed order (residual then margin, each in slice
+//     order), so the row is deterministic.
+template <int LPR, int CH>
+DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool s0, bool s1,
+                               uint32_t pos0, uint32_t pos1, uint32_t uk, uint32_t filled,
+                               uint32_t sk, uint32_t* lds, int stamps) {
+  __shared__ uint32_t scratch[kWaves];
+  const bool stamp = stamps && blockIdx.x == 0 && threadIdx.x == 0;
+  if (stamp) a.meta->spec_stamp[1][0] = wall_clock64();
+  __shared__ uint32_t sh_c0, sh_e0;
+  const int tid = threadIdx.x;
+  const SpecArgs& sp = a.sp;
+  const int hidden = sp.hidden;
+  // LDS (the histogram's, free): residual entries | their aux (pos | sel <<
+  // 31) | their h | margin entries (h already signed) | staged x pairs
+  uint32_t* rlist = lds;
+  uint32_t* raux = lds + kSlice;
+  uint32_t* rh = lds + 2 * kSlice;
+  uint32_t* mlist = lds + 3 * kSlice;
+  uint32_t* xlds = lds + 4 * kSlice;
+  const uint32_t b0 = mine & 0x7FFFu, b1 = (mine >> 16) & 0x7FFFu;
+  const bool c0 = b0 >= sk && b0 < kKeyInf;  // padding (0x7FFF) never qualifies
+  const bool c1 = b1 >= sk && b1 < kKeyInf;
+  const bool fill = my == 0 && filled < uk;
+  const bool r0 = (s0 || fill) && !c0, r1 = s1 && !c1;
+  const bool m0 = c0 && !s0, m1 = c1 && !s1;
+  if (tid == 0 && blockIdx.x == 0) sh_c0 = c0;
+  uint32_t nr, nm;
+  const uint32_t ro = block_offset((uint32_t)r0 + (uint32_t)r1, scratch, &nr);
+  const uint32_t mo = block_offset((uint32_t)m0 + (uint32_t)m1, scratch, &nm);
+  if (r0) {
+    rlist[ro] = (uint32_t)my | (mine << 16);
+    raux[ro] = s0 ? (pos0 | 0x80000000u) : 0u;
+    if (fill) sh_e0 = ro;
+  }
+  if (r1) {
+    rlist[ro + r0] = (uint32_t)(my + 1) | (mine & 0xFFFF0000u);
+    raux[ro + r0] = pos1 | 0x80000000u;
+  }
+  if (m0) mlist[mo] = (uint32_t)my;
+  if (m1) mlist[mo + m0] = (uint32_t)(my + 1);
+  if (stamp) a.meta->spec_stamp[1][1] = wall_clock64();
+
+  // residual h: one row group per entry (x pairs staged in LDS)
+  const int nchunks = hidden / kChunkCols;
+  if (nr > 0) {  // workgroup-uniform
+    uint4 xs[4];
+    load_x_chunk(sp.x, nchunks, xs);
+    stage_x_pairs<LPR>(xs, xlds, nchunks);  // its barrier also publishes the lists
+    const int l = tid % LPR;
+    const size_t row_bytes = (size_t)(hidden >> 1);
+    const int ngr = hidden >> 7;
+    for (int e = tid / LPR; e < (int)nr; e += kThreads / LPR) {
+      const uint32_t ent = rlist[e];
+      RowRegs<CH> Rr;
+      load_row_at<LPR, CH>(sp.up_qw, sp.up_sc, ent & 0xFFFFu, l, row_bytes, ngr, Rr);
+      const float u = group_sum<LPR>(row_dot_lds<LPR, CH>(Rr, xlds, nchunks, l));
+      if (l == 0) {
+        const uint32_t h = h_of(ent >> 16, u);
+        rh[e] = h;
+        sp.h_full[ent & 0xFFFFu] = (uint16_t)h;
+        const uint32_t aux = raux[e];
+        if (aux >> 31) a.h_out[aux & 0x7FFFFFFFu] = (uint16_t)h;
+      }
+    }
+  }
+  __syncthreads();
+  if (stamp) a.meta->spec_stamp[1][2] = wall_clock64();
+  // channel 0's h for the unfilled slots (workgroup 0)
+  uint32_t h0 = 0;
+  if (blockIdx.x == 0 && filled < uk) {  // workgroup-uniform
+    h0 = sh_c0 ? (uint32_t)sp.h_full[0] : rh[sh_e0];
+    for (uint32_t p = filled + (uint32_t)tid; p < uk; p += kThreads) a.h_out[p] = (uint16_t)h0;
+  }
+
+  // the fix-up row: thread t < hidden / 8 owns columns 8t .. 8t + 7
+  const int nd = hidden >> 3;
+  if (tid < nd) {
+    const int grp = (8 * tid) >> 7;
+    const int nfl = (int)(nr + nm);
+    float acc[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) acc[m] = 0.f;
+    constexpr int B = 8;  // entries in flight
+    for (int e0 = 0; e0 < nfl; e0 += B) {
+      uint32_t w[B], sc[B], hb[B];
+      int sgn[B];  // +1 residual, -1 margin, 0 none
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        // branch-free: every load is issued, from clamped indices, and the
+        // entry kind picks the values (loads under branches serialise)
+        const int e = e0 + u;
+        const bool isr = e < (int)nr, ism = !isr && e < nfl;
+        const int er = isr ? e : 0, em = ism ? e - (int)nr : 0;
+        const uint32_t rent = rlist[er], raux_e = raux[er], rhe = rh[er];
+        const uint32_t ment = mlist[em];
+        const uint32_t ch = isr ? (rent & 0xFFFFu) : (ism ? ment : 0u);
+        sgn[u] = isr ? ((raux_e >> 31) ? 1 : 0) : (ism ? -1 : 0);  // fill-only entry: skipped
+        w[u] = reinterpret_cast<const uint32_t*>(a.dn_qw + (size_t)ch * (hidden >> 1))[tid];
+        sc[u] = down_scale(a, ch, grp);
+        const uint32_t hg = sp.h_full[ch];
+        hb[u] = isr ? rhe : (hg ^ 0x8000u);  // margin: the gate launch's h, negated
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const float f = sgn[u] ? bf16_to_f32(hb[u]) * bf16_to_f32(sc[u]) * 16.0f : 0.f;
+        fix_accumulate(w[u], f, acc);
+      }
+    }
+    if (blockIdx.x == 0 && filled < uk) {  // channel 0 once per unfilled slot
+      const uint32_t w = reinterpret_cast<const uint32_t*>(a.dn_qw)[tid];
+      const float f = bf16_to_f32(h0) * bf16_to_f32(down_scale(a, 0u, grp)) * 16.0f;
+      for (uint32_t u = filled; u < uk; ++u) fix_accumulate(w, f, acc);
+    }
+    float* out = a.partial + (size_t)(a.rt_max + (int)blockIdx.x) * hidden + 8 * tid;
+    *reinterpret_cast<float4*>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(out + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+  // h_out of the selected candidates (the gate launch's h), after the
+  // fix-up so that no barrier above waits for these loads
+  if (s0 && c0) a.h_out[pos0] = sp.h_full[my];
+  if (s1 && c1) a.h_out[pos1] = sp.h_full[my + 1];
+  if (stamp) a.meta->spec_stamp[1][3] = wall_clock64();
+}
+
+// Down workgroup w of the split step: the candidates of the gate launch in
+// list order (gate workgroup by gate workgroup), tiles of 256 positions x
+// one column block of 8 chunks; tile t = w + j * ndown goes to sub-tile j %
+// 8, round j / 8 (every sub-tile of the workgroup runs the same rounds, so
+// the barriers match).  A sub-tile is 16 slots of 8 lanes; slot s takes
+// positions 256 rt + s + 16 i (i < 16; lane l holds rows l and l + 8), all
+// loaded before any is used.  Positions past the candidate count, and
+// inactive sub-tiles, contribute 0.  Partial row rt, block cb.
+template <int SL>
+DIP_DEV void split_down_role(const SelDownArgs& a, int w, uint32_t* lds, int stamps) {
+  __shared__ uint32_t scratch[kWaves];
+  const int tid = threadIdx.x;
+  const bool stamp = stamps && w == 0 && tid == 0;
+  if (stamp) a.meta->spec_stamp[0][0] = wall_clock64();
+  const int hidden = a.sp.hidden;
+  uint32_t* pre = lds;                                       // [gate_wgs + 16]
+  uint32_t* first = lds + kMaxCandWgs + 16;                  // [tiles rows]: first gate wg
+  float* red = reinterpret_cast<float*>(lds + 2 * kMaxCandWgs + 64);  // 16 B aligned
+  // exclusive prefix of the gate workgroups' candidate counts
+  const uint32_t cnt = tid < a.gate_wgs ? a.cand_count[tid] : 0u;
+  uint32_t nc;
+  const uint32_t off = block_offset(cnt, scratch, &nc);
+  if (tid < a.gate_wgs) pre[tid] = off;
+  if (tid < 16) pre[a.gate_wgs + tid] = nc;  // sentinels past the last gate workgroup
+  // the gate workgroup holding each tile's first position (a workgroup lists
+  // fewer than 256 candidates, so it starts at most one tile)
+  if (tid < a.gate_wgs && cnt > 0) {
+    const uint32_t t0 = (off + kTilePos - 1) / kTilePos;
+    if (t0 * kTilePos < off + cnt) first[t0] = (uint32_t)tid;
+  }
+  if (w == 0 && tid == 0) a.meta->ncand = nc;
+  __syncthreads();
+  if (stamp) a.meta->spec_stamp[0][1] = wall_clock64();
+  const int cbs = a.col_blocks;
+  const int tiles = (int)((nc + kTilePos - 1) / kTilePos) * cbs;
+  const int jw = tiles > w ? (tiles - w + a.ndown - 1) / a.ndown : 0;
+  const int rounds = (jw + kSubTiles - 1) / kSubTiles;
+  const int sub = tid / kSubThreads, st = tid % kSubThreads;
+  const int l = st % 8, slot = st / 8;
+  const int gbase = (tid & 63) - l;
+  const size_t row_bytes = (size_t)(hidden >> 1);
+  const int ngroups = hidden >> 7;
+  DownArgs da{};  // the fields load_down_scales / load_down_row read
+  da.qw_a = a.dn_qw;
+  da.sc_a = a.dn_sc;
+  da.sc_gm = a.dn_sc_gm;
+  da.qw_safe = a.dn_qw;
+  da.sc_safe = a.dn_sc;
+  da.rows_a = a.n;
+  for (int r = 0; r < rounds; ++r) {
+    const int t = w + (r * kSubTiles + sub) * a.ndown;
+    const bool active = t < tiles;
+    const int rt = active ? t / cbs : 0, cb = active ? t % cbs : 0;
+    // lane l: rows l and l + 8 of the slot
+    uint32_t rid[2], hb[2], sv[2][2];
+    int lo[2];
+    bool live[2];
+    // the gate workgroup holding each of my two positions p: the last b with
+    // pre[b] <= p, from the tile's first one (16 reads at once; a search past
+    // them when the lists are sparse)
+    const int b0 = active ? (int)first[rt] : 0;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t p = (uint32_t)(rt * kTilePos + slot + kSubSlots * (l + 8 * q));
+      live[q] = active && p < nc;
+      int b = b0;
+#pragma unroll
+      for (int j = 1; j < 16; ++j) b += pre[b0 + j] <= p ? 1 : 0;
+      if (live[q] && b == b0 + 15 && pre[b0 + 16] <= p) {
+        int hi = a.gate_wgs - 1;
+        while (b < hi) {
+          const int mid = (b + hi + 1) >> 1;
+          if (pre[mid] <= p) b = mid; else hi = mid - 1;
+        }
+      }
+      lo[q] = live[q] ? b * kCandCap + (int)(p - pre[b]) : 0;
+    }
+    // unconditional loads from clamped indices (loads under branches serialise)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t ent = a.cand_list[lo[q]];
+      uint32_t ch = ent & 0xFFFFu;
+      ch = !live[q] ? kPadRow : (ch < (uint32_t)a.n ? ch : kBadRow);
+      rid[q] = ch;
+      const uint32_t hv = a.sp.h_full[ch < (uint32_t)a.n ? ch : 0u];
+      hb[q] = ch < (uint32_t)a.n ? hv : 0u;
+      load_down_scales<kGather, 2, SL>(da, ch, 2 * cb, ngroups, sv[q]);
+    }
+    DownRow ring[kSlotRows];
+#pragma unroll
+    for (int i = 0; i < kSlotRows; ++i)
+      load_down_row<kGather>(da, __shfl(rid[i / 8], gbase + i % 8, 64), cb * 8 + l, row_bytes,
+                             ring[i]);
+    if (stamp && r == 0) a.meta->spec_stamp[0][2] = wall_clock64();
+    float f[2][2];
+    down_coef<2>(rid[0], hb[0], sv[0], f[0]);
+    down_coef<2>(rid[1], hb[1], sv[1], f[1]);
+    float acc[kDownAcc];
+#pragma unroll
+    for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
+    down_accumulate<8, 2>(ring, f[0], l >= 4, gbase, acc);
+    down_accumulate<8, 2>(ring + 8, f[1], l >= 4, gbase, acc);
+    // the slots of each wave in registers, the sub-tile's two waves via LDS
+#pragma unroll
+    for (int m = 0; m < kDownAcc; ++m) acc[m] += dpp_mov<0x128>(acc[m]);  // row_ror:8
+    float t16[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      permlane16_swap(acc[m], acc[m + 16]);
+      t16[m] = acc[m] + acc[m + 16];
+    }
+    float u8[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      permlane32_swap(t16[m], t16[m + 8]);
+      u8[m] = t16[m] + t16[m + 8];
+    }
+    const int lane = tid & 63, wv = st >> 6;  // wave within the sub-tile
+    float* rs = red + sub * (2 * 256);
+    if ((lane & 15) < 8) {
+      float* dst = rs + wv * 256 + 32 * (lane % 8) + 8 * (lane >> 5) + 16 * ((lane >> 4) & 1);
+      *reinterpret_cast<float4*>(dst) = make_float4(u8[0], u8[1], u8[2], u8[3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(u8[4], u8[5], u8[6], u8[7]);
+    }
+    __syncthreads();
+    if (active) {
+      float* out = a.partial + (size_t)rt * hidden + (size_t)cb * 256;
+      for (int c = st; c < 256; c += kSubThreads) out[c] = rs[c] + rs[256 + c];
+    }
+    __syncthreads();  // the next round reuses the LDS
+  }
+  if (stamp) a.meta->spec_stamp[0][3] = wall_clock64();
+}
+
+template <int R, int LPR, int CH, int SL>
+__global__ __launch_bounds__(kThreads) void select_down_kernel(SelDownArgs a, int stamps) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  if ((int)blockIdx.x < a.sp.ntopk)
+    topk_body<R, kSelSplit, LPR, CH>(a.g, a.n, a.k, a.idx, a.meta, stamps, a.sp.ntopk, a.sp, lds,
+                                     &a);
+  else
+    split_down_role<SL>(a, (int)blockIdx.x - a.sp.ntopk, lds, stamps);
 }
 
 
@@ -804,6 +1151,56 @@ int launch_spec_width(const uint16_t* s, int n, int k, int32_t* idx, TopkMeta* m
 }
 
 }  // namespace
+
+namespace {
+template <int R, int LPR, int CH, int SL>
+int launch_select_down_variant(const SelDownArgs& a, int blocks, hipStream_t stream) {
+  static const bool lds_ok =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&select_down_kernel<R, LPR, CH, SL>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kFineBins * (int)sizeof(uint32_t)) == hipSuccess;
+  if (!lds_ok) return hip_status(hipGetLastError());
+  hipLaunchKernelGGL((select_down_kernel<R, LPR, CH, SL>), dim3(blocks), dim3(kThreads),
+                     kFineBins * sizeof(uint32_t), stream, a, tuning(DIP_TUNE_TOPK_STAMPS));
+  return hip_status(hipGetLastError());
+}
+template <int LPR, int CH, int SL>
+int launch_select_down_width(const SelDownArgs& a, int blocks, hipStream_t stream) {
+  if (a.n <= 4 * 8 * kThreads) return launch_select_down_variant<4, LPR, CH, SL>(a, blocks, stream);
+  return launch_select_down_variant<8, LPR, CH, SL>(a, blocks, stream);
+}
+template <int SL>
+int launch_select_down_sl(const SelDownArgs& a, int blocks, hipStream_t stream) {
+  const int chunks = a.sp.hidden / kChunkCols;
+  if (chunks == 160) return launch_select_down_width<32, 5, SL>(a, blocks, stream);
+  if (chunks == 128) return launch_select_down_width<32, 4, SL>(a, blocks, stream);
+  return launch_select_down_width<16, 5, SL>(a, blocks, stream);
+}
+}  // namespace
+
+bool split_step_supported(int64_t hidden, int64_t inter) {
+  // 8-chunk column blocks, an even number of scale groups per row (the down
+  // tiles' scale pairs) and a gate workgroup count that fits the lists
+  return topk_spec_supported(hidden) && hidden % 256 == 0 && inter >= 1 && inter <= kTopkMaxN &&
+         (hidden / kChunkCols) % 8 == 0;
+}
+
+int launch_select_down(SelDownArgs a, hipStream_t stream) {
+  if (a.n <= 0 || a.k <= 0 || a.k > a.n || a.n > kTopkMaxN) return DIP_ERR_SHAPE;
+  if (!split_step_supported(a.sp.hidden, a.n)) return DIP_ERR_UNSUPPORTED;
+  if (a.gate_wgs < 1 || a.gate_wgs > kMaxCandWgs) return DIP_ERR_UNSUPPORTED;
+  const int ntopk = (a.n + kSlice - 1) / kSlice;
+  a.sp.ntopk = ntopk;
+  a.sp.margin = (int)(a.n * (int64_t)tuning(DIP_TUNE_SPEC_MARGIN) / 1024);
+  a.rt_max = (a.n + kTilePos - 1) / kTilePos;
+  a.col_blocks = a.sp.hidden / (kChunkCols * 8);
+  a.ndown = std::max(device_cus() - ntopk, 1);
+  const int blocks = ntopk + a.ndown;
+  if (a.dn_sc_gm) return launch_select_down_sl<kScGm>(a, blocks, stream);
+  if (((reinterpret_cast<uintptr_t>(a.dn_sc)) & 3u) == 0)
+    return launch_select_down_sl<kScRow4>(a, blocks, stream);
+  return launch_select_down_sl<kScRow>(a, blocks, stream);
+}
 
 bool topk_spec_supported(int64_t hidden) {
   const int64_t chunks = hidden / kChunkCols;

@@ -155,9 +155,15 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_STEP               1: a decode step with speculation state runs
  *                               its top-k, up rows, h and down partials in
  *                               one launch after the gate, then a finish
- *                               launch (three launches); 0: top-k +
- *                               speculative up, then down + reduce (four
- *                               launches) (0: the faster on MI355X today)
+ *                               launch (three launches); 2: the gate also
+ *                               computes h of its candidate channels, then
+ *                               the top-k beside down tiles over every
+ *                               candidate (with a fix-up of the selection),
+ *                               then the reduce (three launches; widths
+ *                               5120, 4096, 2560; dip_mlp_decode only);
+ *                               0: top-k + speculative up, then down +
+ *                               reduce (four launches) (0: the fastest on
+ *                               MI355X today)
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {

@@ -25,11 +25,13 @@ pytestmark = pytest.mark.gpu
 MARGIN_PER_1024 = 8  # DIP_TUNE_SPEC_MARGIN default
 
 
-@pytest.fixture(scope="module", params=[0, 1], ids=["four-launch", "fused"])
+@pytest.fixture(scope="module", params=[0, 1, 2], ids=["four-launch", "fused", "split"])
 def K(request):
     """The library with the decode step's speculative path set to the
-    four-launch form (top-k + up, down, reduce) or the fused one (one launch
-    for top-k, up and down partials, then the finish)."""
+    four-launch form (top-k + up, down, reduce), the fused one (one launch
+    for top-k, up and down partials, then the finish) or the split one (the
+    gate with its candidates' up rows; the select beside the candidates' down
+    tiles; the reduce)."""
     import _dip_hip
     old = _dip_hip.get_tuning("step")
     _dip_hip.set_tuning("step", request.param)
@@ -99,13 +101,13 @@ def _state(key, band=(0, 0)):
 
 def _assert_next_state(K, state, g, k, margin, what, first=False):
     """The state a call leaves: its rank k + margin key as the next key; the
-    four-launch path keeps the key it used in [0] (0 after the first call),
-    the fused one the next key in both and a band that holds the cut (the
-    key of rank k + 1)."""
+    four-launch and split paths keep the key they used in [0] (0 after the
+    first call), the fused one the next key in both and a band that holds the
+    cut (the key of rank k + 1)."""
     st = state.cpu().numpy().view(np.uint32)
     key = _rank_key(g, k + margin)
     assert st[1] == key, what
-    if not K.get_tuning("step"):
+    if K.get_tuning("step") != 1:
         if first:
             assert st[0] == 0, what  # a zeroed state speculates on every channel
         return

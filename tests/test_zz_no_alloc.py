@@ -34,9 +34,10 @@ def _outs(H, I, k, fill):
 
 
 @pytest.mark.parametrize("spec,step,gm", [(False, 0, False), (True, 0, False), (True, 1, False),
-                                          (False, 0, True), (True, 0, True)],
-                         ids=["stagewise", "four-launch", "fused", "stagewise-gm",
-                              "four-launch-gm"])
+                                          (True, 2, False), (False, 0, True), (True, 0, True),
+                                          (True, 2, True)],
+                         ids=["stagewise", "four-launch", "fused", "split", "stagewise-gm",
+                              "four-launch-gm", "split-gm"])
 def test_noalloc_equals_workspace_entry_point(K, spec, step, gm):
     old = K.get_tuning("step")
     K.set_tuning("step", step)
