@@ -16,9 +16,11 @@
 // workgroup redundantly
 //   1. loads all n values into registers and builds the histogram in its LDS
 //      (a global histogram would need device-scope atomics, and the many
-//      channels that share a bf16 magnitude serialise those);
-//   2. finds max|s| and a_{k+1} (only the waves holding rank 1 / rank k+1
-//      search their bins);
+//      channels that share a bf16 magnitude serialise those), reducing the
+//      range [kmin, kmax] of the valid keys on the way;
+//   2. takes max|s| = kmax and finds a_{k+1} by a prefix over per-thread
+//      sums of consecutive bins of that range (only the thread holding rank
+//      k+1 walks its bins);
 //   3. replays the 25 bisection steps on one lane -> the two key cuts;
 //   4. takes the tier totals from the histogram and counts the tiers of the
 //      values on the shorter side of its slice (before or after it);
@@ -78,6 +80,19 @@ DIP_DEV uint32_t tier_counts8(const uint32_t w[4], uint32_t cut_a2, uint32_t spa
     acc_b = pk_add(acc_b, in_span2(pk_sub(k2, cut_b2), span_b2, ones));
   }
   return ((acc_a & 0xFFFFu) + (acc_a >> 16)) | (((acc_b & 0xFFFFu) + (acc_b >> 16)) << 16);
+}
+
+// Maximum over the 64 lanes of a wave (row_shr 1, 2, 4, 8 within rows of
+// 16, then row_bcast:15 / row_bcast:31 across rows; zero fill), returned
+// from lane 63 to every lane.
+DIP_DEV uint32_t wave_max(uint32_t v) {
+  v = max(v, dpp_zero<0x111>(v));
+  v = max(v, dpp_zero<0x112>(v));
+  v = max(v, dpp_zero<0x114>(v));
+  v = max(v, dpp_zero<0x118>(v));
+  v = max(v, dpp_zero<0x142, 0xA>(v));
+  v = max(v, dpp_zero<0x143, 0xC>(v));
+  return lane63(v);
 }
 
 // Elements [base, n) of a chunk that straddles n, 2 per dword; the rest read
@@ -288,7 +303,8 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
   constexpr bool SPEC = MODE != kSelPlain;
   __shared__ uint32_t wtot[kWaves];
   __shared__ uint32_t wsum_a[kWaves], wsum_b[kWaves], wside[kWaves], wown[kWaves];
-  __shared__ uint32_t sh_a, sh_max, sh_cut_a, sh_cut_b, sh_spec, sh_rcount;
+  __shared__ uint32_t wlo[kWaves], whi[kWaves];
+  __shared__ uint32_t sh_a, sh_cut_a, sh_cut_b, sh_spec, sh_rcount;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -323,113 +339,102 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
   }
   if (tid == 0) {
     sh_a = kNoKey;
-    sh_max = kNoKey;
     sh_spec = kNoKey;
     sh_rcount = 0;
   }
   __syncthreads();
 
-  // ---- 2. histogram of every magnitude (NaN / padding bins ignored later) --
+  // ---- 2. histogram of every magnitude, and the range of the valid keys ---
+  // (NaN and padding keys, above 0x7F80, land in bins the search never reads)
+  {
+    uint32_t lo = kNoKey, hi1 = 0;  // smallest valid key, largest + 1
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if ((tid + kThreads * r) * 8 < n) {  // chunks wholly past n would pile onto one bin
+    for (int r = 0; r < R; ++r) {
+      if ((tid + kThreads * r) * 8 < n) {  // chunks wholly past n would pile onto one bin
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        atomicAdd(&hist[key[r][i] & 0x7FFFu], 1u);
-        atomicAdd(&hist[(key[r][i] >> 16) & 0x7FFFu], 1u);
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t b0 = key[r][i] & 0x7FFFu, b1 = (key[r][i] >> 16) & 0x7FFFu;
+          atomicAdd(&hist[b0], 1u);
+          atomicAdd(&hist[b1], 1u);
+          const bool v0 = b0 <= kMaxValidKey, v1 = b1 <= kMaxValidKey;
+          lo = v0 ? min(lo, b0) : lo;
+          hi1 = v0 ? max(hi1, b0 + 1u) : hi1;
+          lo = v1 ? min(lo, b1) : lo;
+          hi1 = v1 ? max(hi1, b1 + 1u) : hi1;
+        }
       }
+    }
+    lo = ~wave_max(~lo);
+    hi1 = wave_max(hi1);
+    if (lane == 0) {
+      wlo[wave] = lo;
+      whi[wave] = hi1;
     }
   }
   __syncthreads();
   if (stamp) meta->stamp[1] = wall_clock64();
+  // Only the bins [kmin, kmax1) can hold valid values: magnitudes span a few
+  // thousand keys in practice, so the scan below reads those and not all
+  // 32768.
+  uint32_t kmin = kNoKey, kmax1 = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    kmin = min(kmin, wlo[w]);
+    kmax1 = max(kmax1, whi[w]);
+  }
+  const int span = kmax1 > kmin ? (int)(kmax1 - kmin) : 0;  // 0: no valid value
 
-  // ---- 3. max and a_{k+1} --------------------------------------------------
-  // Wave w reads its 2048 bins as eight 256-bin rows j; lane L holds bins
-  // 2048w + 256j + 4L .. +3 (consecutive lanes, consecutive 16 B: no bank
-  // conflicts).  Wave totals first; only a wave that holds rank 1 or rank
-  // k+1 (counting from the top bin) scans its rows.
-  uint32_t nvalid = 0;
-  uint32_t sum4[8];
+  // ---- 3. a_{k+1} (and the key of rank k+margin) ---------------------------
+  // Thread t sums the m = ceil(span / 1024) bins [top_t - m, top_t) counted
+  // down from kmax1 (top_t = kmax1 - t m), so an exclusive prefix over t
+  // counts the values above its bins; the thread whose bins hold a rank walks
+  // them.  max|s| is kmax1 - 1.
+  const int m = (span + kThreads - 1) / kThreads;
+  const int top = (int)kmax1 - tid * m;           // my bins: [bot, top)
+  const int bot = max(top - m, (int)kmin);
+  uint32_t mysum = 0;
+  for (int b = top - 1; b >= bot; --b) mysum += hist[b];
+  uint32_t nvalid = 0, above = 0;
   {
-    const uint4* h4 = reinterpret_cast<const uint4*>(hist);
-    uint4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = h4[512 * wave + 64 * j + lane];
-    if (wave == kWaves - 1) {
-      // bins above +inf (NaN magnitudes, padding) never count
-      const uint32_t b0 = 2048u * wave + 256u * 7 + 4u * lane;
-      if (b0 + 0 > kMaxValidKey) v[7].x = 0;
-      if (b0 + 1 > kMaxValidKey) v[7].y = 0;
-      if (b0 + 2 > kMaxValidKey) v[7].z = 0;
-      if (b0 + 3 > kMaxValidKey) v[7].w = 0;
-    }
-    uint32_t lsum = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sum4[j] = v[j].x + v[j].y + v[j].z + v[j].w;
-      lsum += sum4[j];
-    }
-    const uint32_t wsum = lane63(wave_prefix(lsum));
-    if (lane == 0) wtot[wave] = wsum;
+    const uint32_t incl = wave_prefix(mysum);
+    if (lane == 63) wtot[wave] = incl;
     __syncthreads();
-    uint32_t above = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      above += w > wave ? wtot[w] : 0u;
+      above += w < wave ? wtot[w] : 0u;
       nvalid += wtot[w];
     }
-    const uint32_t need = (uint32_t)k + 1u;
-    const uint32_t need_s = SPEC ? (uint32_t)k + (uint32_t)sp.margin : 0u;
-    const bool own1 = above < 1u && wsum >= 1u;
-    const bool ownk = above < need && above + wsum >= need;
-    const bool owns = SPEC && blockIdx.x == 0 && above < need_s && above + wsum >= need_s;
-    if (own1 || ownk || owns) {  // wave-uniform
-      uint32_t carry = above;
-#pragma unroll
-      for (int j = 7; j >= 0; --j) {
-        const uint32_t p = wave_prefix(sum4[j]);
-        const uint32_t t = lane63(p);
-        const uint32_t ge = carry + t - p + sum4[j];  // valid values in bins >= my first bin
-        const uint32_t gt = ge - sum4[j];             // ... in bins >= my first bin + 4
-        carry += t;
-        const uint32_t b0 = 2048u * wave + 256u * j + 4u * lane;
-        const uint32_t cnt[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-        if (own1 && gt < 1u && ge >= 1u) {
-          uint32_t run = gt, b = kNoKey;
-#pragma unroll
-          for (int e = 3; e >= 0; --e) {
-            run += cnt[e];
-            if (b == kNoKey && run >= 1u) b = b0 + e;
-          }
-          sh_max = b;
-        }
-        if (ownk && gt < need && ge >= need) {
-          uint32_t run = gt, b = kNoKey;
-#pragma unroll
-          for (int e = 3; e >= 0; --e) {
-            run += cnt[e];
-            if (b == kNoKey && run >= need) b = b0 + e;
-          }
-          sh_a = b;
-        }
-        if (owns && gt < need_s && ge >= need_s) {
-          uint32_t run = gt, b = kNoKey;
-#pragma unroll
-          for (int e = 3; e >= 0; --e) {
-            run += cnt[e];
-            if (b == kNoKey && run >= need_s) b = b0 + e;
-          }
-          sh_spec = b;
-        }
+    above += incl - mysum;
+  }
+  const uint32_t need = (uint32_t)k + 1u;
+  const uint32_t need_s = SPEC && blockIdx.x == 0 ? (uint32_t)k + (uint32_t)sp.margin : 0u;
+  if (above < need && above + mysum >= need) {
+    uint32_t run = above;
+    for (int b = top - 1; b >= bot; --b) {
+      run += hist[b];
+      if (run >= need) {
+        sh_a = (uint32_t)b;
+        break;
+      }
+    }
+  }
+  if (above < need_s && above + mysum >= need_s) {
+    uint32_t run = above;
+    for (int b = top - 1; b >= bot; --b) {
+      run += hist[b];
+      if (run >= need_s) {
+        sh_spec = (uint32_t)b;
+        break;
       }
     }
   }
   __syncthreads();
+  const uint32_t key_max = span > 0 ? kmax1 - 1u : kNoKey;
   if (stamp) meta->stamp[2] = wall_clock64();
 
   // ---- 4. replay the 25 fp32 bisection steps (topk_select.cu:141-158) -----
   if (tid == 0) {
-    uint32_t ka = sh_a, km = sh_max;
+    uint32_t ka = sh_a, km = key_max;
     if (ka != kNoKey && ka < kMinNormalKey) ka = 0;  // subnormal -> 0
     if (km != kNoKey && km < kMinNormalKey) km = 0;
     // with fewer than k+1 values "c > k" never holds: a = 0 never exceeds t >= 0
@@ -463,26 +468,18 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
   const Cuts c = make_cuts(sh_cut_a, sh_cut_b);
 
   // ---- 5. tier totals from the histogram, tier counts of one side ----------
-  // Totals: #{b >= cut} summed per 4-bin group; the one group a cut splits
-  // is summed bin by bin (bins above +inf were zeroed in sum4).
+  // Totals: #{b >= cut} over my bins [bot, top), whole when the cut is at or
+  // below them, bin by bin when it splits them.
   uint32_t ge_a = 0, ge_b = 0;
   {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t b0 = 2048u * wave + 256u * j + 4u * lane;
-      ge_a += b0 >= c.cut_a ? sum4[j] : 0u;
-      ge_b += b0 >= c.cut_b ? sum4[j] : 0u;
-      const bool split_a = b0 < c.cut_a && b0 + 3 >= c.cut_a;
-      const bool split_b = b0 < c.cut_b && b0 + 3 >= c.cut_b;
-      if (split_a | split_b) {
-        const uint4 v = reinterpret_cast<const uint4*>(hist)[512 * wave + 64 * j + lane];
-        const uint32_t cnt[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 1; e < 4; ++e) {
-          const uint32_t ce = b0 + e <= kMaxValidKey ? cnt[e] : 0u;
-          ge_a += split_a && b0 + e >= c.cut_a ? ce : 0u;
-          ge_b += split_b && b0 + e >= c.cut_b ? ce : 0u;
-        }
+    const int ca = (int)c.cut_a, cb = (int)c.cut_b;
+    ge_a = bot >= ca ? mysum : 0u;
+    ge_b = bot >= cb ? mysum : 0u;
+    if ((bot < ca && top > ca) || (bot < cb && top > cb)) {
+      for (int b = top - 1; b >= bot; --b) {
+        const uint32_t h = hist[b];
+        ge_a += bot < ca && b >= ca ? h : 0u;
+        ge_b += bot < cb && b >= cb ? h : 0u;
       }
     }
   }
