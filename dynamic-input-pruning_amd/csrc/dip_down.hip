@@ -126,41 +126,6 @@ __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
   }
 }
 
-// The split decode step's y: the used down row tiles [0, ceil(ncand/256))
-// then the fix-up rows [rt_max, rt_max + nfix), summed in that order by the
-// down_reduce_kernel scheme (kRedSplit interleaved splits, added in order).
-template <int NB>
-__global__ __launch_bounds__(kRedOut * kRedSplit) void split_reduce_kernel(
-    const float* __restrict__ partial, const TopkMeta* __restrict__ meta, int rt_max, int nfix,
-    int out_features, uint16_t* __restrict__ y) {
-  __shared__ float part[kRedSplit][kRedOut];
-  const int ru = min((int)((meta->ncand + 255u) / 256u), rt_max);
-  const int rows = ru + nfix;
-  const int oo = threadIdx.x % kRedOut;
-  const int p = threadIdx.x / kRedOut;
-  const int o = min(blockIdx.x * kRedOut + oo, out_features - 1);
-  float s = 0.f;
-  for (int r0 = p; r0 < rows; r0 += NB * kRedSplit) {
-    float v[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int r = min(r0 + u * kRedSplit, rows - 1);
-      const int row = r < ru ? r : rt_max + (r - ru);
-      v[u] = partial[(size_t)row * out_features + o];
-    }
-#pragma unroll
-    for (int u = 0; u < NB; ++u) s = r0 + u * kRedSplit < rows ? s + v[u] : s;
-  }
-  part[p][oo] = s;
-  __syncthreads();
-  if (p == 0 && blockIdx.x * kRedOut + oo < out_features) {
-    float t = part[0][oo];
-#pragma unroll
-    for (int q = 1; q < kRedSplit; ++q) t += part[q][oo];
-    y[blockIdx.x * kRedOut + oo] = (uint16_t)f32_to_bf16(t);
-  }
-}
-
 // k == 0: y = bf16(0).
 __global__ void down_zero_kernel(int out_features, uint16_t* __restrict__ y) {
   const int o = blockIdx.x * blockDim.x + threadIdx.x;
@@ -213,15 +178,6 @@ void launch_down(int src, const DownArgs& a, int blocks, hipStream_t stream) {
 int launch_down_reduce(const float* partial, int row_blocks, int out_features, uint16_t* y,
                        hipStream_t stream) {
   launch_reduce(partial, row_blocks, out_features, y, stream);
-  return hip_status(hipGetLastError());
-}
-
-int launch_split_reduce(const float* partial, const TopkMeta* meta, int rt_max, int nfix,
-                        int out_features, uint16_t* y, hipStream_t stream) {
-  if (rt_max < 0 || nfix < 0 || rt_max + nfix < 1 || out_features <= 0) return DIP_ERR_SHAPE;
-  const unsigned blocks = (unsigned)((out_features + kRedOut - 1) / kRedOut);
-  hipLaunchKernelGGL((split_reduce_kernel<16>), dim3(blocks), dim3(kRedOut * kRedSplit), 0,
-                     stream, partial, meta, rt_max, nfix, out_features, y);
   return hip_status(hipGetLastError());
 }
 

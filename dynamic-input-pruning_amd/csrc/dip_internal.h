@@ -118,7 +118,6 @@ struct TopkMeta {
   // of the step writes them, the finish copies them to the layer state)
   uint32_t next_key;
   uint32_t next_band;
-  uint32_t ncand;  // the split step: candidates listed by its gate launch
 };
 
 // The top-k workspace holds the last call's TopkMeta.
@@ -146,17 +145,17 @@ struct SpecArgs {
 //   1. gate_spec: g = bf16(silu(bf16(gate . x))) for every channel, then, in
 //      the same workgroup, h_full[c] = bf16(g[c] * bf16(up[c] . x)) for its
 //      candidate channels c (magnitude key in [state[1], 0x7F80): the
-//      speculation key, NaN and infinities excluded); each gate workgroup b
-//      lists its candidates in cand_list[b * kCandCap ...] (channel | g bits
-//      << 16, group by group, lanes in order) and counts them in
+//      speculation key, NaN and infinities excluded); with cand_list set,
+//      each gate workgroup b also lists its candidates in cand_list[b *
+//      kCandCap ...] (channel | g bits << 16) and counts them in
 //      cand_count[b]; workgroup 0 copies state[1] to state[0];
 //   2. select_down: the top-k select workgroups (idx, h_out, the next key in
 //      state[1], h of the selected channels that are not candidates, and one
 //      fix-up partial row each: + those channels' down rows, - the down rows
 //      of candidates that were not selected, + channel 0 once per unfilled
-//      slot) beside down workgroups that sum h_full[c] * down_t[c] over every
-//      candidate in fixed tiles of 256 list positions;
-//   3. the reduce over the used down rows and the fix-up rows.
+//      slot) beside down workgroups that sum h_full[c] * down_t[c] over the
+//      candidates of a range of channels per tile (the same key test on g);
+//   3. the reduce over the ranges' partial rows and the fix-up rows.
 struct GateSpecArgs {
   const int8_t* qw;      // gate
   const uint16_t* sc;
@@ -166,8 +165,8 @@ struct GateSpecArgs {
   uint16_t* g;
   uint16_t* h_full;
   uint32_t* state;       // [1] the key of this call; workgroup 0 copies it to [0]
-  uint32_t* cand_count;  // [gate workgroups]
-  uint32_t* cand_list;   // [gate workgroups][kCandCap]
+  uint32_t* cand_count;  // optional [gate workgroups]
+  uint32_t* cand_list;   // optional [gate workgroups][kCandCap]
   int nrows;
   int in_features;
   int ngrp;              // set by the launcher
@@ -188,19 +187,17 @@ struct SelDownArgs {
   const int8_t* dn_qw;
   const uint16_t* dn_sc;     // [n][hidden/128]
   const uint16_t* dn_sc_gm;  // optional [hidden/128][n]
-  const uint32_t* cand_count;
-  const uint32_t* cand_list;
-  int gate_wgs;
-  float* partial;        // [rt_max + ntopk][hidden]: down row tiles, then the fix-up rows
-  int rt_max;            // set by the launcher: ceil(n / 256)
+  float* partial;        // [ranges + ntopk][hidden]: the ranges' rows, then the fix-up rows
+  int ranges;            // channel ranges (split_layout)
+  int chan_per_range;    // channels per range (split_layout)
   int col_blocks;        // set by the launcher
   int ndown;             // down workgroups (set by the launcher)
 };
 int launch_select_down(SelDownArgs a, hipStream_t stream);
-// y from the split step's partials: rows [0, ceil(meta->ncand / 256)) and
-// [rt_max, rt_max + nfix), in that order.
-int launch_split_reduce(const float* partial, const TopkMeta* meta, int rt_max, int nfix,
-                        int out_features, uint16_t* y, hipStream_t stream);
+// The split step's channel ranges for (hidden, n, k): false if they do not
+// fit one round of the down workgroups' tiles.
+bool split_layout(int64_t hidden, int64_t n, int64_t k, int* ranges, int* chan_per_range);
+constexpr int kSelectSlice = 2048;  // values placed per top-k select workgroup
 
 // The decode step after the gate in one launch (dip_step.hip): the top-k
 // cut, up rows, h and per-workgroup down partials; then the finish launch

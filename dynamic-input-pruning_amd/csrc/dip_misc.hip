@@ -583,18 +583,29 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
 namespace {
 // The split decode step (dip_internal.h): the gate launch with the
 // candidates' up rows, the select + candidate-down launch, the reduce.
+// The split step runs where its channel ranges fit one round of down tiles
+// and their partial rows fit the workspace; elsewhere the four-launch step
+// runs.
+bool split_step_fits(int64_t hidden, int64_t inter, int64_t k) {
+  int ranges = 0, per = 0;
+  if (gate_spec_blocks(inter, hidden) < 1 || !split_layout(hidden, inter, k, &ranges, &per))
+    return false;
+  const int64_t rows = ranges + (inter + kSelectSlice - 1) / kSelectSlice;
+  return (size_t)rows * (size_t)hidden * sizeof(float) <= mlp_partial_bytes(hidden, k);
+}
+
 int run_split_step(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
                    const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
                    const uint16_t* down_t_sc_gm, const uint16_t* x, uint16_t* y,
                    uint16_t* g_out, int32_t* idx_out, uint16_t* h_out, int64_t hidden,
                    int64_t inter, int64_t k, void* workspace, void* layer_state,
                    hipStream_t s) {
-  const int gate_wgs = gate_spec_blocks(inter, hidden);
-  if (gate_wgs < 1) return DIP_ERR_UNSUPPORTED;
+  if (gate_spec_blocks(inter, hidden) < 1) return DIP_ERR_UNSUPPORTED;
   const MlpWs w = mlp_ws(workspace, hidden, inter, k);
-  const int rt_max = (int)((inter + 255) / 256);
-  const int nfix = (int)((inter + 2047) / 2048);
-  if ((size_t)(rt_max + nfix) * (size_t)hidden * sizeof(float) > w.partial_bytes)
+  int ranges = 0, per = 0;
+  if (!split_layout(hidden, inter, k, &ranges, &per)) return DIP_ERR_UNSUPPORTED;
+  const int nlists = (int)((inter + kSelectSlice - 1) / kSelectSlice);  // fix-up rows: one per select workgroup
+  if ((size_t)(ranges + nlists) * (size_t)hidden * sizeof(float) > w.partial_bytes)
     return DIP_ERR_WORKSPACE;
   GateSpecArgs ga{};
   ga.qw = gate_qw;
@@ -605,8 +616,6 @@ int run_split_step(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t*
   ga.g = g_out;
   ga.h_full = w.h_full;
   ga.state = static_cast<uint32_t*>(layer_state);
-  ga.cand_count = w.cand_count;
-  ga.cand_list = w.cand_list;
   ga.nrows = (int)inter;
   ga.in_features = (int)hidden;
   int st = launch_gate_spec(ga, s);
@@ -627,14 +636,11 @@ int run_split_step(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t*
   sd.dn_qw = down_t_qw;
   sd.dn_sc = down_t_sc;
   sd.dn_sc_gm = down_t_sc_gm;
-  sd.cand_count = w.cand_count;
-  sd.cand_list = w.cand_list;
-  sd.gate_wgs = gate_wgs;
   sd.partial = reinterpret_cast<float*>(w.partial);
   st = launch_select_down(sd, s);
   if (st) return st;
-  return launch_split_reduce(reinterpret_cast<const float*>(w.partial), w.meta, rt_max, nfix,
-                             (int)hidden, y, s);
+  return launch_down_reduce(reinterpret_cast<const float*>(w.partial), ranges + nlists,
+                            (int)hidden, y, s);
 }
 }  // namespace
 
@@ -653,8 +659,7 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
   const size_t hfull_bytes = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
   char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
   const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
-  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) == 2 && split_step_supported(hidden, inter) &&
-      gate_spec_blocks(inter, hidden) > 0) {
+  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) == 2 && split_step_fits(hidden, inter, k)) {
     int st = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, idx_out,
                              h_out, layer_state, ws, hidden, inter);
     if (st) return st;

@@ -203,8 +203,8 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
 // launch, dip_internal.h).  The gate half is rowdot_kernel<LPR, CH, kContig,
 // kSilu, true, ROWS> (the same loads, arithmetic and order, so g is bit for
 // bit the plain gate's).  Then the workgroup's candidates, the rows it just
-// computed whose key |g bits| lies in [key, 0x7F80), are listed in LDS and
-// in cand_list, and its groups take them in turn (entry e goes to group e
+// computed whose key |g bits| lies in [key, 0x7F80), are listed in LDS (and
+// in cand_list when given), and its groups take them in turn (entry e goes to group e
 // mod groups, one row of loads in flight): u = up[c] . x with the x pairs
 // still in VGPRs (row_dot_part, as dip_up_gather_h computes it), h_full[c] =
 // bf16(g[c] * bf16(u)).  The up rows follow the gate rows in the same
@@ -286,9 +286,9 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void gate_spec_kernel(GateSpecAr
     const int e = base + __popc(gm & ((1u << l) - 1u));
     const uint32_t entry = (uint32_t)jl | (v << 16);
     clist[e] = entry;
-    a.cand_list[(size_t)blockIdx.x * kCandCap + e] = entry;
+    if (a.cand_list) a.cand_list[(size_t)blockIdx.x * kCandCap + e] = entry;
   }
-  if (threadIdx.x == 0) a.cand_count[blockIdx.x] = (uint32_t)total;
+  if (a.cand_count && threadIdx.x == 0) a.cand_count[blockIdx.x] = (uint32_t)total;
   if (rot) a.state[0] = key;
   __syncthreads();
 

@@ -616,10 +616,14 @@ __global__ __launch_bounds__(kThreads) void topk_spec_kernel(
 namespace {
 constexpr int kSubThreads = 128;                  // a down sub-tile: two waves
 constexpr int kSubTiles = kThreads / kSubThreads; // per down workgroup
-constexpr int kTilePos = 256;                     // list positions per down tile
+constexpr int kTilePos = kSubThreads;             // list positions per pass of a down sub-tile
 constexpr int kSubSlots = kSubThreads / 8;        // 8-lane slots of a sub-tile
-constexpr int kSlotRows = kTilePos / kSubSlots;   // rows per slot (two per lane)
-constexpr uint32_t kNoEntry = 0xFFFFFFFFu;
+constexpr int kSlotRows = 8;                      // rows per slot and pass (one per lane)
+static_assert(kSelectSlice == kSlice, "one fix-up row per select workgroup");
+constexpr int kRangeMax = 512;                    // channels per range at most (4 per thread)
+constexpr int kFixGroups = 4;                     // entry groups of the fix-up row
+constexpr int kFixLdsWord = 12288;                // the fix-up groups' sums: past the x pairs
+constexpr int kRangeTarget = 224;                 // candidates per range aimed at (two passes)
 
 // Wave-ordered exclusive prefix of per-thread counts c (< 2^16 in total):
 // returns my offset and sets *total; scratch: kWaves words of LDS.  Ends with
@@ -641,7 +645,7 @@ DIP_DEV uint32_t block_offset(uint32_t c, uint32_t* scratch, uint32_t* total) {
   return before + incl - c;
 }
 
-// acc[m] += (q/16)[row ch, columns 8t .. 8t+7] * f for the dword t of the row.
+// acc[m] += (q/16)[row, columns 8t .. 8t+7] * f for the dword t of the row.
 DIP_DEV void fix_accumulate(uint32_t w, float f, float acc[8]) {
   const uint32_t hq = w >> 4;
   acc[0] = fmaf(cvt_nibble_div16<0>(w), f, acc[0]);
@@ -673,7 +677,7 @@ DIP_DEV uint32_t down_scale(const SelDownArgs& a, uint32_t ch, int g) {
 //     candidates that were not selected, + channel 0 once per unfilled slot
 //     (workgroup 0), each as h * (q/16) * 16 s with the products of the down
 //     tiles; entries in a fixed order (residual then margin, each in slice
-//     order), so the row is deterministic.
+//     order) split over fixed thread groups, so the row is deterministic.
 template <int LPR, int CH>
 DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool s0, bool s1,
                                uint32_t pos0, uint32_t pos1, uint32_t uk, uint32_t filled,
@@ -747,48 +751,76 @@ DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool
     for (uint32_t p = filled + (uint32_t)tid; p < uk; p += kThreads) a.h_out[p] = (uint16_t)h0;
   }
 
-  // the fix-up row: thread t < hidden / 8 owns columns 8t .. 8t + 7
-  const int nd = hidden >> 3;
-  if (tid < nd) {
-    const int grp = (8 * tid) >> 7;
+  // the fix-up row: ng groups of hidden / 16 threads; thread (grp, d) owns
+  // columns 16 d .. 16 d + 15 and takes entries grp, grp + ng, ... B at a
+  // time (one round of loads for the few dozen entries of a steady-state
+  // token), and the groups' sums are added in group order through LDS
+  const int nd = hidden >> 4;
+  const int ng = min(kThreads / nd, kFixGroups);
+  const int grp = tid / nd, d = tid % nd;
+  float* gsum = reinterpret_cast<float*>(lds + kFixLdsWord);  // [ng][hidden]
+  if (grp < ng) {
+    const int gcol = (16 * d) >> 7;  // the scale group of my columns
     const int nfl = (int)(nr + nm);
-    float acc[8];
+    float acc[16];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc[m] = 0.f;
-    constexpr int B = 8;  // entries in flight
-    for (int e0 = 0; e0 < nfl; e0 += B) {
-      uint32_t w[B], sc[B], hb[B];
+    for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+    constexpr int B = 12;  // entries in flight per thread
+    for (int e0 = grp; e0 < nfl; e0 += B * ng) {
+      uint2 w[B];
+      uint32_t sc[B], hb[B];
       int sgn[B];  // +1 residual, -1 margin, 0 none
 #pragma unroll
       for (int u = 0; u < B; ++u) {
         // branch-free: every load is issued, from clamped indices, and the
         // entry kind picks the values (loads under branches serialise)
-        const int e = e0 + u;
+        const int e = e0 + u * ng;
         const bool isr = e < (int)nr, ism = !isr && e < nfl;
         const int er = isr ? e : 0, em = ism ? e - (int)nr : 0;
         const uint32_t rent = rlist[er], raux_e = raux[er], rhe = rh[er];
         const uint32_t ment = mlist[em];
         const uint32_t ch = isr ? (rent & 0xFFFFu) : (ism ? ment : 0u);
         sgn[u] = isr ? ((raux_e >> 31) ? 1 : 0) : (ism ? -1 : 0);  // fill-only entry: skipped
-        w[u] = reinterpret_cast<const uint32_t*>(a.dn_qw + (size_t)ch * (hidden >> 1))[tid];
-        sc[u] = down_scale(a, ch, grp);
+        w[u] = reinterpret_cast<const uint2*>(a.dn_qw + (size_t)ch * (hidden >> 1))[d];
+        sc[u] = down_scale(a, ch, gcol);
         const uint32_t hg = sp.h_full[ch];
         hb[u] = isr ? rhe : (hg ^ 0x8000u);  // margin: the gate launch's h, negated
       }
 #pragma unroll
       for (int u = 0; u < B; ++u) {
         const float f = sgn[u] ? bf16_to_f32(hb[u]) * bf16_to_f32(sc[u]) * 16.0f : 0.f;
-        fix_accumulate(w[u], f, acc);
+        fix_accumulate(w[u].x, f, acc);
+        fix_accumulate(w[u].y, f, acc + 8);
       }
     }
-    if (blockIdx.x == 0 && filled < uk) {  // channel 0 once per unfilled slot
-      const uint32_t w = reinterpret_cast<const uint32_t*>(a.dn_qw)[tid];
-      const float f = bf16_to_f32(h0) * bf16_to_f32(down_scale(a, 0u, grp)) * 16.0f;
-      for (uint32_t u = filled; u < uk; ++u) fix_accumulate(w, f, acc);
+    if (grp == 0 && blockIdx.x == 0 && filled < uk) {  // channel 0 once per unfilled slot
+      const uint2 w = reinterpret_cast<const uint2*>(a.dn_qw)[d];
+      const float f = bf16_to_f32(h0) * bf16_to_f32(down_scale(a, 0u, gcol)) * 16.0f;
+      for (uint32_t u = filled; u < uk; ++u) {
+        fix_accumulate(w.x, f, acc);
+        fix_accumulate(w.y, f, acc + 8);
+      }
     }
-    float* out = a.partial + (size_t)(a.rt_max + (int)blockIdx.x) * hidden + 8 * tid;
-    *reinterpret_cast<float4*>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    *reinterpret_cast<float4*>(out + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    float4* dst = reinterpret_cast<float4*>(gsum + (size_t)grp * hidden + 16 * d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dst[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
+  }
+  __syncthreads();
+  {
+    float* out = a.partial + (size_t)(a.ranges + (int)blockIdx.x) * hidden;
+    const float4* g4 = reinterpret_cast<const float4*>(gsum);
+    for (int c4 = tid; c4 < hidden / 4; c4 += kThreads) {
+      float4 v = g4[c4];
+      for (int q = 1; q < ng; ++q) {
+        const float4 u = g4[(size_t)q * (hidden / 4) + c4];
+        v.x += u.x;
+        v.y += u.y;
+        v.z += u.z;
+        v.w += u.w;
+      }
+      reinterpret_cast<float4*>(out)[c4] = v;
+    }
   }
   // h_out of the selected candidates (the gate launch's h), after the
   // fix-up so that no barrier above waits for these loads
@@ -797,46 +829,75 @@ DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool
   if (stamp) a.meta->spec_stamp[1][3] = wall_clock64();
 }
 
-// Down workgroup w of the split step: the candidates of the gate launch in
-// list order (gate workgroup by gate workgroup), tiles of 256 positions x
-// one column block of 8 chunks; tile t = w + j * ndown goes to sub-tile j %
-// 8, round j / 8 (every sub-tile of the workgroup runs the same rounds, so
-// the barriers match).  A sub-tile is 16 slots of 8 lanes; slot s takes
-// positions 256 rt + s + 16 i (i < 16; lane l holds rows l and l + 8), all
-// loaded before any is used.  Positions past the candidate count, and
-// inactive sub-tiles, contribute 0.  Partial row rt, block cb.
+// Down workgroup w of the split step: tiles (channel range r, column block
+// cb), tile t = r * col_blocks + cb on sub-tile t / ndown of workgroup t %
+// ndown (split_layout keeps the tiles within one round).  A sub-tile (128
+// threads: 16 slots of 8 lanes) loads g and h_full of its range's channels at
+// once, lists the candidates (the gate launch's key test) in channel order,
+// and walks them 128 positions per pass: slot s takes positions 128 pass + s
+// + 16 i (i < 8; lane l holds row l), all loaded before any is used;
+// positions past the count contribute 0.  The slot sums are reduced as
+// in the down kernel into partial row r, block cb.
 template <int SL>
-DIP_DEV void split_down_role(const SelDownArgs& a, int w, uint32_t* lds, int stamps) {
-  __shared__ uint32_t scratch[kWaves];
+DIP_DEV void range_down_role(const SelDownArgs& a, int w, uint32_t* lds, int stamps) {
+  constexpr int kPer = kRangeMax / kSubThreads;  // channels per thread
+  __shared__ uint32_t wcnt[kSubTiles][kPer][2];   // candidates per sub-tile, pass q, wave
   const int tid = threadIdx.x;
   const bool stamp = stamps && w == 0 && tid == 0;
   if (stamp) a.meta->spec_stamp[0][0] = wall_clock64();
   const int hidden = a.sp.hidden;
-  uint32_t* pre = lds;                                       // [gate_wgs + 16]
-  uint32_t* first = lds + kMaxCandWgs + 16;                  // [tiles rows]: first gate wg
-  float* red = reinterpret_cast<float*>(lds + 2 * kMaxCandWgs + 64);  // 16 B aligned
-  // exclusive prefix of the gate workgroups' candidate counts
-  const uint32_t cnt = tid < a.gate_wgs ? a.cand_count[tid] : 0u;
-  uint32_t nc;
-  const uint32_t off = block_offset(cnt, scratch, &nc);
-  if (tid < a.gate_wgs) pre[tid] = off;
-  if (tid < 16) pre[a.gate_wgs + tid] = nc;  // sentinels past the last gate workgroup
-  // the gate workgroup holding each tile's first position (a workgroup lists
-  // fewer than 256 candidates, so it starts at most one tile)
-  if (tid < a.gate_wgs && cnt > 0) {
-    const uint32_t t0 = (off + kTilePos - 1) / kTilePos;
-    if (t0 * kTilePos < off + cnt) first[t0] = (uint32_t)tid;
+  const int sub = tid / kSubThreads, st = tid % kSubThreads;
+  const int lane = tid & 63, wv = st >> 6;
+  const int l = st % 8, slot = st / 8;
+  const int gbase = lane - l;
+  const int cbs = a.col_blocks;
+  const int t = w + sub * a.ndown;
+  const bool active = t < a.ranges * cbs;
+  const int r = active ? t / cbs : 0, cb = active ? t % cbs : 0;
+  const int c0 = r * a.chan_per_range, c1 = min(c0 + a.chan_per_range, a.n);
+  uint32_t* list = lds + sub * kRangeMax;
+  float* red = reinterpret_cast<float*>(lds + kSubTiles * kRangeMax);  // [sub][wave][256]
+
+  // 1. the range's candidates (key in [state[0], 0x7F80), as the gate
+  //    launch tested them); the key is read per lane at an offset that is
+  //    always 0, so that it is in flight with g instead of a scalar load
+  const uint32_t zero = (uint32_t)tid & ((uint32_t)hidden >> 30);
+  const uint32_t sk = a.sp.state[zero];
+  uint32_t gv[kPer], hv[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int c = min(c0 + st + kSubThreads * q, a.n - 1);
+    gv[q] = a.g[c];
+    hv[q] = a.sp.h_full[c];
   }
-  if (w == 0 && tid == 0) a.meta->ncand = nc;
+  bool f[kPer];
+  uint64_t m[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int c = c0 + st + kSubThreads * q;
+    const uint32_t key = gv[q] & 0x7FFFu;
+    f[q] = active && c < c1 && key >= sk && key < kKeyInf;
+    m[q] = __ballot(f[q]);
+    if (lane == 0) wcnt[sub][q][wv] = (uint32_t)__popcll(m[q]);
+  }
+  __syncthreads();
+  int total = 0, base[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int n0 = (int)wcnt[sub][q][0];
+    base[q] = total + (wv ? n0 : 0);
+    total += n0 + (int)wcnt[sub][q][1];
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q)
+    if (f[q])
+      list[base[q] + __popcll(m[q] & below)] =
+          (uint32_t)(c0 + st + kSubThreads * q) | (hv[q] << 16);
   __syncthreads();
   if (stamp) a.meta->spec_stamp[0][1] = wall_clock64();
-  const int cbs = a.col_blocks;
-  const int tiles = (int)((nc + kTilePos - 1) / kTilePos) * cbs;
-  const int jw = tiles > w ? (tiles - w + a.ndown - 1) / a.ndown : 0;
-  const int rounds = (jw + kSubTiles - 1) / kSubTiles;
-  const int sub = tid / kSubThreads, st = tid % kSubThreads;
-  const int l = st % 8, slot = st / 8;
-  const int gbase = (tid & 63) - l;
+
+  // 2. their down rows, 256 positions per pass
   const size_t row_bytes = (size_t)(hidden >> 1);
   const int ngroups = hidden >> 7;
   DownArgs da{};  // the fields load_down_scales / load_down_row read
@@ -846,87 +907,52 @@ DIP_DEV void split_down_role(const SelDownArgs& a, int w, uint32_t* lds, int sta
   da.qw_safe = a.dn_qw;
   da.sc_safe = a.dn_sc;
   da.rows_a = a.n;
-  for (int r = 0; r < rounds; ++r) {
-    const int t = w + (r * kSubTiles + sub) * a.ndown;
-    const bool active = t < tiles;
-    const int rt = active ? t / cbs : 0, cb = active ? t % cbs : 0;
-    // lane l: rows l and l + 8 of the slot
-    uint32_t rid[2], hb[2], sv[2][2];
-    int lo[2];
-    bool live[2];
-    // the gate workgroup holding each of my two positions p: the last b with
-    // pre[b] <= p, from the tile's first one (16 reads at once; a search past
-    // them when the lists are sparse)
-    const int b0 = active ? (int)first[rt] : 0;
+  float acc[kDownAcc];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t p = (uint32_t)(rt * kTilePos + slot + kSubSlots * (l + 8 * q));
-      live[q] = active && p < nc;
-      int b = b0;
-#pragma unroll
-      for (int j = 1; j < 16; ++j) b += pre[b0 + j] <= p ? 1 : 0;
-      if (live[q] && b == b0 + 15 && pre[b0 + 16] <= p) {
-        int hi = a.gate_wgs - 1;
-        while (b < hi) {
-          const int mid = (b + hi + 1) >> 1;
-          if (pre[mid] <= p) b = mid; else hi = mid - 1;
-        }
-      }
-      lo[q] = live[q] ? b * kCandCap + (int)(p - pre[b]) : 0;
-    }
-    // unconditional loads from clamped indices (loads under branches serialise)
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t ent = a.cand_list[lo[q]];
-      uint32_t ch = ent & 0xFFFFu;
-      ch = !live[q] ? kPadRow : (ch < (uint32_t)a.n ? ch : kBadRow);
-      rid[q] = ch;
-      const uint32_t hv = a.sp.h_full[ch < (uint32_t)a.n ? ch : 0u];
-      hb[q] = ch < (uint32_t)a.n ? hv : 0u;
-      load_down_scales<kGather, 2, SL>(da, ch, 2 * cb, ngroups, sv[q]);
-    }
+  for (int i = 0; i < kDownAcc; ++i) acc[i] = 0.f;
+  const int passes = (total + kTilePos - 1) / kTilePos;  // uniform within the sub-tile
+  for (int pass = 0; pass < passes; ++pass) {
+    // lane l: the id, h and scales of its slot's row l
+    const int p = pass * kTilePos + slot + kSubSlots * l;
+    const uint32_t ent = list[min(p, total - 1)];
+    const uint32_t rid = p < total ? (ent & 0xFFFFu) : kPadRow;
+    uint32_t sv[2];
+    load_down_scales<kGather, 2, SL>(da, rid, 2 * cb, ngroups, sv);
     DownRow ring[kSlotRows];
 #pragma unroll
     for (int i = 0; i < kSlotRows; ++i)
-      load_down_row<kGather>(da, __shfl(rid[i / 8], gbase + i % 8, 64), cb * 8 + l, row_bytes,
-                             ring[i]);
-    if (stamp && r == 0) a.meta->spec_stamp[0][2] = wall_clock64();
-    float f[2][2];
-    down_coef<2>(rid[0], hb[0], sv[0], f[0]);
-    down_coef<2>(rid[1], hb[1], sv[1], f[1]);
-    float acc[kDownAcc];
+      load_down_row<kGather>(da, __shfl(rid, gbase + i, 64), cb * 8 + l, row_bytes, ring[i]);
+    if (stamp && pass == 0) a.meta->spec_stamp[0][2] = wall_clock64();
+    float fc[2];
+    down_coef<2>(rid, ent >> 16, sv, fc);
+    down_accumulate<kSlotRows, 2>(ring, fc, l >= 4, gbase, acc);
+  }
+
+  // 3. the slots of each wave in registers, the sub-tile's two waves via LDS
 #pragma unroll
-    for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
-    down_accumulate<8, 2>(ring, f[0], l >= 4, gbase, acc);
-    down_accumulate<8, 2>(ring + 8, f[1], l >= 4, gbase, acc);
-    // the slots of each wave in registers, the sub-tile's two waves via LDS
+  for (int i = 0; i < kDownAcc; ++i) acc[i] += dpp_mov<0x128>(acc[i]);  // row_ror:8
+  float t16[16];
 #pragma unroll
-    for (int m = 0; m < kDownAcc; ++m) acc[m] += dpp_mov<0x128>(acc[m]);  // row_ror:8
-    float t16[16];
+  for (int i = 0; i < 16; ++i) {
+    permlane16_swap(acc[i], acc[i + 16]);
+    t16[i] = acc[i] + acc[i + 16];
+  }
+  float u8[8];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      permlane16_swap(acc[m], acc[m + 16]);
-      t16[m] = acc[m] + acc[m + 16];
-    }
-    float u8[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      permlane32_swap(t16[m], t16[m + 8]);
-      u8[m] = t16[m] + t16[m + 8];
-    }
-    const int lane = tid & 63, wv = st >> 6;  // wave within the sub-tile
-    float* rs = red + sub * (2 * 256);
-    if ((lane & 15) < 8) {
-      float* dst = rs + wv * 256 + 32 * (lane % 8) + 8 * (lane >> 5) + 16 * ((lane >> 4) & 1);
-      *reinterpret_cast<float4*>(dst) = make_float4(u8[0], u8[1], u8[2], u8[3]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(u8[4], u8[5], u8[6], u8[7]);
-    }
-    __syncthreads();
-    if (active) {
-      float* out = a.partial + (size_t)rt * hidden + (size_t)cb * 256;
-      for (int c = st; c < 256; c += kSubThreads) out[c] = rs[c] + rs[256 + c];
-    }
-    __syncthreads();  // the next round reuses the LDS
+  for (int i = 0; i < 8; ++i) {
+    permlane32_swap(t16[i], t16[i + 8]);
+    u8[i] = t16[i] + t16[i + 8];
+  }
+  float* rs = red + sub * (2 * 256);
+  if ((lane & 15) < 8) {
+    float* dst = rs + wv * 256 + 32 * (lane % 8) + 8 * (lane >> 5) + 16 * ((lane >> 4) & 1);
+    *reinterpret_cast<float4*>(dst) = make_float4(u8[0], u8[1], u8[2], u8[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(u8[4], u8[5], u8[6], u8[7]);
+  }
+  __syncthreads();
+  if (active) {
+    float* out = a.partial + (size_t)r * hidden + (size_t)cb * 256;
+    for (int c = st; c < 256; c += kSubThreads) out[c] = rs[c] + rs[256 + c];
   }
   if (stamp) a.meta->spec_stamp[0][3] = wall_clock64();
 }
@@ -938,7 +964,7 @@ __global__ __launch_bounds__(kThreads) void select_down_kernel(SelDownArgs a, in
     topk_body<R, kSelSplit, LPR, CH>(a.g, a.n, a.k, a.idx, a.meta, stamps, a.sp.ntopk, a.sp, lds,
                                      &a);
   else
-    split_down_role<SL>(a, (int)blockIdx.x - a.sp.ntopk, lds, stamps);
+    range_down_role<SL>(a, (int)blockIdx.x - a.sp.ntopk, lds, stamps);
 }
 
 
@@ -1176,20 +1202,40 @@ int launch_select_down_sl(const SelDownArgs& a, int blocks, hipStream_t stream) 
 }  // namespace
 
 bool split_step_supported(int64_t hidden, int64_t inter) {
-  // 8-chunk column blocks, an even number of scale groups per row (the down
-  // tiles' scale pairs) and a gate workgroup count that fits the lists
+  // 8-chunk column blocks and an even number of scale groups per row (the
+  // down tiles' scale pairs)
   return topk_spec_supported(hidden) && hidden % 256 == 0 && inter >= 1 && inter <= kTopkMaxN &&
          (hidden / kChunkCols) % 8 == 0;
 }
 
+bool split_layout(int64_t hidden, int64_t n, int64_t k, int* ranges, int* chan_per_range) {
+  if (!split_step_supported(hidden, n) || k < 1 || k > n) return false;
+  const int64_t ntopk = (n + kSlice - 1) / kSlice;
+  const int64_t ndown = std::max<int64_t>(device_cus() - ntopk, 1);
+  const int64_t cbs = hidden / (kChunkCols * 8);
+  // ranges of about kRangeTarget candidates in steady state (the k selected
+  // plus the margin above them), at most one round of the down tiles
+  const int64_t cand = std::min<int64_t>(n, k + n * (int64_t)tuning(DIP_TUNE_SPEC_MARGIN) / 1024);
+  const int64_t c = std::min<int64_t>(
+      kRangeMax, std::max<int64_t>(kSubThreads, kRangeTarget * n / std::max<int64_t>(cand, 1)));
+  const int64_t r = std::min((n + c - 1) / c, kSubTiles * ndown / cbs);
+  if (r < 1) return false;
+  const int64_t per = (n + r - 1) / r;  // the same ranges, evened out
+  if (per > kRangeMax) return false;
+  *ranges = (int)((n + per - 1) / per);
+  *chan_per_range = (int)per;
+  return true;
+}
+
 int launch_select_down(SelDownArgs a, hipStream_t stream) {
   if (a.n <= 0 || a.k <= 0 || a.k > a.n || a.n > kTopkMaxN) return DIP_ERR_SHAPE;
-  if (!split_step_supported(a.sp.hidden, a.n)) return DIP_ERR_UNSUPPORTED;
-  if (a.gate_wgs < 1 || a.gate_wgs > kMaxCandWgs) return DIP_ERR_UNSUPPORTED;
+  int ranges = 0, per = 0;
+  if (!split_layout(a.sp.hidden, a.n, a.k, &ranges, &per)) return DIP_ERR_UNSUPPORTED;
   const int ntopk = (a.n + kSlice - 1) / kSlice;
   a.sp.ntopk = ntopk;
   a.sp.margin = (int)(a.n * (int64_t)tuning(DIP_TUNE_SPEC_MARGIN) / 1024);
-  a.rt_max = (a.n + kTilePos - 1) / kTilePos;
+  a.ranges = ranges;
+  a.chan_per_range = per;
   a.col_blocks = a.sp.hidden / (kChunkCols * 8);
   a.ndown = std::max(device_cus() - ntopk, 1);
   const int blocks = ntopk + a.ndown;
