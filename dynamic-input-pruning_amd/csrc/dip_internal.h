@@ -253,9 +253,9 @@ bool step_supported(int64_t hidden, int64_t inter);
 size_t step_partial_bytes(int64_t hidden);
 int launch_step(const StepArgs& a, hipStream_t stream);
 int launch_finish(const FinishArgs& a, hipStream_t stream);
-// The grid (workgroups) launch_rowdot / launch_rowdot_norm use for a
-// contiguous GEMV of nrows rows of in_features columns.
-int rowdot_contig_blocks(int64_t nrows, int64_t in_features);
+// The grid (workgroups) launch_rowdot (norm false) / launch_rowdot_norm
+// (norm true) use for the SiLU gate of nrows rows of in_features columns.
+int rowdot_contig_blocks(int64_t nrows, int64_t in_features, bool norm);
 // y[o] = bf16(sum over rows rb < row_blocks of partial[rb][o]) in a fixed order.
 int launch_down_reduce(const float* partial, int row_blocks, int out_features, uint16_t* y,
                        hipStream_t stream);

@@ -154,7 +154,7 @@ extern "C" int dip_version(void) { return 100; }
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {2, 0, 8, 0};
+int g_tune[DIP_TUNE_COUNT] = {0, 0, 8, 0};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -176,7 +176,7 @@ int dip::device_cus() {
 extern "C" int dip_set_tuning(int knob, int value) {
   switch (knob) {
     case DIP_TUNE_ROWDOT_WGS_PER_CU:
-      if (value < 1 || value > 16) return DIP_ERR_ARG;
+      if (value < 0 || value > 16) return DIP_ERR_ARG;
       break;
     case DIP_TUNE_TOPK_STAMPS:
       if (value != 0 && value != 1) return DIP_ERR_ARG;
@@ -444,7 +444,7 @@ int run_fused_step(RowdotArgs a, bool norm, const uint16_t* x_step, const int8_t
                    int64_t hidden, int64_t inter, int64_t k, void* workspace, void* layer_state,
                    hipStream_t s) {
   const MlpWs w = mlp_ws(workspace, hidden, inter, k);
-  const int gate_wgs = rowdot_contig_blocks(inter, hidden);
+  const int gate_wgs = rowdot_contig_blocks(inter, hidden, norm);
   if (gate_wgs < 1 || gate_wgs > kMaxCandWgs) return DIP_ERR_UNSUPPORTED;
   a.rotate = nullptr;  // the finish launch writes the state
   a.spec = static_cast<const uint32_t*>(layer_state);

@@ -334,9 +334,9 @@ struct RowdotPlan {
 // keep the fewest of 1, 2, 4, 8 rows per group that hold the grid near
 // wgs_per_cu per CU (the 15360-row up gather: 480 x 8 x 4 rows, 9.9 us,
 // against 10.1 us for 512 x 8 x 3-4 rows).
-RowdotPlan plan_rowdot(int nrows, int lpr, bool balanced) {
+RowdotPlan plan_rowdot(int nrows, int lpr, bool balanced, int wgs_per_cu) {
   const int groups = 256 / lpr;
-  const long long wgs = (long long)device_cus() * tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
+  const long long wgs = (long long)device_cus() * wgs_per_cu;
   const long long need = (nrows + wgs * groups - 1) / (wgs * groups);
   if (need <= 1)  // one row per group: no more workgroups than the rows fill
     return RowdotPlan{1, groups, (int)std::max(1LL, std::min(wgs, (nrows + groups - 1LL) / groups))};
@@ -344,6 +344,54 @@ RowdotPlan plan_rowdot(int nrows, int lpr, bool balanced) {
   int rows = 1;
   while (rows < 8 && rows < lpr && (long long)rows * wgs * groups < nrows) rows *= 2;
   return RowdotPlan{rows, groups, (nrows + rows * groups - 1) / (rows * groups)};
+}
+
+// Workgroups of the SiLU gate instance for `rows` rows per group that fit a
+// CU at once (cached per instance).
+template <int LPR, int CH>
+int gate_occupancy(int rows) {
+  static int cache[9] = {};
+  if (rows < 1 || rows > 8) return 0;
+  if (!cache[rows]) {
+    const void* f = nullptr;
+    switch (rows) {
+#define DIP_ROWS(R) \
+      case R: f = reinterpret_cast<const void*>(&rowdot_kernel<LPR, CH, kContig, kSilu, true, R>); break;
+      DIP_ROWS(1) DIP_ROWS(2) DIP_ROWS(3) DIP_ROWS(4) DIP_ROWS(5) DIP_ROWS(6) DIP_ROWS(7)
+#undef DIP_ROWS
+      default: f = reinterpret_cast<const void*>(&rowdot_kernel<LPR, CH, kContig, kSilu, true, 8>); break;
+    }
+    const size_t lds = x_pairs_lds_bytes(LPR * CH * kChunkCols);
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kRowdotMaxThreads, lds) != hipSuccess)
+      nb = 0;
+    cache[rows] = nb + 1;
+  }
+  return cache[rows] - 1;
+}
+
+// Workgroups per CU of a row-dot grid: the tuning knob when set, else for
+// the SiLU gate three where the instance three workgroups per CU would pick
+// still fits three at once (the Qwen3-8B gate: 2 rows per group, 97 VGPRs;
+// 8.0 -> 7.4 us), else two (the Qwen3-32B gate would need 5 rows per group
+// at 231 VGPRs, two waves per SIMD: 13.5 -> 17.2 us); every other grid two.
+// The gate with the RMSNorm prologue keeps two: every workgroup normalises
+// x itself, and a third per CU cost more than it gained (the whole Qwen3-8B
+// model: 477 against 487 tok/s).
+int rowdot_wpc(int nrows, int chunks, bool gate, bool norm) {
+  const int t = tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
+  if (t > 0) return t;
+  if (!gate || norm) return 2;
+  int lpr = 0, occ = 0;
+  if (chunks == 160) lpr = 32;
+  else if (chunks == 128) lpr = 32;
+  else if (chunks == 80) lpr = 16;
+  else return 2;
+  const int rows = plan_rowdot(nrows, lpr, true, 3).rows;
+  if (chunks == 160) occ = gate_occupancy<32, 5>(rows);
+  else if (chunks == 128) occ = gate_occupancy<32, 4>(rows);
+  else occ = gate_occupancy<16, 5>(rows);
+  return occ >= 3 ? 3 : 2;
 }
 
 template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
@@ -362,7 +410,9 @@ int launch_one(const RowdotArgs& a, hipStream_t stream) {
   constexpr bool hot = (LPR == 32 && (CH == 5 || CH == 4)) || (LPR == 16 && CH == 5) ||
                        (LPR == 64 && CH == 4);
   if constexpr (hot) {
-    const RowdotPlan p = plan_rowdot(a.nrows, LPR, SRC == kContig);
+    const RowdotPlan p = plan_rowdot(a.nrows, LPR, SRC == kContig,
+                                     rowdot_wpc(a.nrows, LPR * CH, SRC == kContig && EPI == kSilu,
+                                                NORM));
     if constexpr (SRC == kContig) {  // balanced plan: any rows per group up to 8
       switch (p.rows) {
         case 1: launch_variant<LPR, CH, SRC, EPI, true, 1, NORM>(a, p, stream); break;
@@ -415,10 +465,10 @@ int dispatch_layout(const RowdotArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-int rowdot_contig_blocks(int64_t nrows, int64_t in_features) {
+int rowdot_contig_blocks(int64_t nrows, int64_t in_features, bool norm) {
   const int64_t chunks = in_features / kChunkCols;
   const int lpr = (chunks == 80 || chunks == 48 || chunks == 16) ? 16 : (chunks == 256 ? 64 : 32);
-  return plan_rowdot((int)nrows, lpr, true).blocks;
+  return plan_rowdot((int)nrows, lpr, true, rowdot_wpc((int)nrows, (int)chunks, true, norm)).blocks;
 }
 
 bool rowdot_norm_supported(int64_t in_features) {
@@ -457,6 +507,11 @@ int launch_spec_after_gate(const uint16_t* g, int64_t inter, int64_t hidden, int
 }
 
 namespace {
+// the split step's gate launch: the tuning knob when set, else two
+int gate_spec_wpc() {
+  const int t = tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
+  return t > 0 ? t : 2;
+}
 template <int LPR, int CH, int ROWS>
 void launch_gate_spec_rows(const GateSpecArgs& a, int blocks, hipStream_t stream) {
   hipLaunchKernelGGL((gate_spec_kernel<LPR, CH, ROWS>), dim3(blocks), dim3(kRowdotMaxThreads),
@@ -464,7 +519,7 @@ void launch_gate_spec_rows(const GateSpecArgs& a, int blocks, hipStream_t stream
 }
 template <int LPR, int CH>
 int launch_gate_spec_width(GateSpecArgs a, hipStream_t stream) {
-  const RowdotPlan p = plan_rowdot(a.nrows, LPR, true);
+  const RowdotPlan p = plan_rowdot(a.nrows, LPR, true, gate_spec_wpc());
   if (p.groups * LPR != kRowdotMaxThreads || p.rows < 1 || p.rows > 8) return DIP_ERR_UNSUPPORTED;
   a.ngrp = p.blocks * p.groups;
   switch (p.rows) {
@@ -487,7 +542,7 @@ int gate_spec_blocks(int64_t nrows, int64_t in_features) {
   const int64_t chunks = in_features / kChunkCols;
   const int lpr = chunks == 80 ? 16 : 32;
   if (!(chunks == 160 || chunks == 128 || chunks == 80) || nrows < 1) return 0;
-  const RowdotPlan p = plan_rowdot((int)nrows, lpr, true);
+  const RowdotPlan p = plan_rowdot((int)nrows, lpr, true, gate_spec_wpc());
   if (p.rows < 1 || p.rows > 8 || (long long)p.blocks > kMaxCandWgs) return 0;
   return p.blocks;
 }

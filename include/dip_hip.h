@@ -146,7 +146,9 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
 /*
  * Launch tuning, no counterpart in the reference (process-wide, host side;
  * speed only):
- *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grids aim at CUs * this workgroups (2)
+ *   DIP_TUNE_ROWDOT_WGS_PER_CU  gate/up grids aim at CUs * this workgroups
+ *                               (0, the default: 3 for a gate whose kernel
+ *                               then still fits 3 workgroups per CU, else 2)
  *   DIP_TUNE_TOPK_STAMPS        1: the top-k records wall-clock phase stamps
  *                               in its workspace (diagnostics, slower) (0)
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates

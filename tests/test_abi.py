@@ -99,7 +99,9 @@ def test_argument_rejection_before_launch():
     assert L.dip_set_tuning(2, 1025) == -6
     assert L.dip_set_tuning(2, -1) == -6
     assert L.dip_set_tuning(1, 7) == -6
-    assert L.dip_set_tuning(0, 0) == -6
+    assert L.dip_get_tuning(0) == 0  # row-dot grids: automatic by default
+    assert L.dip_set_tuning(0, 17) == -6
+    assert L.dip_set_tuning(0, -1) == -6
     assert L.dip_set_tuning(99, 1) == -6
     assert L.dip_get_tuning(99) == -6
     assert L.dip_dequant_rows(p, p, None, p, 10, 5, 128, 0, None) == -2
