@@ -204,6 +204,12 @@ def _topk_cases():
     tiny = np.full(64, 0x0090, np.uint16)
     tiny[::3] = 0x0100
     cases += [(big, 20), (tiny, 10), (tiny, 30)]
+    # magnitudes spread over every bf16 exponent (zero to +inf, either sign):
+    # the select's scan then gives each thread 32 bins and the rank walks
+    # across many of them
+    wide = (rng.integers(0, 0x7F81, size=25600) | (rng.integers(0, 2, size=25600) << 15))
+    wide = wide.astype(np.uint16)
+    cases += [(wide, 1), (wide, 700), (wide, 12800), (wide, 25000)]
     return cases
 
 
