@@ -185,6 +185,33 @@ def whole_model(args) -> int:
     return 0
 
 
+def profiler_env():
+    """Names of the environment variables rocprofv3 sets for its tool
+    library in the profiled process (ROCPROF_OUTPUT_PATH, ROCPROF_STATS, ...):
+    non-empty when this process runs under the profiler."""
+    return sorted(n for n in os.environ if n.startswith(("ROCPROF_", "ROCPROFILER_")))
+
+
+def release_cache_aware(*objs):
+    """Return everything the cache-aware run holds to the HIP runtime while
+    the runtime (and a profiler's tool library, when there is one) is still
+    up: the modules' pinned up/down_t (8.6 GB at the Qwen3-32B shape) and the
+    staging buffers go back to torch's pinned-host cache when their last
+    reference goes, and that cache only frees them with hipHostFree from a
+    static destructor at process exit unless it is emptied here."""
+    import gc
+    import torch
+    torch.cuda.synchronize()
+    for o in objs:
+        if isinstance(o, list):
+            o.clear()
+    del objs
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+    torch.cuda.synchronize()
+
+
 def cache_aware(args) -> int:
     """Cache-aware DIP decode (the reference's CADIPMlp, dip_ca.py:127-188)
     on the --shape stack: every layer keeps round(I * cache_frac) channels'
@@ -315,54 +342,108 @@ def cache_aware(args) -> int:
         "miss_stream_ms_per_token": round(stream_s * 1e3 / args.steps, 3),
     }
     print(json.dumps(out), flush=True)
+    release_cache_aware(cas, hits, tr)
+    del cas, buf, xs, counts, hits, tr
+    release_cache_aware()
     return 0
 
 
 def read_ceiling(args) -> int:
     """The read bandwidth this GPU gives the decode step's two access
-    patterns, measured with the library's probe kernels (no arithmetic):
-    a contiguous read of the gate matrix's bytes (67.584 MB) and of a whole
-    layer's (148.685 MB), the up/down gather (15360 sorted random rows of
-    2560 B out of 25600, keep 0.6, each row read whole by one 32-lane
-    group), and a device-to-device copy of each size.  Buffers rotate through 8 copies (6 matrices for the gather) so
-    the memory-side cache holds none of them.  One JSON line."""
+    patterns, swept over bytes in flight, with the probe kernels of
+    libdip_probe.so (csrc/probe/dip_probe.hip; loads only, no arithmetic):
+      * contiguous: the gate matrix's bytes (67.584 MB) read front to back,
+        grid-stride;
+      * gather: 15360 sorted random rows of 2560 B out of 25600 (the up/down
+        rows at keep 0.6), each row read whole by one 32-lane group;
+    for workgroups of 256 threads in {1, 2, 3, 4, 8} per CU and each
+    thread or group holding {1, 2, 4, 8} loads (rows) in flight.  Rotating:
+    every launch reads the next of 8 buffers (541 MB in all) or 12 gather
+    matrices (472 MB of rows touched), more than the 256 MB memory-side
+    cache holds; resident: every launch re-reads the same buffer, which the
+    memory-side cache then serves.  Each figure is HIP events around
+    `--steps` back-to-back launches (so it includes one launch boundary per
+    launch).  One JSON line."""
+    import ctypes
     import torch
-    import _dip_hip as K
+
+    lib = ctypes.CDLL(str(ROOT / "dynamic-input-pruning_amd" / "libdip_probe.so"))
+    _p, _i64, _i = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.dip_probe_read.argtypes = [_p, ctypes.c_size_t, _i, _i, _p, _p]
+    lib.dip_probe_gather.argtypes = [_p, _i64, _i64, _p, _i64, _i, _i, _p, _p]
+    lib.dip_probe_read.restype = lib.dip_probe_gather.restype = _i
 
     dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     reps = max(8, args.steps)
+    stream = torch.cuda.current_stream(dev)
+
+    def check(st, what):
+        if st != 0:
+            raise RuntimeError(f"{what} failed with status {st}")
 
     def timed(fn):
         fn(0)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
+        e0.record(stream)
         for r in range(reps):
             fn(r)
-        e1.record()
+        e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1000.0 / reps  # us per launch, back to back
 
-    out = {"metric": "HBM read ceiling (probe kernels)", "unit": "TB/s", "reps": reps}
-    for name, nbytes in (("read_67.6MB", 67584000), ("read_148.7MB", 148684800)):
-        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(8)]
-        us = timed(lambda r: K.read_probe(bufs[r % 8], sink))
-        out[name] = {"us": round(us, 2), "TB/s": round(nbytes / us / 1e6, 3)}
-        dst = torch.empty_like(bufs[0])
-        us = timed(lambda r: dst.copy_(bufs[r % 8]))
-        out["d2d_copy_" + name.split("_")[1]] = {"us": round(us, 2),
-                                                 "TB/s_read_plus_write": round(2 * nbytes / us / 1e6, 3)}
-        del bufs, dst
-        torch.cuda.empty_cache()
-    n, k, rb = 25600, 15360, 2560
+    wpcs, rings = (1, 2, 3, 4, 8), (1, 2, 4, 8)
+    out = {"metric": "HBM read ceiling (probe kernels, loads only)", "unit": "TB/s",
+           "reps": reps, "cus": cus, "threads_per_wg": 256}
+    nbytes = 67584000
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(8)]
+    sweep = {}
+    for wpc in wpcs:
+        for ring in rings:
+            us = timed(lambda r: check(lib.dip_probe_read(bufs[r % 8].data_ptr(), nbytes,
+                                                          wpc * cus, ring, sink.data_ptr(),
+                                                          stream.cuda_stream), "read"))
+            sweep[f"wpc{wpc}_ring{ring}"] = {"us": round(us, 2), "TB/s": round(nbytes / us / 1e6, 3)}
+            print(f"[ceiling] read 67.6MB rotating wpc={wpc} ring={ring}: {us:.2f} us",
+                  file=sys.stderr, flush=True)
+    best = min(sweep, key=lambda n: sweep[n]["us"])
+    wpc, ring = (int(v) for v in best.replace("wpc", "").split("_ring"))
+    us = timed(lambda r: check(lib.dip_probe_read(bufs[0].data_ptr(), nbytes, wpc * cus, ring,
+                                                  sink.data_ptr(), stream.cuda_stream), "read"))
+    out["read_67.6MB"] = {"rotating": sweep, "best_rotating": best,
+                          "resident_at_best": {"us": round(us, 2),
+                                               "TB/s": round(nbytes / us / 1e6, 3)}}
+    dst = torch.empty_like(bufs[0])
+    us = timed(lambda r: dst.copy_(bufs[r % 8]))
+    out["d2d_copy_67.6MB"] = {"us": round(us, 2), "TB/s_read_plus_write": round(2 * nbytes / us / 1e6, 3)}
+    del bufs, dst
+    torch.cuda.empty_cache()
+
+    n, k, rb, nmat = 25600, 15360, 2560, 12
     gen = torch.Generator(device="cpu").manual_seed(5)
     mats, idxs = [], []
-    for _ in range(6):
+    for _ in range(nmat):
         mats.append(torch.ones(n, rb, dtype=torch.uint8, device=dev))
         idxs.append(torch.sort(torch.randperm(n, generator=gen)[:k]).values.to(torch.int32).to(dev))
-    us = timed(lambda r: K.gather_probe(mats[r % 6], idxs[r % 6], sink))
-    out["gather_15360x2560B_of_25600"] = {"us": round(us, 2), "TB/s": round(k * rb / us / 1e6, 3)}
+    sweep = {}
+    for wpc in wpcs:
+        for ring in rings:
+            us = timed(lambda r: check(lib.dip_probe_gather(
+                mats[r % nmat].data_ptr(), n, rb, idxs[r % nmat].data_ptr(), k, wpc * cus, ring,
+                sink.data_ptr(), stream.cuda_stream), "gather"))
+            sweep[f"wpc{wpc}_ring{ring}"] = {"us": round(us, 2), "TB/s": round(k * rb / us / 1e6, 3)}
+            print(f"[ceiling] gather rotating wpc={wpc} ring={ring}: {us:.2f} us",
+                  file=sys.stderr, flush=True)
+    best = min(sweep, key=lambda n_: sweep[n_]["us"])
+    wpc, ring = (int(v) for v in best.replace("wpc", "").split("_ring"))
+    us = timed(lambda r: check(lib.dip_probe_gather(mats[0].data_ptr(), n, rb, idxs[0].data_ptr(),
+                                                    k, wpc * cus, ring, sink.data_ptr(),
+                                                    stream.cuda_stream), "gather"))
+    out["gather_15360x2560B_of_25600"] = {"rotating": sweep, "best_rotating": best,
+                                          "resident_at_best": {"us": round(us, 2),
+                                                               "TB/s": round(k * rb / us / 1e6, 3)}}
     print(json.dumps(out), flush=True)
     return 0
 
@@ -383,9 +464,6 @@ def main(argv=None):
     ap.add_argument("--no-spec", action="store_true",
                     help="run every layer stage by stage (no speculative up rows during the "
                          "top-k); same outputs, five launches per layer instead of four")
-    ap.add_argument("--step", type=int, choices=(0, 1, 2), default=None,
-                    help="decode step form with speculation state (DIP_TUNE_STEP): 0 four "
-                         "launches, 1 fused, 2 split; default: the library's")
     ap.add_argument("--no-gm", action="store_true",
                     help="the down stage reads down_t's [inter, hidden/128] scales instead of "
                          "their group-major copy")
@@ -406,8 +484,9 @@ def main(argv=None):
                          "anisotropic decode stream (fixed direction + noise) that the timed "
                          "tokens also follow")
     ap.add_argument("--ceiling", action="store_true",
-                    help="instead of the decode step, measure the read bandwidth of the "
-                         "step's access patterns with probe kernels; prints its own JSON line")
+                    help="instead of the decode step, sweep the read bandwidth of the step's "
+                         "access patterns with the probe kernels of libdip_probe.so; prints its "
+                         "own JSON line")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed run, copy a buffer of this many MiB device to device "
                          "(the reference transfer for scaling HBM byte counters)")
@@ -423,6 +502,13 @@ def main(argv=None):
     if args.whole_model:
         return whole_model(args)
     if args.ca is not None:
+        prof = profiler_env()
+        if prof:
+            # checked before any GPU call: a profiled cache-aware run has
+            # ended in a segmentation fault at exit (after its result)
+            print("bench.py --ca does not run under rocprofv3 (found " + ", ".join(prof[:3]) +
+                  "); its copy rates come from the bench's own HIP events", file=sys.stderr)
+            return 3
         return cache_aware(args)
 
     import torch
@@ -430,8 +516,6 @@ def main(argv=None):
     from dip_stack import SHAPES, DIPStack
 
     dev = torch.device("cuda:0")
-    if args.step is not None:
-        K.set_tuning("step", args.step)
     if args.checkpoint:
         print(f"[bench] loading MLPs of {args.checkpoint} keep={args.keep}", file=sys.stderr,
               flush=True)

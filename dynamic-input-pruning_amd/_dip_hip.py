@@ -68,8 +68,6 @@ _SIGS = {
                                          _p], _i32),
     "dip_scales_group_major": ([_p, _p, _i64, _i64, _p], _i32),
     "dip_quantize_int4": ([_p, _i32, _p, _p, _i64, _i64, _p], _i32),
-    "dip_read_probe": ([_p, _sz, _p, _p], _i32),
-    "dip_gather_probe": ([_p, _i64, _i64, _p, _i64, _p, _p], _i32),
     "dip_transpose_down_int4": ([_p, _p, _p, _p, _i64, _i64, _p], _i32),
     "dip_host_gather_rows": ([_p, _p, _p, _i64, _i64, _i64, _i32], _i32),
     "dip_host_gather_rows_multi": ([_p, _p, _p, _i64, _p, _i64, _i64, _i32], _i32),
@@ -95,6 +93,14 @@ for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)
     _fn.argtypes = _args
     _fn.restype = _res
+
+# The argument lists above follow this version of include/dip_hip.h
+# (DIP_VERSION); a library built from another one would be called with
+# shifted arguments, so it is refused here.
+ABI_VERSION = 300
+if lib.dip_version() != ABI_VERSION:
+    raise ImportError(f"{LIB_PATH} reports ABI version {lib.dip_version()}, these bindings "
+                      f"are written for {ABI_VERSION}; rebuild the library")
 
 GROUP_SIZE = 128
 
@@ -395,20 +401,6 @@ def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out
                                                out_f, k, _ptr(ws), ws.numel(), _stream(dev)),
            "dip_int4_gather_down_by_channel")
     return out
-
-
-def read_probe(buf: torch.Tensor, sink: torch.Tensor) -> None:
-    """Measurement: read all of buf (device, 16-byte multiple) once."""
-    _check(lib.dip_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
-                              _stream(buf.device)), "dip_read_probe")
-
-
-def gather_probe(mat: torch.Tensor, idx: torch.Tensor, sink: torch.Tensor) -> None:
-    """Measurement: read the rows idx of the 2-D byte matrix mat."""
-    idx = _indices(idx)
-    _check(lib.dip_gather_probe(_ptr(mat), mat.shape[0], mat.shape[1] * mat.element_size(),
-                                _ptr(idx), idx.numel(), _ptr(sink), _stream(mat.device)),
-           "dip_gather_probe")
 
 
 def ca_fused_gemv(res_qw, res_sc, str_qw, str_sc, x, src, row, g=None, gid=None, out=None):
@@ -804,7 +796,7 @@ def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res
     return y, g, idx, h, x_out
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "step": 3}
+TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2}
 
 
 def set_tuning(name: str, value: int) -> None:

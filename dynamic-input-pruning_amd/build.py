@@ -5,6 +5,8 @@
 Each csrc/*.hip file is compiled to an object under _build/ (in parallel),
 then linked into libdip_hip.so next to this file.  The library is what the
 Python modules in this directory load; it is rebuilt every time this runs.
+csrc/probe/*.hip (the bench's read-ceiling probes, no part of the decode
+path) is linked into a library of its own, libdip_probe.so.
 """
 from __future__ import annotations
 
@@ -18,6 +20,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libdip_hip.so"
+PROBE_LIB = HERE / "libdip_probe.so"
 ARCH = os.environ.get("DIP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -43,30 +46,38 @@ def _run(cmd):
     return err
 
 
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
+          "-lpthread"])
+    os.replace(tmp, lib)
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip and link libdip_hip.so; returns its path."""
+    """Compile every csrc/*.hip and link libdip_hip.so (and csrc/probe/*.hip
+    into libdip_probe.so); returns the decode library's path."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
+    probes = sorted((CSRC / "probe").glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
 
     def compile_one(src: Path) -> Path:
-        obj = BUILD / (src.stem + ".o")
+        obj = BUILD / (src.parent.name + "_" + src.stem + ".o")
         cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
         msg = _run(cmd)
         if verbose and msg:
             print(msg, file=sys.stderr)
         return obj
 
-    jobs = min(len(sources), max(1, min(16, os.cpu_count() or 1)))
+    jobs = min(len(sources) + len(probes), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(compile_one, sources))
-    tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
-          "-lpthread"])
-    os.replace(tmp, LIB)
+        objs = list(pool.map(compile_one, sources + probes))
+    _link(objs[:len(sources)], LIB)
+    if probes:
+        _link(objs[len(sources):], PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB}" + (f" and {PROBE_LIB}" if probes else ""))
     return LIB
 
 

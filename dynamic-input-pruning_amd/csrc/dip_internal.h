@@ -50,28 +50,7 @@ struct RowdotArgs {
   uint16_t* norm_h_out;
   uint16_t* norm_x_out;  // workgroup 0 also writes the normalised x here (if set)
   float norm_eps;
-  // decode gate (kContig + kSilu) of the fused step, with spec = the layer
-  // state ([1] speculation key, [2] key band lo | hi << 16): each workgroup b
-  // writes
-  //   * its rows whose magnitude key is at or above spec[1] (NaN never) to
-  //     cand_list[b * kCandCap ...] (channel | g bits << 16, in lane order),
-  //     their number to cand_count[b] and its largest flushed key
-  //     (0xFFFFFFFF if none is valid) to cand_max[b];
-  //   * its rows whose key lies in the band [lo, hi) to band_list[b *
-  //     kBandSlot ...] (the first kBandSlot of them, same format), their
-  //     number to band_count[b] and the number of rows whose key is at or
-  //     above hi to above_count[b] (both 0 when the band is empty).
-  uint32_t* cand_list;
-  uint32_t* cand_count;
-  uint32_t* cand_max;
-  const uint32_t* spec;
-  uint32_t* band_list;
-  uint32_t* band_count;
-  uint32_t* above_count;
 };
-constexpr int kCandCap = 128;     // >= rows per gate workgroup (256/LPR groups x at most 8 rows)
-constexpr int kMaxCandWgs = 1024; // gate workgroups with candidate lists (the fused step ranks them)
-constexpr int kBandSlot = 16;     // band entries kept per gate workgroup
 
 struct DownArgs {
   const int8_t* qw_a;
@@ -111,13 +90,8 @@ struct TopkMeta {
   uint64_t stamp[6];   // wall_clock64() at the select kernel's phase boundaries (diagnostics)
   uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
   // wall_clock64() in two speculation workgroups (the first and the middle
-  // one): start, list built, x staged, done; the fused step kernel puts
-  // workgroup 0's cut sub-phases in spec_stamp[0] (diagnostics)
+  // one): start, list built, x staged, done (diagnostics)
   uint64_t spec_stamp[2][4];
-  // the fused step: the next call's speculation key and key band (workgroup 0
-  // of the step writes them, the finish copies them to the layer state)
-  uint32_t next_key;
-  uint32_t next_band;
 };
 
 // The top-k workspace holds the last call's TopkMeta.
@@ -141,118 +115,10 @@ struct SpecArgs {
   int ntopk;          // set by the launcher
 };
 
-// The split decode step (three launches):
-//   1. gate_spec: g = bf16(silu(bf16(gate . x))) for every channel, then, in
-//      the same workgroup, h_full[c] = bf16(g[c] * bf16(up[c] . x)) for its
-//      candidate channels c (magnitude key in [state[1], 0x7F80): the
-//      speculation key, NaN and infinities excluded); with cand_list set,
-//      each gate workgroup b also lists its candidates in cand_list[b *
-//      kCandCap ...] (channel | g bits << 16) and counts them in
-//      cand_count[b]; workgroup 0 copies state[1] to state[0];
-//   2. select_down: the top-k select workgroups (idx, h_out, the next key in
-//      state[1], h of the selected channels that are not candidates, and one
-//      fix-up partial row each: + those channels' down rows, - the down rows
-//      of candidates that were not selected, + channel 0 once per unfilled
-//      slot) beside down workgroups that sum h_full[c] * down_t[c] over the
-//      candidates of a range of channels per tile (the same key test on g);
-//   3. the reduce over the ranges' partial rows and the fix-up rows.
-struct GateSpecArgs {
-  const int8_t* qw;      // gate
-  const uint16_t* sc;
-  const int8_t* up_qw;
-  const uint16_t* up_sc;
-  const uint16_t* x;
-  uint16_t* g;
-  uint16_t* h_full;
-  uint32_t* state;       // [1] the key of this call; workgroup 0 copies it to [0]
-  uint32_t* cand_count;  // optional [gate workgroups]
-  uint32_t* cand_list;   // optional [gate workgroups][kCandCap]
-  int nrows;
-  int in_features;
-  int ngrp;              // set by the launcher
-};
-int launch_gate_spec(GateSpecArgs a, hipStream_t stream);
-int gate_spec_blocks(int64_t nrows, int64_t in_features);
-bool split_step_supported(int64_t hidden, int64_t inter);
-struct SelDownArgs {
-  // select role
-  const uint16_t* g;
-  int n;
-  int k;
-  int32_t* idx;
-  uint16_t* h_out;
-  TopkMeta* meta;
-  SpecArgs sp;           // up rows of the residual channels; sp.state: [0] key in use, [1] next
-  // down role
-  const int8_t* dn_qw;
-  const uint16_t* dn_sc;     // [n][hidden/128]
-  const uint16_t* dn_sc_gm;  // optional [hidden/128][n]
-  float* partial;        // [ranges + ntopk][hidden]: the ranges' rows, then the fix-up rows
-  int ranges;            // channel ranges (split_layout)
-  int chan_per_range;    // channels per range (split_layout)
-  int col_blocks;        // set by the launcher
-  int ndown;             // down workgroups (set by the launcher)
-};
-int launch_select_down(SelDownArgs a, hipStream_t stream);
-// The split step's channel ranges for (hidden, n, k): false if they do not
-// fit one round of the down workgroups' tiles.
-bool split_layout(int64_t hidden, int64_t n, int64_t k, int* ranges, int* chan_per_range);
-constexpr int kSelectSlice = 2048;  // values placed per top-k select workgroup
-
-// The decode step after the gate in one launch (dip_step.hip): the top-k
-// cut, up rows, h and per-workgroup down partials; then the finish launch
-// (dip_topk.hip): y from the partials, idx and h_out.
-constexpr int kStepMaxWorkgroups = 256;
-// Layer state of the fused step: [0] and [1] the speculation key (the
-// four-launch path reads [0] as the key in use and [1] as the next), [2] the
-// key band lo | hi << 16 the gate lists (0: none), [3] unused.  The finish
-// launch writes all of them.
-constexpr int kStepStateWords = 4;
-struct StepArgs {
-  const uint16_t* g;
-  int n;
-  int k;
-  const uint16_t* x;
-  int hidden;
-  const int8_t* up_qw;
-  const uint16_t* up_sc;
-  const int8_t* dn_qw;
-  const uint16_t* dn_sc;
-  uint16_t* h_full;          // [n] h by channel
-  float* partial;            // [grid][hidden]
-  const uint32_t* state;     // kStepStateWords (read only: the finish writes it)
-  TopkMeta* meta;
-  const uint32_t* cand_list; // the gate's lists (RowdotArgs::cand_*, band_*)
-  const uint32_t* cand_count;
-  const uint32_t* cand_max;
-  const uint32_t* band_list;
-  const uint32_t* band_count;
-  const uint32_t* above_count;
-  int gate_wgs;              // gate workgroups (entries of cand_count)
-  int margin;                // set by the launcher
-  int stamps;                // set by the launcher
-};
-struct FinishArgs {
-  const float* partial;
-  int rows;                  // partial rows (the step's grid)
-  int hidden;
-  uint16_t* y;
-  const uint16_t* g;
-  int n;
-  int k;
-  const TopkMeta* meta;
-  const uint16_t* h_full;
-  int32_t* idx;
-  uint16_t* h_out;
-  uint32_t* state;           // if set: gets the next call's key and band from meta
-  int ny;                    // set by the launcher
-};
-int step_grid();
-int step_max_gate_wgs();
-bool step_supported(int64_t hidden, int64_t inter);
-size_t step_partial_bytes(int64_t hidden);
-int launch_step(const StepArgs& a, hipStream_t stream);
-int launch_finish(const FinishArgs& a, hipStream_t stream);
+// Per-layer state of the decode step with speculative up rows: [0] the
+// speculation key in use, [1] the next call's key (the gate launch moves [1]
+// to [0]); [2] and [3] are spare.  Zero before the first call.
+constexpr int kMlpStateWords = 4;
 // The grid (workgroups) launch_rowdot (norm false) / launch_rowdot_norm
 // (norm true) use for the SiLU gate of nrows rows of in_features columns.
 int rowdot_contig_blocks(int64_t nrows, int64_t in_features, bool norm);

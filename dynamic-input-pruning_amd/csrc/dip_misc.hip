@@ -148,13 +148,13 @@ extern "C" const char* dip_status_string(int status) {
   return "unknown status";
 }
 
-extern "C" int dip_version(void) { return 100; }
+extern "C" int dip_version(void) { return DIP_VERSION; }
 
 // ---------------------------------------------------------------------------
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {0, 0, 8, 0};
+int g_tune[DIP_TUNE_COUNT] = {0, 0, 8};
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -183,9 +183,6 @@ extern "C" int dip_set_tuning(int knob, int value) {
       break;
     case DIP_TUNE_SPEC_MARGIN:
       if (value < 0 || value > 1024) return DIP_ERR_ARG;
-      break;
-    case DIP_TUNE_STEP:
-      if (value < 0 || value > 2) return DIP_ERR_ARG;
       break;
     default:
       return DIP_ERR_ARG;
@@ -378,127 +375,11 @@ namespace {
 constexpr size_t kMlpTopkBytes = 512;
 static_assert(kTopkWorkspace <= kMlpTopkBytes, "top-k state");
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-// Arguments of the fused decode step (the checks dip_gate_silu_topk_spec
-// and the down entry points make on the four-launch path).
-int check_step_args(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
-                    const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                    const uint16_t* x, const int32_t* idx, const uint16_t* h, const void* state,
-                    const void* ws, int64_t hidden, int64_t inter) {
-  if (!gate_qw || !gate_sc || !up_qw || !up_sc || !down_t_qw || !down_t_sc || !x || !idx || !h)
-    return DIP_ERR_NULL;
-  if (inter > INT32_MAX || hidden % kGroupSize != 0) return DIP_ERR_SHAPE;
-  if (!aligned16(gate_qw) || !aligned16(up_qw) || !aligned16(down_t_qw) || !aligned16(x) ||
-      !aligned16(ws) || (reinterpret_cast<uintptr_t>(state) & 3u))
-    return DIP_ERR_ALIGN;
-  return DIP_OK;
-}
-
-// The partial-sum region serves the four-launch path (one fp32 row per block
-// of 256 selected positions) and the fused step (one row per workgroup).
-size_t mlp_partial_bytes(int64_t hidden, int64_t k) {
-  return align256(std::max(down_workspace_bytes(k, hidden), step_partial_bytes(hidden)));
-}
-// The gate's lists for the fused step: candidate counts, max keys, band and
-// above counts, candidate lists, band lists.
-constexpr size_t kCandBytes = (size_t)kMaxCandWgs * (4 + kCandCap + kBandSlot) * sizeof(uint32_t);
-
-// Workspace of one resident decode step:
-//   [0, 512) top-k state | h by channel [inter] bf16 | partial rows | the
-//   gate's candidate lists
-struct MlpWs {
-  TopkMeta* meta;
-  uint16_t* h_full;
-  char* partial;
-  size_t partial_bytes;
-  uint32_t* cand_count;
-  uint32_t* cand_max;
-  uint32_t* band_count;
-  uint32_t* above_count;
-  uint32_t* cand_list;
-  uint32_t* band_list;
-};
-MlpWs mlp_ws(void* workspace, int64_t hidden, int64_t inter, int64_t k) {
-  char* ws = static_cast<char*>(workspace);
-  const size_t hfull = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
-  MlpWs w;
-  w.meta = reinterpret_cast<TopkMeta*>(ws);
-  w.h_full = reinterpret_cast<uint16_t*>(ws + kMlpTopkBytes);
-  w.partial = ws + kMlpTopkBytes + hfull;
-  w.partial_bytes = mlp_partial_bytes(hidden, k);
-  char* cand = w.partial + w.partial_bytes;
-  w.cand_count = reinterpret_cast<uint32_t*>(cand);
-  w.cand_max = w.cand_count + kMaxCandWgs;
-  w.band_count = w.cand_max + kMaxCandWgs;
-  w.above_count = w.band_count + kMaxCandWgs;
-  w.cand_list = w.above_count + kMaxCandWgs;
-  w.band_list = w.cand_list + (size_t)kMaxCandWgs * kCandCap;
-  return w;
-}
-
-// The fused decode step after its gate's setup in `a` (x, norm prologue):
-// the gate with the candidate lists, the step, the finish.
-int run_fused_step(RowdotArgs a, bool norm, const uint16_t* x_step, const int8_t* up_qw,
-                   const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                   uint16_t* y, uint16_t* g_out, int32_t* idx_out, uint16_t* h_out,
-                   int64_t hidden, int64_t inter, int64_t k, void* workspace, void* layer_state,
-                   hipStream_t s) {
-  const MlpWs w = mlp_ws(workspace, hidden, inter, k);
-  const int gate_wgs = rowdot_contig_blocks(inter, hidden, norm);
-  if (gate_wgs < 1 || gate_wgs > kMaxCandWgs) return DIP_ERR_UNSUPPORTED;
-  a.rotate = nullptr;  // the finish launch writes the state
-  a.spec = static_cast<const uint32_t*>(layer_state);
-  a.cand_count = w.cand_count;
-  a.cand_max = w.cand_max;
-  a.cand_list = w.cand_list;
-  a.band_count = w.band_count;
-  a.above_count = w.above_count;
-  a.band_list = w.band_list;
-  int st = norm ? launch_rowdot_norm(kSilu, a, s) : launch_rowdot(kContig, kSilu, a, s);
-  if (st) return st;
-  StepArgs sa{};
-  sa.g = g_out;
-  sa.n = (int)inter;
-  sa.k = (int)k;
-  sa.x = x_step;
-  sa.hidden = (int)hidden;
-  sa.up_qw = up_qw;
-  sa.up_sc = up_sc;
-  sa.dn_qw = down_t_qw;
-  sa.dn_sc = down_t_sc;
-  sa.h_full = w.h_full;
-  sa.partial = reinterpret_cast<float*>(w.partial);
-  sa.state = static_cast<const uint32_t*>(layer_state);
-  sa.meta = w.meta;
-  sa.cand_list = w.cand_list;
-  sa.cand_count = w.cand_count;
-  sa.cand_max = w.cand_max;
-  sa.band_list = w.band_list;
-  sa.band_count = w.band_count;
-  sa.above_count = w.above_count;
-  sa.gate_wgs = gate_wgs;
-  st = launch_step(sa, s);
-  if (st) return st;
-  FinishArgs fa{};
-  fa.partial = reinterpret_cast<const float*>(w.partial);
-  fa.rows = step_grid();
-  fa.hidden = (int)hidden;
-  fa.y = y;
-  fa.g = g_out;
-  fa.n = (int)inter;
-  fa.k = (int)k;
-  fa.meta = w.meta;
-  fa.h_full = w.h_full;
-  fa.idx = idx_out;
-  fa.h_out = h_out;
-  fa.state = static_cast<uint32_t*>(layer_state);
-  return launch_finish(fa, s);
-}
 }  // namespace
 
 extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k) {
   const size_t hfull = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
-  return kMlpTopkBytes + hfull + mlp_partial_bytes(hidden, k) + kCandBytes;
+  return kMlpTopkBytes + hfull + align256(down_workspace_bytes(k, hidden));
 }
 
 extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gate_sc,
@@ -549,13 +430,6 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
   const bool spec = layer_state && k > 0 && topk_spec_supported(hidden) && inter <= kTopkMaxN;
   if (spec) {
     if (reinterpret_cast<uintptr_t>(layer_state) & 3u) return DIP_ERR_ALIGN;
-    if (tuning(DIP_TUNE_STEP) == 1 && step_supported(hidden, inter)) {
-      const int cst = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x_out,
-                                      idx_out, h_out, layer_state, ws, hidden, inter);
-      if (cst) return cst;
-      return run_fused_step(a, true, x_out, up_qw, up_sc, down_t_qw, down_t_sc, y, g_out,
-                            idx_out, h_out, hidden, inter, k, workspace, layer_state, s);
-    }
     a.rotate = static_cast<uint32_t*>(layer_state);
     int st = launch_rowdot_norm(kSilu, a, s);
     if (st) return st;
@@ -580,70 +454,6 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
                   down_t_sc_gm);
 }
 
-namespace {
-// The split decode step (dip_internal.h): the gate launch with the
-// candidates' up rows, the select + candidate-down launch, the reduce.
-// The split step runs where its channel ranges fit one round of down tiles
-// and their partial rows fit the workspace; elsewhere the four-launch step
-// runs.
-bool split_step_fits(int64_t hidden, int64_t inter, int64_t k) {
-  int ranges = 0, per = 0;
-  if (gate_spec_blocks(inter, hidden) < 1 || !split_layout(hidden, inter, k, &ranges, &per))
-    return false;
-  const int64_t rows = ranges + (inter + kSelectSlice - 1) / kSelectSlice;
-  return (size_t)rows * (size_t)hidden * sizeof(float) <= mlp_partial_bytes(hidden, k);
-}
-
-int run_split_step(const int8_t* gate_qw, const uint16_t* gate_sc, const int8_t* up_qw,
-                   const uint16_t* up_sc, const int8_t* down_t_qw, const uint16_t* down_t_sc,
-                   const uint16_t* down_t_sc_gm, const uint16_t* x, uint16_t* y,
-                   uint16_t* g_out, int32_t* idx_out, uint16_t* h_out, int64_t hidden,
-                   int64_t inter, int64_t k, void* workspace, void* layer_state,
-                   hipStream_t s) {
-  if (gate_spec_blocks(inter, hidden) < 1) return DIP_ERR_UNSUPPORTED;
-  const MlpWs w = mlp_ws(workspace, hidden, inter, k);
-  int ranges = 0, per = 0;
-  if (!split_layout(hidden, inter, k, &ranges, &per)) return DIP_ERR_UNSUPPORTED;
-  const int nlists = (int)((inter + kSelectSlice - 1) / kSelectSlice);  // fix-up rows: one per select workgroup
-  if ((size_t)(ranges + nlists) * (size_t)hidden * sizeof(float) > w.partial_bytes)
-    return DIP_ERR_WORKSPACE;
-  GateSpecArgs ga{};
-  ga.qw = gate_qw;
-  ga.sc = gate_sc;
-  ga.up_qw = up_qw;
-  ga.up_sc = up_sc;
-  ga.x = x;
-  ga.g = g_out;
-  ga.h_full = w.h_full;
-  ga.state = static_cast<uint32_t*>(layer_state);
-  ga.nrows = (int)inter;
-  ga.in_features = (int)hidden;
-  int st = launch_gate_spec(ga, s);
-  if (st) return st;
-  SelDownArgs sd{};
-  sd.g = g_out;
-  sd.n = (int)inter;
-  sd.k = (int)k;
-  sd.idx = idx_out;
-  sd.h_out = h_out;
-  sd.meta = w.meta;
-  sd.sp.up_qw = up_qw;
-  sd.sp.up_sc = up_sc;
-  sd.sp.x = x;
-  sd.sp.h_full = w.h_full;
-  sd.sp.state = static_cast<uint32_t*>(layer_state);
-  sd.sp.hidden = (int)hidden;
-  sd.dn_qw = down_t_qw;
-  sd.dn_sc = down_t_sc;
-  sd.dn_sc_gm = down_t_sc_gm;
-  sd.partial = reinterpret_cast<float*>(w.partial);
-  st = launch_select_down(sd, s);
-  if (st) return st;
-  return launch_down_reduce(reinterpret_cast<const float*>(w.partial), ranges + nlists,
-                            (int)hidden, y, s);
-}
-}  // namespace
-
 extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
                               const int8_t* up_qw, const uint16_t* up_sc,
                               const int8_t* down_t_qw, const uint16_t* down_t_sc,
@@ -659,33 +469,6 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
   const size_t hfull_bytes = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
   char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
   const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
-  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) == 2 && split_step_fits(hidden, inter, k)) {
-    int st = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, idx_out,
-                             h_out, layer_state, ws, hidden, inter);
-    if (st) return st;
-    if (!aligned16(g_out)) return DIP_ERR_ALIGN;
-    return run_split_step(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, down_t_sc_gm, x,
-                          y, g_out, idx_out, h_out, hidden, inter, k, workspace, layer_state,
-                          (hipStream_t)stream);
-  }
-  if (layer_state && k > 0 && tuning(DIP_TUNE_STEP) == 1 && step_supported(hidden, inter)) {
-    // gate (+ SiLU, candidate and band lists), the fused step, the finish
-    int st = check_step_args(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, x, idx_out,
-                             h_out, layer_state, ws, hidden, inter);
-    if (st) return st;
-    RowdotArgs a{};
-    a.qw_a = gate_qw;
-    a.sc_a = gate_sc;
-    a.qw_safe = gate_qw;
-    a.sc_safe = gate_sc;
-    a.x = x;
-    a.out = g_out;
-    a.nrows = (int)inter;
-    a.in_features = (int)hidden;
-    a.rows_a = (int)inter;
-    return run_fused_step(a, false, x, up_qw, up_sc, down_t_qw, down_t_sc, y, g_out, idx_out,
-                          h_out, hidden, inter, k, workspace, layer_state, (hipStream_t)stream);
-  }
   if (layer_state && k > 0 && topk_spec_supported(hidden) && inter <= kTopkMaxN) {
     uint16_t* h_full = reinterpret_cast<uint16_t*>(ws + kMlpTopkBytes);
     int st = dip_gate_silu_topk_spec(gate_qw, gate_sc, up_qw, up_sc, x, g_out, idx_out, h_full,

@@ -81,21 +81,13 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   for (int d = 0; d < D; ++d)
     load_row<LPR, CH, SRC>(a, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups, ring[d]);
 
-  // 3b. The layer state of a decode step: the fused step's speculation key
-  // and key band (its finish launch rewrites them, never this launch), and
-  // workgroup 0's rotation of the four-launch step's next key into the slot
-  // in use (stored at the end).  Loaded after x and the first rows, so that
-  // waiting for those never waits for these; read at a lane-dependent offset
-  // that is always 0 (in_features < 2^30), since as a uniform value the
-  // compiler would move it to a scalar register right after the load and
-  // wait for it there.
+  // 3b. Workgroup 0's rotation of the decode step's next speculation key
+  // into the slot in use (stored at the end).  Loaded after x and the first
+  // rows, so that waiting for those never waits for it; read at a
+  // lane-dependent offset that is always 0 (in_features < 2^30), since as a
+  // uniform value the compiler would move it to a scalar register right after
+  // the load and wait for it there.
   const uint32_t zero = threadIdx.x & ((uint32_t)a.in_features >> 30);
-  [[maybe_unused]] uint32_t cand_key = 0, band = 0;
-  if constexpr (SRC == kContig && EPI == kSilu)
-    if (a.cand_count) {
-      cand_key = a.spec[1 + zero];
-      band = a.spec[2 + zero];
-    }
   const bool rot = a.rotate && blockIdx.x == 0 && threadIdx.x == 0;
   const uint32_t rot1 = rot ? a.rotate[1 + zero] : 0u;
 
@@ -148,168 +140,7 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
     }
     a.out[(int)jl] = (uint16_t)v;
   }
-  if constexpr (SRC == kContig && EPI == kSilu) {
-    if (a.cand_count) {  // uniform: the decode gate of the fused step
-      // per wave: candidate / band / above counts and the largest key (one
-      // 16-byte LDS record, all read under one wait); then each list gets
-      // its entries in lane order, waves in order
-      __shared__ uint4 wrec[kRowdotMaxThreads / 64];
-      const int wave = threadIdx.x >> 6;
-      const uint32_t kk = v & 0x7FFFu;
-      const bool ok = valid_l && kk <= 0x7F80u;
-      const uint32_t blo = band & 0xFFFFu, bhi = band >> 16;
-      const bool cand = ok && kk >= cand_key;
-      const bool inb = ok && kk >= blo && kk < bhi;
-      const bool abv = ok && bhi != 0u && kk >= bhi;
-      const uint64_t m = __ballot(cand), mb = __ballot(inb), ma = __ballot(abv);
-      float mk = ok ? bf16_to_f32(kk < 0x80u ? 0u : kk) : -1.f;
-      mk = group_max<64>(mk);
-      if (lane == 0)
-        wrec[wave] = make_uint4((uint32_t)__popcll(m), (uint32_t)__popcll(mb),
-                                (uint32_t)__popcll(ma), __float_as_uint(mk));
-      __syncthreads();
-      uint32_t base = 0, total = 0, bbase = 0, btotal = 0, atotal = 0;
-      float bm = -1.f;
-      const int nwv = (int)(blockDim.x >> 6);
-#pragma unroll
-      for (int w = 0; w < kRowdotMaxThreads / 64; ++w) {
-        const uint4 r = wrec[w];  // records past the block's waves are not used
-        const bool in = w < nwv;
-        base += in && w < wave ? r.x : 0u;
-        bbase += in && w < wave ? r.y : 0u;
-        total += in ? r.x : 0u;
-        btotal += in ? r.y : 0u;
-        atotal += in ? r.z : 0u;
-        bm = in ? fmaxf(bm, __uint_as_float(r.w)) : bm;
-      }
-      const uint64_t below = (1ull << lane) - 1ull;
-      const uint32_t entry = (uint32_t)jl | (v << 16);
-      if (cand) a.cand_list[(size_t)blockIdx.x * kCandCap + base + (uint32_t)__popcll(m & below)] = entry;
-      const uint32_t bpos = bbase + (uint32_t)__popcll(mb & below);
-      if (inb && bpos < (uint32_t)kBandSlot) a.band_list[(size_t)blockIdx.x * kBandSlot + bpos] = entry;
-      if (threadIdx.x == 0) {
-        a.cand_count[blockIdx.x] = total;
-        a.cand_max[blockIdx.x] = bm < 0.f ? 0xFFFFFFFFu : (__float_as_uint(bm) >> 16);
-        a.band_count[blockIdx.x] = btotal;
-        a.above_count[blockIdx.x] = atotal;
-      }
-    }
-  }
   if (rot) a.rotate[0] = rot1;
-}
-
-// ---------------------------------------------------------------------------
-// Gate + the workgroup's candidate up rows (the split decode step's first
-// launch, dip_internal.h).  The gate half is rowdot_kernel<LPR, CH, kContig,
-// kSilu, true, ROWS> (the same loads, arithmetic and order, so g is bit for
-// bit the plain gate's).  Then the workgroup's candidates, the rows it just
-// computed whose key |g bits| lies in [key, 0x7F80), are listed in LDS (and
-// in cand_list when given), and its groups take them in turn (entry e goes to group e
-// mod groups, one row of loads in flight): u = up[c] . x with the x pairs
-// still in VGPRs (row_dot_part, as dip_up_gather_h computes it), h_full[c] =
-// bf16(g[c] * bf16(u)).  The up rows follow the gate rows in the same
-// workgroup, so the up stream needs no launch, list or x staging of its own.
-// ---------------------------------------------------------------------------
-template <int LPR, int CH, int ROWS>
-__global__ __launch_bounds__(kRowdotMaxThreads) void gate_spec_kernel(GateSpecArgs a) {
-  constexpr int D = ROWS < 2 ? ROWS : 2;  // gate rows of loads in flight per group
-  constexpr int kGroups = kRowdotMaxThreads / LPR;
-  static_assert(kGroups * ROWS <= kCandCap, "candidate list");
-  extern __shared__ __align__(16) uint32_t xlds[];
-  __shared__ uint32_t clist[kGroups * ROWS];
-  __shared__ uint32_t gcnt[kGroups];
-  const int l = threadIdx.x % LPR;
-  const int lane = threadIdx.x & 63;
-  const int gbase = lane - l;
-  const int gw = threadIdx.x / LPR;  // group within the workgroup
-  const size_t row_bytes = (size_t)(a.in_features >> 1);
-  const int ngroups = a.in_features >> 7;
-  const int nchunks = a.in_features / kChunkCols;
-  const int grp = blockIdx.x * kGroups + gw;
-  const int ngrp = a.ngrp;
-
-  uint4 xs[4];
-  load_x_chunk(a.x, nchunks, xs);
-  __builtin_amdgcn_sched_barrier(0);
-  const long long jl = grp + (long long)l * ngrp;
-  const bool valid_l = l < ROWS && jl < a.nrows;
-  const uint32_t rid_lane = (uint32_t)min(jl, (long long)a.nrows - 1);
-  RowRegs<CH> ring[D];
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    load_row_at<LPR, CH>(a.qw, a.sc, __shfl(rid_lane, gbase + d, 64), l, row_bytes, ngroups,
-                         ring[d]);
-  // the key, after the first rows (a lane-dependent offset that is always 0:
-  // as a uniform load it would be a scalar load waited for before them)
-  const uint32_t zero = threadIdx.x & ((uint32_t)a.in_features >> 30);
-  const uint32_t key = a.state[1 + zero];
-  const bool rot = blockIdx.x == 0 && threadIdx.x == 0;
-
-  uint32_t xp[CH][4][4];
-  float bias[CH];
-  stage_x_pairs<LPR>(xs, xlds, nchunks);
-  x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
-
-  float mine = 0.f;
-#pragma unroll
-  for (int i = 0; i < ROWS; ++i) {
-    RowRegs<CH>& R = ring[i % D];
-    float acc = row_dot_part<CH>(R, xp, bias);
-    if (i + D < ROWS)
-      load_row_at<LPR, CH>(a.qw, a.sc, __shfl(rid_lane, gbase + i + D, 64), l, row_bytes,
-                           ngroups, R);
-    acc = group_sum<LPR>(acc);
-    mine = l == i ? acc : mine;
-  }
-  uint32_t v = 0;
-  if (valid_l) {
-    v = f32_to_bf16(mine);
-    const float f = bf16_to_f32(v);
-    v = f32_to_bf16(f / (1.0f + expf(-f)));
-    a.g[(int)jl] = (uint16_t)v;
-  }
-
-  // the workgroup's candidate list: groups in order, lanes in order
-  const uint32_t kk = v & 0x7FFFu;
-  const bool cand = valid_l && kk >= key && kk < kKeyInf;
-  const uint64_t m = __ballot(cand);
-  const uint32_t gm = (uint32_t)(m >> gbase) & (LPR == 32 ? 0xFFFFFFFFu : ((1u << LPR) - 1u));
-  if (l == 0) gcnt[gw] = (uint32_t)__popc(gm);
-  __syncthreads();
-  int base = 0, total = 0;
-#pragma unroll
-  for (int q = 0; q < kGroups; ++q) {
-    base += q < gw ? (int)gcnt[q] : 0;
-    total += (int)gcnt[q];
-  }
-  if (cand) {
-    const int e = base + __popc(gm & ((1u << l) - 1u));
-    const uint32_t entry = (uint32_t)jl | (v << 16);
-    clist[e] = entry;
-    if (a.cand_list) a.cand_list[(size_t)blockIdx.x * kCandCap + e] = entry;
-  }
-  if (a.cand_count && threadIdx.x == 0) a.cand_count[blockIdx.x] = (uint32_t)total;
-  if (rot) a.state[0] = key;
-  __syncthreads();
-
-  // the candidates' up rows: group gw takes entries gw, gw + kGroups, ...
-  const int mycnt = total > gw ? (total - gw + kGroups - 1) / kGroups : 0;
-  if (mycnt == 0) return;  // uniform within the group
-  RowRegs<CH> ur;
-  uint32_t ent = clist[gw];
-  load_row_at<LPR, CH>(a.up_qw, a.up_sc, ent & 0xFFFFu, l, row_bytes, ngroups, ur);
-#pragma unroll
-  for (int i = 0; i < ROWS; ++i) {
-    if (i >= mycnt) break;  // uniform within the group
-    float acc = row_dot_part<CH>(ur, xp, bias);
-    const uint32_t e = ent;
-    if (i + 1 < mycnt) {
-      ent = clist[gw + kGroups * (i + 1)];
-      load_row_at<LPR, CH>(a.up_qw, a.up_sc, ent & 0xFFFFu, l, row_bytes, ngroups, ur);
-    }
-    acc = group_sum<LPR>(acc);
-    if (l == 0) a.h_full[e & 0xFFFFu] = (uint16_t)h_of(e >> 16, acc);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -506,55 +337,6 @@ int launch_spec_after_gate(const uint16_t* g, int64_t inter, int64_t hidden, int
   return launch_topk_spec(g, inter, k, idx, workspace, sp, stream);
 }
 
-namespace {
-// the split step's gate launch: the tuning knob when set, else two
-int gate_spec_wpc() {
-  const int t = tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
-  return t > 0 ? t : 2;
-}
-template <int LPR, int CH, int ROWS>
-void launch_gate_spec_rows(const GateSpecArgs& a, int blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((gate_spec_kernel<LPR, CH, ROWS>), dim3(blocks), dim3(kRowdotMaxThreads),
-                     x_pairs_lds_bytes(a.in_features), stream, a);
-}
-template <int LPR, int CH>
-int launch_gate_spec_width(GateSpecArgs a, hipStream_t stream) {
-  const RowdotPlan p = plan_rowdot(a.nrows, LPR, true, gate_spec_wpc());
-  if (p.groups * LPR != kRowdotMaxThreads || p.rows < 1 || p.rows > 8) return DIP_ERR_UNSUPPORTED;
-  a.ngrp = p.blocks * p.groups;
-  switch (p.rows) {
-    case 1: launch_gate_spec_rows<LPR, CH, 1>(a, p.blocks, stream); break;
-    case 2: launch_gate_spec_rows<LPR, CH, 2>(a, p.blocks, stream); break;
-    case 3: launch_gate_spec_rows<LPR, CH, 3>(a, p.blocks, stream); break;
-    case 4: launch_gate_spec_rows<LPR, CH, 4>(a, p.blocks, stream); break;
-    case 5: launch_gate_spec_rows<LPR, CH, 5>(a, p.blocks, stream); break;
-    case 6: launch_gate_spec_rows<LPR, CH, 6>(a, p.blocks, stream); break;
-    case 7: launch_gate_spec_rows<LPR, CH, 7>(a, p.blocks, stream); break;
-    default: launch_gate_spec_rows<LPR, CH, 8>(a, p.blocks, stream); break;
-  }
-  return hip_status(hipGetLastError());
-}
-}  // namespace
-
-// Workgroups of the split step's gate launch (0: the width or the row count
-// is not supported).
-int gate_spec_blocks(int64_t nrows, int64_t in_features) {
-  const int64_t chunks = in_features / kChunkCols;
-  const int lpr = chunks == 80 ? 16 : 32;
-  if (!(chunks == 160 || chunks == 128 || chunks == 80) || nrows < 1) return 0;
-  const RowdotPlan p = plan_rowdot((int)nrows, lpr, true, gate_spec_wpc());
-  if (p.rows < 1 || p.rows > 8 || (long long)p.blocks > kMaxCandWgs) return 0;
-  return p.blocks;
-}
-
-int launch_gate_spec(GateSpecArgs a, hipStream_t stream) {
-  const int chunks = a.in_features / kChunkCols;
-  if (chunks == 160) return launch_gate_spec_width<32, 5>(a, stream);
-  if (chunks == 128) return launch_gate_spec_width<32, 4>(a, stream);
-  if (chunks == 80) return launch_gate_spec_width<16, 5>(a, stream);
-  return DIP_ERR_UNSUPPORTED;
-}
-
 int launch_rowdot(int src, int epi, const RowdotArgs& a, hipStream_t stream) {
   if (a.nrows == 0) return DIP_OK;
 #define DIP_CASE(S, E) \
@@ -655,7 +437,7 @@ extern "C" int dip_gate_silu_topk(const int8_t* gate_qw, const uint16_t* gate_sc
   return launch_topk_select(g, inter, k, idx, workspace, (hipStream_t)stream);
 }
 
-extern "C" size_t dip_mlp_state_size(void) { return kStepStateWords * sizeof(uint32_t); }
+extern "C" size_t dip_mlp_state_size(void) { return kMlpStateWords * sizeof(uint32_t); }
 
 extern "C" int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
                                        const int8_t* up_qw, const uint16_t* up_sc,

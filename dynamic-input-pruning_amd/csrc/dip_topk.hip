@@ -288,18 +288,12 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
 // kSelSpec (the decode step with speculative up rows): also records the
 // magnitude key at rank k + margin for the next call and computes h for the
 // selected channels that the speculation workgroups skip (residual_rows).
-// MODE kSelSplit (the split step's second launch): the same key, then
-// split_select_tail.
-enum SelMode : int { kSelPlain = 0, kSelSpec = 1, kSelSplit = 2 };
-template <int LPR, int CH>
-DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool s0, bool s1,
-                               uint32_t pos0, uint32_t pos1, uint32_t uk, uint32_t filled,
-                               uint32_t sk, uint32_t* lds);
+enum SelMode : int { kSelPlain = 0, kSelSpec = 1 };
 
 template <int R, int MODE, int LPR, int CH>
 DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
                        TopkMeta* __restrict__ meta, int stamps, int nblk, const SpecArgs& sp,
-                       uint32_t* hist, const SelDownArgs* sd = nullptr) {
+                       uint32_t* hist) {
   constexpr bool SPEC = MODE != kSelPlain;
   __shared__ uint32_t wtot[kWaves];
   __shared__ uint32_t wsum_a[kWaves], wsum_b[kWaves], wside[kWaves], wown[kWaves];
@@ -571,11 +565,6 @@ DIP_DEV void topk_body(const uint16_t* __restrict__ s, int n, int k, int32_t* __
   if constexpr (MODE == kSelSpec) {
     if (rcount > 0) residual_rows<LPR, CH>(sp, hist, rcount, hist + kSlice);
   }
-  if constexpr (MODE == kSelSplit) {
-    __syncthreads();  // every wave is past the histogram reads: its LDS is reused
-    split_select_tail<LPR, CH>(*sd, my, mine, (a0 | q0) && pos0 < uk, (a1 | q1) && pos1 < uk,
-                               pos0, pos1, uk, filled, sk, hist, stamps);
-  }
   if (stamp) {
     meta->stamp[5] = wall_clock64();
     meta->cycles[1] = clock64();
@@ -606,525 +595,6 @@ __global__ __launch_bounds__(kThreads) void topk_spec_kernel(
   else
     spec_rows<LPR, CH>(s, n, sp, (int)blockIdx.x - sp.ntopk, lds, meta, stamps,
                        (int)gridDim.x - sp.ntopk);
-}
-
-
-// ---------------------------------------------------------------------------
-// The split decode step's second launch (dip_internal.h): select workgroups
-// [0, ntopk) and down workgroups after them.  No workgroup waits for another.
-// ---------------------------------------------------------------------------
-namespace {
-constexpr int kSubThreads = 128;                  // a down sub-tile: two waves
-constexpr int kSubTiles = kThreads / kSubThreads; // per down workgroup
-constexpr int kTilePos = kSubThreads;             // list positions per pass of a down sub-tile
-constexpr int kSubSlots = kSubThreads / 8;        // 8-lane slots of a sub-tile
-constexpr int kSlotRows = 8;                      // rows per slot and pass (one per lane)
-static_assert(kSelectSlice == kSlice, "one fix-up row per select workgroup");
-constexpr int kRangeMax = 512;                    // channels per range at most (4 per thread)
-constexpr int kFixGroups = 4;                     // entry groups of the fix-up row
-constexpr int kFixLdsWord = 12288;                // the fix-up groups' sums: past the x pairs
-constexpr int kRangeTarget = 224;                 // candidates per range aimed at (two passes)
-
-// Wave-ordered exclusive prefix of per-thread counts c (< 2^16 in total):
-// returns my offset and sets *total; scratch: kWaves words of LDS.  Ends with
-// a block barrier.
-DIP_DEV uint32_t block_offset(uint32_t c, uint32_t* scratch, uint32_t* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t incl = wave_prefix(c);
-  if (lane == 63) scratch[wave] = incl;
-  __syncthreads();
-  uint32_t before = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const uint32_t v = scratch[w];
-    before += w < wave ? v : 0u;
-    tot += v;
-  }
-  *total = tot;
-  __syncthreads();  // scratch may be reused
-  return before + incl - c;
-}
-
-// acc[m] += (q/16)[row, columns 8t .. 8t+7] * f for the dword t of the row.
-DIP_DEV void fix_accumulate(uint32_t w, float f, float acc[8]) {
-  const uint32_t hq = w >> 4;
-  acc[0] = fmaf(cvt_nibble_div16<0>(w), f, acc[0]);
-  acc[1] = fmaf(cvt_nibble_div16<0>(hq), f, acc[1]);
-  acc[2] = fmaf(cvt_nibble_div16<1>(w), f, acc[2]);
-  acc[3] = fmaf(cvt_nibble_div16<1>(hq), f, acc[3]);
-  acc[4] = fmaf(cvt_nibble_div16<2>(w), f, acc[4]);
-  acc[5] = fmaf(cvt_nibble_div16<2>(hq), f, acc[5]);
-  acc[6] = fmaf(cvt_nibble_div16<3>(w), f, acc[6]);
-  acc[7] = fmaf(cvt_nibble_div16<3>(hq), f, acc[7]);
-}
-
-// scale of (row ch, group g) of the down matrix, group-major copy if given
-DIP_DEV uint32_t down_scale(const SelDownArgs& a, uint32_t ch, int g) {
-  return a.dn_sc_gm ? a.dn_sc_gm[(size_t)g * a.n + ch]
-                    : a.dn_sc[(size_t)ch * (a.sp.hidden >> 7) + g];
-}
-}  // namespace
-
-// After the placement of a select workgroup's slice (values my, my + 1; s0
-// / s1: selected at pos0 / pos1): candidates are the values whose raw key
-// lies in [sk, 0x7F80) (the gate launch computed their h).
-//   * residual channels: selected non-candidates, and channel 0 when it
-//     fills unfilled slots without being a candidate: h from their up rows
-//     (h_full, and h_out for the selected ones);
-//   * h_out of the selected candidates from h_full; the unfilled slots
-//     (workgroup 0) get channel 0's h;
-//   * one fix-up partial row: + the selected residual rows, - the rows of
-//     candidates that were not selected, + channel 0 once per unfilled slot
-//     (workgroup 0), each as h * (q/16) * 16 s with the products of the down
-//     tiles; entries in a fixed order (residual then margin, each in slice
-//     order) split over fixed thread groups, so the row is deterministic.
-template <int LPR, int CH>
-DIP_DEV void split_select_tail(const SelDownArgs& a, int my, uint32_t mine, bool s0, bool s1,
-                               uint32_t pos0, uint32_t pos1, uint32_t uk, uint32_t filled,
-                               uint32_t sk, uint32_t* lds, int stamps) {
-  __shared__ uint32_t scratch[kWaves];
-  const bool stamp = stamps && blockIdx.x == 0 && threadIdx.x == 0;
-  if (stamp) a.meta->spec_stamp[1][0] = wall_clock64();
-  __shared__ uint32_t sh_c0, sh_e0;
-  const int tid = threadIdx.x;
-  const SpecArgs& sp = a.sp;
-  const int hidden = sp.hidden;
-  // LDS (the histogram's, free): residual entries | their aux (pos | sel <<
-  // 31) | their h | margin entries (h already signed) | staged x pairs
-  uint32_t* rlist = lds;
-  uint32_t* raux = lds + kSlice;
-  uint32_t* rh = lds + 2 * kSlice;
-  uint32_t* mlist = lds + 3 * kSlice;
-  uint32_t* xlds = lds + 4 * kSlice;
-  const uint32_t b0 = mine & 0x7FFFu, b1 = (mine >> 16) & 0x7FFFu;
-  const bool c0 = b0 >= sk && b0 < kKeyInf;  // padding (0x7FFF) never qualifies
-  const bool c1 = b1 >= sk && b1 < kKeyInf;
-  const bool fill = my == 0 && filled < uk;
-  const bool r0 = (s0 || fill) && !c0, r1 = s1 && !c1;
-  const bool m0 = c0 && !s0, m1 = c1 && !s1;
-  if (tid == 0 && blockIdx.x == 0) sh_c0 = c0;
-  uint32_t nr, nm;
-  const uint32_t ro = block_offset((uint32_t)r0 + (uint32_t)r1, scratch, &nr);
-  const uint32_t mo = block_offset((uint32_t)m0 + (uint32_t)m1, scratch, &nm);
-  if (r0) {
-    rlist[ro] = (uint32_t)my | (mine << 16);
-    raux[ro] = s0 ? (pos0 | 0x80000000u) : 0u;
-    if (fill) sh_e0 = ro;
-  }
-  if (r1) {
-    rlist[ro + r0] = (uint32_t)(my + 1) | (mine & 0xFFFF0000u);
-    raux[ro + r0] = pos1 | 0x80000000u;
-  }
-  if (m0) mlist[mo] = (uint32_t)my;
-  if (m1) mlist[mo + m0] = (uint32_t)(my + 1);
-  if (stamp) a.meta->spec_stamp[1][1] = wall_clock64();
-
-  // residual h: one row group per entry (x pairs staged in LDS)
-  const int nchunks = hidden / kChunkCols;
-  if (nr > 0) {  // workgroup-uniform
-    uint4 xs[4];
-    load_x_chunk(sp.x, nchunks, xs);
-    stage_x_pairs<LPR>(xs, xlds, nchunks);  // its barrier also publishes the lists
-    const int l = tid % LPR;
-    const size_t row_bytes = (size_t)(hidden >> 1);
-    const int ngr = hidden >> 7;
-    for (int e = tid / LPR; e < (int)nr; e += kThreads / LPR) {
-      const uint32_t ent = rlist[e];
-      RowRegs<CH> Rr;
-      load_row_at<LPR, CH>(sp.up_qw, sp.up_sc, ent & 0xFFFFu, l, row_bytes, ngr, Rr);
-      const float u = group_sum<LPR>(row_dot_lds<LPR, CH>(Rr, xlds, nchunks, l));
-      if (l == 0) {
-        const uint32_t h = h_of(ent >> 16, u);
-        rh[e] = h;
-        sp.h_full[ent & 0xFFFFu] = (uint16_t)h;
-        const uint32_t aux = raux[e];
-        if (aux >> 31) a.h_out[aux & 0x7FFFFFFFu] = (uint16_t)h;
-      }
-    }
-  }
-  __syncthreads();
-  if (stamp) a.meta->spec_stamp[1][2] = wall_clock64();
-  // channel 0's h for the unfilled slots (workgroup 0)
-  uint32_t h0 = 0;
-  if (blockIdx.x == 0 && filled < uk) {  // workgroup-uniform
-    h0 = sh_c0 ? (uint32_t)sp.h_full[0] : rh[sh_e0];
-    for (uint32_t p = filled + (uint32_t)tid; p < uk; p += kThreads) a.h_out[p] = (uint16_t)h0;
-  }
-
-  // the fix-up row: ng groups of hidden / 16 threads; thread (grp, d) owns
-  // columns 16 d .. 16 d + 15 and takes entries grp, grp + ng, ... B at a
-  // time (one round of loads for the few dozen entries of a steady-state
-  // token), and the groups' sums are added in group order through LDS
-  const int nd = hidden >> 4;
-  const int ng = min(kThreads / nd, kFixGroups);
-  const int grp = tid / nd, d = tid % nd;
-  float* gsum = reinterpret_cast<float*>(lds + kFixLdsWord);  // [ng][hidden]
-  if (grp < ng) {
-    const int gcol = (16 * d) >> 7;  // the scale group of my columns
-    const int nfl = (int)(nr + nm);
-    float acc[16];
-#pragma unroll
-    for (int m = 0; m < 16; ++m) acc[m] = 0.f;
-    constexpr int B = 12;  // entries in flight per thread
-    for (int e0 = grp; e0 < nfl; e0 += B * ng) {
-      uint2 w[B];
-      uint32_t sc[B], hb[B];
-      int sgn[B];  // +1 residual, -1 margin, 0 none
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        // branch-free: every load is issued, from clamped indices, and the
-        // entry kind picks the values (loads under branches serialise)
-        const int e = e0 + u * ng;
-        const bool isr = e < (int)nr, ism = !isr && e < nfl;
-        const int er = isr ? e : 0, em = ism ? e - (int)nr : 0;
-        const uint32_t rent = rlist[er], raux_e = raux[er], rhe = rh[er];
-        const uint32_t ment = mlist[em];
-        const uint32_t ch = isr ? (rent & 0xFFFFu) : (ism ? ment : 0u);
-        sgn[u] = isr ? ((raux_e >> 31) ? 1 : 0) : (ism ? -1 : 0);  // fill-only entry: skipped
-        w[u] = reinterpret_cast<const uint2*>(a.dn_qw + (size_t)ch * (hidden >> 1))[d];
-        sc[u] = down_scale(a, ch, gcol);
-        const uint32_t hg = sp.h_full[ch];
-        hb[u] = isr ? rhe : (hg ^ 0x8000u);  // margin: the gate launch's h, negated
-      }
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const float f = sgn[u] ? bf16_to_f32(hb[u]) * bf16_to_f32(sc[u]) * 16.0f : 0.f;
-        fix_accumulate(w[u].x, f, acc);
-        fix_accumulate(w[u].y, f, acc + 8);
-      }
-    }
-    if (grp == 0 && blockIdx.x == 0 && filled < uk) {  // channel 0 once per unfilled slot
-      const uint2 w = reinterpret_cast<const uint2*>(a.dn_qw)[d];
-      const float f = bf16_to_f32(h0) * bf16_to_f32(down_scale(a, 0u, gcol)) * 16.0f;
-      for (uint32_t u = filled; u < uk; ++u) {
-        fix_accumulate(w.x, f, acc);
-        fix_accumulate(w.y, f, acc + 8);
-      }
-    }
-    float4* dst = reinterpret_cast<float4*>(gsum + (size_t)grp * hidden + 16 * d);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dst[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
-  }
-  __syncthreads();
-  {
-    float* out = a.partial + (size_t)(a.ranges + (int)blockIdx.x) * hidden;
-    const float4* g4 = reinterpret_cast<const float4*>(gsum);
-    for (int c4 = tid; c4 < hidden / 4; c4 += kThreads) {
-      float4 v = g4[c4];
-      for (int q = 1; q < ng; ++q) {
-        const float4 u = g4[(size_t)q * (hidden / 4) + c4];
-        v.x += u.x;
-        v.y += u.y;
-        v.z += u.z;
-        v.w += u.w;
-      }
-      reinterpret_cast<float4*>(out)[c4] = v;
-    }
-  }
-  // h_out of the selected candidates (the gate launch's h), after the
-  // fix-up so that no barrier above waits for these loads
-  if (s0 && c0) a.h_out[pos0] = sp.h_full[my];
-  if (s1 && c1) a.h_out[pos1] = sp.h_full[my + 1];
-  if (stamp) a.meta->spec_stamp[1][3] = wall_clock64();
-}
-
-// Down workgroup w of the split step: tiles (channel range r, column block
-// cb), tile t = r * col_blocks + cb on sub-tile t / ndown of workgroup t %
-// ndown (split_layout keeps the tiles within one round).  A sub-tile (128
-// threads: 16 slots of 8 lanes) loads g and h_full of its range's channels at
-// once, lists the candidates (the gate launch's key test) in channel order,
-// and walks them 128 positions per pass: slot s takes positions 128 pass + s
-// + 16 i (i < 8; lane l holds row l), all loaded before any is used;
-// positions past the count contribute 0.  The slot sums are reduced as
-// in the down kernel into partial row r, block cb.
-template <int SL>
-DIP_DEV void range_down_role(const SelDownArgs& a, int w, uint32_t* lds, int stamps) {
-  constexpr int kPer = kRangeMax / kSubThreads;  // channels per thread
-  __shared__ uint32_t wcnt[kSubTiles][kPer][2];   // candidates per sub-tile, pass q, wave
-  const int tid = threadIdx.x;
-  const bool stamp = stamps && w == 0 && tid == 0;
-  if (stamp) a.meta->spec_stamp[0][0] = wall_clock64();
-  const int hidden = a.sp.hidden;
-  const int sub = tid / kSubThreads, st = tid % kSubThreads;
-  const int lane = tid & 63, wv = st >> 6;
-  const int l = st % 8, slot = st / 8;
-  const int gbase = lane - l;
-  const int cbs = a.col_blocks;
-  const int t = w + sub * a.ndown;
-  const bool active = t < a.ranges * cbs;
-  const int r = active ? t / cbs : 0, cb = active ? t % cbs : 0;
-  const int c0 = r * a.chan_per_range, c1 = min(c0 + a.chan_per_range, a.n);
-  uint32_t* list = lds + sub * kRangeMax;
-  float* red = reinterpret_cast<float*>(lds + kSubTiles * kRangeMax);  // [sub][wave][256]
-
-  // 1. the range's candidates (key in [state[0], 0x7F80), as the gate
-  //    launch tested them); the key is read per lane at an offset that is
-  //    always 0, so that it is in flight with g instead of a scalar load
-  const uint32_t zero = (uint32_t)tid & ((uint32_t)hidden >> 30);
-  const uint32_t sk = a.sp.state[zero];
-  uint32_t gv[kPer], hv[kPer];
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int c = min(c0 + st + kSubThreads * q, a.n - 1);
-    gv[q] = a.g[c];
-    hv[q] = a.sp.h_full[c];
-  }
-  bool f[kPer];
-  uint64_t m[kPer];
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int c = c0 + st + kSubThreads * q;
-    const uint32_t key = gv[q] & 0x7FFFu;
-    f[q] = active && c < c1 && key >= sk && key < kKeyInf;
-    m[q] = __ballot(f[q]);
-    if (lane == 0) wcnt[sub][q][wv] = (uint32_t)__popcll(m[q]);
-  }
-  __syncthreads();
-  int total = 0, base[kPer];
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    const int n0 = (int)wcnt[sub][q][0];
-    base[q] = total + (wv ? n0 : 0);
-    total += n0 + (int)wcnt[sub][q][1];
-  }
-  const uint64_t below = (1ull << lane) - 1ull;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q)
-    if (f[q])
-      list[base[q] + __popcll(m[q] & below)] =
-          (uint32_t)(c0 + st + kSubThreads * q) | (hv[q] << 16);
-  __syncthreads();
-  if (stamp) a.meta->spec_stamp[0][1] = wall_clock64();
-
-  // 2. their down rows, 256 positions per pass
-  const size_t row_bytes = (size_t)(hidden >> 1);
-  const int ngroups = hidden >> 7;
-  DownArgs da{};  // the fields load_down_scales / load_down_row read
-  da.qw_a = a.dn_qw;
-  da.sc_a = a.dn_sc;
-  da.sc_gm = a.dn_sc_gm;
-  da.qw_safe = a.dn_qw;
-  da.sc_safe = a.dn_sc;
-  da.rows_a = a.n;
-  float acc[kDownAcc];
-#pragma unroll
-  for (int i = 0; i < kDownAcc; ++i) acc[i] = 0.f;
-  const int passes = (total + kTilePos - 1) / kTilePos;  // uniform within the sub-tile
-  for (int pass = 0; pass < passes; ++pass) {
-    // lane l: the id, h and scales of its slot's row l
-    const int p = pass * kTilePos + slot + kSubSlots * l;
-    const uint32_t ent = list[min(p, total - 1)];
-    const uint32_t rid = p < total ? (ent & 0xFFFFu) : kPadRow;
-    uint32_t sv[2];
-    load_down_scales<kGather, 2, SL>(da, rid, 2 * cb, ngroups, sv);
-    DownRow ring[kSlotRows];
-#pragma unroll
-    for (int i = 0; i < kSlotRows; ++i)
-      load_down_row<kGather>(da, __shfl(rid, gbase + i, 64), cb * 8 + l, row_bytes, ring[i]);
-    if (stamp && pass == 0) a.meta->spec_stamp[0][2] = wall_clock64();
-    float fc[2];
-    down_coef<2>(rid, ent >> 16, sv, fc);
-    down_accumulate<kSlotRows, 2>(ring, fc, l >= 4, gbase, acc);
-  }
-
-  // 3. the slots of each wave in registers, the sub-tile's two waves via LDS
-#pragma unroll
-  for (int i = 0; i < kDownAcc; ++i) acc[i] += dpp_mov<0x128>(acc[i]);  // row_ror:8
-  float t16[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    permlane16_swap(acc[i], acc[i + 16]);
-    t16[i] = acc[i] + acc[i + 16];
-  }
-  float u8[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    permlane32_swap(t16[i], t16[i + 8]);
-    u8[i] = t16[i] + t16[i + 8];
-  }
-  float* rs = red + sub * (2 * 256);
-  if ((lane & 15) < 8) {
-    float* dst = rs + wv * 256 + 32 * (lane % 8) + 8 * (lane >> 5) + 16 * ((lane >> 4) & 1);
-    *reinterpret_cast<float4*>(dst) = make_float4(u8[0], u8[1], u8[2], u8[3]);
-    *reinterpret_cast<float4*>(dst + 4) = make_float4(u8[4], u8[5], u8[6], u8[7]);
-  }
-  __syncthreads();
-  if (active) {
-    float* out = a.partial + (size_t)r * hidden + (size_t)cb * 256;
-    for (int c = st; c < 256; c += kSubThreads) out[c] = rs[c] + rs[256 + c];
-  }
-  if (stamp) a.meta->spec_stamp[0][3] = wall_clock64();
-}
-
-template <int R, int LPR, int CH, int SL>
-__global__ __launch_bounds__(kThreads) void select_down_kernel(SelDownArgs a, int stamps) {
-  extern __shared__ __align__(16) uint32_t lds[];
-  if ((int)blockIdx.x < a.sp.ntopk)
-    topk_body<R, kSelSplit, LPR, CH>(a.g, a.n, a.k, a.idx, a.meta, stamps, a.sp.ntopk, a.sp, lds,
-                                     &a);
-  else
-    range_down_role<SL>(a, (int)blockIdx.x - a.sp.ntopk, lds, stamps);
-}
-
-
-// ---------------------------------------------------------------------------
-// Finish of the fused decode step (after dip_step.hip's launch), one launch of
-// two kinds of workgroups:
-//   * workgroups [0, ny): y[o] = bf16(sum of the step workgroups' partial
-//     rows), the rows in a fixed order (four interleaved ascending splits,
-//     added in order);
-//   * workgroups [ny, ny + ceil(n/2048)): idx and h_out for one slice of
-//     2048 channels.  The step recorded the bisection's lo / hi (so the tier
-//     cuts) and the tier totals; each workgroup counts the tiers of the
-//     channels before its slice (packed 16-bit counting), places its slice's
-//     selected channels at their positions — tier A in ascending id, then
-//     tier B in ascending id up to k (topk_select.cu:64-132) — and copies
-//     each one's h from h_full.  The first one also fills the unfilled slots
-//     with channel 0 (topk_select.cu:160).
-// ---------------------------------------------------------------------------
-namespace {
-constexpr int kFinThreads = 256;
-constexpr int kFinOut = 32;                   // outputs per y workgroup
-constexpr int kFinSplit = kFinThreads / kFinOut;
-constexpr int kFinBatch = 32;                 // partial rows in flight per thread
-constexpr int kFinSlice = 2048;               // channels per idx workgroup
-constexpr int kFinCountBatch = 16;            // 8-channel chunks in flight per thread
-}  // namespace
-
-__global__ __launch_bounds__(kFinThreads) void finish_kernel(FinishArgs a) {
-  __shared__ float part[kFinSplit][kFinOut];
-  __shared__ uint32_t wtot[kFinThreads / 64][3];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if ((int)blockIdx.x < a.ny) {
-    // split p sums rows p, p + kFinSplit, ... (all loads of a batch issued
-    // before the adds), then the splits in order
-    const int oo = tid % kFinOut, p = tid / kFinOut;
-    const int o = min((int)blockIdx.x * kFinOut + oo, a.hidden - 1);
-    float s = 0.f;
-    for (int r0 = p; r0 < a.rows; r0 += kFinBatch * kFinSplit) {
-      float v[kFinBatch];
-#pragma unroll
-      for (int u = 0; u < kFinBatch; ++u) {
-        const int rb = min(r0 + u * kFinSplit, a.rows - 1);
-        v[u] = a.partial[(size_t)rb * a.hidden + o];
-      }
-#pragma unroll
-      for (int u = 0; u < kFinBatch; ++u) s = r0 + u * kFinSplit < a.rows ? s + v[u] : s;
-    }
-    part[p][oo] = s;
-    __syncthreads();
-    if (p == 0 && (int)blockIdx.x * kFinOut + oo < a.hidden) {
-      float t = part[0][oo];
-#pragma unroll
-      for (int qq = 1; qq < kFinSplit; ++qq) t += part[qq][oo];
-      a.y[blockIdx.x * kFinOut + oo] = (uint16_t)f32_to_bf16(t);
-    }
-    return;
-  }
-  const int n = a.n;
-  const uint32_t uk = (uint32_t)a.k;
-  const int slice0 = ((int)blockIdx.x - a.ny) * kFinSlice;
-  const uint32_t cut_a = max((__float_as_uint(a.meta->hi) >> 16) + 1u, kMinNormalKey);
-  const uint32_t cut_b = max((__float_as_uint(a.meta->lo) >> 16) + 1u, kMinNormalKey);
-  const Cuts c = make_cuts(cut_a, cut_b);
-  const uint32_t tot_a = (uint32_t)a.meta->count_a, tot_b = (uint32_t)a.meta->count_b;
-  // tier counts of the channels before the slice (whole 8-channel chunks:
-  // slice0 <= n is a multiple of 8), a batch of chunks in flight at a time
-  uint32_t pa = 0, pb = 0;
-  for (int base0 = tid * 8; base0 < slice0; base0 += kFinThreads * 8 * kFinCountBatch) {
-    uint32_t w[kFinCountBatch][4];
-    // unconditional loads (chunk 0 stands in past the slice), masked after
-    // all of them are issued
-#pragma unroll
-    for (int u = 0; u < kFinCountBatch; ++u) {
-      const int base = base0 + u * kFinThreads * 8;
-      const uint4 v = *reinterpret_cast<const uint4*>(a.g + (base < slice0 ? base : 0));
-      w[u][0] = v.x;
-      w[u][1] = v.y;
-      w[u][2] = v.z;
-      w[u][3] = v.w;
-    }
-#pragma unroll
-    for (int u = 0; u < kFinCountBatch; ++u) {
-      if (base0 + u * kFinThreads * 8 >= slice0) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[u][e] = 0xFFFFFFFFu;  // NaN: in no tier
-      }
-      const uint32_t t = tier_counts8(w[u], c.cut_a2, c.span_a2, c.cut_b2, c.span_b2);
-      pa += t & 0xFFFFu;
-      pb += t >> 16;
-    }
-  }
-  // my 8 channels of the slice, in order
-  const int my = slice0 + tid * 8;
-  uint32_t w[4];
-  load_chunk8(a.g, n, my, w);
-  if (my < n && my + 8 > n) load_tail8(a.g, n, my, w);
-  // their h, in one load (h_full spans whole 256-byte blocks past n)
-  const uint4 hq = *reinterpret_cast<const uint4*>(a.h_full + (my < n ? my : 0));
-  const uint32_t hw[4] = {hq.x, hq.y, hq.z, hq.w};
-  uint32_t ta = 0, tb = 0, flags = 0;  // flags: 2 bits per value (1 = A, 2 = B)
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t kk = (w[e >> 1] >> (16 * (e & 1))) & 0x7FFFu;
-    const bool ia = kk - c.cut_a < c.span_a;
-    const bool ib = kk - c.cut_b < c.span_b;
-    ta += ia ? 1u : 0u;
-    tb += ib ? 1u : 0u;
-    flags |= (ia ? 1u : (ib ? 2u : 0u)) << (2 * e);
-  }
-  const uint32_t own = ta | (tb << 16);
-  const uint32_t incl = wave_prefix(own);
-  const uint32_t sa = lane63(wave_prefix(pa)), sb = lane63(wave_prefix(pb));
-  if (lane == 63) wtot[wave][0] = incl;
-  if (lane == 0) {
-    wtot[wave][1] = sa;
-    wtot[wave][2] = sb;
-  }
-  __syncthreads();
-  uint32_t before = 0, pre_a = 0, pre_b = 0;
-#pragma unroll
-  for (int wv = 0; wv < kFinThreads / 64; ++wv) {
-    before += wv < wave ? wtot[wv][0] : 0u;
-    pre_a += wtot[wv][1];
-    pre_b += wtot[wv][2];
-  }
-  const uint32_t ex = before + incl - own;
-  uint32_t pos_a = pre_a + (ex & 0xFFFFu), pos_b = tot_a + pre_b + (ex >> 16);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t f = (flags >> (2 * e)) & 3u;
-    const uint32_t pos = f == 1u ? pos_a : pos_b;
-    if (f != 0u && pos < uk) {
-      a.idx[pos] = my + e;
-      a.h_out[pos] = (uint16_t)(hw[e >> 1] >> (16 * (e & 1)));
-    }
-    pos_a += f == 1u ? 1u : 0u;
-    pos_b += f == 2u ? 1u : 0u;
-  }
-  if (slice0 == 0) {  // unfilled slots: channel 0
-    const uint32_t filled = min(uk, tot_a + tot_b);
-    for (uint32_t pp = filled + (uint32_t)tid; pp < uk; pp += kFinThreads) {
-      a.idx[pp] = 0;
-      a.h_out[pp] = a.h_full[0];
-    }
-    if (a.state && tid == 0) {  // the next call's speculation key and band
-      const uint32_t key = a.meta->next_key, band = a.meta->next_band;
-      a.state[0] = key;
-      a.state[1] = key;
-      a.state[2] = band;
-      a.state[3] = 0u;
-    }
-  }
-}
-
-int launch_finish(const FinishArgs& args, hipStream_t stream) {
-  FinishArgs a = args;
-  a.ny = (a.hidden + kFinOut - 1) / kFinOut;
-  const int ni = (a.n + kFinSlice - 1) / kFinSlice;
-  hipLaunchKernelGGL(finish_kernel, dim3(a.ny + ni), dim3(kFinThreads), 0, stream, a);
-  return hip_status(hipGetLastError());
 }
 
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,
@@ -1174,76 +644,6 @@ int launch_spec_width(const uint16_t* s, int n, int k, int32_t* idx, TopkMeta* m
 }
 
 }  // namespace
-
-namespace {
-template <int R, int LPR, int CH, int SL>
-int launch_select_down_variant(const SelDownArgs& a, int blocks, hipStream_t stream) {
-  static const bool lds_ok =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&select_down_kernel<R, LPR, CH, SL>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                          kFineBins * (int)sizeof(uint32_t)) == hipSuccess;
-  if (!lds_ok) return hip_status(hipGetLastError());
-  hipLaunchKernelGGL((select_down_kernel<R, LPR, CH, SL>), dim3(blocks), dim3(kThreads),
-                     kFineBins * sizeof(uint32_t), stream, a, tuning(DIP_TUNE_TOPK_STAMPS));
-  return hip_status(hipGetLastError());
-}
-template <int LPR, int CH, int SL>
-int launch_select_down_width(const SelDownArgs& a, int blocks, hipStream_t stream) {
-  if (a.n <= 4 * 8 * kThreads) return launch_select_down_variant<4, LPR, CH, SL>(a, blocks, stream);
-  return launch_select_down_variant<8, LPR, CH, SL>(a, blocks, stream);
-}
-template <int SL>
-int launch_select_down_sl(const SelDownArgs& a, int blocks, hipStream_t stream) {
-  const int chunks = a.sp.hidden / kChunkCols;
-  if (chunks == 160) return launch_select_down_width<32, 5, SL>(a, blocks, stream);
-  if (chunks == 128) return launch_select_down_width<32, 4, SL>(a, blocks, stream);
-  return launch_select_down_width<16, 5, SL>(a, blocks, stream);
-}
-}  // namespace
-
-bool split_step_supported(int64_t hidden, int64_t inter) {
-  // 8-chunk column blocks and an even number of scale groups per row (the
-  // down tiles' scale pairs)
-  return topk_spec_supported(hidden) && hidden % 256 == 0 && inter >= 1 && inter <= kTopkMaxN &&
-         (hidden / kChunkCols) % 8 == 0;
-}
-
-bool split_layout(int64_t hidden, int64_t n, int64_t k, int* ranges, int* chan_per_range) {
-  if (!split_step_supported(hidden, n) || k < 1 || k > n) return false;
-  const int64_t ntopk = (n + kSlice - 1) / kSlice;
-  const int64_t ndown = std::max<int64_t>(device_cus() - ntopk, 1);
-  const int64_t cbs = hidden / (kChunkCols * 8);
-  // ranges of about kRangeTarget candidates in steady state (the k selected
-  // plus the margin above them), at most one round of the down tiles
-  const int64_t cand = std::min<int64_t>(n, k + n * (int64_t)tuning(DIP_TUNE_SPEC_MARGIN) / 1024);
-  const int64_t c = std::min<int64_t>(
-      kRangeMax, std::max<int64_t>(kSubThreads, kRangeTarget * n / std::max<int64_t>(cand, 1)));
-  const int64_t r = std::min((n + c - 1) / c, kSubTiles * ndown / cbs);
-  if (r < 1) return false;
-  const int64_t per = (n + r - 1) / r;  // the same ranges, evened out
-  if (per > kRangeMax) return false;
-  *ranges = (int)((n + per - 1) / per);
-  *chan_per_range = (int)per;
-  return true;
-}
-
-int launch_select_down(SelDownArgs a, hipStream_t stream) {
-  if (a.n <= 0 || a.k <= 0 || a.k > a.n || a.n > kTopkMaxN) return DIP_ERR_SHAPE;
-  int ranges = 0, per = 0;
-  if (!split_layout(a.sp.hidden, a.n, a.k, &ranges, &per)) return DIP_ERR_UNSUPPORTED;
-  const int ntopk = (a.n + kSlice - 1) / kSlice;
-  a.sp.ntopk = ntopk;
-  a.sp.margin = (int)(a.n * (int64_t)tuning(DIP_TUNE_SPEC_MARGIN) / 1024);
-  a.ranges = ranges;
-  a.chan_per_range = per;
-  a.col_blocks = a.sp.hidden / (kChunkCols * 8);
-  a.ndown = std::max(device_cus() - ntopk, 1);
-  const int blocks = ntopk + a.ndown;
-  if (a.dn_sc_gm) return launch_select_down_sl<kScGm>(a, blocks, stream);
-  if (((reinterpret_cast<uintptr_t>(a.dn_sc)) & 3u) == 0)
-    return launch_select_down_sl<kScRow4>(a, blocks, stream);
-  return launch_select_down_sl<kScRow>(a, blocks, stream);
-}
 
 bool topk_spec_supported(int64_t hidden) {
   const int64_t chunks = hidden / kChunkCols;

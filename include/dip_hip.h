@@ -48,21 +48,16 @@ enum { DIP_ACT_NONE = 0, DIP_ACT_SILU = 1 };
 /* Human-readable text for a status returned by this library. */
 const char* dip_status_string(int status);
 
-/* Library version as an integer (major * 10000 + minor * 100 + patch). */
-int dip_version(void);
-
 /*
- * Measurement kernels (no counterpart in the reference: they calibrate the
- * roofline this build is measured against).  dip_read_probe reads `bytes`
- * (a multiple of 16) of src front to back; dip_gather_probe reads the rows
- * idx[0..k) (sorted ids below nrows; others read row 0) of a row-major
- * matrix of 2560-byte rows, each row whole by one 32-lane group.  Neither computes
- * anything; `sink` (4 bytes) is written only if the folded words hit a
- * fixed constant.
+ * Library version as an integer (major * 10000 + minor * 100 + patch).  The
+ * minor number changes whenever an entry point's argument list changes, so
+ * a binding written against this header checks dip_version() == DIP_VERSION
+ * before its first call.  0.3.0: the measurement probes and the
+ * DIP_TUNE_STEP knob are gone; 0.2.0 added down_t_sc_gm to the decode and
+ * gather-down entry points and g_len to dip_ca_fused_gemv.
  */
-int dip_read_probe(const void* src, size_t bytes, uint32_t* sink, void* stream);
-int dip_gather_probe(const void* rows, int64_t nrows, int64_t row_bytes, const int32_t* idx,
-                     int64_t k, uint32_t* sink, void* stream);
+#define DIP_VERSION 300
+int dip_version(void);
 
 /* Highest row count the top-k supports (its keys are staged in LDS). */
 int64_t dip_topk_max_n(void);
@@ -154,26 +149,13 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
  *                               on the channels at or above the magnitude of
  *                               rank k + inter * this / 1024 (0..1024) (8)
- *   DIP_TUNE_STEP               1: a decode step with speculation state runs
- *                               its top-k, up rows, h and down partials in
- *                               one launch after the gate, then a finish
- *                               launch (three launches); 2: the gate also
- *                               computes h of its candidate channels, then
- *                               the top-k beside down tiles over every
- *                               candidate (with a fix-up of the selection),
- *                               then the reduce (three launches; widths
- *                               5120, 4096, 2560; dip_mlp_decode only);
- *                               0: top-k + speculative up, then down +
- *                               reduce (four launches) (0: the fastest on
- *                               MI355X today)
  * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
  */
 enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
   DIP_TUNE_TOPK_STAMPS = 1,
   DIP_TUNE_SPEC_MARGIN = 2,
-  DIP_TUNE_STEP = 3,
-  DIP_TUNE_COUNT = 4
+  DIP_TUNE_COUNT = 3
 };
 int dip_set_tuning(int knob, int value);
 int dip_get_tuning(int knob);

@@ -50,3 +50,40 @@ def test_traffic_from_the_committed_summary():
         assert b.measured_traffic("qwen3-32b", 0.6, "gate_silu", K) is None
     finally:
         K.set_tuning("spec_margin", old)
+
+
+def test_probe_library_is_separate_and_checks_its_arguments():
+    """The read-ceiling probes are a library of their own (bench.py --ceiling
+    loads it); the decode library exports none of them.  Bad arguments are
+    rejected before any launch (no GPU needed)."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "dynamic-input-pruning_amd" / "libdip_probe.so"))
+    _p, _i64, _i = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.dip_probe_read.argtypes = [_p, ctypes.c_size_t, _i, _i, _p, _p]
+    lib.dip_probe_gather.argtypes = [_p, _i64, _i64, _p, _i64, _i, _i, _p, _p]
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
+    assert lib.dip_probe_read(None, 16, 1, 4, p, None) == -1
+    assert lib.dip_probe_read(p, 24, 1, 4, p, None) == -2
+    assert lib.dip_probe_read(p + 2, 32, 1, 4, p, None) == -3
+    assert lib.dip_probe_read(p, 32, 0, 4, p, None) == -6
+    assert lib.dip_probe_read(p, 32, 1, 3, p, None) == -6
+    assert lib.dip_probe_gather(p, 100, 2560, None, 10, 1, 4, p, None) == -1
+    assert lib.dip_probe_gather(p, 100, 2600, p, 10, 1, 4, p, None) == -2
+    assert lib.dip_probe_gather(p, 100, 8192, p, 10, 1, 4, p, None) == -2
+    assert lib.dip_probe_gather(p, 0, 2560, p, 10, 1, 4, p, None) == -2
+    assert lib.dip_probe_gather(p, 100, 2560, p, 10, 1, 5, p, None) == -6
+    assert not hasattr(K.lib, "dip_probe_read") and not hasattr(K.lib, "dip_gather_probe")
+
+
+def test_cache_aware_mode_refuses_the_profiler(monkeypatch, capsys):
+    """bench.py --ca exits with status 3 before any GPU call when rocprofv3's
+    environment is present, and runs otherwise (here: no variable set)."""
+    b = _bench()
+    for n in [n for n in list(__import__("os").environ) if n.startswith("ROCPROF")]:
+        monkeypatch.delenv(n)
+    assert b.profiler_env() == []
+    monkeypatch.setenv("ROCPROF_OUTPUT_PATH", "/tmp/prof")
+    assert b.profiler_env() == ["ROCPROF_OUTPUT_PATH"]
+    assert b.main(["--ca", "0.3"]) == 3
+    assert "does not run under rocprofv3" in capsys.readouterr().err

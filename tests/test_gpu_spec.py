@@ -1,17 +1,16 @@
 """GPU parity of the decode step with speculative up rows.
 
-dip_mlp_decode with a layer state runs the gate (which also lists, per
-workgroup, its candidate channels and the channels inside the state's key
-band), one launch holding the top-k cut, the up rows, h and each workgroup's
-down partial, then the finish (y, idx, h, the next state).  Whatever the
-state holds, g, idx and h must be bit-identical to the stage-by-stage step
-(no state), which the other GPU tests pin against the oracle.  y is the same
-sum of the same exact products in another fp32 order (which workgroup sums
-which channel depends on the state), so it must agree to within a few fp32
-roundings: one bf16 ulp, except where the sum cancels to near zero; a missing
-or doubled channel moves y by about 1/sqrt(k) of its size.  For a given state
-the step is deterministic.  The state itself must then hold the magnitude key
-of rank k + margin of the call's g and a key band that contains its cut.
+dip_mlp_decode with a layer state runs four launches: the gate, one launch
+holding the top-k select and the up rows (with h) of the channels the
+state's speculation key picks, the down partials and the down reduce.
+Whatever the state holds, g, idx and h must be bit-identical to the
+stage-by-stage step (no state), which the other GPU tests pin against the
+oracle.  y is the same sum of the same exact products, read by channel
+instead of by position; it must agree to within a few fp32 roundings: one
+bf16 ulp, except where the sum cancels to near zero; a missing or doubled
+channel moves y by about 1/sqrt(k) of its size.  For a given state the step
+is deterministic.  The state itself must then hold the magnitude key of rank
+k + margin of the call's g.
 """
 import numpy as np
 import pytest
@@ -25,18 +24,10 @@ pytestmark = pytest.mark.gpu
 MARGIN_PER_1024 = 8  # DIP_TUNE_SPEC_MARGIN default
 
 
-@pytest.fixture(scope="module", params=[0, 1, 2], ids=["four-launch", "fused", "split"])
-def K(request):
-    """The library with the decode step's speculative path set to the
-    four-launch form (top-k + up, down, reduce), the fused one (one launch
-    for top-k, up and down partials, then the finish) or the split one (the
-    gate with its candidates' up rows; the select beside the candidates' down
-    tiles; the reduce)."""
+@pytest.fixture(scope="module")
+def K():
     import _dip_hip
-    old = _dip_hip.get_tuning("step")
-    _dip_hip.set_tuning("step", request.param)
-    yield _dip_hip
-    _dip_hip.set_tuning("step", old)
+    return _dip_hip
 
 
 def _weights(H, I, seed):
@@ -92,30 +83,18 @@ def _assert_step(a, b, what):
     _assert_y_close(a[0], b[0], what)
 
 
-def _state(key, band=(0, 0)):
-    """A decode state: the speculation key (twice) and the key band [lo, hi)
-    the gate lists ((0, 0): none, the whole-g path)."""
-    lo, hi = band
-    return torch.tensor([key, key, lo | (hi << 16), 0], dtype=torch.int32, device="cuda")
+def _state(key):
+    """A decode state holding the speculation key in use and the next one."""
+    return torch.tensor([key, key, 0, 0], dtype=torch.int32, device="cuda")
 
 
 def _assert_next_state(K, state, g, k, margin, what, first=False):
-    """The state a call leaves: its rank k + margin key as the next key; the
-    four-launch and split paths keep the key they used in [0] (0 after the
-    first call), the fused one the next key in both and a band that holds the
-    cut (the key of rank k + 1)."""
+    """The state a call leaves: its rank k + margin key as the next key, the
+    key it used in [0] (0 after the first call)."""
     st = state.cpu().numpy().view(np.uint32)
-    key = _rank_key(g, k + margin)
-    assert st[1] == key, what
-    if K.get_tuning("step") != 1:
-        if first:
-            assert st[0] == 0, what  # a zeroed state speculates on every channel
-        return
-    assert st[0] == key, what
-    lo, hi = int(st[2]) & 0xFFFF, int(st[2]) >> 16
-    cut = _rank_key(g, k + 1)
-    if cut >= 0x80:
-        assert 0x80 <= lo <= cut < hi <= 0x7F81 and hi - lo <= 256, (what, lo, cut, hi)
+    assert st[1] == _rank_key(g, k + margin), what
+    if first:
+        assert st[0] == 0, what  # a zeroed state speculates on every channel
 
 
 def _rank_key(g, r):
@@ -154,17 +133,9 @@ def test_spec_any_state_value(K):
     g = ref[1]
     keys = [0, 0xFFFF, _rank_key(g, k), _rank_key(g, k // 2), _rank_key(g, k + 2000), 0x7F80,
             0x7FFF, 1]
-    cut = _rank_key(g, k + 1)
-    lo, hi = _rank_key(g, k + 300), _rank_key(g, k - 100) + 1
-    # key bands: none (the whole-g path), around the cut, off by a few keys
-    # (a tier outside: the whole-g path), far off, one key wide, wider than
-    # the band path takes, reaching below normal keys, empty
-    bands = [(0, 0), (lo, hi), (lo + 3, hi), (lo, cut), (cut + 1, cut + 40), (cut, cut + 1),
-             (cut - 255, cut + 1), (cut - 256, cut + 1), (0x40, cut + 5), (cut, cut)]
-    for band in bands:
-        for key in keys:
-            got = _step(K, W, x, k, _state(key, band))
-            _assert_step(got, ref, f"key {key:#x} band {band}")
+    for key in keys:
+        got = _step(K, W, x, k, _state(key))
+        _assert_step(got, ref, f"key {key:#x}")
 
 
 def test_spec_unfilled_slots_use_channel_0(K):
@@ -182,8 +153,7 @@ def test_spec_unfilled_slots_use_channel_0(K):
     ref = _step(K, W0, x, k)
     assert (ref[2][200:] == 0).all()  # unfilled slots hold channel 0
     for key in (0, 1, 0xFFFF, _rank_key(ref[1], 100)):
-        for band in ((0, 0), (_rank_key(ref[1], 190), _rank_key(ref[1], 100) + 1)):
-            _assert_step(_step(K, W0, x, k, _state(key, band)), ref, f"key {key:#x}")
+        _assert_step(_step(K, W0, x, k, _state(key)), ref, f"key {key:#x}")
     gs[0] = W[1][0]         # channel 0 nonzero again
     ref = _step(K, W0, x, k)
     for key in (0, 0xFFFF):
