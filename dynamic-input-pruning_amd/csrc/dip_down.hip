@@ -8,12 +8,14 @@
 // A block of 256 threads holds 256/LPR "slots" of LPR lanes; slot s walks the
 // LPR rows j = 256*rb + s + i*(256/LPR), i < LPR.  Lane l of a slot fetches
 // the id, h and the scales of the slot's column groups (one or two) of the
-// slot's l-th row, and turns them into the row's coefficients 16*h*s; each
-// row's id and coefficient are shuffled to the slot when it comes up, so
-// every lane issues one memory instruction per row (its 16-byte chunk).  The row loop is straight-line code (LPR is a
-// compile-time constant; positions past k are clamped and contribute 0), so
-// every load is unconditional and all of a slot's rows are in flight at once.
-// Each lane keeps 32 fp32 accumulators (its outputs).
+// slot's l-th row and turns them into the row's coefficients 16*h*s.  The
+// ids and coefficients reach the slot's lanes through a per-wave LDS
+// exchange (each lane writes its row's, then reads its slot's LPR: two
+// 128-bit reads each, no per-row shuffles), so every lane issues one memory
+// instruction per row (its 16-byte chunk).  The row loop is straight-line
+// code (LPR is a compile-time constant; positions past k are clamped and
+// contribute 0), so every load is unconditional and all of a slot's rows are
+// in flight at once.  Each lane keeps 32 fp32 accumulators (its outputs).
 //
 // Dequant: v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for
 // the low nibble of any byte (high nibbles after one shift), so each weight
@@ -42,12 +44,21 @@ constexpr int kRedOut = 32;              // outputs per reduce block
 constexpr int kRedSplit = 8;             // interleaved row-block splits per output
 }  // namespace
 
-template <int LPR, int SRC, int SL>
+// OFF32 (one matrix below 4 GiB): the exchange carries each row's 32-bit
+// byte offset instead of its id, and the row loads add it to the matrix's
+// base in a scalar register (one VGPR per address, no 64-bit multiply).
+template <int LPR, int SRC, int SL, bool OFF32>
 __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
+  static_assert(!OFF32 || SRC != kDual, "32-bit offsets: one matrix");
   static_assert(LPR % kChunksPerGroup == 0 && LPR / kChunksPerGroup <= 2, "groups per slot");
   constexpr int kSlots = kThreads / LPR;
   constexpr int kCols = LPR * kDownAcc;  // outputs per column block
+  constexpr int NG = LPR / kChunksPerGroup;
   __shared__ __align__(16) float red[down_red_floats<LPR>()];
+  // the per-wave exchange: lane t's row id, and its row's coefficient for
+  // each of the slot's column groups (a slot's lanes are all in one wave)
+  __shared__ __align__(16) uint32_t xid[kThreads];
+  __shared__ __align__(16) float xcoef[NG][kThreads];
 
   // XCD-aware tile order: workgroups go to the 8 XCDs round-robin, so tile
   // (rb, cb) runs as workgroup b with b % 8 == rb % 8.  All column blocks of
@@ -60,7 +71,6 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   if (rb >= a.row_blocks) return;  // padding tile (row blocks rounded up to 8)
   const int l = threadIdx.x % LPR;
   const int slot = threadIdx.x / LPR;
-  const int gbase = (threadIdx.x & 63) - l;
   const int cc0 = cb * LPR + l;  // my chunk within a row
   const size_t row_bytes = (size_t)(a.out_features >> 1);
   const int ngroups = a.out_features >> 7;
@@ -72,25 +82,131 @@ __global__ __launch_bounds__(kThreads) void down_kernel(DownArgs a) {
   const uint32_t rid_l = jl < a.k ? rid_c : kPadRow;
   const int hix = !a.h_by_row ? jc : (rid_c < (uint32_t)a.rows_a ? (int)rid_c : 0);
   const uint32_t h_l = a.h[hix];
-  if (a.h_out && cb == 0 && jl < a.k) a.h_out[jl] = (uint16_t)h_l;
 
   // lane l: the scales of row l for the slot's NG column groups
-  constexpr int NG = LPR / kChunksPerGroup;
   const int g0 = cb * LPR / kChunksPerGroup;
   uint32_t s_l[NG];
   load_down_scales<SRC, NG, SL>(a, rid_l, g0, ngroups, s_l);
 
+  // the slot's LPR row ids (the exchange stays inside one wave, so a wave
+  // barrier, which only orders the wave's own LDS accesses, suffices)
+  const uint32_t r_off = rid_l >= kPadRow ? 0u : rid_l;  // bad and padding rows read row 0
+  xid[threadIdx.x] = OFF32 ? r_off * (uint32_t)row_bytes : rid_l;
+  __builtin_amdgcn_wave_barrier();
+  uint32_t ids[LPR];
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(xid + slot * LPR);
+#pragma unroll
+    for (int v = 0; v < LPR / 4; ++v) {
+      const uint4 q = src[v];
+      ids[4 * v] = q.x;
+      ids[4 * v + 1] = q.y;
+      ids[4 * v + 2] = q.z;
+      ids[4 * v + 3] = q.w;
+    }
+  }
   DownRow ring[LPR];
 #pragma unroll
-  for (int d = 0; d < LPR; ++d)
-    load_down_row<SRC>(a, __shfl(rid_l, gbase + d, 64), cc0, row_bytes, ring[d]);
+  for (int d = 0; d < LPR; ++d) {
+    if constexpr (OFF32)
+      ring[d].w = ldg_nt(reinterpret_cast<const uint4*>(a.qw_a + (size_t)(ids[d] + 16u * (uint32_t)cc0)));
+    else
+      load_down_row<SRC>(a, ids[d], cc0, row_bytes, ring[d]);
+  }
 
+  // h by position (the API's h_out), stored once the rows are in flight:
+  // before them it would hold up the first column block's tiles by a round
+  // trip for h
+  if (a.h_out && cb == 0 && jl < a.k) a.h_out[jl] = (uint16_t)h_l;
+
+  // each row's coefficient for my column group
   float f_l[NG];
   down_coef<NG>(rid_l, h_l, s_l, f_l);
+#pragma unroll
+  for (int g = 0; g < NG; ++g) xcoef[g][threadIdx.x] = f_l[g];
+  __builtin_amdgcn_wave_barrier();
+  float f[LPR];
+  {
+    const float4* src = reinterpret_cast<const float4*>(&xcoef[l / kChunksPerGroup][slot * LPR]);
+#pragma unroll
+    for (int v = 0; v < LPR / 4; ++v) {
+      const float4 q = src[v];
+      f[4 * v] = q.x;
+      f[4 * v + 1] = q.y;
+      f[4 * v + 2] = q.z;
+      f[4 * v + 3] = q.w;
+    }
+  }
   float acc[kDownAcc];
 #pragma unroll
   for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
-  down_accumulate<LPR, NG>(ring, f_l, cc0 / kChunksPerGroup - g0, gbase, acc);
+  down_accumulate<LPR>(ring, f, acc);
+  down_block_partial<LPR>(acc, red, a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols);
+}
+
+// The decode step's form of down_kernel<8, kGather, kScGm, true> (h by
+// channel, group-major scales, one matrix under 4 GiB), with a compact
+// argument block: the same tiles, loads, exchange and arithmetic, so y and
+// h_out are bit for bit the general kernel's; measured 12.4 against
+// 12.9-13.3 us per launch (partials + reduce) on the Qwen3-32B layer.
+struct DownGmArgs {
+  const int8_t* qw;
+  const uint16_t* sc_gm;  // [groups][rows]
+  const uint16_t* h;      // by channel
+  const int32_t* sel;
+  float* partial;
+  uint16_t* h_out;
+  int rows, k, out_features, col_blocks, row_blocks;
+};
+
+__global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
+  constexpr int LPR = 8, kSlots = kThreads / LPR, kCols = LPR * kDownAcc, kWaves = kThreads / 64;
+  __shared__ __align__(16) float red[down_red_floats<LPR>()];
+  __shared__ __align__(16) uint32_t xoff[kWaves][64];
+  __shared__ __align__(16) float xcoef[kWaves][2][64];
+  const int xcd = blockIdx.x % kXcds, w = blockIdx.x / kXcds;
+  const int rb = xcd + kXcds * (w / a.col_blocks);
+  const int cb = w % a.col_blocks;
+  if (rb >= a.row_blocks) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l = tid % LPR, slot = tid / LPR, sw = lane / LPR;
+  const int cc0 = cb * LPR + l;
+  const int g0 = cb * 2;
+  const uint32_t row_bytes = (uint32_t)(a.out_features >> 1);
+  const uint32_t lane_off = (uint32_t)cc0 * 16u;
+  const int jl = rb * kRowsPerBlock + slot + l * kSlots;
+  const bool live = jl < a.k;
+  const uint32_t raw = (uint32_t)a.sel[min(jl, a.k - 1)];
+  const uint32_t rid = !live ? kPadRow : (raw < (uint32_t)a.rows ? raw : kBadRow);
+  const uint32_t r = rid >= kPadRow ? 0u : rid;  // bad and padding rows read row 0
+  const uint32_t hb = a.h[r];
+  uint32_t sv[2];
+  sv[0] = a.sc_gm[(size_t)g0 * a.rows + r];
+  sv[1] = a.sc_gm[(size_t)(g0 + 1) * a.rows + r];
+  // the slot's row offsets through the per-wave exchange
+  xoff[wave][lane] = r * row_bytes;
+  __builtin_amdgcn_wave_barrier();
+  const uint4 o0 = *reinterpret_cast<const uint4*>(&xoff[wave][sw * LPR]);
+  const uint4 o1 = *reinterpret_cast<const uint4*>(&xoff[wave][sw * LPR + 4]);
+  const uint32_t off[LPR] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+  DownRow ring[LPR];
+#pragma unroll
+  for (int d = 0; d < LPR; ++d)
+    ring[d].w = ldg_nt(reinterpret_cast<const uint4*>(a.qw + (size_t)(off[d] + lane_off)));
+  if (a.h_out && cb == 0 && live) a.h_out[jl] = (uint16_t)hb;
+  float f2[2];
+  down_coef<2>(rid, hb, sv, f2);
+  xcoef[wave][0][lane] = f2[0];
+  xcoef[wave][1][lane] = f2[1];
+  __builtin_amdgcn_wave_barrier();
+  const int myg = l / kChunksPerGroup;
+  const float4 c0 = *reinterpret_cast<const float4*>(&xcoef[wave][myg][sw * LPR]);
+  const float4 c1 = *reinterpret_cast<const float4*>(&xcoef[wave][myg][sw * LPR + 4]);
+  const float f[LPR] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  float acc[kDownAcc];
+#pragma unroll
+  for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
+  down_accumulate<LPR>(ring, f, acc);
   down_block_partial<LPR>(acc, red, a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols);
 }
 
@@ -134,6 +250,8 @@ __global__ void down_zero_kernel(int out_features, uint16_t* __restrict__ y) {
 
 namespace {
 
+uint64_t row_bytes_of(int64_t out_features) { return (uint64_t)(out_features / 2); }
+
 // Lanes per row segment: 8 (128 B per row, 256 outputs per column block)
 // wherever the width allows, else 4.
 int down_lpr(int64_t out_features) {
@@ -157,20 +275,18 @@ void launch_reduce(const float* partial, int row_blocks, int out_features, uint1
 }
 
 template <int LPR, int SL>
-void launch_down(int src, const DownArgs& a, int blocks, hipStream_t stream) {
-  if constexpr (SL == kScGm) {
-    if (src == kContig)
-      hipLaunchKernelGGL((down_kernel<LPR, kContig, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((down_kernel<LPR, kGather, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
-  } else {
-    if (src == kContig)
-      hipLaunchKernelGGL((down_kernel<LPR, kContig, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
-    else if (src == kGather)
-      hipLaunchKernelGGL((down_kernel<LPR, kGather, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((down_kernel<LPR, kDual, SL>), dim3(blocks), dim3(kThreads), 0, stream, a);
-  }
+void launch_down(int src, bool off32, const DownArgs& a, int blocks, hipStream_t stream) {
+  const dim3 grid(blocks), block(kThreads);
+  if (src == kContig && off32)
+    hipLaunchKernelGGL((down_kernel<LPR, kContig, SL, true>), grid, block, 0, stream, a);
+  else if (src == kContig)
+    hipLaunchKernelGGL((down_kernel<LPR, kContig, SL, false>), grid, block, 0, stream, a);
+  else if (src == kGather && off32)
+    hipLaunchKernelGGL((down_kernel<LPR, kGather, SL, true>), grid, block, 0, stream, a);
+  else if (src == kGather)
+    hipLaunchKernelGGL((down_kernel<LPR, kGather, SL, false>), grid, block, 0, stream, a);
+  else if constexpr (SL != kScGm)
+    hipLaunchKernelGGL((down_kernel<LPR, kDual, SL, false>), grid, block, 0, stream, a);
 }
 
 }  // namespace
@@ -240,15 +356,31 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   // 4-byte aligned (rows of an even number of groups, pairs at even groups)
   const bool a4 = lpr == 8 && ((reinterpret_cast<uintptr_t>(sc_a) |
                                 reinterpret_cast<uintptr_t>(sc_b)) & 3u) == 0;
-  if (sc_gm) {
-    if (lpr == 8) launch_down<8, kScGm>(src, a, blocks, stream);
-    else launch_down<4, kScGm>(src, a, blocks, stream);
+  // one matrix whose every row offset fits 32 bits
+  const bool off32 = src != kDual && (uint64_t)rows_a * row_bytes_of(out_features) <= 0xFFFFFFFFull;
+  if (sc_gm && src == kGather && h_by_row && lpr == 8 && off32) {
+    DownGmArgs g{};
+    g.qw = qw_a;
+    g.sc_gm = sc_gm;
+    g.h = h;
+    g.sel = sel;
+    g.partial = a.partial;
+    g.h_out = h_out;
+    g.rows = a.rows_a;
+    g.k = a.k;
+    g.out_features = a.out_features;
+    g.col_blocks = a.col_blocks;
+    g.row_blocks = a.row_blocks;
+    hipLaunchKernelGGL(down_gm_kernel, dim3(blocks), dim3(kThreads), 0, stream, g);
+  } else if (sc_gm) {
+    if (lpr == 8) launch_down<8, kScGm>(src, off32, a, blocks, stream);
+    else launch_down<4, kScGm>(src, off32, a, blocks, stream);
   } else if (lpr == 8 && a4) {
-    launch_down<8, kScRow4>(src, a, blocks, stream);
+    launch_down<8, kScRow4>(src, off32, a, blocks, stream);
   } else if (lpr == 8) {
-    launch_down<8, kScRow>(src, a, blocks, stream);
+    launch_down<8, kScRow>(src, off32, a, blocks, stream);
   } else {
-    launch_down<4, kScRow>(src, a, blocks, stream);
+    launch_down<4, kScRow>(src, off32, a, blocks, stream);
   }
   int st = hip_status(hipGetLastError());
   if (st) return st;

@@ -1,5 +1,5 @@
 // dip_tiles.h — device building blocks shared by the row-dot kernels (gate,
-// up), the down kernels and the fused up+down launch.
+// up, the speculative up rows of the top-k launch) and the down kernel.
 //
 // Row dot (one output per weight row, reduced across the row):
 //   LPR lanes ("a row group") own one row at a time; lane l of the group owns
@@ -12,9 +12,10 @@
 // Down (outputs along the row, reduced across rows):
 //   LPR lanes ("a slot") each own one 16-byte chunk (32 outputs) of every row
 //   the slot walks; a block of 256 threads holds 256/LPR slots that walk the
-//   LPR rows j = j0 + slot + i*(256/LPR).  Lane l of a slot holds the id and
-//   h of the slot's row l; each row's id and h are shuffled to the slot when
-//   it comes up.  All LPR rows of a slot are loaded before any is consumed.
+//   LPR rows j = j0 + slot + i*(256/LPR).  Lane l of a slot resolves the id,
+//   h and scales of the slot's row l; the slot's ids and coefficients reach
+//   its lanes through a per-wave LDS exchange.  All LPR rows of a slot are
+//   loaded before any is consumed.
 #pragma once
 
 #include "dip_common.h"
@@ -335,39 +336,50 @@ DIP_DEV void down_coef(uint32_t rid, uint32_t h, const uint32_t s[NG], float f[N
   }
 }
 
-// acc[m] += (q/16)[row, 32*cc0 + m] * 16*h*s over the slot's LPR rows; row
-// i's coefficient comes from lane gbase + i (f[hi] for this lane's group).
-// v_cvt_off_f32_i4 with an SDWA byte select gives q/16 exactly for the low
-// nibble of any byte (high nibbles after one shift): one convert and one FMA
-// per weight.
-template <int LPR, int NG>
-DIP_DEV void down_accumulate(const DownRow ring[LPR], const float f[NG], int hi, int gbase,
-                             float acc[kDownAcc]) {
+// acc[0..7] += (q/16) * f for the 8 nibbles of w: the low nibble of byte b
+// goes to acc[2b], the high one to acc[2b+1].  v_cvt_off_f32_i4 with an SDWA
+// byte select gives q/16 exactly for the low nibble of a byte (high nibbles
+// after one shift), so a weight costs one convert and one FMA.  The block is
+// one asm statement so that every convert stays next to its FMA: written as
+// separate operations, the compiler computes every convert of a row (or of
+// several rows) first and holds them all in registers (over 140 VGPRs for
+// one tile, spills for two).
+DIP_DEV void down_word(uint32_t w, float f, float* acc) {
+  const uint32_t hq = w >> 4;
+  float t0, t1;
+  asm volatile(
+      "v_cvt_off_f32_i4_sdwa %[t0], %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t1], %[h] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+      "v_fmac_f32 %[a0], %[t0], %[f]\n\t"
+      "v_fmac_f32 %[a1], %[t1], %[f]\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t0], %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t1], %[h] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+      "v_fmac_f32 %[a2], %[t0], %[f]\n\t"
+      "v_fmac_f32 %[a3], %[t1], %[f]\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t0], %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t1], %[h] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+      "v_fmac_f32 %[a4], %[t0], %[f]\n\t"
+      "v_fmac_f32 %[a5], %[t1], %[f]\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t0], %[w] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+      "v_cvt_off_f32_i4_sdwa %[t1], %[h] dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+      "v_fmac_f32 %[a6], %[t0], %[f]\n\t"
+      "v_fmac_f32 %[a7], %[t1], %[f]"
+      : [a0] "+v"(acc[0]), [a1] "+v"(acc[1]), [a2] "+v"(acc[2]), [a3] "+v"(acc[3]),
+        [a4] "+v"(acc[4]), [a5] "+v"(acc[5]), [a6] "+v"(acc[6]), [a7] "+v"(acc[7]),
+        [t0] "=&v"(t0), [t1] "=&v"(t1)
+      : [w] "v"(w), [h] "v"(hq), [f] "v"(f));
+}
+
+// acc[m] += (q/16)[row i, 32*cc0 + m] * f[i] over the slot's LPR rows, in
+// row order (f[i] = 16*h*s of row i for this lane's column group).
+template <int LPR>
+DIP_DEV void down_accumulate(const DownRow ring[LPR], const float f[LPR], float acc[kDownAcc]) {
 #pragma unroll
   for (int i = 0; i < LPR; ++i) {
-    const DownRow& R = ring[i];
-    float f16 = __shfl(f[0], gbase + i, 64);
-    if constexpr (NG == 2) {
-      const float f1 = __shfl(f[1], gbase + i, 64);
-      f16 = hi ? f1 : f16;
-    }
-    const uint32_t wv[4] = {R.w.x, R.w.y, R.w.z, R.w.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t hq = wv[q] >> 4;
-      acc[8 * q + 0] = fmaf(cvt_nibble_div16<0>(wv[q]), f16, acc[8 * q + 0]);
-      acc[8 * q + 1] = fmaf(cvt_nibble_div16<0>(hq), f16, acc[8 * q + 1]);
-      acc[8 * q + 2] = fmaf(cvt_nibble_div16<1>(wv[q]), f16, acc[8 * q + 2]);
-      acc[8 * q + 3] = fmaf(cvt_nibble_div16<1>(hq), f16, acc[8 * q + 3]);
-      acc[8 * q + 4] = fmaf(cvt_nibble_div16<2>(wv[q]), f16, acc[8 * q + 4]);
-      acc[8 * q + 5] = fmaf(cvt_nibble_div16<2>(hq), f16, acc[8 * q + 5]);
-      acc[8 * q + 6] = fmaf(cvt_nibble_div16<3>(wv[q]), f16, acc[8 * q + 6]);
-      acc[8 * q + 7] = fmaf(cvt_nibble_div16<3>(hq), f16, acc[8 * q + 7]);
-    }
-    // Keep each row's conversions next to their FMAs: left free, the
-    // scheduler hoists every row's conversions ahead of the FMAs and needs
-    // over 140 VGPRs (three blocks per CU instead of five).
-    __builtin_amdgcn_sched_barrier(0);
+    down_word(ring[i].w.x, f[i], acc);
+    down_word(ring[i].w.y, f[i], acc + 8);
+    down_word(ring[i].w.z, f[i], acc + 16);
+    down_word(ring[i].w.w, f[i], acc + 24);
   }
 }
 
