@@ -356,14 +356,16 @@ def read_ceiling(args) -> int:
         grid-stride;
       * gather: 15360 sorted random rows of 2560 B out of 25600 (the up/down
         rows at keep 0.6), each row read whole by one 32-lane group;
+      * rows: all 25600 rows the same way (the gate's pattern);
     for workgroups of 256 threads in {1, 2, 3, 4, 8} per CU and each
     thread or group holding {1, 2, 4, 8} loads (rows) in flight.  Rotating:
     every launch reads the next of 8 buffers (541 MB in all) or 12 gather
     matrices (472 MB of rows touched), more than the 256 MB memory-side
     cache holds; resident: every launch re-reads the same buffer, which the
-    memory-side cache then serves.  Each figure is HIP events around
-    `--steps` back-to-back launches (so it includes one launch boundary per
-    launch).  One JSON line."""
+    memory-side cache then serves.  Each figure is HIP events around one
+    replay of a HIP graph of `--steps` back-to-back launches (the median of
+    5), so it includes one launch boundary per launch, as the decode step's
+    stage figures do.  One JSON line."""
     import ctypes
     import torch
 
@@ -379,20 +381,37 @@ def read_ceiling(args) -> int:
     reps = max(8, args.steps)
     stream = torch.cuda.current_stream(dev)
 
+    def cur():
+        return torch.cuda.current_stream(dev).cuda_stream
+
     def check(st, what):
         if st != 0:
             raise RuntimeError(f"{what} failed with status {st}")
 
     def timed(fn):
-        fn(0)
+        """us per launch: `reps` back-to-back launches captured in one HIP
+        graph (as the decode step runs), the median of 5 replays."""
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(stream)
+        with torch.cuda.stream(s):
+            fn(0)
+        stream.wait_stream(s)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for r in range(reps):
-            fn(r)
-        e1.record(stream)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for r in range(reps):
+                fn(r)
+        g.replay()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / reps  # us per launch, back to back
+        ts = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1000.0 / reps)
+        return sorted(ts)[2]
 
     wpcs, rings = (1, 2, 3, 4, 8), (1, 2, 4, 8)
     out = {"metric": "HBM read ceiling (probe kernels, loads only)", "unit": "TB/s",
@@ -404,14 +423,14 @@ def read_ceiling(args) -> int:
         for ring in rings:
             us = timed(lambda r: check(lib.dip_probe_read(bufs[r % 8].data_ptr(), nbytes,
                                                           wpc * cus, ring, sink.data_ptr(),
-                                                          stream.cuda_stream), "read"))
+                                                          cur()), "read"))
             sweep[f"wpc{wpc}_ring{ring}"] = {"us": round(us, 2), "TB/s": round(nbytes / us / 1e6, 3)}
             print(f"[ceiling] read 67.6MB rotating wpc={wpc} ring={ring}: {us:.2f} us",
                   file=sys.stderr, flush=True)
     best = min(sweep, key=lambda n: sweep[n]["us"])
     wpc, ring = (int(v) for v in best.replace("wpc", "").split("_ring"))
     us = timed(lambda r: check(lib.dip_probe_read(bufs[0].data_ptr(), nbytes, wpc * cus, ring,
-                                                  sink.data_ptr(), stream.cuda_stream), "read"))
+                                                  sink.data_ptr(), cur()), "read"))
     out["read_67.6MB"] = {"rotating": sweep, "best_rotating": best,
                           "resident_at_best": {"us": round(us, 2),
                                                "TB/s": round(nbytes / us / 1e6, 3)}}
@@ -432,7 +451,7 @@ def read_ceiling(args) -> int:
         for ring in rings:
             us = timed(lambda r: check(lib.dip_probe_gather(
                 mats[r % nmat].data_ptr(), n, rb, idxs[r % nmat].data_ptr(), k, wpc * cus, ring,
-                sink.data_ptr(), stream.cuda_stream), "gather"))
+                sink.data_ptr(), cur()), "gather"))
             sweep[f"wpc{wpc}_ring{ring}"] = {"us": round(us, 2), "TB/s": round(k * rb / us / 1e6, 3)}
             print(f"[ceiling] gather rotating wpc={wpc} ring={ring}: {us:.2f} us",
                   file=sys.stderr, flush=True)
@@ -440,10 +459,23 @@ def read_ceiling(args) -> int:
     wpc, ring = (int(v) for v in best.replace("wpc", "").split("_ring"))
     us = timed(lambda r: check(lib.dip_probe_gather(mats[0].data_ptr(), n, rb, idxs[0].data_ptr(),
                                                     k, wpc * cus, ring, sink.data_ptr(),
-                                                    stream.cuda_stream), "gather"))
+                                                    cur()), "gather"))
     out["gather_15360x2560B_of_25600"] = {"rotating": sweep, "best_rotating": best,
                                           "resident_at_best": {"us": round(us, 2),
                                                                "TB/s": round(k * rb / us / 1e6, 3)}}
+    # the gate's pattern: every row, whole, one row per 32-lane group
+    allrows = torch.arange(n, dtype=torch.int32, device=dev)
+    sweep = {}
+    for wpc in wpcs:
+        for ring in rings:
+            us = timed(lambda r: check(lib.dip_probe_gather(
+                mats[r % nmat].data_ptr(), n, rb, allrows.data_ptr(), n, wpc * cus, ring,
+                sink.data_ptr(), cur()), "rows"))
+            sweep[f"wpc{wpc}_ring{ring}"] = {"us": round(us, 2), "TB/s": round(n * rb / us / 1e6, 3)}
+            print(f"[ceiling] all rows rotating wpc={wpc} ring={ring}: {us:.2f} us",
+                  file=sys.stderr, flush=True)
+    best = min(sweep, key=lambda n_: sweep[n_]["us"])
+    out["rows_25600x2560B"] = {"rotating": sweep, "best_rotating": best}
     print(json.dumps(out), flush=True)
     return 0
 
