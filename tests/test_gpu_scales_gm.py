@@ -32,10 +32,13 @@ def test_scales_group_major_is_the_transpose(K, rows, groups):
 
 
 @pytest.mark.parametrize("rows,k,out_f", [(25600, 15360, 5120), (12288, 7373, 4096),
-                                          (3000, 1000, 384), (500, 500, 1024)])
+                                          (3000, 1000, 384), (500, 500, 1024),
+                                          (300, 1, 1024), (300, 7, 2048), (300, 257, 1024),
+                                          (4000, 2049, 5120)])
 def test_down_by_channel_same_bits_with_group_major_scales(K, rows, k, out_f):
-    """out_f 384 runs the 4-lane tiles, the others the 8-lane ones; k = rows
-    selects every row."""
+    """out_f 384 runs the 4-lane tiles, the others the 8-lane ones (with the
+    group-major copy: the decode step's kernel); k = rows selects every row;
+    k of 1, 7, 257 and 2049 leave tiles and slots partly empty."""
     rng = np.random.default_rng(k)
     qw, sc = random_int4(rng, rows, out_f)
     idx = np.sort(rng.permutation(rows)[:k]).astype(np.int32)
@@ -52,6 +55,28 @@ def test_down_by_channel_same_bits_with_group_major_scales(K, rows, k, out_f):
     ref = O.down_f64(qw, sc, h_full[idx], rows=idx)
     err = np.abs(O.bf16_to_f32(host_bf16(outs[1][0])) - ref).max() / np.abs(ref).max()
     assert err < 1e-2
+
+
+def test_down_by_channel_bad_ids_same_bits_with_group_major_scales(K):
+    """Out-of-range channel ids poison y (NaN) and read row 0 for h_out, the
+    same bits through the decode step's kernel as through the general one."""
+    rng = np.random.default_rng(11)
+    rows, k, out_f = 600, 300, 1024
+    qw, sc = random_int4(rng, rows, out_f)
+    idx = np.sort(rng.permutation(rows)[:k]).astype(np.int32)
+    idx[[5, 100]] = [rows, -3]
+    h_full = random_bf16(rng, rows)
+    d_qw, d_sc, d_h, d_idx = dev(qw), dev_bf16(sc), dev_bf16(h_full), dev(idx)
+    gm = K.scales_group_major(d_sc)
+    outs = []
+    for g in (None, gm):
+        h_out = torch.empty(k, dtype=torch.bfloat16, device="cuda")
+        y = K.int4_gather_down_by_channel(d_qw, d_sc, d_h, d_idx, h_out=h_out, scales_gm=g)
+        outs.append((y.clone(), h_out))
+    assert torch.equal(_bits(outs[0][0]), _bits(outs[1][0]))
+    assert torch.equal(_bits(outs[0][1]), _bits(outs[1][1]))
+    assert torch.isnan(outs[1][0].float()).all()
+    assert _bits(outs[1][1])[5].item() == _bits(dev_bf16(h_full[:1]))[0].item()
 
 
 def test_group_major_scales_rejected_with_wrong_shape(K):
