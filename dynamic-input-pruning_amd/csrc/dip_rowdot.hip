@@ -43,20 +43,23 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   const int grp = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
   const int ngrp = a.ngrp;
 
-  // 1. x loads first (XS: one chunk per thread, index clamped)
+  // 1. x loads first (XS: one chunk per thread, index clamped; NORM: h, the
+  // residual addend and the norm weight in 8-value units spread over all
+  // threads)
+  constexpr int UPT = NORM ? (LPR * CH * 4 + kRowdotMaxThreads - 1) / kRowdotMaxThreads : 1;
   uint4 xs[XS ? 4 : CH * 4];
-  [[maybe_unused]] uint4 xa[NORM ? 4 : 1], xw[NORM ? 4 : 1];
-  if constexpr (XS) {
-    load_x_chunk(a.x, nchunks, xs);
-    if constexpr (NORM) {
-      load_x_chunk(a.norm_w, nchunks, xw);
-      if (a.norm_add) {
-        load_x_chunk(a.norm_add, nchunks, xa);
-      } else {
+  [[maybe_unused]] uint4 nh[UPT], na[UPT], nw[UPT];
+  if constexpr (NORM) {
+    load_x_units<UPT>(a.x, nchunks * 4, nh);
+    load_x_units<UPT>(a.norm_w, nchunks * 4, nw);
+    if (a.norm_add) {
+      load_x_units<UPT>(a.norm_add, nchunks * 4, na);
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xa[i] = make_uint4(0, 0, 0, 0);
-      }
+      for (int j = 0; j < UPT; ++j) na[j] = make_uint4(0, 0, 0, 0);
     }
+  } else if constexpr (XS) {
+    load_x_chunk(a.x, nchunks, xs);
   } else {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -96,9 +99,11 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   float bias[CH];
   if constexpr (XS) {
     if constexpr (NORM)
-      norm_x_chunk(xs, xa, xw, nchunks, a.norm_eps, a.norm_h_out, a.norm_x_out,
-                   reinterpret_cast<float*>(xlds + x_pairs_lds_bytes(a.in_features) / 4));
-    stage_x_pairs<LPR>(xs, xlds, nchunks);
+      norm_stage_x<LPR, UPT>(nh, na, nw, nchunks, a.norm_eps, a.norm_h_out, a.norm_x_out,
+                             reinterpret_cast<float*>(xlds + x_pairs_lds_bytes(a.in_features) / 4),
+                             xlds);
+    else
+      stage_x_pairs<LPR>(xs, xlds, nchunks);
     x_pairs_to_regs<LPR, CH>(xlds, nchunks, l, xp, bias);
   } else {
 #pragma unroll

@@ -128,61 +128,98 @@ DIP_DEV void stage_x_pairs(const uint4 xs[4], uint32_t* xlds, int nchunks) {
   __syncthreads();
 }
 
-// RMSNorm prologue of the staged x: thread t < nchunks holds chunk t of h
-// (xs), of the residual addend (xa, zeros when there is none) and of the
-// norm weight (xw).  v = bf16(h + add); the block sums v^2 (red: 4 floats of
-// LDS, one block barrier); xs becomes bf16(w * bf16(v * rsqrt(mean + eps))),
-// the rounding of transformers' Qwen3RMSNorm.  Workgroup 0 writes v to
-// h_out and the normalised x to x_out (when given).
-DIP_DEV void norm_x_chunk(uint4 xs[4], const uint4 xa[4], const uint4 xw[4], int nchunks,
-                          float eps, uint16_t* h_out, uint16_t* x_out, float* red) {
-  const bool mine = (int)threadIdx.x < nchunks;
-  uint32_t vw[16];
+// ---------------------------------------------------------------------------
+// RMSNorm prologue of the norm-fused GEMVs, spread over every thread of the
+// workgroup: thread t handles the 8-value units t, t + blockDim, ... (unit u
+// is word u % 4 of chunk u / 4) of h, of the residual addend and of the norm
+// weight, so the four units of a chunk sit on four consecutive lanes.
+// ---------------------------------------------------------------------------
+template <int UPT>
+DIP_DEV void load_x_units(const uint16_t* p, int nunits, uint4 v[UPT]) {
+  const uint4* src = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) v[j] = src[min((int)(threadIdx.x + j * blockDim.x), nunits - 1)];
+}
+
+// v = bf16(h + add) and x = bf16(w * bf16(v * rsqrt(mean(v^2) + eps))) (the
+// rounding of transformers' Qwen3RMSNorm), the block's sum of squares through
+// red (4 floats of LDS, one barrier); workgroup 0 writes v to h_out and x to
+// x_out (when given).  Then the pairs and chunk biases of x are staged in LDS
+// exactly as stage_x_pairs stages them (the same pairs, each chunk's bias
+// summed in the same order as pairs_of), ending with a block barrier.
+template <int LPR, int UPT>
+DIP_DEV void norm_stage_x(const uint4 hs[UPT], const uint4 as[UPT], const uint4 ws[UPT],
+                          int nchunks, float eps, uint16_t* h_out, uint16_t* x_out, float* red,
+                          uint32_t* xlds) {
+  const int nunits = nchunks * 4;
+  uint4 v[UPT];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t hw[4] = {xs[i].x, xs[i].y, xs[i].z, xs[i].w};
-    const uint32_t aw[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w};
+  for (int j = 0; j < UPT; ++j) {
+    const bool mine = (int)(threadIdx.x + j * blockDim.x) < nunits;
+    const uint32_t hw[4] = {hs[j].x, hs[j].y, hs[j].z, hs[j].w};
+    const uint32_t aw[4] = {as[j].x, as[j].y, as[j].z, as[j].w};
+    uint32_t vw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = f32_to_bf16(bf16_to_f32(hw[e] & 0xFFFFu) + bf16_to_f32(aw[e] & 0xFFFFu));
-      const uint32_t hi = f32_to_bf16(bf16_to_f32(hw[e] >> 16) + bf16_to_f32(aw[e] >> 16));
-      vw[4 * i + e] = lo | (hi << 16);
-      const float a = bf16_to_f32(lo), b = bf16_to_f32(hi);
-      ss += a * a + b * b;
+      vw[e] = f32x2_to_bf16x2(bf16_to_f32(hw[e] & 0xFFFFu) + bf16_to_f32(aw[e] & 0xFFFFu),
+                              bf16_to_f32(hw[e] >> 16) + bf16_to_f32(aw[e] >> 16));
+      const float a = bf16_to_f32(vw[e] & 0xFFFFu), b = bf16_to_f32(vw[e] >> 16);
+      ss += mine ? a * a + b * b : 0.f;
     }
+    v[j] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
   }
-  ss = group_sum<64>(mine ? ss : 0.f);
+  ss = group_sum<64>(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += red[w];
   const float r = rsqrtf(tot * (1.0f / (float)(nchunks * kChunkCols)) + eps);
-  if (blockIdx.x == 0 && mine && h_out) {
-    uint4* dst = reinterpret_cast<uint4*>(h_out) + threadIdx.x * 4;
+  uint4* dst = reinterpret_cast<uint4*>(xlds);
+  float* bias = reinterpret_cast<float*>(xlds + nchunks * 16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(vw[4 * i], vw[4 * i + 1], vw[4 * i + 2], vw[4 * i + 3]);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t ww[4] = {xw[i].x, xw[i].y, xw[i].z, xw[i].w};
-    uint32_t o[4];
+  for (int j = 0; j < UPT; ++j) {
+    const int u = (int)(threadIdx.x + j * blockDim.x);
+    const bool mine = u < nunits;
+    const uint32_t vw[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    const uint32_t ww[4] = {ws[j].x, ws[j].y, ws[j].z, ws[j].w};
+    uint32_t xw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t v = vw[4 * i + e];
-      const uint32_t lo = f32_to_bf16(bf16_to_f32(ww[e] & 0xFFFFu) *
-                                      bf16_to_f32(f32_to_bf16(bf16_to_f32(v & 0xFFFFu) * r)));
-      const uint32_t hi = f32_to_bf16(bf16_to_f32(ww[e] >> 16) *
-                                      bf16_to_f32(f32_to_bf16(bf16_to_f32(v >> 16) * r)));
-      o[e] = lo | (hi << 16);
+      const uint32_t t = f32x2_to_bf16x2(bf16_to_f32(vw[e] & 0xFFFFu) * r,
+                                         bf16_to_f32(vw[e] >> 16) * r);
+      xw[e] = f32x2_to_bf16x2(bf16_to_f32(ww[e] & 0xFFFFu) * bf16_to_f32(t & 0xFFFFu),
+                              bf16_to_f32(ww[e] >> 16) * bf16_to_f32(t >> 16));
     }
-    xs[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    if (blockIdx.x == 0 && mine) {
+      if (h_out) reinterpret_cast<uint4*>(h_out)[u] = v[j];
+      if (x_out) reinterpret_cast<uint4*>(x_out)[u] = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+    }
+    uint32_t p[4];
+    make_xpairs(xw[0], xw[1], xw[2], xw[3], p);
+    // this word's sum in the order of pairs_of, then the chunk's four words'
+    // sums added in word order on the chunk's first lane
+    const float part = bf16_to_f32(xw[0] & 0xFFFFu) + bf16_to_f32(xw[0] >> 16) +
+                       bf16_to_f32(xw[1] & 0xFFFFu) + bf16_to_f32(xw[1] >> 16) +
+                       bf16_to_f32(xw[2] & 0xFFFFu) + bf16_to_f32(xw[2] >> 16) +
+                       bf16_to_f32(xw[3] & 0xFFFFu) + bf16_to_f32(xw[3] >> 16);
+    const float p1 = dpp_mov<0x55>(part);  // quad_perm [1,1,1,1]
+    const float p2 = dpp_mov<0xAA>(part);  // quad_perm [2,2,2,2]
+    const float p3 = dpp_mov<0xFF>(part);  // quad_perm [3,3,3,3]
+    if (mine) {
+      const int c = u >> 2, i = u & 3;
+      dst[((c / LPR) * 4 + i) * LPR + c % LPR] = make_uint4(p[0], p[1], p[2], p[3]);
+      if (i == 0) {
+        float s = 0.f;
+        s += part;
+        s += p1;
+        s += p2;
+        s += p3;
+        bias[c] = -kPairBias * s;
+      }
+    }
   }
-  if (blockIdx.x == 0 && mine && x_out) {
-    uint4* dst = reinterpret_cast<uint4*>(x_out) + threadIdx.x * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = xs[i];
-  }
+  __syncthreads();
 }
 
 // Lane l's CH chunks of staged pairs and biases, into VGPRs.
