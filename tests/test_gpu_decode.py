@@ -224,6 +224,51 @@ def test_int4_gemv_rmsnorm(K, rows, cols):
         K.int4_gemv_rmsnorm(dev(qw), dev_bf16(sc), h, add, w, 1e-6, h_out=h)
 
 
+@pytest.mark.parametrize("cols", [5120, 4096, 2560])
+def test_int4_gemv_rmsnorm_special_values(K, cols):
+    """The folded RMSNorm's roundings (one v_cvt_pk_bf16_f32 per pair) on
+    special values: the residual bf16(h + add) it writes equals torch's bit
+    for bit with signed zeros, cancellation, subnormals and the largest
+    finite values, where the output stays within the GEMV bars; and with
+    +-inf and NaN inputs (NaN becomes 0x7FC0), where every output is NaN."""
+    import dip_oracle as O
+    from gpu_util import dev, dev_bf16, host_bf16, random_int4, rel_err
+    print(f"int4_gemv_rmsnorm special values cols={cols}", flush=True)
+    rng = np.random.default_rng(cols + 1)
+    rows = 64
+    qw, sc = random_int4(rng, rows, cols)
+    g = torch.Generator(device="cuda").manual_seed(cols + 1)
+    h = (torch.randn(cols, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    add = torch.randn(cols, device="cuda", generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(cols, device="cuda", generator=g)).to(torch.bfloat16)
+    # (h, add) bit pairs: +-0, subnormal sums, the smallest normal, a large
+    # value (its square still finite), cancellation to +0, 1 + tiny (ties and
+    # rounding)
+    pairs = [(0x0000, 0x8000), (0x8000, 0x8000), (0x0001, 0x0001), (0x807F, 0x0001),
+             (0x0080, 0x8001), (0x5F00, 0x0000), (0x4040, 0xC040), (0x3F80, 0x3381),
+             (0xBF81, 0x3381), (0x3F80, 0x3B80)]
+    hb, ab = h.view(torch.int16), add.view(torch.int16)
+    for i, (x, y) in enumerate(pairs):
+        hb[37 * i + 5] = x - 65536 if x > 32767 else x
+        ab[37 * i + 5] = y - 65536 if y > 32767 else y
+    h_out = torch.full_like(h, 7.0)
+    out = K.int4_gemv_rmsnorm(dev(qw), dev_bf16(sc), h, add, w, 1e-6, h_out=h_out)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(h_out), _bits(h + add))
+    ref = O.gemv_f64(qw, sc, _bits(_hf_rmsnorm(h + add, w, 1e-6)))
+    assert rel_err(host_bf16(out), ref) < 1e-2
+    # non-finite residuals: +-inf, inf - inf, and a NaN with a payload
+    for i, (x, y) in enumerate([(0x7F80, 0x3F80), (0xFF80, 0x0000), (0x7F80, 0xFF80),
+                                (0x7FC1, 0x3F80), (0xFFC0, 0x0000)]):
+        hb[41 * i + 3] = x - 65536 if x > 32767 else x
+        ab[41 * i + 3] = y - 65536 if y > 32767 else y
+    out = K.int4_gemv_rmsnorm(dev(qw), dev_bf16(sc), h, add, w, 1e-6, h_out=h_out)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(h_out), _bits(h + add))
+    assert 0x7FC0 in set(_bits(h_out).tolist())
+    assert torch.isnan(out.float()).all()
+
+
 def test_decode_attention_rejects_bad_arguments(K):
     q = torch.zeros(3 * 128, dtype=torch.bfloat16, device="cuda")
     kc = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device="cuda")
