@@ -259,10 +259,11 @@ void launch_tokens(const int8_t* qw, const uint16_t* sc, const uint16_t* x, uint
 //     (the K ranges of a split are added by int4_gemm_t_reduce_kernel, in
 //     a fixed order);
 //   * per 128-row step the 256 threads read 128 rows x 32 bytes of nibbles
-//     (thread t: row t / 2, 32 columns) and their scales, and write the
-//     dequantised values transposed into LDS [column][k] (double-buffered,
-//     one barrier per step); nibbles and scales run kGemmTPrefetch steps
-//     ahead in registers;
+//     (thread t: rows 2 (t / 4) and 2 (t / 4) + 1, 16 columns) and their
+//     scales, and write the dequantised values transposed into LDS
+//     [column][k], one 32-bit word (the two rows) per column: each pair is
+//     one v_cvt_pk_bf16_f32 (double-buffered, one barrier per step);
+//     nibbles and scales run kGemmTPrefetch steps ahead in registers;
 //   * wave w reads A = 16 columns x 8 consecutive k (one 16-byte LDS read
 //     per slice) and B = x[token][k .. k + 7] straight from L2, and
 //     accumulates on v_mfma_f32_16x16x32_bf16.
@@ -284,29 +285,46 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_t_kernel(
   const int nsteps = (k1 - k0 + kGemmTStep - 1) / kGemmTStep;
   const int ngroups_n = N >> 7;
 
-  // staging role: row r of the step, columns n0 + 32 c .. + 31
-  const int sr = threadIdx.x >> 1, scol = 32 * (threadIdx.x & 1);
+  // staging role: rows sr, sr + 1 of the step, columns n0 + scol .. + 15
+  const int sr = 2 * (threadIdx.x >> 2), scol = 16 * (threadIdx.x & 3);
   const bool col_ok = n0 + scol < N;
-  auto load_w = [&](int step, uint4& wv, uint32_t& s) {
+  struct WPair {
+    uint2 w0, w1;   // 16 nibbles of each row
+    uint32_t s01;   // the two rows' scales (row sr low)
+  };
+  auto load_w = [&](int step, WPair& wp) {
     const int row = k0 + step * kGemmTStep + sr;
+    const size_t off = (size_t)((n0 + scol) >> 1);
+    const int g = (n0 + scol) >> 7;
+    wp.w0 = make_uint2(0, 0);
+    wp.w1 = make_uint2(0, 0);
+    wp.s01 = 0u;
     if (row < k1 && col_ok) {
-      wv = *reinterpret_cast<const uint4*>(qw + (size_t)row * (N >> 1) + ((n0 + scol) >> 1));
-      s = sc[(size_t)row * ngroups_n + ((n0 + scol) >> 7)];
-    } else {
-      wv = make_uint4(0, 0, 0, 0);
-      s = 0u;
+      wp.w0 = *reinterpret_cast<const uint2*>(qw + (size_t)row * (N >> 1) + off);
+      wp.s01 = sc[(size_t)row * ngroups_n + g];
+    }
+    if (row + 1 < k1 && col_ok) {
+      wp.w1 = *reinterpret_cast<const uint2*>(qw + (size_t)(row + 1) * (N >> 1) + off);
+      wp.s01 |= (uint32_t)sc[(size_t)(row + 1) * ngroups_n + g] << 16;
     }
   };
-  auto stage = [&](int buf, const uint4& wv, uint32_t s) {
-    const float sf = bf16_to_f32(s);
-    const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+  // bf16(q * s) of both rows for each of the 16 columns, as one word per
+  // column: the signed nibble is one bit-field extract, and the pair of
+  // roundings one f32x2_to_bf16x2 (f32_to_bf16's bits, NaN included).
+  auto stage = [&](int buf, const WPair& wp) {
+    const float s0 = bf16_to_f32(wp.s01 & 0xFFFFu), s1 = bf16_to_f32(wp.s01 >> 16);
+    const uint32_t a4[2] = {wp.w0.x, wp.w0.y}, b4[2] = {wp.w1.x, wp.w1.y};
+    // word k/2 of column c sits at (k/2) ^ (16 * ((c / 16) & 3)): the four
+    // 16-column groups written by one instruction land in different banks
+    uint32_t* dst = reinterpret_cast<uint32_t*>(&wt[buf][scol][0]) + ((sr >> 1) ^ (scol & 48));
+    constexpr int kColWords = kGemmTStride / 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
-        const int q = (int)((w4[i] >> (4 * b)) & 0xFu);
-        const float v = (float)(q - ((q & 8) << 1)) * sf;
-        wt[buf][scol + 8 * i + b][sr] = (uint16_t)f32_to_bf16(v);
+        const float va = (float)(int)__builtin_amdgcn_sbfe(a4[i], 4 * b, 4) * s0;
+        const float vb = (float)(int)__builtin_amdgcn_sbfe(b4[i], 4 * b, 4) * s1;
+        dst[(8 * i + b) * kColWords] = f32x2_to_bf16x2(va, vb);
       }
     }
   };
@@ -332,17 +350,16 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_t_kernel(
   [[maybe_unused]] uint4 xc[kGemmTStep / 32][TM];
   if constexpr (kXAhead) load_x(0, xc);
 
-  uint4 wq[kGemmTPrefetch];
-  uint32_t sq[kGemmTPrefetch];
+  WPair wq[kGemmTPrefetch];
 #pragma unroll
   for (int p = 0; p < kGemmTPrefetch; ++p) {
-    if (p < nsteps) load_w(p, wq[p], sq[p]);
+    if (p < nsteps) load_w(p, wq[p]);
   }
   floatx4 acc[TM];
 #pragma unroll
   for (int t = 0; t < TM; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-  if (nsteps > 0) stage(0, wq[0], sq[0]);
-  if (kGemmTPrefetch < nsteps) load_w(kGemmTPrefetch, wq[0], sq[0]);
+  if (nsteps > 0) stage(0, wq[0]);
+  if (kGemmTPrefetch < nsteps) load_w(kGemmTPrefetch, wq[0]);
   __syncthreads();
 
   for (int i0 = 0; i0 < nsteps; i0 += kGemmTPrefetch) {
@@ -354,8 +371,8 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_t_kernel(
         // stage step i + 1 into the other buffer while this one is read
         if (i + 1 < nsteps) {
           const int pn = (p + 1) % kGemmTPrefetch;
-          stage(buf ^ 1, wq[pn], sq[pn]);
-          if (i + 1 + kGemmTPrefetch < nsteps) load_w(i + 1 + kGemmTPrefetch, wq[pn], sq[pn]);
+          stage(buf ^ 1, wq[pn]);
+          if (i + 1 + kGemmTPrefetch < nsteps) load_w(i + 1 + kGemmTPrefetch, wq[pn]);
         }
         if constexpr (kXAhead) {
           // the next step's x operands, in flight while this step multiplies
@@ -364,7 +381,7 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_t_kernel(
 #pragma unroll
           for (int j = 0; j < kGemmTStep / 32; ++j) {
             const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(
-                &wt[buf][16 * wave + l16][32 * j + 8 * kb]);
+                &wt[buf][16 * wave + l16][(32 * j + 8 * kb) ^ (32 * (wave & 3))]);
 #pragma unroll
             for (int t = 0; t < TM; ++t)
               acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(xc[j][t]), acc[t], 0,
@@ -379,7 +396,7 @@ __global__ __launch_bounds__(kGemmThreads) void int4_gemm_t_kernel(
 #pragma unroll
           for (int j = 0; j < kGemmTStep / 32; ++j) {
             const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(
-                &wt[buf][16 * wave + l16][32 * j + 8 * kb]);
+                &wt[buf][16 * wave + l16][(32 * j + 8 * kb) ^ (32 * (wave & 3))]);
             const int kk = kbase + 32 * j + 8 * kb;
 #pragma unroll
             for (int t = 0; t < TM; ++t) {

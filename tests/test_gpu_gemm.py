@@ -103,3 +103,33 @@ def test_int4_gemm_t_matches_dense_route(K, m):
     got = K.int4_gemm_t(qw, sc, h).float()
     ref = (h @ dequantize(qw, sc)).float()
     assert float((got - ref).abs().max() / ref.abs().max()) < 1e-2
+
+
+@pytest.mark.parametrize("m,k,n", [(7, 25600, 5120), (32, 25600, 5120), (64, 1000, 256),
+                                   (20, 3072, 2560)])
+def test_int4_gemm_t_weights_bit_exact(K, m, k, n):
+    """Token t is one-hot at row r_t, so out[t] is row r_t of the staged
+    weights (one nonzero product per sum): equal, bit for bit, to the
+    reference's bf16(q*s) row.  Scales span 2^-100 .. 2^100 with both signs
+    and random significands, so q*s needs rounding and every exponent path
+    of the conversion runs; the rows cover both rows of a staged pair, step
+    and K-split edges, and the last row."""
+    print(f"int4_gemm_t one-hot m={m} k={k} n={n}", flush=True)
+    rng = np.random.default_rng(k + m)
+    q = rng.integers(-8, 8, size=(k, n)).astype(np.int8)
+    mant = rng.random((k, n // 128), dtype=np.float32) + 1.0
+    expo = rng.integers(-100, 101, size=(k, n // 128)).astype(np.float32)
+    sign = np.where(rng.random((k, n // 128)) < 0.5, -1.0, 1.0).astype(np.float32)
+    sc = O.f32_to_bf16((sign * np.ldexp(mant, expo.astype(np.int32))).astype(np.float32))
+    qw = O.pack_int4(q)
+    edges = [0, 1, 126, 127, 128, 129, k - 2, k - 1]
+    rows = (edges + list(rng.integers(0, k, size=m)))[:m]
+    x = np.zeros((m, k), dtype=np.uint16)
+    x[np.arange(m), rows] = 0x3F80  # bf16 1.0
+    out = host_bf16(K.int4_gemm_t(dev(qw), dev_bf16(sc), dev_bf16(x)))
+    want = O.dequantize(qw, sc)[rows]
+    got_f, want_f = O.bf16_to_f32(out), O.bf16_to_f32(want)
+    # +0 and -0 both sum to +0 in fp32, so zeros are compared by value
+    assert np.array_equal(got_f, want_f)
+    nz = want_f != 0
+    assert np.array_equal(out[nz], want[nz])
