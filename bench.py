@@ -480,6 +480,85 @@ def read_ceiling(args) -> int:
     return 0
 
 
+def timeline(args) -> int:
+    """One layer's timeline from the timeline build of the library
+    (libdip_hip_timeline.so, per-workgroup wall-clock stamps in the decode
+    step's four kernels): the stack decodes `steps` tokens from its captured
+    graph, then the last layer's records give each kernel's first and last
+    workgroup start, the spread of workgroup ends and the gaps between the
+    kernels, in microseconds from the gate's first workgroup start, next to
+    the layer period (token time / layers).  Prints its own JSON line."""
+    import numpy as np
+    lib_path = ROOT / "dynamic-input-pruning_amd" / "libdip_hip_timeline.so"
+    if not lib_path.exists():
+        print(f"{lib_path} is not built; run __graft_entry__.build()", file=sys.stderr)
+        return 2
+    os.environ["DIP_HIP_LIB"] = str(lib_path)
+    import torch
+    import _dip_hip as K
+    from dip_stack import SHAPES, DIPStack
+
+    dev = torch.device("cuda:0")
+    shape = dict(SHAPES[args.shape])
+    if args.layers:
+        shape["layers"] = args.layers
+    print(f"[bench] timeline build, {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
+          flush=True)
+    stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    xs = (torch.randn(args.warmup + args.steps, stack.hidden, device=dev, generator=gen)
+          .to(torch.bfloat16))
+    stack.capture()
+    for i in range(args.warmup):
+        stack.step(xs[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.warmup, args.warmup + args.steps):
+        stack.step(xs[i])
+    e1.record()
+    torch.cuda.synchronize()
+    ms_token = e0.elapsed_time(e1) / args.steps
+    period = ms_token * 1e3 / stack.layers
+
+    recs = {name: K.timeline_read(name) for name in K.TIMELINE_KERNELS}
+    t0 = int(recs["gate"][0].min())
+    us = lambda v: round((float(v) - t0) * 0.01, 2)
+    kernels = {}
+    for name, (start, end, xcc) in recs.items():
+        wg_end = np.where(end >= start[:, None], end, 0).max(axis=1)
+        done = wg_end > 0  # workgroups whose waves reached the end (not padding tiles)
+        ends = wg_end[done]
+        kernels[name] = {
+            "workgroups": int(len(start)), "finished": int(done.sum()),
+            "first_start": us(start.min()), "last_start": us(start.max()),
+            "first_end": us(ends.min()), "end_p10": us(np.percentile(ends, 10)),
+            "end_p50": us(np.percentile(ends, 50)), "end_p90": us(np.percentile(ends, 90)),
+            "last_end": us(ends.max()),
+            "end_mean_by_xcc": {int(x): us(ends[xcc[done] == x].mean())
+                                for x in sorted(set(xcc[done].tolist()))},
+        }
+    order = list(K.TIMELINE_KERNELS)
+    gaps = {f"{a}->{b}": round(kernels[b]["first_start"] - kernels[a]["last_end"], 2)
+            for a, b in zip(order, order[1:])}
+    spans = {n: round(k["last_end"] - k["first_start"], 2) for n, k in kernels.items()}
+    out = {
+        "metric": "one decode layer's timeline (per-workgroup wall-clock stamps)",
+        "unit": "us", "shape": args.shape, "layers": stack.layers, "keep": args.keep,
+        "steps": args.steps, "ms_per_token": round(ms_token, 5), "layer_period_us": round(period, 2),
+        "layer_span_us": kernels[order[-1]]["last_end"],
+        # the launch gap to the next layer's gate, with the per-token graph
+        # launch and input copy spread over the layers (and this layer's own
+        # deviation from the average layer)
+        "rest_of_period_us": round(period - kernels[order[-1]]["last_end"], 2),
+        "span_us": spans, "gap_us": gaps, "kernels": kernels,
+        "note": "timeline build (stamps add a few stores per workgroup); the last layer of the "
+                "last token; microseconds from the gate's first workgroup start",
+    }
+    print(json.dumps(out))
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -519,6 +598,10 @@ def main(argv=None):
                     help="instead of the decode step, sweep the read bandwidth of the step's "
                          "access patterns with the probe kernels of libdip_probe.so; prints its "
                          "own JSON line")
+    ap.add_argument("--timeline", action="store_true",
+                    help="instead of the bench line, decode with the timeline build of the "
+                         "library (libdip_hip_timeline.so) and print one layer's per-kernel "
+                         "workgroup start/end times and the gaps between the kernels")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the timed run, copy a buffer of this many MiB device to device "
                          "(the reference transfer for scaling HBM byte counters)")
@@ -531,6 +614,8 @@ def main(argv=None):
 
     if args.ceiling:
         return read_ceiling(args)
+    if args.timeline:
+        return timeline(args)
     if args.whole_model:
         return whole_model(args)
     if args.ca is not None:

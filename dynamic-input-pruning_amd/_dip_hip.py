@@ -87,6 +87,7 @@ _SIGS = {
     "dip_decode_attention": ([_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _sz,
                               _p], _i32),
     "dip_set_tuning": ([_i32, _i32], _i32),
+    "dip_timeline_read": ([_i32, _p], _i32),
     "dip_get_tuning": ([_i32], _i32),
 }
 for _name, (_args, _res) in _SIGS.items():
@@ -97,7 +98,7 @@ for _name, (_args, _res) in _SIGS.items():
 # The argument lists above follow this version of include/dip_hip.h
 # (DIP_VERSION); a library built from another one would be called with
 # shifted arguments, so it is refused here.
-ABI_VERSION = 300
+ABI_VERSION = 301
 if lib.dip_version() != ABI_VERSION:
     raise ImportError(f"{LIB_PATH} reports ABI version {lib.dip_version()}, these bindings "
                       f"are written for {ABI_VERSION}; rebuild the library")
@@ -797,6 +798,29 @@ def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res
 
 
 TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2}
+
+
+TIMELINE_KERNELS = {"gate": 0, "topk_spec_up": 1, "down_partials": 2, "down_reduce": 3}
+STAMP_BLOCKS, STAMP_WAVES = 2048, 16
+
+
+def timeline_read(kernel: str):
+    """The last launch's per-workgroup stamps of one decode kernel (the
+    timeline build of the library only; dip_timeline_read): (start [blocks],
+    end [blocks, waves], xcc [blocks]) as numpy arrays in s_memrealtime ticks
+    (100 MHz), end entries older than their workgroup's start being waves that
+    did not reach the end of this launch."""
+    import numpy as np
+    buf = np.zeros(STAMP_BLOCKS + STAMP_BLOCKS * STAMP_WAVES + STAMP_BLOCKS // 2 + 1,
+                   dtype=np.uint64)
+    _check(lib.dip_timeline_read(TIMELINE_KERNELS[kernel], buf.ctypes.data), "dip_timeline_read")
+    start = buf[:STAMP_BLOCKS].astype(np.int64)
+    end = buf[STAMP_BLOCKS:STAMP_BLOCKS * (1 + STAMP_WAVES)].astype(np.int64).reshape(
+        STAMP_BLOCKS, STAMP_WAVES)
+    tail = buf[STAMP_BLOCKS * (1 + STAMP_WAVES):].view(np.uint32)
+    xcc = tail[:STAMP_BLOCKS].astype(np.int64)
+    blocks = int(min(tail[STAMP_BLOCKS], STAMP_BLOCKS))
+    return start[:blocks], end[:blocks], xcc[:blocks]
 
 
 def set_tuning(name: str, value: int) -> None:

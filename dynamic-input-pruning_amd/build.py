@@ -6,7 +6,10 @@ Each csrc/*.hip file is compiled to an object under _build/ (in parallel),
 then linked into libdip_hip.so next to this file.  The library is what the
 Python modules in this directory load; it is rebuilt every time this runs.
 csrc/probe/*.hip (the bench's read-ceiling probes, no part of the decode
-path) is linked into a library of its own, libdip_probe.so.
+path) is linked into a library of its own, libdip_probe.so.  The decode
+sources are built a second time with DIP_WG_STAMPS into
+libdip_hip_timeline.so, whose decode kernels record per-workgroup timeline
+stamps (dip_timeline_read; `bench.py --timeline`).
 """
 from __future__ import annotations
 
@@ -21,6 +24,8 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libdip_hip.so"
 PROBE_LIB = HERE / "libdip_probe.so"
+# the same sources with per-workgroup timeline stamps (dip_timeline_read)
+TIMELINE_LIB = HERE / "libdip_hip_timeline.so"
 ARCH = os.environ.get("DIP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -62,22 +67,28 @@ def build(verbose: bool = False) -> Path:
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
 
-    def compile_one(src: Path) -> Path:
-        obj = BUILD / (src.parent.name + "_" + src.stem + ".o")
-        cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    def compile_one(job) -> Path:
+        src, timeline = job
+        tag = "tl_" if timeline else ""
+        obj = BUILD / (tag + src.parent.name + "_" + src.stem + ".o")
+        cmd = [HIPCC, *COMMON, *(["-DDIP_WG_STAMPS"] if timeline else []), "-c", str(src), "-o",
+               str(obj)]
         msg = _run(cmd)
         if verbose and msg:
             print(msg, file=sys.stderr)
         return obj
 
-    jobs = min(len(sources) + len(probes), max(1, min(16, os.cpu_count() or 1)))
+    jobs_list = [(p, False) for p in sources + probes] + [(p, True) for p in sources]
+    jobs = min(len(jobs_list), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(compile_one, sources + probes))
-    _link(objs[:len(sources)], LIB)
+        objs = list(pool.map(compile_one, jobs_list))
+    n, m = len(sources), len(sources) + len(probes)
+    _link(objs[:n], LIB)
     if probes:
-        _link(objs[len(sources):], PROBE_LIB)
+        _link(objs[n:m], PROBE_LIB)
+    _link(objs[m:], TIMELINE_LIB)
     if verbose:
-        print(f"built {LIB}" + (f" and {PROBE_LIB}" if probes else ""))
+        print(f"built {LIB}" + (f", {PROBE_LIB}" if probes else "") + f" and {TIMELINE_LIB}")
     return LIB
 
 

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/dip_hip.h"
+
 #define DIP_DEV __device__ __forceinline__
 
 namespace dip {
@@ -222,6 +224,31 @@ DIP_DEV uint32_t wave_prefix(uint32_t v) {
 }
 
 DIP_DEV uint32_t lane63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
+
+// Layer timeline stamps (the timeline build only, DIP_WG_STAMPS; the record
+// layout is dip_wg_stamps of dip_hip.h): the first thread of a workgroup
+// stamps its start and XCD, lane 0 of every wave its end.
+#ifdef DIP_WG_STAMPS
+DIP_DEV void stamp_start(dip_wg_stamps* s) {
+  if (blockIdx.x < DIP_STAMP_BLOCKS && threadIdx.x == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    s->start[blockIdx.x] = wall_clock64();
+    s->xcc[blockIdx.x] = xcc;
+    if (blockIdx.x == 0) s->blocks = gridDim.x;
+  }
+}
+DIP_DEV void stamp_end(dip_wg_stamps* s) {
+  if (blockIdx.x < DIP_STAMP_BLOCKS && (threadIdx.x & 63) == 0 &&
+      (threadIdx.x >> 6) < DIP_STAMP_WAVES)
+    s->end[blockIdx.x][threadIdx.x >> 6] = wall_clock64();
+}
+#define DIP_STAMP_START(sym) ::dip::stamp_start(&(sym))
+#define DIP_STAMP_END(sym) ::dip::stamp_end(&(sym))
+#else
+#define DIP_STAMP_START(sym) ((void)0)
+#define DIP_STAMP_END(sym) ((void)0)
+#endif
 
 // 128-bit streaming load (weights are read once per call: non-temporal).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));

@@ -44,6 +44,19 @@ constexpr int kRedOut = 32;              // outputs per reduce block
 constexpr int kRedSplit = 8;             // interleaved row-block splits per output
 }  // namespace
 
+#ifdef DIP_WG_STAMPS
+__device__ dip_wg_stamps g_stamps_down;
+__device__ dip_wg_stamps g_stamps_reduce;
+int timeline_read_down(int reduce, dip_wg_stamps* dst) {
+  return reduce ? hip_status(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps_reduce),
+                                                 sizeof(dip_wg_stamps), 0, hipMemcpyDeviceToHost))
+                : hip_status(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps_down),
+                                                 sizeof(dip_wg_stamps), 0, hipMemcpyDeviceToHost));
+}
+#else
+int timeline_read_down(int, dip_wg_stamps*) { return DIP_ERR_UNSUPPORTED; }
+#endif
+
 // OFF32 (one matrix below 4 GiB): the exchange carries each row's 32-bit
 // byte offset instead of its id, and the row loads add it to the matrix's
 // base in a scalar register (one VGPR per address, no 64-bit multiply).
@@ -160,6 +173,7 @@ struct DownGmArgs {
 };
 
 __global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
+  DIP_STAMP_START(g_stamps_down);
   constexpr int LPR = 8, kSlots = kThreads / LPR, kCols = LPR * kDownAcc, kWaves = kThreads / 64;
   __shared__ __align__(16) float red[down_red_floats<LPR>()];
   __shared__ __align__(16) uint32_t xoff[kWaves][64];
@@ -208,6 +222,7 @@ __global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
   for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
   down_accumulate<LPR>(ring, f, acc);
   down_block_partial<LPR>(acc, red, a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols);
+  DIP_STAMP_END(g_stamps_down);
 }
 
 // y[o] = bf16(sum over row blocks rb of partial[rb][o]), rb ascending in
@@ -218,6 +233,7 @@ template <int NB>
 __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
     const float* __restrict__ partial, int row_blocks, int out_features, uint16_t* __restrict__ y) {
   __shared__ float part[kRedSplit][kRedOut];
+  DIP_STAMP_START(g_stamps_reduce);
   const int oo = threadIdx.x % kRedOut;
   const int p = threadIdx.x / kRedOut;
   const int o = min(blockIdx.x * kRedOut + oo, out_features - 1);
@@ -240,6 +256,7 @@ __global__ __launch_bounds__(kRedOut * kRedSplit) void down_reduce_kernel(
     for (int q = 1; q < kRedSplit; ++q) t += part[q][oo];
     y[blockIdx.x * kRedOut + oo] = (uint16_t)f32_to_bf16(t);
   }
+  DIP_STAMP_END(g_stamps_reduce);
 }
 
 // k == 0: y = bf16(0).

@@ -153,6 +153,11 @@ int launch_topk_spec(const uint16_t* g, int64_t n, int64_t k, int32_t* idx, void
                      SpecArgs sp, hipStream_t stream);
 
 
+// Layer timeline records (the timeline build; DIP_ERR_UNSUPPORTED otherwise).
+int timeline_read_rowdot(dip_wg_stamps* dst);
+int timeline_read_topk(dip_wg_stamps* dst);
+int timeline_read_down(int reduce, dip_wg_stamps* dst);
+
 // Launch tuning (process-wide, host side): see DIP_TUNE_* in dip_hip.h.
 int tuning(int knob);
 // Compute units of the current device (cached per device).

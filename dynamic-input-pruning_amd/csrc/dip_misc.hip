@@ -150,6 +150,20 @@ extern "C" const char* dip_status_string(int status) {
 
 extern "C" int dip_version(void) { return DIP_VERSION; }
 
+extern "C" int dip_timeline_read(int kernel, dip_wg_stamps* dst) {
+  if (!dst) return DIP_ERR_NULL;
+  if (kernel < DIP_STAMP_GATE || kernel > DIP_STAMP_REDUCE) return DIP_ERR_ARG;
+#ifdef DIP_WG_STAMPS
+  if (hipDeviceSynchronize() != hipSuccess) return hip_status(hipGetLastError());
+#endif
+  switch (kernel) {
+    case DIP_STAMP_GATE: return timeline_read_rowdot(dst);
+    case DIP_STAMP_TOPK: return timeline_read_topk(dst);
+    case DIP_STAMP_DOWN: return timeline_read_down(0, dst);
+    default: return timeline_read_down(1, dst);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------

@@ -26,11 +26,22 @@
 
 namespace dip {
 
+#ifdef DIP_WG_STAMPS
+__device__ dip_wg_stamps g_stamps_rowdot;
+int timeline_read_rowdot(dip_wg_stamps* dst) {
+  return hip_status(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps_rowdot), sizeof(dip_wg_stamps), 0,
+                                        hipMemcpyDeviceToHost));
+}
+#else
+int timeline_read_rowdot(dip_wg_stamps*) { return DIP_ERR_UNSUPPORTED; }
+#endif
+
 constexpr int kRowdotMaxThreads = 256;
 
 template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
 __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a) {
   static_assert(!NORM || XS, "the RMSNorm prologue needs the staged x");
+  DIP_STAMP_START(g_stamps_rowdot);
   constexpr int D = ROWS < 2 ? ROWS : 2;  // rows of loads in flight per group
   static_assert(ROWS <= LPR, "rows per group");
   extern __shared__ __align__(16) uint32_t xlds[];
@@ -146,6 +157,7 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
     a.out[(int)jl] = (uint16_t)v;
   }
   if (rot) a.rotate[0] = rot1;
+  DIP_STAMP_END(g_stamps_rowdot);
 }
 
 // ---------------------------------------------------------------------------

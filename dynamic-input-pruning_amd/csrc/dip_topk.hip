@@ -585,16 +585,28 @@ __global__ __launch_bounds__(kThreads) void topk_select_kernel(
 // Top-k + speculative up rows in one launch: workgroups [0, sp.ntopk) run
 // the select (and the residual rows), the rest compute h for the channels at
 // or above the speculation key.  No workgroup waits for another.
+#ifdef DIP_WG_STAMPS
+__device__ dip_wg_stamps g_stamps_topk;
+int timeline_read_topk(dip_wg_stamps* dst) {
+  return hip_status(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps_topk), sizeof(dip_wg_stamps), 0,
+                                        hipMemcpyDeviceToHost));
+}
+#else
+int timeline_read_topk(dip_wg_stamps*) { return DIP_ERR_UNSUPPORTED; }
+#endif
+
 template <int R, int LPR, int CH>
 __global__ __launch_bounds__(kThreads) void topk_spec_kernel(
     const uint16_t* __restrict__ s, int n, int k, int32_t* __restrict__ idx,
     TopkMeta* __restrict__ meta, int stamps, SpecArgs sp) {
   extern __shared__ __align__(16) uint32_t lds[];  // 128-bit LDS accesses: keep aligned
+  DIP_STAMP_START(g_stamps_topk);
   if ((int)blockIdx.x < sp.ntopk)
     topk_body<R, kSelSpec, LPR, CH>(s, n, k, idx, meta, stamps, sp.ntopk, sp, lds);
   else
     spec_rows<LPR, CH>(s, n, sp, (int)blockIdx.x - sp.ntopk, lds, meta, stamps,
                        (int)gridDim.x - sp.ntopk);
+  DIP_STAMP_END(g_stamps_topk);
 }
 
 int launch_topk_select(const uint16_t* s, int64_t n, int64_t k, int32_t* idx, void* ws,

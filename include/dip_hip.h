@@ -52,11 +52,12 @@ const char* dip_status_string(int status);
  * Library version as an integer (major * 10000 + minor * 100 + patch).  The
  * minor number changes whenever an entry point's argument list changes, so
  * a binding written against this header checks dip_version() == DIP_VERSION
- * before its first call.  0.3.0: the measurement probes and the
- * DIP_TUNE_STEP knob are gone; 0.2.0 added down_t_sc_gm to the decode and
- * gather-down entry points and g_len to dip_ca_fused_gemv.
+ * before its first call.  0.3.1 adds dip_timeline_read.  0.3.0: the
+ * measurement probes and the DIP_TUNE_STEP knob are gone; 0.2.0 added
+ * down_t_sc_gm to the decode and gather-down entry points and g_len to
+ * dip_ca_fused_gemv.
  */
-#define DIP_VERSION 300
+#define DIP_VERSION 301
 int dip_version(void);
 
 /* Highest row count the top-k supports (its keys are staged in LDS). */
@@ -159,6 +160,36 @@ enum {
 };
 int dip_set_tuning(int knob, int value);
 int dip_get_tuning(int knob);
+
+/*
+ * Layer timeline (diagnostics, no counterpart in the reference; for callers
+ * that profile the decode step).  In the timeline build of this library,
+ * libdip_hip_timeline.so (the same sources compiled with DIP_WG_STAMPS), the
+ * decode step's kernels record, per workgroup, the wall clock (s_memrealtime
+ * ticks: 100 MHz, one clock for the whole device) when the workgroup's first
+ * wave starts and when each of its waves ends, and the XCD it ran on
+ * (HW_REG_XCC_ID).  Each launch of a kernel overwrites that kernel's record;
+ * a wave that ends early (a padding tile) keeps its last launch's stamp,
+ * which is older than the workgroup's start.
+ *   DIP_STAMP_GATE    the row-dot kernel (the decode step's gate + SiLU)
+ *   DIP_STAMP_TOPK    the top-k + speculative-up launch
+ *   DIP_STAMP_DOWN    the decode step's down partials
+ *   DIP_STAMP_REDUCE  the down reduce
+ * dip_timeline_read copies a kernel's record to host memory after every
+ * queued kernel has finished (it synchronises the device).  The product
+ * build records nothing and returns DIP_ERR_UNSUPPORTED.
+ */
+enum { DIP_STAMP_GATE = 0, DIP_STAMP_TOPK = 1, DIP_STAMP_DOWN = 2, DIP_STAMP_REDUCE = 3 };
+#define DIP_STAMP_BLOCKS 2048
+#define DIP_STAMP_WAVES 16
+typedef struct {
+  uint64_t start[DIP_STAMP_BLOCKS];
+  uint64_t end[DIP_STAMP_BLOCKS][DIP_STAMP_WAVES];
+  uint32_t xcc[DIP_STAMP_BLOCKS];
+  uint32_t blocks; /* grid size of the kernel's last launch */
+  uint32_t pad;
+} dip_wg_stamps;
+int dip_timeline_read(int kernel, dip_wg_stamps* dst);
 
 /*
  * Cache-aware dual-source up GEMV: row j comes from the resident cache

@@ -297,3 +297,25 @@ def test_python_layer_rejects_host_tensors():
         K.int4_gemv(torch.zeros(8, 50, dtype=torch.int8), sc, x)
     with pytest.raises(RuntimeError, match="must be torch.bfloat16"):
         K.int4_gemv(qw, sc.float(), x)
+
+
+def test_timeline_entry_point():
+    """dip_timeline_read: the product build records nothing and says so; the
+    timeline build (libdip_hip_timeline.so, the same sources with per-workgroup
+    stamps) carries the same ABI and rejects bad arguments before any HIP
+    call."""
+    buf = np.zeros(286728 // 8, dtype=np.uint64)
+    assert ctypes.sizeof(ctypes.c_uint64) * buf.size == 2048 * 8 * 17 + 2048 * 4 + 8
+    L = K.lib
+    assert L.dip_timeline_read(0, buf.ctypes.data) == -4  # DIP_ERR_UNSUPPORTED
+    assert L.dip_timeline_read(0, None) == -1
+    assert L.dip_timeline_read(4, buf.ctypes.data) == -6
+    path = K.LIB_PATH.parent / "libdip_hip_timeline.so"
+    assert path.exists(), "the timeline build is built with the library"
+    T = ctypes.CDLL(str(path))
+    assert T.dip_version() == K.ABI_VERSION
+    for n in _declared():
+        assert hasattr(T, n), n
+    T.dip_timeline_read.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    assert T.dip_timeline_read(1, None) == -1
+    assert T.dip_timeline_read(-1, buf.ctypes.data) == -6
