@@ -521,39 +521,62 @@ def timeline(args) -> int:
     ms_token = e0.elapsed_time(e1) / args.steps
     period = ms_token * 1e3 / stack.layers
 
-    recs = {name: K.timeline_read(name) for name in K.TIMELINE_KERNELS}
-    t0 = int(recs["gate"][0].min())
-    us = lambda v: round((float(v) - t0) * 0.01, 2)
+    def layer(recs):
+        """Per-kernel statistics of one layer's records, in microseconds from
+        the gate's first workgroup start."""
+        t0 = int(recs["gate"][0].min())
+        us = lambda v: (float(v) - t0) * 0.01
+        kernels = {}
+        for name, (start, end, xcc) in recs.items():
+            if len(start) == 0:  # not launched (the in-launch reduce has no reduce kernel)
+                continue
+            wg_end = np.where(end >= start[:, None], end, 0).max(axis=1)
+            done = wg_end > 0  # workgroups whose waves reached the end (not padding tiles)
+            ends = wg_end[done]
+            kernels[name] = {
+                "workgroups": int(len(start)), "finished": int(done.sum()),
+                "first_start": us(start.min()), "last_start": us(start.max()),
+                "first_end": us(ends.min()), "end_p10": us(np.percentile(ends, 10)),
+                "end_p50": us(np.percentile(ends, 50)), "end_p90": us(np.percentile(ends, 90)),
+                "last_end": us(ends.max()),
+                "end_mean_by_xcc": {int(x): us(ends[xcc[done] == x].mean())
+                                    for x in sorted(set(xcc[done].tolist()))},
+            }
+        return kernels
+
+    # the stamps hold the last layer of the last token: 5 samples, one token
+    # replayed before each, and every figure below is the median over them
+    samples = []
+    for j in range(5):
+        stack.step(xs[(args.warmup + j) % len(xs)])
+        torch.cuda.synchronize()
+        samples.append(layer({name: K.timeline_read(name) for name in K.TIMELINE_KERNELS}))
+    med = lambda vals: round(float(np.median(vals)), 2)
     kernels = {}
-    for name, (start, end, xcc) in recs.items():
-        wg_end = np.where(end >= start[:, None], end, 0).max(axis=1)
-        done = wg_end > 0  # workgroups whose waves reached the end (not padding tiles)
-        ends = wg_end[done]
-        kernels[name] = {
-            "workgroups": int(len(start)), "finished": int(done.sum()),
-            "first_start": us(start.min()), "last_start": us(start.max()),
-            "first_end": us(ends.min()), "end_p10": us(np.percentile(ends, 10)),
-            "end_p50": us(np.percentile(ends, 50)), "end_p90": us(np.percentile(ends, 90)),
-            "last_end": us(ends.max()),
-            "end_mean_by_xcc": {int(x): us(ends[xcc[done] == x].mean())
-                                for x in sorted(set(xcc[done].tolist()))},
-        }
-    order = list(K.TIMELINE_KERNELS)
-    gaps = {f"{a}->{b}": round(kernels[b]["first_start"] - kernels[a]["last_end"], 2)
+    for name in samples[0]:
+        ks = [smp[name] for smp in samples]
+        kernels[name] = {f: (ks[0][f] if f in ("workgroups", "finished") else
+                             {x: med([k[f][x] for k in ks if x in k[f]]) for x in ks[0][f]}
+                             if f == "end_mean_by_xcc" else med([k[f] for k in ks]))
+                         for f in ks[0]}
+    order = [n for n in K.TIMELINE_KERNELS if n in kernels]
+    gaps = {f"{a}->{b}": med([smp[b]["first_start"] - smp[a]["last_end"] for smp in samples])
             for a, b in zip(order, order[1:])}
-    spans = {n: round(k["last_end"] - k["first_start"], 2) for n, k in kernels.items()}
+    spans = {n: med([smp[n]["last_end"] - smp[n]["first_start"] for smp in samples])
+             for n in order}
+    span = med([smp[order[-1]]["last_end"] for smp in samples])
     out = {
         "metric": "one decode layer's timeline (per-workgroup wall-clock stamps)",
         "unit": "us", "shape": args.shape, "layers": stack.layers, "keep": args.keep,
         "steps": args.steps, "ms_per_token": round(ms_token, 5), "layer_period_us": round(period, 2),
-        "layer_span_us": kernels[order[-1]]["last_end"],
+        "layer_span_us": span,
         # the launch gap to the next layer's gate, with the per-token graph
-        # launch and input copy spread over the layers (and this layer's own
-        # deviation from the average layer)
-        "rest_of_period_us": round(period - kernels[order[-1]]["last_end"], 2),
+        # launch and input copy spread over the layers
+        "rest_of_period_us": round(period - span, 2),
         "span_us": spans, "gap_us": gaps, "kernels": kernels,
         "note": "timeline build (stamps add a few stores per workgroup); the last layer of the "
-                "last token; microseconds from the gate's first workgroup start",
+                "last token, median of 5 tokens; microseconds from the gate's first workgroup "
+                "start",
     }
     print(json.dumps(out))
     return 0
@@ -704,10 +727,12 @@ def main(argv=None):
                    # top-k + the up rows of the k selected channels (rows
                    # speculated on but not selected are not counted)
                    "topk_spec_up": 2 * I + 4 * k + k * row}
-    # the roofline names one kernel: the longest single-kernel stage (the down
-    # stage is two launches, the partial-sum kernel and its reduction, and is
-    # reported in stage_ms)
-    single = {name: v for name, v in stages.items() if name != "down_gather"}
+    # the roofline names one kernel: the longest single-kernel stage (where
+    # the down stage is two launches, the partial-sum kernel and its
+    # reduction, it is reported in stage_ms only)
+    down_launches = stack.down_launches
+    single = {name: v for name, v in stages.items()
+              if name != "down_gather" or down_launches == 1}
     dom = max(single, key=single.get)
     ach = stage_bytes[dom] / (stages[dom] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -747,6 +772,8 @@ def main(argv=None):
             "activations": "bf16, fp32 accumulate",
             "speculative_up": not args.no_spec,
             "down_scales": "row-major" if args.no_gm else "group-major copy",
+            "down_reduce": "in the partials' launch (XCD-local)" if down_launches == 1
+                           else "separate launch",
             "bytes_per_token": stack.bytes_per_token,
         },
         "step_hbm_gbs": round(step_gbs, 1),

@@ -26,11 +26,19 @@
 //      permlane swaps that halve the live accumulators at each step), the
 //      four waves' sums are added in wave order through 4 KB of LDS, and the
 //      block stores its fp32 partial row segment;
-//   2. a reduce kernel sums the row blocks' partials of every output in a
-//      fixed order and rounds to bf16.
-// (A last-arriving-block reduce inside the partial kernel was measured and
-// dropped: the 64 arrivals on each column block's device-scope counter
-// serialise and cost more than the second launch.)
+//   2. the row blocks' partials of every output are summed in a fixed order
+//      (row blocks rb = p, p + 4, ... ascending for p = 0..3, then the four
+//      sums in order of p) and rounded to bf16: by a reduce kernel, or, in
+//      the decode step's kernel on a device whose workgroups reach its 8 XCDs
+//      round-robin, by the last tile of each column block inside the same
+//      launch (down_gm_kernel<true>: every tile of a column block runs on one
+//      XCD, so its partials and its arrival counter stay in that XCD's L2).
+// (A last-arriving-block reduce with the column blocks of a row block spread
+// over every XCD was measured and dropped: the 64 arrivals on each column
+// block's device-scope counter serialise and cost more than the second
+// launch.)
+#include <string.h>
+
 #include "dip_tiles.h"
 
 namespace dip {
@@ -41,7 +49,8 @@ constexpr int kRowsPerBlock = kThreads;  // 256/LPR slots x LPR rows each
 constexpr int kXcds = 8;                 // MI355X: 8 XCDs, workgroups dispatched round-robin
 constexpr int kMaxRowBlocks = 512;       // k <= 131072
 constexpr int kRedOut = 32;              // outputs per reduce block
-constexpr int kRedSplit = 8;             // interleaved row-block splits per output
+constexpr int kRedSplit = 4;             // interleaved row-block splits per output
+constexpr int kMaxXcdColBlocks = kDownCounterBytes / kDownCounterStride;
 }  // namespace
 
 #ifdef DIP_WG_STAMPS
@@ -169,18 +178,78 @@ struct DownGmArgs {
   const int32_t* sel;
   float* partial;
   uint16_t* h_out;
+  uint32_t* counters;  // XCD-local reduce: one arrival counter per column block
+  uint16_t* y;         // XCD-local reduce: the output
   int rows, k, out_features, col_blocks, row_blocks;
 };
 
+// The XCD-local reduce at the end of a tile of down_gm_kernel<true>.  Every
+// tile of column block cb runs on the same XCD (workgroups b with the same
+// b % 8 share an XCD), so the partial stores and the arrival counter of cb
+// meet in that XCD's L2: each thread waits until its partial store is
+// acknowledged by the L2, the block synchronises, one L2 atomic counts the
+// arrival, and the tile that arrives last (it sees row_blocks - 1) resets
+// the counter for the next launch and sums the column block's partials,
+// which it reads back from the same L2, in the order of down_reduce_kernel.
+DIP_DEV void down_xcd_tail(const DownGmArgs& a, int cb, float* red, uint32_t* last) {
+  constexpr int kCols = 8 * kDownAcc, kWaves = kThreads / 64;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* ctr = a.counters + (size_t)cb * (kDownCounterStride / sizeof(uint32_t));
+    const uint32_t old =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const bool is_last = old == (uint32_t)(a.row_blocks - 1);
+    if (is_last) *ctr = 0u;
+    *last = is_last;
+  }
+  __syncthreads();
+  if (!*last) return;
+  // wave w sums row blocks w, w + 4, ... in ascending order (4 columns per
+  // lane, 8 row blocks per round trip), then the waves' sums meet in LDS
+  const int w = threadIdx.x >> 6, ln = threadIdx.x & 63;
+  const float4* base = reinterpret_cast<const float4*>(a.partial + (size_t)cb * kCols) + ln;
+  const size_t stride = (size_t)a.out_features / 4;
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int b0 = w; b0 < a.row_blocks; b0 += kWaves * 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = base[(size_t)min(b0 + kWaves * u, a.row_blocks - 1) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (b0 + kWaves * u < a.row_blocks) {
+        sum.x += v[u].x;
+        sum.y += v[u].y;
+        sum.z += v[u].z;
+        sum.w += v[u].w;
+      }
+    }
+  }
+  *reinterpret_cast<float4*>(red + w * kCols + 4 * ln) = sum;
+  __syncthreads();
+  float t = red[threadIdx.x];
+#pragma unroll
+  for (int q = 1; q < kWaves; ++q) t += red[q * kCols + threadIdx.x];
+  a.y[(size_t)cb * kCols + threadIdx.x] = (uint16_t)f32_to_bf16(t);
+}
+
+// XCD_REDUCE: the tiles of column block cb run as workgroups b with b % 8 ==
+// cb / (col_blocks / 8) (col_blocks a multiple of 8), and the last tile of
+// each column block writes its y (down_xcd_tail); otherwise tile (rb, cb)
+// runs with b % 8 == rb % 8 and a reduce kernel follows.
+template <bool XCD_REDUCE>
 __global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
   DIP_STAMP_START(g_stamps_down);
   constexpr int LPR = 8, kSlots = kThreads / LPR, kCols = LPR * kDownAcc, kWaves = kThreads / 64;
   __shared__ __align__(16) float red[down_red_floats<LPR>()];
   __shared__ __align__(16) uint32_t xoff[kWaves][64];
   __shared__ __align__(16) float xcoef[kWaves][2][64];
+  __shared__ uint32_t last;
   const int xcd = blockIdx.x % kXcds, w = blockIdx.x / kXcds;
-  const int rb = xcd + kXcds * (w / a.col_blocks);
-  const int cb = w % a.col_blocks;
+  const int cpx = a.col_blocks / kXcds;
+  const int rb = XCD_REDUCE ? w / cpx : xcd + kXcds * (w / a.col_blocks);
+  const int cb = XCD_REDUCE ? xcd * cpx + w % cpx : w % a.col_blocks;
   if (rb >= a.row_blocks) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l = tid % LPR, slot = tid / LPR, sw = lane / LPR;
@@ -222,6 +291,7 @@ __global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
   for (int m = 0; m < kDownAcc; ++m) acc[m] = 0.f;
   down_accumulate<LPR>(ring, f, acc);
   down_block_partial<LPR>(acc, red, a.partial + (size_t)rb * a.out_features + (size_t)cb * kCols);
+  if constexpr (XCD_REDUCE) down_xcd_tail(a, cb, red, &last);
   DIP_STAMP_END(g_stamps_down);
 }
 
@@ -315,10 +385,28 @@ int launch_down_reduce(const float* partial, int row_blocks, int out_features, u
 }
 
 size_t down_workspace_bytes(int64_t k, int64_t out_features) {
+  // the XCD-local reduce's arrival counters (kept zero between calls), then
   // one fp32 partial row of out_features per block of 256 selected positions
-  if (out_features <= 0) return 256;
+  if (out_features <= 0) return kDownCounterBytes + 256;
   const int64_t blocks = k > 0 ? (k + kRowsPerBlock - 1) / kRowsPerBlock : 1;
-  return (size_t)blocks * (size_t)out_features * sizeof(float);
+  return kDownCounterBytes + (size_t)blocks * (size_t)out_features * sizeof(float);
+}
+
+// The XCD-local reduce needs every tile of a column block on one XCD: a
+// full 256-CU gfx950 (MI350X / MI355X: 8 XCDs of 32 CUs), whose dispatcher
+// hands workgroup b to XCD (b + c) mod 8 for one c per launch.  Cached per
+// device.
+bool xcd_reduce_device() {
+  static int cache[64] = {0};  // 0 unknown, 1 no, 2 yes
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (!cache[dev]) {
+    hipDeviceProp_t p{};
+    const bool ok = hipGetDeviceProperties(&p, dev) == hipSuccess &&
+                    strncmp(p.gcnArchName, "gfx950", 6) == 0 && p.multiProcessorCount == 256;
+    cache[dev] = ok ? 2 : 1;
+  }
+  return cache[dev] == 2;
 }
 
 int64_t down_max_k() { return (int64_t)kMaxRowBlocks * kRowsPerBlock; }
@@ -359,7 +447,7 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
   a.h = h;
   a.sel = sel;
   a.sel2 = sel2;
-  a.partial = reinterpret_cast<float*>(workspace);
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kDownCounterBytes);
   a.h_out = h_out;
   a.h_by_row = h_by_row;
   a.rows_a = (int)rows_a;
@@ -388,7 +476,14 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
     g.out_features = a.out_features;
     g.col_blocks = a.col_blocks;
     g.row_blocks = a.row_blocks;
-    hipLaunchKernelGGL(down_gm_kernel, dim3(blocks), dim3(kThreads), 0, stream, g);
+    if (a.col_blocks % kXcds == 0 && a.col_blocks <= kMaxXcdColBlocks && xcd_reduce_device()) {
+      g.counters = static_cast<uint32_t*>(workspace);
+      g.y = y;
+      const int xblocks = kXcds * (a.col_blocks / kXcds) * a.row_blocks;
+      hipLaunchKernelGGL((down_gm_kernel<true>), dim3(xblocks), dim3(kThreads), 0, stream, g);
+      return hip_status(hipGetLastError());
+    }
+    hipLaunchKernelGGL((down_gm_kernel<false>), dim3(blocks), dim3(kThreads), 0, stream, g);
   } else if (sc_gm) {
     if (lpr == 8) launch_down<8, kScGm>(src, off32, a, blocks, stream);
     else launch_down<4, kScGm>(src, off32, a, blocks, stream);

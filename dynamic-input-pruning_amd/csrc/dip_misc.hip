@@ -383,7 +383,9 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
 
 // ---------------------------------------------------------------------------
 // One resident DIP MLP decode step.
-//   workspace: [0, 512) top-k state | h by channel [inter] bf16 | down partials
+//   workspace: [0, 512) top-k state | the down workspace (the XCD-local
+//   reduce's counters at a fixed offset, then the partials) | h by channel
+//   [inter] bf16
 // ---------------------------------------------------------------------------
 namespace {
 constexpr size_t kMlpTopkBytes = 512;
@@ -393,7 +395,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 extern "C" size_t dip_mlp_workspace_size(int64_t hidden, int64_t inter, int64_t k) {
   const size_t hfull = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
-  return kMlpTopkBytes + hfull + align256(down_workspace_bytes(k, hidden));
+  return kMlpTopkBytes + align256(down_workspace_bytes(k, hidden)) + hfull;
 }
 
 extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gate_sc,
@@ -422,9 +424,9 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
   if (!workspace || ws_bytes < dip_mlp_workspace_size(hidden, inter, k)) return DIP_ERR_WORKSPACE;
   if (!aligned16(workspace)) return DIP_ERR_ALIGN;
   char* ws = static_cast<char*>(workspace);
-  const size_t hfull_bytes = align256((size_t)inter * sizeof(uint16_t));
-  char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
-  const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
+  char* down_ws = ws + kMlpTopkBytes;
+  const size_t down_bytes = align256(down_workspace_bytes(k, hidden));
+  uint16_t* h_full = reinterpret_cast<uint16_t*>(down_ws + down_bytes);
   hipStream_t s = (hipStream_t)stream;
   RowdotArgs a{};
   a.qw_a = gate_qw;
@@ -447,7 +449,6 @@ extern "C" int dip_mlp_decode_rmsnorm(const int8_t* gate_qw, const uint16_t* gat
     a.rotate = static_cast<uint32_t*>(layer_state);
     int st = launch_rowdot_norm(kSilu, a, s);
     if (st) return st;
-    uint16_t* h_full = reinterpret_cast<uint16_t*>(ws + kMlpTopkBytes);
     st = launch_spec_after_gate(g_out, inter, hidden, k, idx_out, h_full, up_qw, up_sc, x_out, ws,
                                 layer_state, s);
     if (st) return st;
@@ -480,11 +481,10 @@ extern "C" int dip_mlp_decode(const int8_t* gate_qw, const uint16_t* gate_sc,
   if (k > 0 && (!idx_out || !h_out)) return DIP_ERR_NULL;
   if (!workspace || ws_bytes < dip_mlp_workspace_size(hidden, inter, k)) return DIP_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
-  const size_t hfull_bytes = inter > 0 ? align256((size_t)inter * sizeof(uint16_t)) : 0;
-  char* down_ws = ws + kMlpTopkBytes + hfull_bytes;
-  const size_t down_bytes = ws_bytes - kMlpTopkBytes - hfull_bytes;
+  char* down_ws = ws + kMlpTopkBytes;
+  const size_t down_bytes = align256(down_workspace_bytes(k, hidden));
+  uint16_t* h_full = reinterpret_cast<uint16_t*>(down_ws + down_bytes);
   if (layer_state && k > 0 && topk_spec_supported(hidden) && inter <= kTopkMaxN) {
-    uint16_t* h_full = reinterpret_cast<uint16_t*>(ws + kMlpTopkBytes);
     int st = dip_gate_silu_topk_spec(gate_qw, gate_sc, up_qw, up_sc, x, g_out, idx_out, h_full,
                                      inter, hidden, k, ws, kMlpTopkBytes, layer_state, stream);
     if (st) return st;

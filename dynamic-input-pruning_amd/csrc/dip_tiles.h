@@ -295,6 +295,10 @@ DIP_DEV uint32_t h_of(uint32_t g_bits, float u) {
 // Down
 // ---------------------------------------------------------------------------
 constexpr int kDownThreads = 256;
+// The down workspace starts with the XCD-local reduce's arrival counters, one
+// per column block on its own 256 bytes (no two XCDs' L2s hold one line).
+constexpr size_t kDownCounterStride = 256;
+constexpr size_t kDownCounterBytes = 8192;  // 32 column blocks: out_features <= 8192
 constexpr int kDownAcc = kChunkCols;  // outputs per lane: one 16-byte chunk
 
 // Row id for position j (j < k); kBadRow if out of range.  Branch-free.

@@ -91,6 +91,20 @@ class DIPStack:
                    scales_gm=scales_gm)
 
     @property
+    def down_launches(self) -> int:
+        """Launches of the decode step's down stage: 1 when its last tiles
+        reduce the partial sums inside the launch (the speculative step's
+        down kernel with the group-major scales, hidden a multiple of 2048 up
+        to 8192, on a full 256-CU gfx950: the rule of
+        dip_int4_gather_down_by_channel), else 2 (partials + reduce)."""
+        props = torch.cuda.get_device_properties(self.device)
+        xcd_local = (self.spec and self.w[0]["down_t_sc_gm"] is not None
+                     and self.hidden % 2048 == 0 and self.hidden <= 8192
+                     and props.gcnArchName.startswith("gfx950")
+                     and props.multi_processor_count == 256)
+        return 1 if xcd_local else 2
+
+    @property
     def bytes_per_token(self) -> int:
         return self.layers * bytes_per_layer(self.hidden, self.inter, self.k)
 
@@ -137,13 +151,14 @@ class DIPStack:
         up_gather_h and down_gather."""
         lib = K.lib
         H, I, k = self.hidden, self.inter, self.k
+        # the decode step's workspace: [0, 512) top-k state | the down
+        # workspace (dip_gather_down_workspace_size, 256-byte aligned) | h by
+        # channel
         topk_bytes = 512
-        hfull_bytes = (2 * I + 255) // 256 * 256
         ws_ptr = self.ws.data_ptr()
-        ws_n = self.ws.numel()
-        down_ws = ws_ptr + topk_bytes + hfull_bytes
-        down_n = ws_n - topk_bytes - hfull_bytes
-        h_full = ws_ptr + topk_bytes
+        down_ws = ws_ptr + topk_bytes
+        down_n = (lib.dip_gather_down_workspace_size(k, H) + 255) // 256 * 256
+        h_full = down_ws + down_n
         x = self.x.data_ptr()
 
         def gate(st):

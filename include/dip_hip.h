@@ -52,12 +52,14 @@ const char* dip_status_string(int status);
  * Library version as an integer (major * 10000 + minor * 100 + patch).  The
  * minor number changes whenever an entry point's argument list changes, so
  * a binding written against this header checks dip_version() == DIP_VERSION
- * before its first call.  0.3.1 adds dip_timeline_read.  0.3.0: the
+ * before its first call.  0.3.2: the down and decode workspaces grow by
+ * 8 KB of arrival counters (the sizes functions report it).  0.3.1 adds
+ * dip_timeline_read.  0.3.0: the
  * measurement probes and the DIP_TUNE_STEP knob are gone; 0.2.0 added
  * down_t_sc_gm to the decode and gather-down entry points and g_len to
  * dip_ca_fused_gemv.
  */
-#define DIP_VERSION 301
+#define DIP_VERSION 302
 int dip_version(void);
 
 /* Highest row count the top-k supports (its keys are staged in LDS). */
@@ -129,7 +131,9 @@ int dip_up_gather_h(const int8_t* qweight, const uint16_t* scales, const uint16_
  * or j when indices == NULL (the staged-copy layout of the reference).
  * Deterministic: fp32 partial sums over fixed blocks of 256 positions
  * reduced in a fixed order by a second launch, no float atomics.
- * k <= 131072; the workspace holds ceil(k/256) * out_features fp32 partials.
+ * k <= 131072; the workspace holds 8 KB of arrival counters (used by
+ * dip_int4_gather_down_by_channel) and ceil(k/256) * out_features fp32
+ * partials.
  * Replaces int4_down_ops::int4_gather_down
  * (kernels/int4_down/int4_gather_down.cu:77-102).
  */
@@ -300,7 +304,11 @@ int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
  * NULL): the same scales group-major, [out_features/128][rows]
  * (dip_scales_group_major); when given the kernel reads the scales there
  * (same values, same y bit for bit) instead of a few bytes of every
- * selected row's own scale line.
+ * selected row's own scale line.  With scales_gm, a matrix under 4 GiB,
+ * out_features a multiple of 2048 (at most 8192) and a full 256-CU gfx950,
+ * the partial sums are reduced inside the same launch: every tile of a
+ * column block runs on one XCD and the last one to finish sums them, in the
+ * same order as the reduce launch (same y bit for bit, one launch).
  */
 int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint16_t* scales,
                                     const uint16_t* scales_gm,

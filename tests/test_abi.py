@@ -156,12 +156,14 @@ def test_argument_rejection_before_launch():
 def test_workspace_sizes():
     L = K.lib
     assert L.dip_topk_workspace_size(25600) >= 16
-    # down partials: one fp32 row of `out` per block of 256 selected positions
+    # down: 8 KB of arrival counters (the in-launch reduce), then one fp32
+    # row of `out` per block of 256 selected positions
     need = L.dip_gather_down_workspace_size(15360, 5120)
-    assert need == 60 * 5120 * 4
-    assert L.dip_gather_down_workspace_size(15361, 5120) == 61 * 5120 * 4
-    assert L.dip_gather_down_workspace_size(1, 128) == 128 * 4
-    assert L.dip_mlp_workspace_size(5120, 25600, 15360) >= need
+    assert need == 8192 + 60 * 5120 * 4
+    assert L.dip_gather_down_workspace_size(15361, 5120) == 8192 + 61 * 5120 * 4
+    assert L.dip_gather_down_workspace_size(1, 128) == 8192 + 128 * 4
+    # decode: 512 B of top-k state, the down workspace, h by channel
+    assert L.dip_mlp_workspace_size(5120, 25600, 15360) == 512 + need + 2 * 25600
     # attention partials: (m, l, 128 sums) per query head per 32 cache rows
     assert L.dip_decode_attention_workspace_size(64, 128, 300) == 10 * 64 * 130 * 4
     assert L.dip_decode_attention_workspace_size(64, 96, 300) == 0

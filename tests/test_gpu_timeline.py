@@ -21,7 +21,14 @@ def test_layer_timeline_is_ordered(shape):
     assert out.returncode == 0, out.stderr[-2000:]
     rec = json.loads(out.stdout.strip().splitlines()[-1])
     ks = rec["kernels"]
-    assert list(ks) == ["gate", "topk_spec_up", "down_partials", "down_reduce"]
+    # hidden 4096 on a full 256-CU gfx950: the down partials' launch reduces
+    # them itself (no reduce kernel); hidden 5120 keeps the reduce launch
+    import torch
+    props = torch.cuda.get_device_properties(0)
+    in_launch = (shape == "qwen3-8b" and props.gcnArchName.startswith("gfx950")
+                 and props.multi_processor_count == 256)
+    assert list(ks) == ["gate", "topk_spec_up", "down_partials"] + ([] if in_launch
+                                                                    else ["down_reduce"])
     for name, k in ks.items():
         assert k["finished"] > 0, name
         assert k["first_start"] <= k["last_start"] <= k["last_end"], name
@@ -36,4 +43,4 @@ def test_layer_timeline_is_ordered(shape):
     # start but never reach the end of the kernel
     assert ks["down_partials"]["finished"] <= ks["down_partials"]["workgroups"]
     # one layer's kernels fit in one layer period
-    assert ks["down_reduce"]["last_end"] <= rec["layer_period_us"] * 1.5
+    assert rec["layer_span_us"] <= rec["layer_period_us"] * 1.5
