@@ -103,12 +103,16 @@ def measured_traffic(shape: str, keep: float, stage: str, K):
     tuning, table = None, {}
     for line in path.read_text().splitlines():
         if line.startswith("tuning:"):
-            tuning = [int(v) for v in line.split(":", 1)[1].split(",")]
+            tuning = {}
+            for item in line.split(":", 1)[1].split():
+                name, val = item.split("=")
+                tuning[name] = int(val)
         elif line.startswith("traffic_bytes_per_launch:"):
             for item in line.split(":", 1)[1].split():
                 name, val = item.split("=")
                 table[name] = int(val)
-    live = [K.lib.dip_get_tuning(i) for i in range(len(tuning or []))]
+    # every knob, by name, as it was when the counters were read
+    live = {name: K.get_tuning(name) for name in K.TUNE}
     if tuning != live:
         return None
     return table.get(stage)

@@ -98,7 +98,7 @@ for _name, (_args, _res) in _SIGS.items():
 # The argument lists above follow this version of include/dip_hip.h
 # (DIP_VERSION); a library built from another one would be called with
 # shifted arguments, so it is refused here.
-ABI_VERSION = 302
+ABI_VERSION = 303
 if lib.dip_version() != ABI_VERSION:
     raise ImportError(f"{LIB_PATH} reports ABI version {lib.dip_version()}, these bindings "
                       f"are written for {ABI_VERSION}; rebuild the library")
@@ -797,7 +797,7 @@ def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res
     return y, g, idx, h, x_out
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2}
+TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "gate_tiers": 4}
 
 
 TIMELINE_KERNELS = {"gate": 0, "topk_spec_up": 1, "down_partials": 2, "down_reduce": 3}

@@ -42,6 +42,10 @@ struct RowdotArgs {
   int rows_a;  // rows of matrix A (row ids outside [0, rows_a) yield NaN)
   int rows_b;  // rows of matrix B (kDual)
   int ngrp;    // row groups (set by the launcher)
+  // two tiers of workgroups (set by the launcher; tier_wgs 0: one tier):
+  // workgroups [0, tier_wgs) compute rows [0, tier_rows), the others the rest
+  int tier_wgs;
+  int tier_rows;
   uint32_t* rotate;  // if set: workgroup 0 copies rotate[1] to rotate[0] (speculation state)
   // RMSNorm prologue (dip_int4_gemv_rmsnorm): x = bf16(w * bf16(v * rsqrt(mean(v^2)
   // + eps))) with v = bf16(x + norm_add); workgroup 0 writes v to norm_h_out

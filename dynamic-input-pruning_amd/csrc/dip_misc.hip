@@ -168,7 +168,7 @@ extern "C" int dip_timeline_read(int kernel, dip_wg_stamps* dst) {
 // Tuning table and device facts.
 // ---------------------------------------------------------------------------
 namespace {
-int g_tune[DIP_TUNE_COUNT] = {0, 0, 8};
+int g_tune[DIP_TUNE_COUNT] = {0, 0, 8, 0, 1};  // [3]: not a knob
 }  // namespace
 
 int dip::tuning(int knob) { return g_tune[knob]; }
@@ -198,6 +198,9 @@ extern "C" int dip_set_tuning(int knob, int value) {
     case DIP_TUNE_SPEC_MARGIN:
       if (value < 0 || value > 1024) return DIP_ERR_ARG;
       break;
+    case DIP_TUNE_GATE_TIERS:
+      if (value != 0 && value != 1) return DIP_ERR_ARG;
+      break;
     default:
       return DIP_ERR_ARG;
   }
@@ -206,7 +209,7 @@ extern "C" int dip_set_tuning(int knob, int value) {
 }
 
 extern "C" int dip_get_tuning(int knob) {
-  if (knob < 0 || knob >= DIP_TUNE_COUNT) return DIP_ERR_ARG;
+  if (knob < 0 || knob >= DIP_TUNE_COUNT || knob == 3) return DIP_ERR_ARG;
   return g_tune[knob];
 }
 

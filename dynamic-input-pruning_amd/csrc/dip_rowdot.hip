@@ -12,8 +12,9 @@
 //     while the next row stays in flight.  Loads under data-dependent
 //     branches would make it wait for everything.
 //   * Workgroups are 256 threads (plan_rowdot): a Qwen3-32B gate runs exactly
-//     2 per CU, 512 workgroups of 8 groups x 6-7 rows; its up gather 480 of
-//     8 groups x 4 rows.
+//     2 per CU, 512 workgroups of 8 groups, split over two tiers (the first
+//     256 workgroups 9 rows per group, the rest 3-4: gate_tier_rows); its up
+//     gather 480 of 8 groups x 4 rows.
 //   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
 //     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
 //     touches no LDS; otherwise each lane builds its own pairs from global
@@ -38,10 +39,10 @@ int timeline_read_rowdot(dip_wg_stamps*) { return DIP_ERR_UNSUPPORTED; }
 
 constexpr int kRowdotMaxThreads = 256;
 
-template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
-__global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a) {
-  static_assert(!NORM || XS, "the RMSNorm prologue needs the staged x");
-  DIP_STAMP_START(g_stamps_rowdot);
+// Rows row_base + grp + i*ngrp (i < ROWS) below row_end, for group grp.
+template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM>
+__device__ __forceinline__ void rowdot_rows(const RowdotArgs& a, const int grp, const int ngrp,
+                                            const int row_base, const int row_end) {
   constexpr int D = ROWS < 2 ? ROWS : 2;  // rows of loads in flight per group
   static_assert(ROWS <= LPR, "rows per group");
   extern __shared__ __align__(16) uint32_t xlds[];
@@ -51,8 +52,6 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   const size_t row_bytes = (size_t)(a.in_features >> 1);
   const int ngroups = a.in_features >> 7;
   const int nchunks = a.in_features / kChunkCols;
-  const int grp = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
-  const int ngrp = a.ngrp;
 
   // 1. x loads first (XS: one chunk per thread, index clamped; NORM: h, the
   // residual addend and the norm weight in 8-value units spread over all
@@ -85,9 +84,9 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. row ids: lane l resolves row l of the group (clamped, unconditional)
-  const long long jl = grp + (long long)l * ngrp;
-  const bool valid_l = l < ROWS && jl < a.nrows;
-  const uint32_t rid_lane = resolve_row<SRC>(a, (int)min(jl, (long long)a.nrows - 1));
+  const long long jl = row_base + grp + (long long)l * ngrp;
+  const bool valid_l = l < ROWS && jl < row_end;
+  const uint32_t rid_lane = resolve_row<SRC>(a, (int)min(jl, (long long)row_end - 1));
 
   // 3. first D rows of loads
   RowRegs<CH> ring[D];
@@ -157,6 +156,27 @@ __global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a)
     a.out[(int)jl] = (uint16_t)v;
   }
   if (rot) a.rotate[0] = rot1;
+}
+
+// R1 > 0: two tiers of workgroups, ROWS rows per group in the first
+// (blockIdx < a.tier_wgs, rows [0, a.tier_rows)) and R1 in the second.
+template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false, int R1 = 0>
+__global__ __launch_bounds__(kRowdotMaxThreads) void rowdot_kernel(RowdotArgs a) {
+  static_assert(!NORM || XS, "the RMSNorm prologue needs the staged x");
+  DIP_STAMP_START(g_stamps_rowdot);
+  constexpr int G = kRowdotMaxThreads / LPR;
+  const int b = (int)blockIdx.x;
+  const int gw = (int)threadIdx.x / LPR;
+  if constexpr (R1 > 0) {
+    const int ngrp = a.tier_wgs * G;  // groups per tier
+    if (b < a.tier_wgs)
+      rowdot_rows<LPR, CH, SRC, EPI, XS, ROWS, NORM>(a, b * G + gw, ngrp, 0, a.tier_rows);
+    else
+      rowdot_rows<LPR, CH, SRC, EPI, XS, R1, NORM>(a, (b - a.tier_wgs) * G + gw, ngrp,
+                                                   a.tier_rows, a.nrows);
+  } else {
+    rowdot_rows<LPR, CH, SRC, EPI, XS, ROWS, NORM>(a, b * G + gw, a.ngrp, 0, a.nrows);
+  }
   DIP_STAMP_END(g_stamps_rowdot);
 }
 
@@ -242,10 +262,41 @@ int rowdot_wpc(int nrows, int chunks, bool gate, bool norm) {
   return occ >= 3 ? 3 : 2;
 }
 
+// The SiLU gate at two workgroups per CU, split over two tiers.  The first
+// workgroup each CU receives (blockIdx < CUs) wins its SIMDs' issue
+// arbitration over the second: on the Qwen3-32B gate at an even split (6-7
+// rows per group in both) the first tier ends at about 9.7 us and the second
+// at about 12 us.  Giving the first tier 9 rows per group and the second the
+// rest (3.5) ends them together: 13.5 -> 12.9-13.0 us per launch (the gate
+// stage timed in a graph; 8 or 8.5 rows in the first tier gained less, 9.5
+// lost).  Every row is still one group's dot product in the same order, so
+// g is bit for bit the even split's.  (The Qwen3-8B gate runs three per CU with 2 rows
+// per group, all in flight at once; 3/2/1 rows over its three tiers was
+// slower: a third row waits for a ring slot.)  Returns the rows per group
+// of the first tier, 0 for the even split.
+int gate_tier_rows(int nrows, int blocks, int groups) {
+  const int cus = device_cus();
+  if (!tuning(DIP_TUNE_GATE_TIERS) || blocks != 2 * cus) return 0;
+  const long long g = (long long)cus * groups;  // groups per tier
+  // the measured split: 9 rows per group in the first tier, at most 4 in the
+  // second (12 g < nrows <= 13 g)
+  return (nrows > 12 * g && nrows <= 13 * g) ? 9 : 0;
+}
+
 template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
 void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   a.ngrp = p.blocks * p.groups;
   const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) + (NORM ? 16 : 0) : 0;
+  // (built for the measured width, hidden 5120)
+  if constexpr (SRC == kContig && EPI == kSilu && XS && !NORM && LPR == 32 && CH == 5) {
+    if (gate_tier_rows(a.nrows, p.blocks, p.groups) == 9) {
+      a.tier_wgs = p.blocks / 2;
+      a.tier_rows = 9 * a.tier_wgs * p.groups;
+      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, 9, false, 4>), dim3(p.blocks),
+                         dim3(p.groups * LPR), lds, stream, a);
+      return;
+    }
+  }
   hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, ROWS, NORM>), dim3(p.blocks),
                      dim3(p.groups * LPR), lds, stream, a);
 }

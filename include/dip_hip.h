@@ -52,14 +52,15 @@ const char* dip_status_string(int status);
  * Library version as an integer (major * 10000 + minor * 100 + patch).  The
  * minor number changes whenever an entry point's argument list changes, so
  * a binding written against this header checks dip_version() == DIP_VERSION
- * before its first call.  0.3.2: the down and decode workspaces grow by
+ * before its first call.  0.3.3 adds the DIP_TUNE_GATE_TIERS knob (no
+ * argument list changes).  0.3.2: the down and decode workspaces grow by
  * 8 KB of arrival counters (the sizes functions report it).  0.3.1 adds
  * dip_timeline_read.  0.3.0: the
  * measurement probes and the DIP_TUNE_STEP knob are gone; 0.2.0 added
  * down_t_sc_gm to the decode and gather-down entry points and g_len to
  * dip_ca_fused_gemv.
  */
-#define DIP_VERSION 302
+#define DIP_VERSION 303
 int dip_version(void);
 
 /* Highest row count the top-k supports (its keys are staged in LDS). */
@@ -154,13 +155,22 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
  *                               on the channels at or above the magnitude of
  *                               rank k + inter * this / 1024 (0..1024) (8)
- * dip_set_tuning returns DIP_ERR_ARG for an unknown knob or value.
+ *   DIP_TUNE_GATE_TIERS         1: a SiLU gate of hidden 5120 at two workgroups
+ *                               per CU gives the first workgroup on each CU
+ *                               9 rows per lane group and the second the rest
+ *                               where 12 < rows / (8 * CUs) <= 13 (the
+ *                               Qwen3-32B gate); 0: every group the same
+ *                               rows.  Same bits either way. (1)
+ * Knob 3 (a removed step-form switch) is not a knob.  dip_set_tuning and
+ * dip_get_tuning return DIP_ERR_ARG for an unknown knob, dip_set_tuning also
+ * for a value out of range.
  */
 enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
   DIP_TUNE_TOPK_STAMPS = 1,
   DIP_TUNE_SPEC_MARGIN = 2,
-  DIP_TUNE_COUNT = 3
+  DIP_TUNE_GATE_TIERS = 4,
+  DIP_TUNE_COUNT = 5
 };
 int dip_set_tuning(int knob, int value);
 int dip_get_tuning(int knob);

@@ -94,6 +94,10 @@ def test_argument_rejection_before_launch():
     assert L.dip_mlp_state_size() == 16  # speculation key (twice), key band, spare
     assert not hasattr(L, "dip_read_probe")  # the probes live in libdip_probe.so
     assert L.dip_set_tuning(3, 1) == -6  # the removed step-form knob
+    assert L.dip_get_tuning(3) == -6
+    assert L.dip_get_tuning(4) == 1  # the two-tier gate split: on by default
+    assert L.dip_set_tuning(4, 2) == -6
+    assert L.dip_set_tuning(4, -1) == -6
     assert L.dip_set_tuning(2, 1025) == -6
     assert L.dip_set_tuning(2, -1) == -6
     assert L.dip_set_tuning(1, 7) == -6

@@ -1,0 +1,78 @@
+"""The SiLU gate's two-tier split (DIP_TUNE_GATE_TIERS, on by default): at
+hidden 5120 and two workgroups per CU, the first workgroup on each CU takes
+9 rows per lane group and the second the rest, for 12 < rows / (8 * CUs) <=
+13 (the Qwen3-32B gate).  Each row is still one group's dot product in the
+same order, so g must be bit for bit the even split's, at the row counts on
+both sides of that range; the even split is pinned to the oracle by the
+kernel tests, and the split's g is checked against the oracle here too."""
+import numpy as np
+import pytest
+import torch
+
+import dip_oracle as O
+from gpu_util import dev, dev_bf16, host_bf16, random_bf16, random_int4, rel_err, ulp_diff
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def K():
+    import _dip_hip
+    return _dip_hip
+
+
+def _groups_per_tier():
+    return torch.cuda.get_device_properties(0).multi_processor_count * 8
+
+
+@pytest.mark.parametrize("tier_units", [12, 12.0001, 12.5, 13, 13.0001])
+def test_gate_tiers_same_bits_as_even_split(K, tier_units):
+    rows = int(np.ceil(tier_units * _groups_per_tier()))
+    print(f"gate tiers rows={rows} hidden=5120", flush=True)
+    rng = np.random.default_rng(rows)
+    qw, sc = random_int4(rng, rows, 5120)
+    x = random_bf16(rng, 5120)
+    qd, sd, xd = dev(qw), dev_bf16(sc), dev_bf16(x)
+    assert K.get_tuning("gate_tiers") == 1
+    split = K.int4_gemv(qd, sd, xd, act=1)
+    try:
+        K.set_tuning("gate_tiers", 0)
+        even = K.int4_gemv(qd, sd, xd, act=1)
+    finally:
+        K.set_tuning("gate_tiers", 1)
+    torch.cuda.synchronize()
+    assert torch.equal(split, even)
+    # against the oracle: SiLU of the pre-activation (within one bf16 ulp of
+    # the correctly rounded SiLU), the pre-activation itself within the
+    # reference's relative error
+    pre = host_bf16(K.int4_gemv(qd, sd, xd))
+    assert rel_err(pre, O.gemv_f64(qw, sc, x)) < 1e-2
+    d = ulp_diff(host_bf16(split), O.silu_bf16(pre))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3
+
+
+def test_gate_tiers_in_the_decode_step(K):
+    """The speculative decode step at the Qwen3-32B shape: y, g, idx and h
+    with the split equal those with the even split, token after token."""
+    H, I, keep = 5120, 25600, 0.6
+    L = O.make_layer(H, I, seed=11)
+    D = {n: (dev_bf16(v) if v.dtype == np.uint16 else dev(v)) for n, v in L.items()}
+    gm = K.scales_group_major(D["down_t_sc"])
+    k = O.keep_count(I, keep)
+    st = [K.mlp_state(torch.device("cuda:0")) for _ in range(2)]
+    for tok in range(3):
+        print(f"gate tiers decode token {tok}", flush=True)
+        x = dev_bf16(O.make_x(H, seed=40 + tok))
+        outs = []
+        for tiers in (1, 0):
+            K.set_tuning("gate_tiers", tiers)
+            try:
+                outs.append(K.mlp_decode(D["gate_qw"], D["gate_sc"], D["up_qw"], D["up_sc"],
+                                         D["down_t_qw"], D["down_t_sc"], x, k, state=st[tiers],
+                                         down_t_sc_gm=gm))
+            finally:
+                K.set_tuning("gate_tiers", 1)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "g", "idx", "h"), *outs):
+            assert torch.equal(a, b), (name, tok)
+        assert np.array_equal(outs[0][2].cpu().numpy(), O.topk_select(host_bf16(outs[0][1]), k))
