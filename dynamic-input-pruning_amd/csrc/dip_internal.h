@@ -94,7 +94,8 @@ struct TopkMeta {
   uint64_t stamp[6];   // wall_clock64() at the select kernel's phase boundaries (diagnostics)
   uint64_t cycles[2];  // clock64() (shader clock) at the start and end (diagnostics)
   // wall_clock64() in two speculation workgroups (the first and the middle
-  // one): start, list built, x staged, done (diagnostics)
+  // one): start, x staged and the list counted, list published, done
+  // (diagnostics)
   uint64_t spec_stamp[2][4];
 };
 

@@ -111,8 +111,9 @@ DIP_DEV void load_x_chunk(const uint16_t* x, int nchunks, uint4 xs[4]) {
 // l + LPR*c sit at 16-byte slot (c*4 + q)*LPR + l, so the LPR lanes of a
 // group read consecutive 16 B (no bank conflicts; the other groups of the
 // wave read the same addresses, a broadcast); then [nchunks] biases.
-// Needs nchunks <= blockDim.x; ends with a block barrier.
-template <int LPR>
+// Needs nchunks <= blockDim.x; ends with a block barrier (BARRIER false:
+// the caller's next barrier publishes the pairs).
+template <int LPR, bool BARRIER = true>
 DIP_DEV void stage_x_pairs(const uint4 xs[4], uint32_t* xlds, int nchunks) {
   if ((int)threadIdx.x < nchunks) {
     uint32_t p[4][4];
@@ -125,7 +126,7 @@ DIP_DEV void stage_x_pairs(const uint4 xs[4], uint32_t* xlds, int nchunks) {
       dst[(cc * 4 + i) * LPR + lc] = make_uint4(p[i][0], p[i][1], p[i][2], p[i][3]);
     reinterpret_cast<float*>(xlds + nchunks * 16)[threadIdx.x] = b;
   }
-  __syncthreads();
+  if constexpr (BARRIER) __syncthreads();
 }
 
 // ---------------------------------------------------------------------------

@@ -191,18 +191,28 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
   const bool stamp = stamps && sw >= 0 && tid == 0;
   if (stamp) meta->spec_stamp[sw][0] = wall_clock64();
 
+  // x first, then g and the key: staging x's pairs then waits for x alone
   uint4 xs[4];
   load_x_chunk(sp.x, nchunks, xs);
+  __builtin_amdgcn_sched_barrier(0);
   const int c = c0 + tid;
   const uint32_t gb = c < c1 ? (uint32_t)g[c] : 0u;
   // the speculation key at a lane-dependent offset that is always 0 (hidden
   // < 2^30): a uniform load would be a scalar load, waited for before the
   // load of g is even issued; this way both are in flight together
   const uint32_t sk = sp.state[threadIdx.x & ((uint32_t)sp.hidden >> 30)];
+  __builtin_amdgcn_sched_barrier(0);
+  // x pairs are staged before any row load is issued (with the whole chip
+  // streaming, issuing a wave's row loads stalls until data drains, and
+  // compute must be able to start as soon as the first rows arrive), and
+  // while g is still in flight: the barrier after the counts publishes them
+  uint32_t* xlds = lds + kThreads;  // after the list
+  stage_x_pairs<LPR, false>(xs, xlds, nchunks);
   const bool f = c < c1 && (gb & 0x7FFFu) >= sk;
   const uint64_t m = __ballot(f);
   if (lane == 0) wcnt[wave] = (uint32_t)__popcll(m);
   __syncthreads();
+  if (stamp) meta->spec_stamp[sw][1] = wall_clock64();
   int base = 0, total = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -211,12 +221,7 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
     total += v;
   }
   if (f) lds[base + __popcll(m & ((1ull << lane) - 1ull))] = (uint32_t)c | (gb << 16);
-  if (stamp) meta->spec_stamp[sw][1] = wall_clock64();
-  // x pairs are staged before any row load is issued: with the whole chip
-  // streaming, issuing a wave's row loads stalls until data drains, and
-  // compute must be able to start as soon as the first rows arrive.
-  uint32_t* xlds = lds + kThreads;  // after the list
-  stage_x_pairs<LPR>(xs, xlds, nchunks);  // its barrier also publishes the list
+  __syncthreads();  // publishes the list
   if (stamp) meta->spec_stamp[sw][2] = wall_clock64();
   if (total == 0) return;  // workgroup-uniform
 
