@@ -180,7 +180,7 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
   // rows in flight per group (16-lane groups: twice the groups, and more
   // rows in flight spill registers)
   constexpr int D = LPR >= 32 ? 3 : 1;
-  __shared__ uint32_t wcnt[kWaves];
+  __shared__ uint32_t lcount;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -202,26 +202,28 @@ DIP_DEV void spec_rows(const uint16_t* __restrict__ g, int n, const SpecArgs& sp
   // load of g is even issued; this way both are in flight together
   const uint32_t sk = sp.state[threadIdx.x & ((uint32_t)sp.hidden >> 30)];
   __builtin_amdgcn_sched_barrier(0);
+  // the list's length, zero before any wave claims its part
+  if (tid == 0) lcount = 0u;
+  __syncthreads();
   // x pairs are staged before any row load is issued (with the whole chip
   // streaming, issuing a wave's row loads stalls until data drains, and
   // compute must be able to start as soon as the first rows arrive), and
-  // while g is still in flight: the barrier after the counts publishes them
+  // while g is still in flight: the barrier after the list publishes them
   uint32_t* xlds = lds + kThreads;  // after the list
   stage_x_pairs<LPR, false>(xs, xlds, nchunks);
   const bool f = c < c1 && (gb & 0x7FFFu) >= sk;
   const uint64_t m = __ballot(f);
-  if (lane == 0) wcnt[wave] = (uint32_t)__popcll(m);
-  __syncthreads();
   if (stamp) meta->spec_stamp[sw][1] = wall_clock64();
-  int base = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int v = (int)wcnt[w];
-    base += w < wave ? v : 0;
-    total += v;
-  }
-  if (f) lds[base + __popcll(m & ((1ull << lane) - 1ull))] = (uint32_t)c | (gb << 16);
-  __syncthreads();  // publishes the list
+  // each wave claims its part of the list with one LDS atomic, in whatever
+  // order the waves get there: which group computes which channel's h then
+  // varies from call to call, the h values do not (each is one row's dot
+  // product in a fixed order)
+  uint32_t wbase = 0;
+  if (lane == 0 && m) wbase = atomicAdd(&lcount, (uint32_t)__popcll(m));
+  wbase = __shfl(wbase, 0, 64);
+  if (f) lds[wbase + __popcll(m & ((1ull << lane) - 1ull))] = (uint32_t)c | (gb << 16);
+  __syncthreads();  // publishes the list and x's pairs
+  const int total = (int)lcount;
   if (stamp) meta->spec_stamp[sw][2] = wall_clock64();
   if (total == 0) return;  // workgroup-uniform
 
