@@ -13,8 +13,9 @@
 //     branches would make it wait for everything.
 //   * Workgroups are 256 threads (plan_rowdot): a Qwen3-32B gate runs exactly
 //     2 per CU, 512 workgroups of 8 groups, split over two tiers (the first
-//     256 workgroups 9 rows per group, the rest 3-4: gate_tier_rows); its up
-//     gather 480 of 8 groups x 4 rows.
+//     256 workgroups 9 rows per group, the rest 3-4: gate_tier_rows; the
+//     Qwen3-8B gate likewise 4 and 2); its up gather 480 of 8 groups x 4
+//     rows.
 //   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
 //     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
 //     touches no LDS; otherwise each lane builds its own pairs from global
@@ -238,11 +239,38 @@ int gate_occupancy(int rows) {
   return cache[rows] - 1;
 }
 
+// The SiLU gate at two workgroups per CU, split over two tiers.  The first
+// workgroup each CU receives (blockIdx < CUs) wins its SIMDs' issue
+// arbitration over the second: on the Qwen3-32B gate at an even split (6-7
+// rows per lane group in both) the first tier ends at about 9.7 us and the
+// second at about 12 us.  Giving the first tier about 0.7 of the rows per
+// group-column ends them together:
+//   * Qwen3-32B (hidden 5120, 25600 rows = 12.5 per group-column on 256
+//     CUs): 9 and 3.5 rows, 13.5 -> 12.9-13.2 us per launch (8, 8.5 or 9.5
+//     rows in the first tier gained less or lost);
+//   * Qwen3-8B (hidden 4096, 12288 rows = 6 per group-column): 4 and 2 rows
+//     at two workgroups per CU instead of 2 rows in each of three, 7.3-7.6
+//     -> 7.0-7.1 us (3.5 : 2.5 and 4.5 : 1.5, whose second tier ends on a
+//     partly clamped row, were slower than the even split).
+// Every row is still one group's dot product in the same order, so g is
+// bit for bit the even split's.  Returns the rows per group of the first
+// tier for a gate of `chunks` 32-column chunks (32-lane groups), 0 where
+// no split was measured.
+int gate_tier_rows(int nrows, int chunks) {
+  if (!tuning(DIP_TUNE_GATE_TIERS)) return 0;
+  const long long g = (long long)device_cus() * 8;  // 32-lane groups per tier
+  if (chunks == 160 && nrows > 12 * g && nrows <= 13 * g) return 9;
+  if (chunks == 128 && nrows == 6 * g) return 4;
+  return 0;
+}
+
 // Workgroups per CU of a row-dot grid: the tuning knob when set, else for
-// the SiLU gate three where the instance three workgroups per CU would pick
-// still fits three at once (the Qwen3-8B gate: 2 rows per group, 97 VGPRs;
-// 8.0 -> 7.4 us), else two (the Qwen3-32B gate would need 5 rows per group
-// at 231 VGPRs, two waves per SIMD: 13.5 -> 17.2 us); every other grid two.
+// the SiLU gate two where a two-tier split applies (gate_tier_rows, above),
+// three where the instance three workgroups per CU would pick still fits
+// three at once (the Qwen3-8B gate with its tiers off: 2 rows per group, 97
+// VGPRs; 8.0 -> 7.4 us against an even split at two), else two (the
+// Qwen3-32B gate would need 5 rows per group at 231 VGPRs, two waves per
+// SIMD: 13.5 -> 17.2 us); every other grid two.
 // The gate with the RMSNorm prologue keeps two: every workgroup normalises
 // x itself, and a third per CU cost more than it gained (the whole Qwen3-8B
 // model: 477 against 487 tok/s).
@@ -250,6 +278,7 @@ int rowdot_wpc(int nrows, int chunks, bool gate, bool norm) {
   const int t = tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
   if (t > 0) return t;
   if (!gate || norm) return 2;
+  if (gate_tier_rows(nrows, chunks)) return 2;
   int lpr = 0, occ = 0;
   if (chunks == 160) lpr = 32;
   else if (chunks == 128) lpr = 32;
@@ -262,37 +291,19 @@ int rowdot_wpc(int nrows, int chunks, bool gate, bool norm) {
   return occ >= 3 ? 3 : 2;
 }
 
-// The SiLU gate at two workgroups per CU, split over two tiers.  The first
-// workgroup each CU receives (blockIdx < CUs) wins its SIMDs' issue
-// arbitration over the second: on the Qwen3-32B gate at an even split (6-7
-// rows per group in both) the first tier ends at about 9.7 us and the second
-// at about 12 us.  Giving the first tier 9 rows per group and the second the
-// rest (3.5) ends them together: 13.5 -> 12.9-13.0 us per launch (the gate
-// stage timed in a graph; 8 or 8.5 rows in the first tier gained less, 9.5
-// lost).  Every row is still one group's dot product in the same order, so
-// g is bit for bit the even split's.  (The Qwen3-8B gate runs three per CU with 2 rows
-// per group, all in flight at once; 3/2/1 rows over its three tiers was
-// slower: a third row waits for a ring slot.)  Returns the rows per group
-// of the first tier, 0 for the even split.
-int gate_tier_rows(int nrows, int blocks, int groups) {
-  const int cus = device_cus();
-  if (!tuning(DIP_TUNE_GATE_TIERS) || blocks != 2 * cus) return 0;
-  const long long g = (long long)cus * groups;  // groups per tier
-  // the measured split: 9 rows per group in the first tier, at most 4 in the
-  // second (12 g < nrows <= 13 g)
-  return (nrows > 12 * g && nrows <= 13 * g) ? 9 : 0;
-}
-
 template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = false>
 void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   a.ngrp = p.blocks * p.groups;
   const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) + (NORM ? 16 : 0) : 0;
-  // (built for the measured width, hidden 5120)
-  if constexpr (SRC == kContig && EPI == kSilu && XS && !NORM && LPR == 32 && CH == 5) {
-    if (gate_tier_rows(a.nrows, p.blocks, p.groups) == 9) {
+  // the two-tier splits (built for the measured widths, hidden 5120 and 4096)
+  if constexpr (SRC == kContig && EPI == kSilu && XS && !NORM && LPR == 32 &&
+                (CH == 5 || CH == 4)) {
+    constexpr int R0 = CH == 5 ? 9 : 4, R1 = CH == 5 ? 4 : 2;
+    if (p.blocks == 2 * device_cus() && p.groups == 8 &&
+        gate_tier_rows(a.nrows, LPR * CH) == R0) {
       a.tier_wgs = p.blocks / 2;
-      a.tier_rows = 9 * a.tier_wgs * p.groups;
-      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, 9, false, 4>), dim3(p.blocks),
+      a.tier_rows = R0 * a.tier_wgs * p.groups;
+      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, R0, false, R1>), dim3(p.blocks),
                          dim3(p.groups * LPR), lds, stream, a);
       return;
     }

@@ -155,12 +155,15 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
  *                               on the channels at or above the magnitude of
  *                               rank k + inter * this / 1024 (0..1024) (8)
- *   DIP_TUNE_GATE_TIERS         1: a SiLU gate of hidden 5120 at two workgroups
- *                               per CU gives the first workgroup on each CU
- *                               9 rows per lane group and the second the rest
- *                               where 12 < rows / (8 * CUs) <= 13 (the
- *                               Qwen3-32B gate); 0: every group the same
- *                               rows.  Same bits either way. (1)
+ *   DIP_TUNE_GATE_TIERS         1: a SiLU gate runs two workgroups per CU
+ *                               and gives the first on each CU more rows per
+ *                               lane group than the second where a split was
+ *                               measured: hidden 5120 with 12 < rows /
+ *                               (8 * CUs) <= 13 (the Qwen3-32B gate: 9 and
+ *                               the rest), hidden 4096 with rows = 6 * 8 *
+ *                               CUs (the Qwen3-8B gate: 4 and 2); 0: every
+ *                               group the same rows.  Same bits either way.
+ *                               (1)
  * Knob 3 (a removed step-form switch) is not a knob.  dip_set_tuning and
  * dip_get_tuning return DIP_ERR_ARG for an unknown knob, dip_set_tuning also
  * for a value out of range.

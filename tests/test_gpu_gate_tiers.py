@@ -1,10 +1,12 @@
 """The SiLU gate's two-tier split (DIP_TUNE_GATE_TIERS, on by default): at
-hidden 5120 and two workgroups per CU, the first workgroup on each CU takes
-9 rows per lane group and the second the rest, for 12 < rows / (8 * CUs) <=
-13 (the Qwen3-32B gate).  Each row is still one group's dot product in the
-same order, so g must be bit for bit the even split's, at the row counts on
-both sides of that range; the even split is pinned to the oracle by the
-kernel tests, and the split's g is checked against the oracle here too."""
+two workgroups per CU, the first workgroup on each CU takes more rows per
+lane group than the second where a split was measured (hidden 5120 with
+12 < rows / (8 * CUs) <= 13: 9 rows and the rest, the Qwen3-32B gate;
+hidden 4096 with rows = 6 * 8 * CUs: 4 and 2, the Qwen3-8B gate).  Each row
+is still one group's dot product in the same order, so g must be bit for
+bit the even split's, at the row counts on both sides of each rule; the
+even split is pinned to the oracle by the kernel tests, and the split's g
+is checked against the oracle here too."""
 import numpy as np
 import pytest
 import torch
@@ -25,13 +27,15 @@ def _groups_per_tier():
     return torch.cuda.get_device_properties(0).multi_processor_count * 8
 
 
-@pytest.mark.parametrize("tier_units", [12, 12.0001, 12.5, 13, 13.0001])
-def test_gate_tiers_same_bits_as_even_split(K, tier_units):
+@pytest.mark.parametrize("hidden,tier_units", [(5120, 12), (5120, 12.0001), (5120, 12.5),
+                                               (5120, 13), (5120, 13.0001), (4096, 5.9995),
+                                               (4096, 6), (4096, 6.0001)])
+def test_gate_tiers_same_bits_as_even_split(K, hidden, tier_units):
     rows = int(np.ceil(tier_units * _groups_per_tier()))
-    print(f"gate tiers rows={rows} hidden=5120", flush=True)
+    print(f"gate tiers rows={rows} hidden={hidden}", flush=True)
     rng = np.random.default_rng(rows)
-    qw, sc = random_int4(rng, rows, 5120)
-    x = random_bf16(rng, 5120)
+    qw, sc = random_int4(rng, rows, hidden)
+    x = random_bf16(rng, hidden)
     qd, sd, xd = dev(qw), dev_bf16(sc), dev_bf16(x)
     assert K.get_tuning("gate_tiers") == 1
     split = K.int4_gemv(qd, sd, xd, act=1)
@@ -51,17 +55,19 @@ def test_gate_tiers_same_bits_as_even_split(K, tier_units):
     assert d.max() <= 1 and (d > 0).mean() < 1e-3
 
 
-def test_gate_tiers_in_the_decode_step(K):
-    """The speculative decode step at the Qwen3-32B shape: y, g, idx and h
-    with the split equal those with the even split, token after token."""
-    H, I, keep = 5120, 25600, 0.6
+@pytest.mark.parametrize("H,I", [(5120, 25600), (4096, 12288)])
+def test_gate_tiers_in_the_decode_step(K, H, I):
+    """The speculative decode step at the Qwen3-32B and Qwen3-8B shapes: y,
+    g, idx and h with the split equal those with the even split, token after
+    token."""
+    keep = 0.6
     L = O.make_layer(H, I, seed=11)
     D = {n: (dev_bf16(v) if v.dtype == np.uint16 else dev(v)) for n, v in L.items()}
     gm = K.scales_group_major(D["down_t_sc"])
     k = O.keep_count(I, keep)
     st = [K.mlp_state(torch.device("cuda:0")) for _ in range(2)]
     for tok in range(3):
-        print(f"gate tiers decode token {tok}", flush=True)
+        print(f"gate tiers decode H={H} token {tok}", flush=True)
         x = dev_bf16(O.make_x(H, seed=40 + tok))
         outs = []
         for tiers in (1, 0):
