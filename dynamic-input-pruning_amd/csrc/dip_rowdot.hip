@@ -295,15 +295,15 @@ template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = fals
 void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   a.ngrp = p.blocks * p.groups;
   const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) + (NORM ? 16 : 0) : 0;
-  // the two-tier splits (built for the measured widths, hidden 5120 and 4096)
-  if constexpr (SRC == kContig && EPI == kSilu && XS && !NORM && LPR == 32 &&
-                (CH == 5 || CH == 4)) {
+  // the two-tier splits (built for the measured widths, hidden 5120 and
+  // 4096; with or without the folded RMSNorm)
+  if constexpr (SRC == kContig && EPI == kSilu && XS && LPR == 32 && (CH == 5 || CH == 4)) {
     constexpr int R0 = CH == 5 ? 9 : 4, R1 = CH == 5 ? 4 : 2;
     if (p.blocks == 2 * device_cus() && p.groups == 8 &&
         gate_tier_rows(a.nrows, LPR * CH) == R0) {
       a.tier_wgs = p.blocks / 2;
       a.tier_rows = R0 * a.tier_wgs * p.groups;
-      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, R0, false, R1>), dim3(p.blocks),
+      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, R0, NORM, R1>), dim3(p.blocks),
                          dim3(p.groups * LPR), lds, stream, a);
       return;
     }

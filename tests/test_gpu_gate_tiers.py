@@ -82,3 +82,35 @@ def test_gate_tiers_in_the_decode_step(K, H, I):
         for name, a, b in zip(("y", "g", "idx", "h"), *outs):
             assert torch.equal(a, b), (name, tok)
         assert np.array_equal(outs[0][2].cpu().numpy(), O.topk_select(host_bf16(outs[0][1]), k))
+
+
+@pytest.mark.parametrize("H,I", [(5120, 25600), (4096, 12288)])
+def test_gate_tiers_with_the_folded_rmsnorm(K, H, I):
+    """The decode step with the post-attention RMSNorm folded into the gate
+    (the whole-model decode's MLP): the split and the even split give the
+    same y, g, idx, h, residual and x, token after token."""
+    L = O.make_layer(H, I, seed=13)
+    D = {n: (dev_bf16(v) if v.dtype == np.uint16 else dev(v)) for n, v in L.items()}
+    W = [D[n] for n in ("gate_qw", "gate_sc", "up_qw", "up_sc", "down_t_qw", "down_t_sc")]
+    gm = K.scales_group_major(D["down_t_sc"])
+    k = O.keep_count(I, 0.6)
+    gen = torch.Generator(device="cuda").manual_seed(H)
+    w = (1 + 0.1 * torch.randn(H, device="cuda", generator=gen)).to(torch.bfloat16)
+    st = [K.mlp_state(torch.device("cuda:0")) for _ in range(2)]
+    for tok in range(3):
+        print(f"gate tiers rmsnorm decode H={H} token {tok}", flush=True)
+        res = (torch.randn(H, device="cuda", generator=gen) * 3).to(torch.bfloat16)
+        add = torch.randn(H, device="cuda", generator=gen).to(torch.bfloat16)
+        outs = []
+        for tiers in (1, 0):
+            K.set_tuning("gate_tiers", tiers)
+            try:
+                res_out, x_out = torch.empty_like(res), torch.empty_like(res)
+                o = K.mlp_decode_rmsnorm(*W, res, add, w, 1e-6, k, res_out=res_out, x_out=x_out,
+                                         state=st[tiers], down_t_sc_gm=gm)
+                outs.append([v.clone() for v in o[:4]] + [res_out, x_out])
+            finally:
+                K.set_tuning("gate_tiers", 1)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "g", "idx", "h", "res", "x"), *outs):
+            assert torch.equal(a, b), (name, tok)
