@@ -308,6 +308,42 @@ extern "C" int dip_host_gather_rows_multi(const void* const* src, void* const* d
   return gather_rows((int)npieces, src, dst, row_bytes, ids, n, src_rows, threads);
 }
 
+namespace {
+
+// The miss stream's second copy stream on the current device and the events
+// that fork it from and join it to the caller's stream (created on first
+// use, kept for the life of the process; default priority).
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+int side_stream(SideStream** out) {
+  static SideStream table[64];
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= 64) return DIP_ERR_ARG;
+  std::lock_guard<std::mutex> lock(mu);
+  SideStream& t = table[dev];
+  if (!t.stream) {
+    e = hipStreamCreateWithFlags(&t.stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&t.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&t.join, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      if (t.fork) (void)hipEventDestroy(t.fork);
+      if (t.stream) (void)hipStreamDestroy(t.stream);
+      t = SideStream{};
+      return (int)e;
+    }
+  }
+  *out = &t;
+  return DIP_OK;
+}
+
+}  // namespace
+
 extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
                                     void* const* dst, const int64_t* row_bytes, int64_t npieces,
                                     const int32_t* ids, int64_t n, int64_t src_rows,
@@ -320,12 +356,28 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
   st = check_pieces((int)npieces, pinned, dst, row_bytes, ids, n, src_rows);
   if (st || n == 0 || npieces == 0) return st;
   const int np = (int)npieces;
-  const int64_t nchunks = (n + chunk_rows - 1) / chunk_rows;
+  // Chunk c covers rows [cut[c], cut[c + 1]).  The first chunks ramp up from
+  // chunk_rows / 8, doubling, so the first copy starts after a short gather
+  // instead of a whole chunk's; the rest are chunk_rows.
+  std::vector<int64_t> cut{0};
+  for (int64_t c = std::max<int64_t>(chunk_rows / 8, 1); cut.back() < n;
+       c = std::min(chunk_rows, 2 * c))
+    cut.push_back(std::min(n, cut.back() + c));
+  const int64_t nchunks = (int64_t)cut.size() - 1;
   const int nt = std::min(pool_threads(threads, chunk_rows), HostPool::max_async_jobs());
   hipStream_t s = (hipStream_t)stream;
+  // Pieces [0, np/2) are copied on the caller's stream, the rest on a side
+  // stream, so two DMA engines share each chunk; the caller's stream waits
+  // for the side stream before the call returns.
+  // (without it, as without a device, the gather still runs to the end and
+  // the call returns the error, as for a failed copy)
+  SideStream* side = nullptr;
+  const int st_side = side_stream(&side);
+  hipStream_t ss = side ? side->stream : nullptr;
+  const int np0 = np / 2 > 0 ? np / 2 : np;  // one piece: the caller's stream alone
   std::vector<hipEvent_t> ev;
-  if (copy_ms) {
-    ev.assign(2 * nchunks, nullptr);
+  if (copy_ms && st_side == DIP_OK) {
+    ev.assign(4 * nchunks, nullptr);
     for (auto& e : ev)
       if (hipEventCreate(&e) != hipSuccess) {
         for (auto& e2 : ev)
@@ -341,41 +393,56 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
   // a named std::function: the workers call it until pool.finish() returns
   const std::function<void(int)> work = [&](int t) {
     for (int64_t c = 0; c < nchunks; ++c) {
-      const int64_t c0 = c * chunk_rows, c1 = std::min(n, c0 + chunk_rows);
+      const int64_t c0 = cut[c], c1 = cut[c + 1];
       const int64_t per = (c1 - c0 + nt - 1) / nt;
       copy_rows(np, src, pinned, row_bytes, ids, std::min(c1, c0 + t * per),
                 std::min(c1, c0 + (t + 1) * per));
       left[c].fetch_sub(1, std::memory_order_release);
     }
   };
+  // the side stream starts after the work already queued on the caller's
   hipError_t e = hipSuccess;
+  if (st_side == DIP_OK) {
+    e = hipEventRecord(side->fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(ss, side->fork, 0);
+  }
+  const bool copies = st_side == DIP_OK;
   HostPool& pool = HostPool::get();
   pool.start(nt, &work);
   for (int64_t c = 0; c < nchunks; ++c) {
     while (left[c].load(std::memory_order_acquire) != 0) std::this_thread::yield();
-    if (e != hipSuccess) continue;  // let the gather finish; report the first error
-    const int64_t c0 = c * chunk_rows, c1 = std::min(n, c0 + chunk_rows);
-    if (copy_ms) e = hipEventRecord(ev[2 * c], s);
+    // let the gather finish; report the first error
+    if (!copies || e != hipSuccess) continue;
+    const int64_t c0 = cut[c], c1 = cut[c + 1];
+    if (copy_ms) e = hipEventRecord(ev[4 * c], s);
+    if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[4 * c + 2], ss);
     for (int p = 0; p < np && e == hipSuccess; ++p) {
       const int64_t rb = row_bytes[p];
       if (rb == 0) continue;
       e = hipMemcpyAsync(static_cast<char*>(dst[p]) + c0 * rb,
                          static_cast<const char*>(pinned[p]) + c0 * rb,
-                         (size_t)((c1 - c0) * rb), hipMemcpyHostToDevice, s);
+                         (size_t)((c1 - c0) * rb), hipMemcpyHostToDevice, p < np0 ? s : ss);
     }
-    if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[2 * c + 1], s);
+    if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[4 * c + 1], s);
+    if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[4 * c + 3], ss);
   }
   pool.finish();
-  st = e == hipSuccess ? DIP_OK : (int)e;
-  if (copy_ms) {
+  if (copies && e == hipSuccess) e = hipEventRecord(side->join, ss);
+  if (copies && e == hipSuccess) e = hipStreamWaitEvent(s, side->join, 0);
+  st = !copies ? st_side : (e == hipSuccess ? DIP_OK : (int)e);
+  if (copy_ms && copies) {
+    // a chunk's copy time: the longer of its two streams' spans
     float total = 0.f;
     if (!st) {
       for (int64_t c = 0; c < nchunks && !st; ++c) {
-        float ms = 0.f;
-        hipError_t e2 = hipEventSynchronize(ev[2 * c + 1]);
-        if (e2 == hipSuccess) e2 = hipEventElapsedTime(&ms, ev[2 * c], ev[2 * c + 1]);
-        if (e2 != hipSuccess) st = (int)e2;
-        total += ms;
+        float ms[2] = {0.f, 0.f};
+        for (int k = 0; k < 2 && !st; ++k) {
+          hipError_t e2 = hipEventSynchronize(ev[4 * c + 2 * k + 1]);
+          if (e2 == hipSuccess) e2 = hipEventElapsedTime(&ms[k], ev[4 * c + 2 * k],
+                                                         ev[4 * c + 2 * k + 1]);
+          if (e2 != hipSuccess) st = (int)e2;
+        }
+        total += std::max(ms[0], ms[1]);
       }
     }
     for (auto& ev1 : ev) (void)hipEventDestroy(ev1);

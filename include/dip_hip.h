@@ -418,15 +418,20 @@ int dip_host_gather_rows_multi(const void* const* src, void* const* dst,
 /*
  * The cache-aware miss stream (dip_ca.py:146-156: pinned index_select, then
  * non_blocking H2D copies on a side stream) as one pipelined call: the ids
- * are taken in chunks of chunk_rows; for each chunk the library's host
- * threads gather the rows of every piece into pinned[p] (host, pinned, at
- * least n rows), and the calling thread queues the chunk's copies
- * pinned[p] -> dst[p] (device, at least n rows) on `stream` as soon as it is
- * gathered, so a chunk's copy runs while the next chunk is gathered.  Only
- * the calling thread makes HIP calls.  Returns once every copy is
- * queued (not finished).  When copy_ms is non-NULL, each chunk's copies are
- * bracketed by events, the call waits for them and writes the summed copy
- * time in milliseconds.  Returns DIP_OK, a DIP_ERR_* code or a hipError_t.
+ * are taken in chunks (the first ramping up from chunk_rows / 8, doubling,
+ * then chunk_rows each); for each chunk the library's host threads gather
+ * the rows of every piece into pinned[p] (host, pinned, at least n rows),
+ * and the calling thread queues the chunk's copies pinned[p] -> dst[p]
+ * (device, at least n rows) as soon as it is gathered, so a chunk's copy
+ * runs while the next chunk is gathered.  Pieces [0, npieces/2) are copied
+ * on `stream`, the rest on a library-owned second stream of the current
+ * device (so two DMA engines share each chunk), which `stream` waits for
+ * before the call returns: work queued on `stream` afterwards sees every
+ * copy.  Only the calling thread makes HIP calls.  Returns once every copy
+ * is queued (not finished).  When copy_ms is non-NULL, each chunk's copies
+ * on each stream are bracketed by events, the call waits for them and
+ * writes the sum over chunks of the longer stream's copy time, in
+ * milliseconds.  Returns DIP_OK, a DIP_ERR_* code or a hipError_t.
  */
 int dip_host_stream_rows(const void* const* src, void* const* pinned, void* const* dst,
                          const int64_t* row_bytes, int64_t npieces, const int32_t* ids,
