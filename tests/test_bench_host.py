@@ -45,7 +45,7 @@ def test_traffic_from_the_committed_summary():
     try:
         live = b.measured_traffic("qwen3-32b", 0.6, "gate_silu", K)
         assert live == int(table["gate_silu"])
-        assert b.measured_traffic("qwen3-8b", 0.6, "gate_silu", K) is None  # no summary
+        assert b.measured_traffic("qwen3-32b", 0.3, "gate_silu", K) is None  # no summary
         K.set_tuning("spec_margin", old + 1)  # other tuning: the figure no longer applies
         assert b.measured_traffic("qwen3-32b", 0.6, "gate_silu", K) is None
     finally:
