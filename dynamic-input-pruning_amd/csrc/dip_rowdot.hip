@@ -14,7 +14,7 @@
 //   * Workgroups are 256 threads (plan_rowdot): a Qwen3-32B gate runs exactly
 //     2 per CU, 512 workgroups of 8 groups, split over two tiers (the first
 //     256 workgroups 9 rows per group, the rest 3-4: gate_tier_rows; the
-//     Qwen3-8B gate likewise 4 and 2); its up gather 480 of 8 groups x 4
+//     Qwen3-8B gate likewise 5 and 1); its up gather 480 of 8 groups x 4
 //     rows.
 //   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
 //     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
@@ -248,10 +248,11 @@ int gate_occupancy(int rows) {
 //   * Qwen3-32B (hidden 5120, 25600 rows = 12.5 per group-column on 256
 //     CUs): 9 and 3.5 rows, 13.5 -> 12.9-13.2 us per launch (8, 8.5 or 9.5
 //     rows in the first tier gained less or lost);
-//   * Qwen3-8B (hidden 4096, 12288 rows = 6 per group-column): 4 and 2 rows
+//   * Qwen3-8B (hidden 4096, 12288 rows = 6 per group-column): 5 and 1 rows
 //     at two workgroups per CU instead of 2 rows in each of three, 7.3-7.6
-//     -> 7.0-7.1 us (3.5 : 2.5 and 4.5 : 1.5, whose second tier ends on a
-//     partly clamped row, were slower than the even split).
+//     -> 6.5-6.7 us (4 : 2 gave 7.0-7.1 us, one workgroup per CU with 6 rows
+//     6.9-7.0; 3.5 : 2.5, 4.5 : 1.5 and 5.5 : 0.5, whose second tier ends on
+//     a partly clamped row, were slower).
 // Every row is still one group's dot product in the same order, so g is
 // bit for bit the even split's.  Returns the rows per group of the first
 // tier for a gate of `chunks` 32-column chunks (32-lane groups), 0 where
@@ -260,7 +261,7 @@ int gate_tier_rows(int nrows, int chunks) {
   if (!tuning(DIP_TUNE_GATE_TIERS)) return 0;
   const long long g = (long long)device_cus() * 8;  // 32-lane groups per tier
   if (chunks == 160 && nrows > 12 * g && nrows <= 13 * g) return 9;
-  if (chunks == 128 && nrows == 6 * g) return 4;
+  if (chunks == 128 && nrows == 6 * g) return 5;
   return 0;
 }
 
@@ -298,7 +299,7 @@ void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   // the two-tier splits (built for the measured widths, hidden 5120 and
   // 4096; with or without the folded RMSNorm)
   if constexpr (SRC == kContig && EPI == kSilu && XS && LPR == 32 && (CH == 5 || CH == 4)) {
-    constexpr int R0 = CH == 5 ? 9 : 4, R1 = CH == 5 ? 4 : 2;
+    constexpr int R0 = CH == 5 ? 9 : 5, R1 = CH == 5 ? 4 : 1;
     if (p.blocks == 2 * device_cus() && p.groups == 8 &&
         gate_tier_rows(a.nrows, LPR * CH) == R0) {
       a.tier_wgs = p.blocks / 2;

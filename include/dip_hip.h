@@ -161,7 +161,7 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *                               measured: hidden 5120 with 12 < rows /
  *                               (8 * CUs) <= 13 (the Qwen3-32B gate: 9 and
  *                               the rest), hidden 4096 with rows = 6 * 8 *
- *                               CUs (the Qwen3-8B gate: 4 and 2); 0: every
+ *                               CUs (the Qwen3-8B gate: 5 and 1); 0: every
  *                               group the same rows.  Same bits either way.
  *                               (1)
  * Knob 3 (a removed step-form switch) is not a knob.  dip_set_tuning and

@@ -2,7 +2,7 @@
 two workgroups per CU, the first workgroup on each CU takes more rows per
 lane group than the second where a split was measured (hidden 5120 with
 12 < rows / (8 * CUs) <= 13: 9 rows and the rest, the Qwen3-32B gate;
-hidden 4096 with rows = 6 * 8 * CUs: 4 and 2, the Qwen3-8B gate).  Each row
+hidden 4096 with rows = 6 * 8 * CUs: 5 and 1, the Qwen3-8B gate).  Each row
 is still one group's dot product in the same order, so g must be bit for
 bit the even split's, at the row counts on both sides of each rule; the
 even split is pinned to the oracle by the kernel tests, and the split's g
