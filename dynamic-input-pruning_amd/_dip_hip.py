@@ -900,11 +900,14 @@ def host_gather_rows_multi(srcs, ids: torch.Tensor, dsts, threads: int = 8) -> N
 def host_stream_rows(srcs, ids: torch.Tensor, pinned, dsts, chunk_rows: int = 2048,
                      threads: int = 8, stream=None, timing: bool = False):
     """Gather rows srcs[p][ids] into the pinned host staging pinned[p] and
-    copy them to the device tensors dsts[p] (rows 0 .. n-1) on `stream`
-    (default: the current stream of dsts' device), chunk by chunk so that a
-    chunk's copy overlaps the next chunk's gather: the miss stream of
-    dip_ca.py:146-156.  Returns once the copies are queued; with timing,
-    waits for them and returns their summed copy time in ms (else None)."""
+    copy them to the device tensors dsts[p] (rows 0 .. n-1), chunk by chunk
+    so that a chunk's copy overlaps the next chunk's gather: the miss stream
+    of dip_ca.py:146-156.  The first half of the pieces is copied on
+    `stream` (default: the current stream of dsts' device), the rest on the
+    library's second copy stream, which `stream` then waits for.  Returns
+    once the copies are queued; with timing, waits for them and returns the
+    summed copy time in ms (per chunk, the longer of the two streams), else
+    None."""
     if ids.device.type != "cpu":
         raise RuntimeError("host_stream_rows takes host ids")
     ids = ids.to(torch.int32).contiguous()

@@ -400,15 +400,17 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
       left[c].fetch_sub(1, std::memory_order_release);
     }
   };
-  // the side stream starts after the work already queued on the caller's
+  const bool copies = st_side == DIP_OK;
   hipError_t e = hipSuccess;
-  if (st_side == DIP_OK) {
+  HostPool& pool = HostPool::get();
+  // Callers run one at a time from start() to finish(), so the side stream
+  // and its two events serve one call at a time.
+  pool.start(nt, &work);
+  // the side stream starts after the work already queued on the caller's
+  if (copies) {
     e = hipEventRecord(side->fork, s);
     if (e == hipSuccess) e = hipStreamWaitEvent(ss, side->fork, 0);
   }
-  const bool copies = st_side == DIP_OK;
-  HostPool& pool = HostPool::get();
-  pool.start(nt, &work);
   for (int64_t c = 0; c < nchunks; ++c) {
     while (left[c].load(std::memory_order_acquire) != 0) std::this_thread::yield();
     // let the gather finish; report the first error
@@ -426,9 +428,9 @@ extern "C" int dip_host_stream_rows(const void* const* src, void* const* pinned,
     if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[4 * c + 1], s);
     if (copy_ms && e == hipSuccess) e = hipEventRecord(ev[4 * c + 3], ss);
   }
-  pool.finish();
   if (copies && e == hipSuccess) e = hipEventRecord(side->join, ss);
   if (copies && e == hipSuccess) e = hipStreamWaitEvent(s, side->join, 0);
+  pool.finish();
   st = !copies ? st_side : (e == hipSuccess ? DIP_OK : (int)e);
   if (copy_ms && copies) {
     // a chunk's copy time: the longer of its two streams' spans

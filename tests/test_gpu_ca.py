@@ -136,3 +136,57 @@ def test_ca_module_all_hits_and_all_misses(layer, case):
                        L["down_t_sc"], id2slot, x, k, idx=idx_dev)
     assert buf.last_n_hit == ref["n_hit"] == (k if case == "all_hits" else 0)
     assert rel_err(host_bf16(y.reshape(-1)), ref["y_f64"]) < 1e-2
+
+
+def _bits(t):
+    """The tensor's storage as int64 values (an exact checksum of its bits)."""
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int8).to(torch.int64)
+
+
+def test_host_stream_rows_from_two_threads():
+    """Two host threads stream rows at once, each on its own stream into its
+    own device rows: every call gets exactly src[ids] (the calls take the
+    library's second copy stream one at a time), and work queued on each
+    caller's stream after its call sees all of that call's rows."""
+    import threading
+    import _dip_hip as K
+    d = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    rows, n = 4000, 1500
+    srcs = [torch.randint(-128, 127, (rows, 2560), dtype=torch.int8, generator=g),
+            torch.randn(rows, 40, generator=g).to(torch.bfloat16),
+            torch.randint(-128, 127, (rows, 2560), dtype=torch.int8, generator=g),
+            torch.randn(rows, 40, generator=g).to(torch.bfloat16)]
+    jobs = []
+    for j in range(2):
+        ids = torch.randperm(rows, generator=g)[:n].to(torch.int32)
+        pins = [torch.empty(n, *s.shape[1:], dtype=s.dtype).pin_memory() for s in srcs]
+        dsts = [torch.full((n, *s.shape[1:]), 3, dtype=s.dtype, device=d) for s in srcs]
+        jobs.append((ids, pins, dsts, torch.cuda.Stream(device=d)))
+    sums = [None, None]
+    errors = []
+
+    def run(j):
+        ids, pins, dsts, st = jobs[j]
+        try:
+            for rep in range(5):
+                with torch.cuda.stream(st):
+                    K.host_stream_rows(srcs, ids, pins, dsts, chunk_rows=512, threads=4)
+                    # queued after the call on the same stream: sees every row
+                    sums[j] = [_bits(t).sum() for t in dsts]
+                st.synchronize()
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    ts = [threading.Thread(target=run, args=(j,)) for j in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for j, (ids, pins, dsts, st) in enumerate(jobs):
+        for s_, d_, got in zip(srcs, dsts, sums[j]):
+            want = s_[ids.long()]
+            assert torch.equal(d_.cpu(), want), j
+            assert int(got.cpu()) == int(_bits(want).sum()), j
