@@ -797,7 +797,7 @@ def mlp_decode_rmsnorm(gate_qw, gate_sc, up_qw, up_sc, down_t_qw, down_t_sc, res
     return y, g, idx, h, x_out
 
 
-TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "gate_tiers": 4}
+TUNE = {"rowdot_wgs_per_cu": 0, "topk_stamps": 1, "spec_margin": 2, "row_tiers": 4}
 
 
 TIMELINE_KERNELS = {"gate": 0, "topk_spec_up": 1, "down_partials": 2, "down_reduce": 3}

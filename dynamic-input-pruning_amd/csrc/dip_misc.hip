@@ -198,7 +198,7 @@ extern "C" int dip_set_tuning(int knob, int value) {
     case DIP_TUNE_SPEC_MARGIN:
       if (value < 0 || value > 1024) return DIP_ERR_ARG;
       break;
-    case DIP_TUNE_GATE_TIERS:
+    case DIP_TUNE_ROW_TIERS:
       if (value != 0 && value != 1) return DIP_ERR_ARG;
       break;
     default:

@@ -13,9 +13,9 @@
 //     branches would make it wait for everything.
 //   * Workgroups are 256 threads (plan_rowdot): a Qwen3-32B gate runs exactly
 //     2 per CU, 512 workgroups of 8 groups, split over two tiers (the first
-//     256 workgroups 9 rows per group, the rest 3-4: gate_tier_rows; the
-//     Qwen3-8B gate likewise 5 and 1); its up gather 480 of 8 groups x 4
-//     rows.
+//     256 workgroups 9 rows per group, the rest 3-4: row_tier_rows; the
+//     Qwen3-8B gate and the Qwen3-32B q|k|v and o GEMVs likewise); its up
+//     gather 480 of 8 groups x 4 rows.
 //   * x pairs: XS (the hot widths): the workgroup stages all pairs once in LDS
 //     and each lane copies its CH chunks' pairs into VGPRs, so the row loop
 //     touches no LDS; otherwise each lane builds its own pairs from global
@@ -239,34 +239,40 @@ int gate_occupancy(int rows) {
   return cache[rows] - 1;
 }
 
-// The SiLU gate at two workgroups per CU, split over two tiers.  The first
-// workgroup each CU receives (blockIdx < CUs) wins its SIMDs' issue
-// arbitration over the second: on the Qwen3-32B gate at an even split (6-7
-// rows per lane group in both) the first tier ends at about 9.7 us and the
-// second at about 12 us.  Giving the first tier about 0.7 of the rows per
-// group-column ends them together:
-//   * Qwen3-32B (hidden 5120, 25600 rows = 12.5 per group-column on 256
-//     CUs): 9 and 3.5 rows, 13.5 -> 12.9-13.2 us per launch (8, 8.5 or 9.5
-//     rows in the first tier gained less or lost);
-//   * Qwen3-8B (hidden 4096, 12288 rows = 6 per group-column): 5 and 1 rows
-//     at two workgroups per CU instead of 2 rows in each of three, 7.3-7.6
-//     -> 6.5-6.7 us (4 : 2 gave 7.0-7.1 us, one workgroup per CU with 6 rows
-//     6.9-7.0; 3.5 : 2.5, 4.5 : 1.5 and 5.5 : 0.5, whose second tier ends on
-//     a partly clamped row, were slower).
-// Every row is still one group's dot product in the same order, so g is
-// bit for bit the even split's.  Returns the rows per group of the first
-// tier for a gate of `chunks` 32-column chunks (32-lane groups), 0 where
-// no split was measured.
-int gate_tier_rows(int nrows, int chunks) {
-  if (!tuning(DIP_TUNE_GATE_TIERS)) return 0;
-  const long long g = (long long)device_cus() * 8;  // 32-lane groups per tier
-  if (chunks == 160 && nrows > 12 * g && nrows <= 13 * g) return 9;
-  if (chunks == 128 && nrows == 6 * g) return 5;
+// Contiguous row-dot GEMVs at two workgroups per CU, split over two tiers.
+// The first workgroup each CU receives (blockIdx < CUs) wins its SIMDs'
+// issue arbitration over the second: on the Qwen3-32B gate at an even split
+// (6-7 rows per lane group in both) the first tier ends at about 9.7 us and
+// the second at about 12 us.  Giving the first tier more of the rows ends
+// them together (rows per group-column = nrows / groups per tier):
+//   * the Qwen3-32B SiLU gate (hidden 5120, 12.5 per group-column on 256
+//     CUs): 9 and 3.5 rows, 13.5 -> 12.9-13.2 us per launch (8, 8.5, 9.5,
+//     10 or 10.5 rows in the first tier gained less or lost);
+//   * the Qwen3-8B SiLU gate (hidden 4096, 6 per group-column): 5 and 1
+//     rows at two workgroups per CU instead of 2 rows in each of three,
+//     7.3-7.6 -> 6.5-6.7 us (4 : 2 gave 7.0-7.1 us, one workgroup per CU
+//     with 6 rows 6.9-7.0; 3.5 : 2.5, 4.5 : 1.5 and 5.5 : 0.5, whose second
+//     tier ends on a partly clamped row, were slower);
+//   * the Qwen3-32B q|k|v GEMV (10240 rows x 5120, 5 per group-column) and
+//     o projection (5120 rows x 8192, 64-lane groups, 5 per group-column):
+//     4 and 1 rows each, the whole-model decode 223.5-223.7 -> 228.8 tok/s
+//     (each alone 226.2-226.3).
+// Every row is still one group's dot product in the same order, so the
+// output is bit for bit the even split's.  Returns the rows per group of
+// the first tier for a GEMV of `chunks` 32-column chunks with `lpr`-lane
+// groups and epilogue `epi`, 0 where no split was measured.
+int row_tier_rows(int nrows, int lpr, int chunks, int epi) {
+  if (!tuning(DIP_TUNE_ROW_TIERS) || lpr <= 0) return 0;
+  const long long g = (long long)device_cus() * (kRowdotMaxThreads / lpr);  // groups per tier
+  if (epi == kSilu && lpr == 32 && chunks == 160 && nrows > 12 * g && nrows <= 13 * g) return 9;
+  if (epi == kSilu && lpr == 32 && chunks == 128 && nrows == 6 * g) return 5;
+  if (epi == kRaw && lpr == 32 && chunks == 160 && nrows == 5 * g) return 4;
+  if (epi == kRaw && lpr == 64 && chunks == 256 && nrows == 5 * g) return 4;
   return 0;
 }
 
 // Workgroups per CU of a row-dot grid: the tuning knob when set, else for
-// the SiLU gate two where a two-tier split applies (gate_tier_rows, above),
+// the SiLU gate two where a two-tier split applies (row_tier_rows, above),
 // three where the instance three workgroups per CU would pick still fits
 // three at once (the Qwen3-8B gate with its tiers off: 2 rows per group, 97
 // VGPRs; 8.0 -> 7.4 us against an even split at two), else two (the
@@ -279,7 +285,7 @@ int rowdot_wpc(int nrows, int chunks, bool gate, bool norm) {
   const int t = tuning(DIP_TUNE_ROWDOT_WGS_PER_CU);
   if (t > 0) return t;
   if (!gate || norm) return 2;
-  if (gate_tier_rows(nrows, chunks)) return 2;
+  if (row_tier_rows(nrows, chunks == 80 ? 16 : 32, chunks, kSilu)) return 2;
   int lpr = 0, occ = 0;
   if (chunks == 160) lpr = 32;
   else if (chunks == 128) lpr = 32;
@@ -296,12 +302,15 @@ template <int LPR, int CH, int SRC, int EPI, bool XS, int ROWS, bool NORM = fals
 void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   a.ngrp = p.blocks * p.groups;
   const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) + (NORM ? 16 : 0) : 0;
-  // the two-tier splits (built for the measured widths, hidden 5120 and
-  // 4096; with or without the folded RMSNorm)
-  if constexpr (SRC == kContig && EPI == kSilu && XS && LPR == 32 && (CH == 5 || CH == 4)) {
-    constexpr int R0 = CH == 5 ? 9 : 5, R1 = CH == 5 ? 4 : 1;
-    if (p.blocks == 2 * device_cus() && p.groups == 8 &&
-        gate_tier_rows(a.nrows, LPR * CH) == R0) {
+  // the two-tier splits, instantiated for the measured shapes only (with or
+  // without the folded RMSNorm where the width has it)
+  if constexpr (SRC == kContig && XS &&
+                ((EPI == kSilu && LPR == 32 && (CH == 5 || CH == 4)) ||
+                 (EPI == kRaw && ((LPR == 32 && CH == 5) || (LPR == 64 && CH == 4))))) {
+    constexpr int R0 = EPI == kSilu ? (CH == 5 ? 9 : 5) : 4;
+    constexpr int R1 = EPI == kSilu ? (CH == 5 ? 4 : 1) : 1;
+    if (p.blocks == 2 * device_cus() && p.groups * LPR == kRowdotMaxThreads &&
+        row_tier_rows(a.nrows, LPR, LPR * CH, EPI) == R0) {
       a.tier_wgs = p.blocks / 2;
       a.tier_rows = R0 * a.tier_wgs * p.groups;
       hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, R0, NORM, R1>), dim3(p.blocks),

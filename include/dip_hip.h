@@ -52,7 +52,7 @@ const char* dip_status_string(int status);
  * Library version as an integer (major * 10000 + minor * 100 + patch).  The
  * minor number changes whenever an entry point's argument list changes, so
  * a binding written against this header checks dip_version() == DIP_VERSION
- * before its first call.  0.3.3 adds the DIP_TUNE_GATE_TIERS knob (no
+ * before its first call.  0.3.3 adds the DIP_TUNE_ROW_TIERS knob (no
  * argument list changes).  0.3.2: the down and decode workspaces grow by
  * 8 KB of arrival counters (the sizes functions report it).  0.3.1 adds
  * dip_timeline_read.  0.3.0: the
@@ -155,15 +155,17 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *   DIP_TUNE_SPEC_MARGIN        speculative up rows: the next call speculates
  *                               on the channels at or above the magnitude of
  *                               rank k + inter * this / 1024 (0..1024) (8)
- *   DIP_TUNE_GATE_TIERS         1: a SiLU gate runs two workgroups per CU
+ *   DIP_TUNE_ROW_TIERS          1: a contiguous row-dot GEMV whose shape has a
+ *                               measured split runs two workgroups per CU
  *                               and gives the first on each CU more rows per
- *                               lane group than the second where a split was
- *                               measured: hidden 5120 with 12 < rows /
- *                               (8 * CUs) <= 13 (the Qwen3-32B gate: 9 and
- *                               the rest), hidden 4096 with rows = 6 * 8 *
- *                               CUs (the Qwen3-8B gate: 5 and 1); 0: every
- *                               group the same rows.  Same bits either way.
- *                               (1)
+ *                               lane group than the second: the SiLU gate at
+ *                               hidden 5120 with 12 < rows / (8 * CUs) <= 13
+ *                               (9 and the rest) and at hidden 4096 with
+ *                               rows = 6 * 8 * CUs (5 and 1); the plain GEMV
+ *                               at 5120 columns with rows = 5 * 8 * CUs and
+ *                               at 8192 columns with rows = 5 * 4 * CUs (4
+ *                               and 1); 0: every group the same rows.  Same
+ *                               bits either way. (1)
  * Knob 3 (a removed step-form switch) is not a knob.  dip_set_tuning and
  * dip_get_tuning return DIP_ERR_ARG for an unknown knob, dip_set_tuning also
  * for a value out of range.
@@ -172,7 +174,7 @@ enum {
   DIP_TUNE_ROWDOT_WGS_PER_CU = 0,
   DIP_TUNE_TOPK_STAMPS = 1,
   DIP_TUNE_SPEC_MARGIN = 2,
-  DIP_TUNE_GATE_TIERS = 4,
+  DIP_TUNE_ROW_TIERS = 4,
   DIP_TUNE_COUNT = 5
 };
 int dip_set_tuning(int knob, int value);

@@ -1,12 +1,15 @@
-"""The SiLU gate's two-tier split (DIP_TUNE_GATE_TIERS, on by default): at
-two workgroups per CU, the first workgroup on each CU takes more rows per
-lane group than the second where a split was measured (hidden 5120 with
-12 < rows / (8 * CUs) <= 13: 9 rows and the rest, the Qwen3-32B gate;
-hidden 4096 with rows = 6 * 8 * CUs: 5 and 1, the Qwen3-8B gate).  Each row
-is still one group's dot product in the same order, so g must be bit for
-bit the even split's, at the row counts on both sides of each rule; the
-even split is pinned to the oracle by the kernel tests, and the split's g
-is checked against the oracle here too."""
+"""The two-tier split of contiguous row-dot GEMVs (DIP_TUNE_ROW_TIERS, on by
+default): at two workgroups per CU, the first workgroup on each CU takes
+more rows per lane group than the second where a split was measured (the
+SiLU gate at hidden 5120 with 12 < rows / (8 * CUs) <= 13: 9 rows and the
+rest, the Qwen3-32B gate; at hidden 4096 with rows = 6 * 8 * CUs: 5 and 1,
+the Qwen3-8B gate; the plain GEMV at 5120 columns with rows = 5 * 8 * CUs
+and at 8192 columns with rows = 5 * 4 * CUs: 4 and 1, the Qwen3-32B q|k|v
+and o projections).  Each row is still one group's dot product in the same
+order, so the output must be bit for bit the even split's, at the row
+counts on both sides of each rule; the even split is pinned to the oracle
+by the kernel tests, and the split's outputs are checked against the oracle
+here too."""
 import numpy as np
 import pytest
 import torch
@@ -37,13 +40,13 @@ def test_gate_tiers_same_bits_as_even_split(K, hidden, tier_units):
     qw, sc = random_int4(rng, rows, hidden)
     x = random_bf16(rng, hidden)
     qd, sd, xd = dev(qw), dev_bf16(sc), dev_bf16(x)
-    assert K.get_tuning("gate_tiers") == 1
+    assert K.get_tuning("row_tiers") == 1
     split = K.int4_gemv(qd, sd, xd, act=1)
     try:
-        K.set_tuning("gate_tiers", 0)
+        K.set_tuning("row_tiers", 0)
         even = K.int4_gemv(qd, sd, xd, act=1)
     finally:
-        K.set_tuning("gate_tiers", 1)
+        K.set_tuning("row_tiers", 1)
     torch.cuda.synchronize()
     assert torch.equal(split, even)
     # against the oracle: SiLU of the pre-activation (within one bf16 ulp of
@@ -71,13 +74,13 @@ def test_gate_tiers_in_the_decode_step(K, H, I):
         x = dev_bf16(O.make_x(H, seed=40 + tok))
         outs = []
         for tiers in (1, 0):
-            K.set_tuning("gate_tiers", tiers)
+            K.set_tuning("row_tiers", tiers)
             try:
                 outs.append(K.mlp_decode(D["gate_qw"], D["gate_sc"], D["up_qw"], D["up_sc"],
                                          D["down_t_qw"], D["down_t_sc"], x, k, state=st[tiers],
                                          down_t_sc_gm=gm))
             finally:
-                K.set_tuning("gate_tiers", 1)
+                K.set_tuning("row_tiers", 1)
         torch.cuda.synchronize()
         for name, a, b in zip(("y", "g", "idx", "h"), *outs):
             assert torch.equal(a, b), (name, tok)
@@ -103,14 +106,45 @@ def test_gate_tiers_with_the_folded_rmsnorm(K, H, I):
         add = torch.randn(H, device="cuda", generator=gen).to(torch.bfloat16)
         outs = []
         for tiers in (1, 0):
-            K.set_tuning("gate_tiers", tiers)
+            K.set_tuning("row_tiers", tiers)
             try:
                 res_out, x_out = torch.empty_like(res), torch.empty_like(res)
                 o = K.mlp_decode_rmsnorm(*W, res, add, w, 1e-6, k, res_out=res_out, x_out=x_out,
                                          state=st[tiers], down_t_sc_gm=gm)
                 outs.append([v.clone() for v in o[:4]] + [res_out, x_out])
             finally:
-                K.set_tuning("gate_tiers", 1)
+                K.set_tuning("row_tiers", 1)
         torch.cuda.synchronize()
         for name, a, b in zip(("y", "g", "idx", "h", "res", "x"), *outs):
             assert torch.equal(a, b), (name, tok)
+
+
+@pytest.mark.parametrize("cols,units", [(5120, 5), (5120, 4.9995), (5120, 5.0005), (8192, 5),
+                                        (8192, 4.999), (8192, 5.001)])
+def test_plain_gemv_tiers_same_bits_as_even_split(K, cols, units):
+    """The plain GEMV (the q|k|v and o projections' kernel), and with the
+    folded RMSNorm where the width has it."""
+    lanes = 64 if cols == 8192 else 32
+    rows = int(np.ceil(units * _groups_per_tier() * 32 / lanes))
+    print(f"plain gemv tiers rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows + cols)
+    qw, sc = random_int4(rng, rows, cols)
+    x = random_bf16(rng, cols)
+    qd, sd, xd = dev(qw), dev_bf16(sc), dev_bf16(x)
+    gen = torch.Generator(device="cuda").manual_seed(cols)
+    add = torch.randn(cols, device="cuda", generator=gen).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(cols, device="cuda", generator=gen)).to(torch.bfloat16)
+    outs = []
+    for tiers in (1, 0):
+        K.set_tuning("row_tiers", tiers)
+        try:
+            o = [K.int4_gemv(qd, sd, xd)]
+            if cols == 5120:
+                o.append(K.int4_gemv_rmsnorm(qd, sd, xd, add, w, 1e-6))
+            outs.append(o)
+        finally:
+            K.set_tuning("row_tiers", 1)
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert rel_err(host_bf16(outs[0][0]), O.gemv_f64(qw, sc, x)) < 1e-2
