@@ -508,6 +508,10 @@ def timeline(args) -> int:
         shape["layers"] = args.layers
     print(f"[bench] timeline build, {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
           flush=True)
+    if args.keep >= 0.999:
+        print("--timeline reads the DIP step's kernels; keep >= 0.999 runs the dense route "
+              "(no top-k launch)", file=sys.stderr)
+        return 2
     stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0)
     gen = torch.Generator(device=dev).manual_seed(7)
     xs = (torch.randn(args.warmup + args.steps, stack.hidden, device=dev, generator=gen)
@@ -774,7 +778,9 @@ def main(argv=None):
             "weights": ("int4 g128 symmetric, bf16 scales; " +
                         ("N(0,0.02) draws" if not args.checkpoint else "from the checkpoint")),
             "activations": "bf16, fp32 accumulate",
-            "speculative_up": not args.no_spec,
+            "route": ("dense: every channel, no top-k (keep >= 0.999, as the reference "
+                      "routes it)" if stack.dense else "DIP: gate, top-k, k up and down rows"),
+            "speculative_up": not args.no_spec and not stack.dense,
             "down_scales": "row-major" if args.no_gm else "group-major copy",
             "down_reduce": "in the partials' launch (XCD-local)" if down_launches == 1
                            else "separate launch",

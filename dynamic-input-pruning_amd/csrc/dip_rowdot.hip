@@ -264,8 +264,11 @@ int gate_occupancy(int rows) {
 int row_tier_rows(int nrows, int lpr, int chunks, int epi) {
   if (!tuning(DIP_TUNE_ROW_TIERS) || lpr <= 0) return 0;
   const long long g = (long long)device_cus() * (kRowdotMaxThreads / lpr);  // groups per tier
-  if (epi == kSilu && lpr == 32 && chunks == 160 && nrows > 12 * g && nrows <= 13 * g) return 9;
-  if (epi == kSilu && lpr == 32 && chunks == 128 && nrows == 6 * g) return 5;
+  // the SiLU gate, and the up rows with h over every channel (the dense
+  // step's up launch: the gate's shape, rows gathered through idx)
+  const bool gate_like = epi == kSilu || epi == kH;
+  if (gate_like && lpr == 32 && chunks == 160 && nrows > 12 * g && nrows <= 13 * g) return 9;
+  if (gate_like && lpr == 32 && chunks == 128 && nrows == 6 * g) return 5;
   if (epi == kRaw && lpr == 32 && chunks == 160 && nrows == 5 * g) return 4;
   if (epi == kRaw && lpr == 64 && chunks == 256 && nrows == 5 * g) return 4;
   return 0;
@@ -303,17 +306,22 @@ void launch_variant(RowdotArgs a, const RowdotPlan& p, hipStream_t stream) {
   a.ngrp = p.blocks * p.groups;
   const size_t lds = XS ? x_pairs_lds_bytes(a.in_features) + (NORM ? 16 : 0) : 0;
   // the two-tier splits, instantiated for the measured shapes only (with or
-  // without the folded RMSNorm where the width has it)
-  if constexpr (SRC == kContig && XS &&
-                ((EPI == kSilu && LPR == 32 && (CH == 5 || CH == 4)) ||
-                 (EPI == kRaw && ((LPR == 32 && CH == 5) || (LPR == 64 && CH == 4))))) {
-    constexpr int R0 = EPI == kSilu ? (CH == 5 ? 9 : 5) : 4;
-    constexpr int R1 = EPI == kSilu ? (CH == 5 ? 4 : 1) : 1;
-    if (p.blocks == 2 * device_cus() && p.groups * LPR == kRowdotMaxThreads &&
+  // without the folded RMSNorm where the width has it; the gathered up + h
+  // rows take the gate's split whatever grid their own plan chose)
+  if constexpr (XS &&
+                ((SRC == kContig &&
+                  ((EPI == kSilu && LPR == 32 && (CH == 5 || CH == 4)) ||
+                   (EPI == kRaw && ((LPR == 32 && CH == 5) || (LPR == 64 && CH == 4))))) ||
+                 (SRC == kGather && EPI == kH && !NORM && LPR == 32 && (CH == 5 || CH == 4)))) {
+    constexpr int R0 = EPI == kRaw ? 4 : (CH == 5 ? 9 : 5);
+    constexpr int R1 = EPI == kRaw ? 1 : (CH == 5 ? 4 : 1);
+    const int cus = device_cus();
+    if ((SRC == kGather || p.blocks == 2 * cus) && p.groups * LPR == kRowdotMaxThreads &&
         row_tier_rows(a.nrows, LPR, LPR * CH, EPI) == R0) {
-      a.tier_wgs = p.blocks / 2;
-      a.tier_rows = R0 * a.tier_wgs * p.groups;
-      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, R0, NORM, R1>), dim3(p.blocks),
+      a.tier_wgs = cus;
+      a.tier_rows = R0 * cus * p.groups;
+      a.ngrp = 2 * cus * p.groups;
+      hipLaunchKernelGGL((rowdot_kernel<LPR, CH, SRC, EPI, XS, R0, NORM, R1>), dim3(2 * cus),
                          dim3(p.groups * LPR), lds, stream, a);
       return;
     }

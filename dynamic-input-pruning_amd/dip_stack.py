@@ -47,7 +47,10 @@ class DIPStack:
                  scales_gm: bool = True):
         self.hidden, self.inter, self.layers = hidden, inter, layers
         self.keep_ratio = keep_ratio
-        self.k = keep_count(inter, keep_ratio)
+        # keep >= 0.999: every channel, without a top-k, as the reference
+        # routes it (dip_stream_predispatch.py:177-179 -> _dense)
+        self.dense = keep_ratio >= 0.999
+        self.k = inter if self.dense else keep_count(inter, keep_ratio)
         self.device = torch.device(device)
         dev = self.device
         if weights is not None:  # per layer: gate/up/down_t qweight + scales on `device`
@@ -70,7 +73,8 @@ class DIPStack:
         self.x = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
         self.y = [torch.empty(hidden, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
         self.g = torch.empty(inter, dtype=torch.bfloat16, device=dev)
-        self.idx = torch.empty(self.k, dtype=torch.int32, device=dev)
+        self.idx = (torch.arange(inter, dtype=torch.int32, device=dev) if self.dense
+                    else torch.empty(self.k, dtype=torch.int32, device=dev))
         self.h = torch.empty(self.k, dtype=torch.bfloat16, device=dev)
         self.ws = torch.zeros(K.mlp_workspace_bytes(hidden, inter, self.k), dtype=torch.uint8,
                               device=dev)
@@ -98,7 +102,7 @@ class DIPStack:
         to 8192, on a full 256-CU gfx950: the rule of
         dip_int4_gather_down_by_channel), else 2 (partials + reduce)."""
         props = torch.cuda.get_device_properties(self.device)
-        xcd_local = (self.spec and self.w[0]["down_t_sc_gm"] is not None
+        xcd_local = ((self.spec or self.dense) and self.w[0]["down_t_sc_gm"] is not None
                      and self.hidden % 2048 == 0 and self.hidden <= 8192
                      and props.gcnArchName.startswith("gfx950")
                      and props.multi_processor_count == 256)
@@ -115,8 +119,36 @@ class DIPStack:
             if st is not None:
                 st.zero_()
 
+    def _dense_layer(self, lw, y, stream):
+        """One layer over every channel (keep >= 0.999): g = SiLU(gate x),
+        h[c] = bf16(g[c] * bf16(up[c] . x)) for every c (idx = 0..I-1), y =
+        down over every row with h by channel (the group-major scales when
+        present); the down workspace is the stack's own."""
+        lib = K.lib
+        H, I = self.hidden, self.inter
+        down_ws = self.ws.data_ptr() + 512
+        down_n = (lib.dip_gather_down_workspace_size(I, H) + 255) // 256 * 256
+        K._check(lib.dip_int4_gemv(lw["gate_qw"].data_ptr(), lw["gate_sc"].data_ptr(),
+                                   self.x.data_ptr(), self.g.data_ptr(), I, H, 1, stream),
+                 "dense gate")
+        K._check(lib.dip_up_gather_h(lw["up_qw"].data_ptr(), lw["up_sc"].data_ptr(),
+                                     self.x.data_ptr(), self.idx.data_ptr(), self.g.data_ptr(),
+                                     self.h.data_ptr(), I, H, I, stream), "dense up")
+        gm = lw["down_t_sc_gm"]
+        K._check(lib.dip_int4_gather_down_by_channel(
+            lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(),
+            None if gm is None else gm.data_ptr(), self.h.data_ptr(), self.idx.data_ptr(),
+            y.data_ptr(), None, I, H, I, ctypes.c_void_p(down_ws), down_n, stream),
+            "dense down")
+
     def run_token(self):
-        """All layers on self.x, in stream order (one dip_mlp_decode each)."""
+        """All layers on self.x, in stream order (one dip_mlp_decode each;
+        at keep >= 0.999 the three dense launches)."""
+        if self.dense:
+            st = torch.cuda.current_stream(self.device).cuda_stream
+            for lw, y in zip(self.w, self.y):
+                self._dense_layer(lw, y, st)
+            return
         for lw, y, st in zip(self.w, self.y, self.state):
             K.mlp_decode(lw["gate_qw"], lw["gate_sc"], lw["up_qw"], lw["up_sc"],
                          lw["down_t_qw"], lw["down_t_sc"], self.x, self.k, y=y, g=self.g,
@@ -148,7 +180,8 @@ class DIPStack:
         layer back to back (on the intermediates the last token left).  With
         speculation: gate_silu, gate_topk (gate + the top-k / speculative-up
         launch) and down_gather (h by channel); without: gate_silu, gate_topk,
-        up_gather_h and down_gather."""
+        up_gather_h and down_gather; at keep >= 0.999 (no top-k): gate_silu,
+        up_gather_h (every row) and down_gather (every row, h by channel)."""
         lib = K.lib
         H, I, k = self.hidden, self.inter, self.k
         # the decode step's workspace: [0, 512) top-k state | the down
@@ -186,6 +219,15 @@ class DIPStack:
                                              self.idx.data_ptr(), self.g.data_ptr(),
                                              self.h.data_ptr(), I, H, k, st), "up")
 
+        def down_dense(st):
+            for lw, y in zip(self.w, self.y):
+                gm = lw["down_t_sc_gm"]
+                K._check(lib.dip_int4_gather_down_by_channel(
+                    lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(),
+                    None if gm is None else gm.data_ptr(), self.h.data_ptr(),
+                    self.idx.data_ptr(), y.data_ptr(), None, I, H, k,
+                    ctypes.c_void_p(down_ws), down_n, st), "dense down")
+
         def down(st):
             for lw, y in zip(self.w, self.y):
                 if self.spec:
@@ -203,10 +245,13 @@ class DIPStack:
                                                       ctypes.c_void_p(down_ws), down_n, st),
                              "down")
 
-        stages = [("gate_silu", gate), ("gate_topk", gate_topk)]
-        if not self.spec:
-            stages.append(("up_gather_h", up))
-        stages.append(("down_gather", down))
+        if self.dense:  # every channel, no top-k
+            stages = [("gate_silu", gate), ("up_gather_h", up), ("down_gather", down_dense)]
+        else:
+            stages = [("gate_silu", gate), ("gate_topk", gate_topk)]
+            if not self.spec:
+                stages.append(("up_gather_h", up))
+            stages.append(("down_gather", down))
         graphs = {}
         for name, fn in stages:
             s = torch.cuda.Stream(device=self.device)
@@ -249,6 +294,8 @@ class DIPStack:
                 torch.cuda.synchronize(self.device)
                 means.append(e0.elapsed_time(e1) / (reps * self.layers))
             out[name] = statistics.median(means)
+        if self.dense:
+            return out
         topk = max(out.pop("gate_topk") - out["gate_silu"], 0.0)
         res = {"gate_silu": out["gate_silu"]}
         if self.spec:

@@ -148,3 +148,33 @@ def test_plain_gemv_tiers_same_bits_as_even_split(K, cols, units):
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     assert rel_err(host_bf16(outs[0][0]), O.gemv_f64(qw, sc, x)) < 1e-2
+
+
+@pytest.mark.parametrize("hidden,tier_units", [(5120, 12), (5120, 12.0001), (5120, 12.5),
+                                               (5120, 13), (4096, 6), (4096, 6.0001)])
+def test_up_h_tiers_same_bits_as_even_split(K, hidden, tier_units):
+    """The gathered up rows with h (dip_up_gather_h) take the gate's split at
+    the gate's row counts (the keep >= 0.999 step gathers every channel):
+    same bits as the even split, in a shuffled row order, and h = bf16(g[c] *
+    u[c]) against the oracle."""
+    k = int(np.ceil(tier_units * _groups_per_tier()))
+    print(f"up+h tiers k={k} hidden={hidden}", flush=True)
+    rng = np.random.default_rng(k + 1)
+    qw, sc = random_int4(rng, k, hidden)
+    x = random_bf16(rng, hidden)
+    g = random_bf16(rng, k)
+    idx = rng.permutation(k).astype(np.int32)
+    qd, sd, xd, gd = dev(qw), dev_bf16(sc), dev_bf16(x), dev_bf16(g)
+    idd = dev(idx)
+    assert K.get_tuning("row_tiers") == 1
+    split = K.up_gather_h(qd, sd, xd, idd, gd)
+    try:
+        K.set_tuning("row_tiers", 0)
+        even = K.up_gather_h(qd, sd, xd, idd, gd)
+    finally:
+        K.set_tuning("row_tiers", 1)
+    torch.cuda.synchronize()
+    assert torch.equal(split, even)
+    u = host_bf16(K.int4_gather_gemv(qd, sd, xd, idd))
+    assert rel_err(u, O.gemv_f64(qw, sc, x)[idx]) < 1e-2
+    assert np.array_equal(host_bf16(split), O.h_bf16(g[idx], u))

@@ -275,3 +275,41 @@ def test_stack_qwen3_32b_shape_two_layers(K):
             err = rel_err(host_bf16(stack.y[i]), ref["y_f64"])
             print(f"token {t} layer {i}: rel err {err:.2e}", flush=True)
             assert err < 1e-2, (t, i)
+
+
+def test_stack_dense_route_at_keep_one(K):
+    """keep >= 0.999 routes every layer to the dense computation, as the
+    reference does (dip_stream_predispatch.py:177-179 -> _dense): no top-k,
+    idx = 0..I-1, g and h = bf16(g * u) within the step's ulp bounds of the
+    oracle's dense forward, y within 1e-2 of it (and of the reference's literal
+    bf16-weight dense route) on every layer, replayed as one HIP graph; the
+    stage timing names the three dense launches."""
+    from dip_stack import DIPStack
+    H, I = 2560, 9728
+    stack = DIPStack(H, I, 2, 1.0, "cuda", seed=17, spec=True)
+    assert stack.dense and stack.k == I
+    host = [tuple(lw[n].cpu().numpy() if n.endswith("_qw") else host_bf16(lw[n])
+                  for n in ("gate_qw", "gate_sc", "up_qw", "up_sc", "down_t_qw", "down_t_sc"))
+            for lw in stack.w]
+    stack.capture()
+    for t in range(3):
+        x = O.make_x(H, seed=60 + t)
+        stack.step(torch.from_numpy(x.view(np.int16)).to("cuda").view(torch.bfloat16))
+        torch.cuda.synchronize()
+        assert np.array_equal(stack.idx.cpu().numpy(), np.arange(I, dtype=np.int32))
+        for i, w in enumerate(host):
+            ref = O.dense_forward(*w, x)
+            if i == len(host) - 1:  # g and h are shared: the last layer's
+                # g = silu(bf16(gate . x)): fp32 summation order may move it
+                # by up to 2 ulps; h = bf16(g * u) on the device's g
+                g_h = host_bf16(stack.g)
+                d = ulp_diff(g_h, ref["g"])
+                assert d.max() <= 2 and (d > 0).mean() < 5e-3, t
+                hd = ulp_diff(host_bf16(stack.h), O.h_bf16(g_h, ref["u"]))
+                assert (hd > 0).mean() < 0.02, t
+            err = rel_err(host_bf16(stack.y[i]), ref["y_f64"])
+            lit = rel_err(host_bf16(stack.y[i]), O.dense_literal_forward(*w, x)["y_f64"])
+            print(f"dense token {t} layer {i}: rel err {err:.2e} (literal {lit:.2e})", flush=True)
+            assert err < 1e-2 and lit < 2e-2, (t, i)
+    st = stack.stage_times_ms(reps=1, samples=1)
+    assert list(st) == ["gate_silu", "up_gather_h", "down_gather"]
