@@ -492,6 +492,10 @@ def timeline(args) -> int:
     workgroup start, the spread of workgroup ends and the gaps between the
     kernels, in microseconds from the gate's first workgroup start, next to
     the layer period (token time / layers).  Prints its own JSON line."""
+    if args.keep >= 0.999:
+        print("--timeline reads the DIP step's kernels; keep >= 0.999 runs the dense route "
+              "(no top-k launch)", file=sys.stderr)
+        return 2
     import numpy as np
     lib_path = ROOT / "dynamic-input-pruning_amd" / "libdip_hip_timeline.so"
     if not lib_path.exists():
@@ -508,10 +512,6 @@ def timeline(args) -> int:
         shape["layers"] = args.layers
     print(f"[bench] timeline build, {args.shape} stack {shape} keep={args.keep}", file=sys.stderr,
           flush=True)
-    if args.keep >= 0.999:
-        print("--timeline reads the DIP step's kernels; keep >= 0.999 runs the dense route "
-              "(no top-k launch)", file=sys.stderr)
-        return 2
     stack = DIPStack(shape["hidden"], shape["inter"], shape["layers"], args.keep, dev, seed=0)
     gen = torch.Generator(device=dev).manual_seed(7)
     xs = (torch.randn(args.warmup + args.steps, stack.hidden, device=dev, generator=gen)

@@ -87,3 +87,12 @@ def test_cache_aware_mode_refuses_the_profiler(monkeypatch, capsys):
     assert b.profiler_env() == ["ROCPROF_OUTPUT_PATH"]
     assert b.main(["--ca", "0.3"]) == 3
     assert "does not run under rocprofv3" in capsys.readouterr().err
+
+
+def test_timeline_refuses_the_dense_route(capsys):
+    """--timeline reads the DIP step's per-workgroup stamps; at keep >= 0.999
+    the stack runs the dense route (no top-k launch), so the mode exits with
+    status 2 before any GPU call."""
+    b = _bench()
+    assert b.main(["--timeline", "--keep", "1.0"]) == 2
+    assert "dense route" in capsys.readouterr().err
