@@ -164,7 +164,11 @@ int dip_int4_gather_down(const int8_t* down_t, const uint16_t* scales, const uin
  *                               rows = 6 * 8 * CUs (5 and 1); the plain GEMV
  *                               at 5120 columns with rows = 5 * 8 * CUs and
  *                               at 8192 columns with rows = 5 * 4 * CUs (4
- *                               and 1); 0: every group the same rows.  Same
+ *                               and 1); the gathered up rows with h
+ *                               (dip_up_gather_h) at the SiLU gate's row
+ *                               counts, whatever the grid its own plan
+ *                               picks (the split of the gate of that
+ *                               width); 0: every group the same rows.  Same
  *                               bits either way. (1)
  * Knob 3 (a removed step-form switch) is not a knob.  dip_set_tuning and
  * dip_get_tuning return DIP_ERR_ARG for an unknown knob, dip_set_tuning also
