@@ -382,14 +382,18 @@ def int4_gather_down_by_channel(down_t, scales, h_full, indices, out=None, h_out
                                 scales_gm=None):
     """y[o] = bf16(sum_j h_full[indices[j]] * (q*s)[indices[j], o]) with h
     indexed by channel (the decode step's form); h_out[j] (if given) gets
-    h_full[indices[j]].  scales_gm: the group-major copy of scales
+    h_full[indices[j]].  indices=None: every row in order (indices[j] = j,
+    k = rows).  scales_gm: the group-major copy of scales
     (scales_group_major), read instead of scales when given."""
     down_t, scales, rows, out_f = _weights(down_t, scales, "int4_gather_down_by_channel")
     scales_gm = _scales_gm(scales_gm, scales)
-    dev = _dev(down_t, scales, h_full, indices)
+    dev = _dev(down_t, scales, h_full, *(() if indices is None else (indices,)))
     h_full = _want(h_full.reshape(-1), torch.bfloat16, "h_full", (rows,))
-    indices = _indices(indices)
-    k = indices.numel()
+    if indices is None:
+        k = rows
+    else:
+        indices = _indices(indices)
+        k = indices.numel()
     if h_out is not None:
         h_out = _want(h_out, torch.bfloat16, "h_out", (k,))
     if out is None:

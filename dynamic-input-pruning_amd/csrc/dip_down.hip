@@ -237,8 +237,10 @@ DIP_DEV void down_xcd_tail(const DownGmArgs& a, int cb, float* red, uint32_t* la
 // XCD_REDUCE: the tiles of column block cb run as workgroups b with b % 8 ==
 // cb / (col_blocks / 8) (col_blocks a multiple of 8), and the last tile of
 // each column block writes its y (down_xcd_tail); otherwise tile (rb, cb)
-// runs with b % 8 == rb % 8 and a reduce kernel follows.
-template <bool XCD_REDUCE>
+// runs with b % 8 == rb % 8 and a reduce kernel follows.  IDENT: position j
+// is row j (no id list: the every-row down of a dense layer), so the row
+// loads do not wait for an id load.
+template <bool XCD_REDUCE, bool IDENT>
 __global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
   DIP_STAMP_START(g_stamps_down);
   constexpr int LPR = 8, kSlots = kThreads / LPR, kCols = LPR * kDownAcc, kWaves = kThreads / 64;
@@ -259,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void down_gm_kernel(DownGmArgs a) {
   const uint32_t lane_off = (uint32_t)cc0 * 16u;
   const int jl = rb * kRowsPerBlock + slot + l * kSlots;
   const bool live = jl < a.k;
-  const uint32_t raw = (uint32_t)a.sel[min(jl, a.k - 1)];
+  const uint32_t raw = IDENT ? (uint32_t)jl : (uint32_t)a.sel[min(jl, a.k - 1)];
   const uint32_t rid = !live ? kPadRow : (raw < (uint32_t)a.rows ? raw : kBadRow);
   const uint32_t r = rid >= kPadRow ? 0u : rid;  // bad and padding rows read row 0
   const uint32_t hb = a.h[r];
@@ -463,7 +465,8 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
                                 reinterpret_cast<uintptr_t>(sc_b)) & 3u) == 0;
   // one matrix whose every row offset fits 32 bits
   const bool off32 = src != kDual && (uint64_t)rows_a * row_bytes_of(out_features) <= 0xFFFFFFFFull;
-  if (sc_gm && src == kGather && h_by_row && lpr == 8 && off32) {
+  if (sc_gm && (src == kGather || src == kContig) && h_by_row && lpr == 8 && off32) {
+    const bool ident = src == kContig;
     DownGmArgs g{};
     g.qw = qw_a;
     g.sc_gm = sc_gm;
@@ -480,10 +483,16 @@ int run_down(int src, const int8_t* qw_a, const uint16_t* sc_a, int64_t rows_a,
       g.counters = static_cast<uint32_t*>(workspace);
       g.y = y;
       const int xblocks = kXcds * (a.col_blocks / kXcds) * a.row_blocks;
-      hipLaunchKernelGGL((down_gm_kernel<true>), dim3(xblocks), dim3(kThreads), 0, stream, g);
+      if (ident)
+        hipLaunchKernelGGL((down_gm_kernel<true, true>), dim3(xblocks), dim3(kThreads), 0, stream, g);
+      else
+        hipLaunchKernelGGL((down_gm_kernel<true, false>), dim3(xblocks), dim3(kThreads), 0, stream, g);
       return hip_status(hipGetLastError());
     }
-    hipLaunchKernelGGL((down_gm_kernel<false>), dim3(blocks), dim3(kThreads), 0, stream, g);
+    if (ident)
+      hipLaunchKernelGGL((down_gm_kernel<false, true>), dim3(blocks), dim3(kThreads), 0, stream, g);
+    else
+      hipLaunchKernelGGL((down_gm_kernel<false, false>), dim3(blocks), dim3(kThreads), 0, stream, g);
   } else if (sc_gm) {
     if (lpr == 8) launch_down<8, kScGm>(src, off32, a, blocks, stream);
     else launch_down<4, kScGm>(src, off32, a, blocks, stream);
@@ -524,8 +533,9 @@ extern "C" int dip_int4_gather_down_by_channel(const int8_t* down_t, const uint1
                                                uint16_t* y, uint16_t* h_out, int64_t rows,
                                                int64_t out_features, int64_t k, void* workspace,
                                                size_t ws_bytes, void* stream) {
-  if (k > 0 && !indices) return DIP_ERR_NULL;
-  return run_down(kGather, down_t, scales, rows, nullptr, nullptr, 0, h_full, indices, nullptr,
+  if (!indices && k > rows) return DIP_ERR_SHAPE;
+  return run_down(indices ? kGather : kContig, down_t, scales, rows, nullptr, nullptr, 0, h_full,
+                  indices, nullptr,
                   k, out_features, y, workspace, ws_bytes, (hipStream_t)stream, 1, h_out,
                   scales_gm);
 }

@@ -122,8 +122,8 @@ class DIPStack:
     def _dense_layer(self, lw, y, stream):
         """One layer over every channel (keep >= 0.999): g = SiLU(gate x),
         h[c] = bf16(g[c] * bf16(up[c] . x)) for every c (idx = 0..I-1), y =
-        down over every row with h by channel (the group-major scales when
-        present); the down workspace is the stack's own."""
+        down over every row in order (no id list; the group-major scales
+        when present); the down workspace is the stack's own."""
         lib = K.lib
         H, I = self.hidden, self.inter
         down_ws = self.ws.data_ptr() + 512
@@ -137,9 +137,8 @@ class DIPStack:
         gm = lw["down_t_sc_gm"]
         K._check(lib.dip_int4_gather_down_by_channel(
             lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(),
-            None if gm is None else gm.data_ptr(), self.h.data_ptr(), self.idx.data_ptr(),
-            y.data_ptr(), None, I, H, I, ctypes.c_void_p(down_ws), down_n, stream),
-            "dense down")
+            None if gm is None else gm.data_ptr(), self.h.data_ptr(), None, y.data_ptr(),
+            None, I, H, I, ctypes.c_void_p(down_ws), down_n, stream), "dense down")
 
     def run_token(self):
         """All layers on self.x, in stream order (one dip_mlp_decode each;
@@ -224,9 +223,9 @@ class DIPStack:
                 gm = lw["down_t_sc_gm"]
                 K._check(lib.dip_int4_gather_down_by_channel(
                     lw["down_t_qw"].data_ptr(), lw["down_t_sc"].data_ptr(),
-                    None if gm is None else gm.data_ptr(), self.h.data_ptr(),
-                    self.idx.data_ptr(), y.data_ptr(), None, I, H, k,
-                    ctypes.c_void_p(down_ws), down_n, st), "dense down")
+                    None if gm is None else gm.data_ptr(), self.h.data_ptr(), None,
+                    y.data_ptr(), None, I, H, k, ctypes.c_void_p(down_ws), down_n, st),
+                    "dense down")
 
         def down(st):
             for lw, y in zip(self.w, self.y):

@@ -319,6 +319,9 @@ int dip_gate_silu_topk_spec(const int8_t* gate_qw, const uint16_t* gate_sc,
  * dip_int4_gather_down with h indexed by channel: y = sum_j h_full[idx[j]] *
  * down_t[idx[j]] (the down half of dip_stream_predispatch.py:196-203 after
  * dip_gate_silu_topk_spec); h_out[j] = h_full[idx[j]] when h_out != NULL.
+ * indices == NULL: idx[j] = j for j < k (k <= rows), the every-row down of
+ * the keep >= 0.999 route (dip_stream_predispatch.py:177-179), whose row
+ * loads then wait for no id.
  * Same workspace as dip_int4_gather_down.  scales_gm (optional, may be
  * NULL): the same scales group-major, [out_features/128][rows]
  * (dip_scales_group_major); when given the kernel reads the scales there

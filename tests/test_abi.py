@@ -85,8 +85,9 @@ def test_argument_rejection_before_launch():
                                      None) == -3
     assert L.dip_gate_silu_topk_spec(p, p, p, p, p, p, p, p, 25600, 5120, 100, p, 8, p,
                                      None) == -5
-    assert L.dip_int4_gather_down_by_channel(p, p, None, p, None, p, None, 25600, 5120, 10, p,
-                                             need, None) == -1
+    # no indices: every row in order, so k may not exceed the rows
+    assert L.dip_int4_gather_down_by_channel(p, p, None, p, None, p, None, 10, 5120, 20, p,
+                                             need, None) == -2
     # group-major scales: NULL, shapes
     assert L.dip_scales_group_major(None, p, 10, 40, None) == -1
     assert L.dip_scales_group_major(p, p, -1, 40, None) == -2

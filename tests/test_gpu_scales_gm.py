@@ -104,3 +104,28 @@ def test_mlp_decode_same_bits_with_group_major_scales(K, H, I, keep, spec):
         for name, u, v in zip(("y", "g", "idx", "h"), a, b):
             assert torch.equal(_bits(u), _bits(v)), (name, tok)
         assert np.array_equal(b[2].cpu().numpy(), O.topk_select(host_bf16(b[1]), k))
+
+
+@pytest.mark.parametrize("rows,out_f", [(25600, 5120), (12288, 4096), (3000, 1152), (777, 1024)])
+@pytest.mark.parametrize("use_gm", [True, False], ids=["gm", "row-major"])
+def test_down_by_channel_without_indices_is_every_row(K, rows, out_f, use_gm):
+    """indices=None (the dense route's every-row down: position j is row j,
+    no id list) gives the bits of indices = 0..rows-1, with and without the
+    group-major scales, on the shapes of each down kernel (hidden 5120: the
+    reduce launch; 4096: the in-launch reduce on a full gfx950; 1152: four
+    lanes per row segment; 1024: one row block short), and y within 1e-2 of
+    the oracle's fp64 sum."""
+    print(f"down without indices rows={rows} out={out_f} gm={use_gm}", flush=True)
+    rng = np.random.default_rng(rows + out_f + use_gm)
+    qw, sc = random_int4(rng, rows, out_f)
+    h = random_bf16(rng, rows)
+    qd, sd, hd = dev(qw), dev_bf16(sc), dev_bf16(h)
+    gm = K.scales_group_major(sd) if use_gm else None
+    every = K.int4_gather_down_by_channel(qd, sd, hd, None, scales_gm=gm)
+    ar = torch.arange(rows, dtype=torch.int32, device="cuda")
+    ref = K.int4_gather_down_by_channel(qd, sd, hd, ar, scales_gm=gm)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(every), _bits(ref))
+    y64 = O.down_f64(qw, sc, h)
+    err = np.abs(O.bf16_to_f32(host_bf16(every)) - y64).max() / np.abs(y64).max()
+    assert err < 1e-2
