@@ -98,7 +98,7 @@ for _name, (_args, _res) in _SIGS.items():
 # The argument lists above follow this version of include/dip_hip.h
 # (DIP_VERSION); a library built from another one would be called with
 # shifted arguments, so it is refused here.
-ABI_VERSION = 303
+ABI_VERSION = 304
 if lib.dip_version() != ABI_VERSION:
     raise ImportError(f"{LIB_PATH} reports ABI version {lib.dip_version()}, these bindings "
                       f"are written for {ABI_VERSION}; rebuild the library")

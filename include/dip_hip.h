@@ -52,15 +52,16 @@ const char* dip_status_string(int status);
  * Library version as an integer (major * 10000 + minor * 100 + patch).  The
  * minor number changes whenever an entry point's argument list changes, so
  * a binding written against this header checks dip_version() == DIP_VERSION
- * before its first call.  0.3.3 adds the DIP_TUNE_ROW_TIERS knob (no
- * argument list changes).  0.3.2: the down and decode workspaces grow by
+ * before its first call.  0.3.4: dip_int4_gather_down_by_channel takes
+ * indices == NULL (every row in order; it was an error).  0.3.3 adds the
+ * DIP_TUNE_ROW_TIERS knob (no argument list changes).  0.3.2: the down and decode workspaces grow by
  * 8 KB of arrival counters (the sizes functions report it).  0.3.1 adds
  * dip_timeline_read.  0.3.0: the
  * measurement probes and the DIP_TUNE_STEP knob are gone; 0.2.0 added
  * down_t_sc_gm to the decode and gather-down entry points and g_len to
  * dip_ca_fused_gemv.
  */
-#define DIP_VERSION 303
+#define DIP_VERSION 304
 int dip_version(void);
 
 /* Highest row count the top-k supports (its keys are staged in LDS). */
