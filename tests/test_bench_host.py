@@ -96,3 +96,13 @@ def test_timeline_refuses_the_dense_route(capsys):
     b = _bench()
     assert b.main(["--timeline", "--keep", "1.0"]) == 2
     assert "dense route" in capsys.readouterr().err
+
+
+def test_traffic_of_the_dense_route():
+    """keep 1.0 (the dense route) has its own summary: the stages the dense
+    stack times, each at least the I weight rows it must read."""
+    b = _bench()
+    for stage in ("gate_silu", "up_gather_h", "down_gather"):
+        v = b.measured_traffic("qwen3-32b", 1.0, stage, K)
+        assert v is not None and v >= 25600 * 2640, stage
+    assert b.measured_traffic("qwen3-32b", 1.0, "topk_spec_up", K) is None
